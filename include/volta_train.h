@@ -1,0 +1,191 @@
+/*
+ * volta_train.h -- C ABI of the MI355X (gfx950) compile-train MLP step.
+ *
+ * The first six entry points are the exported symbols of the training
+ * library that Volta's `compile-train` generates; argument order, types and
+ * meaning are kept so a caller of that library can link this one instead:
+ *
+ *   Rust generator: /root/reference/src/engine/ir/codegen/mlp_train_rust_codegen.rs
+ *     volta_train_init        :640-667
+ *     volta_train_set_params  :669-675
+ *     volta_train_get_params  :677-684
+ *     volta_train_loss        :686
+ *     volta_train_free        :688-696
+ *     volta_train_step        :698-994
+ *   C generator export list:  /root/reference/src/engine/ir/codegen/mlp_train_codegen.rs:112-124
+ *
+ * Everything after those six is an extension under a new name.  The
+ * reference bakes the topology and the optimizer constants into the
+ * generated library; here they live in a `volta_mlp_spec`, set once per
+ * process with volta_train_configure() (or the VOLTA_MLP_SPEC environment
+ * variable) or passed per handle to volta_train_init_spec().
+ *
+ * Two libraries implement this header:
+ *   volta_amd/libvolta_hip.so      -- the product: HIP kernels for gfx950
+ *   oracle/liboracle_volta.so      -- the CPU restatement used as the checker
+ *
+ * Layout conventions (all row-major fp32, as in the reference):
+ *   W_i  [L[i] x L[i+1]],  b_i [L[i+1]],  X [B x L[0]],  Y [B x L[n]]
+ *
+ * Threading: a handle is not thread-safe (same as the reference).  Calls on
+ * different handles may run concurrently.
+ */
+#ifndef VOLTA_TRAIN_H
+#define VOLTA_TRAIN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct VoltaTrainHandle VoltaTrainHandle;
+
+/* ---------------------------------------------------------------------- */
+/* Reference ABI (six symbols)                                             */
+/* ---------------------------------------------------------------------- */
+
+/* Allocate a handle for a fixed batch size using the process-wide spec
+ * (volta_train_configure / VOLTA_MLP_SPEC).  Weights are drawn with the
+ * reference's LCG Xavier-uniform stream, seed 42, in layer order; biases and
+ * optimizer state start at zero (mlp_train_rust_codegen.rs:629-667).
+ * Returns NULL on failure (see volta_train_last_error). */
+VoltaTrainHandle* volta_train_init(int32_t batch);
+
+/* One training step on host arrays X [B x L0] and Y [B x Ln] with learning
+ * rate lr (mlp_train_rust_codegen.rs:698-994): forward, MSE loss, backward,
+ * optimizer update.  The GPU library may return before the step has
+ * finished on the device; volta_train_loss / volta_train_get_params /
+ * volta_train_sync wait for it.  X and Y may be reused by the caller as soon
+ * as the call returns. */
+void volta_train_step(VoltaTrainHandle* h, const float* X, const float* Y, float lr);
+
+/* Loss of the most recent step (mean over B*Ln for MSE, mean over B for
+ * softmax-CE).  mlp_train_rust_codegen.rs:686 */
+float volta_train_loss(VoltaTrainHandle* h);
+
+/* Fill wo[i] / bo[i] (i < n_weight_layers) with pointers to host arrays
+ * holding the current W_i and b_i.  The pointers stay valid until
+ * volta_train_free; the GPU library refreshes the host mirror on each call.
+ * mlp_train_rust_codegen.rs:677-684 */
+void volta_train_get_params(VoltaTrainHandle* h, float** wo, float** bo);
+
+/* Copy W_i [L[li] x L[li+1]] and b_i [L[li+1]] into layer li.  An
+ * out-of-range li is ignored, as in the reference (:669-675); the
+ * extension volta_train_status reports it. */
+void volta_train_set_params(VoltaTrainHandle* h, int32_t li, const float* w, const float* b);
+
+/* Release the handle and everything it owns.  NULL is allowed (:688-696). */
+void volta_train_free(VoltaTrainHandle* h);
+
+/* ---------------------------------------------------------------------- */
+/* Extensions (no counterpart among the reference's exports)               */
+/* ---------------------------------------------------------------------- */
+
+#define VOLTA_MAX_LAYER_SIZES 17 /* up to 16 weight layers */
+
+/* Hidden activation; names follow mlp_train_rust_codegen.rs:272-278. */
+enum volta_activation {
+  VOLTA_ACT_RELU = 0,
+  VOLTA_ACT_SIGMOID = 1,
+  VOLTA_ACT_TANH = 2,
+  VOLTA_ACT_LEAKY_RELU = 3,
+  VOLTA_ACT_SILU = 4,
+  VOLTA_ACT_GELU = 5 /* tanh approximation, :580-596 */
+};
+
+/* Optimizer; mlp_train_rust_codegen.rs:264-268. */
+enum volta_optimizer {
+  VOLTA_OPT_SGD = 0,
+  VOLTA_OPT_ADAM = 1,
+  VOLTA_OPT_ADAMW = 2,
+  VOLTA_OPT_ADAGRAD = 3
+};
+
+/* Loss head.  MSE is the generated step's loss (:792-798).  Softmax
+ * cross-entropy follows the IR runtime (interpreter.rs:762-812,
+ * autograd.rs:467-534) and takes int32 class labels. */
+enum volta_loss {
+  VOLTA_LOSS_MSE = 0,
+  VOLTA_LOSS_SOFTMAX_CE = 1
+};
+
+typedef struct volta_mlp_spec {
+  int32_t n_sizes;                       /* layer sizes incl. input and output, 2..17 */
+  int32_t sizes[VOLTA_MAX_LAYER_SIZES];  /* L[0..n_sizes-1] */
+  int32_t activation;                    /* enum volta_activation (hidden layers) */
+  int32_t optimizer;                     /* enum volta_optimizer */
+  int32_t loss;                          /* enum volta_loss */
+  /* Optimizer constants.  The reference hard-codes beta1=0.9, beta2=0.999,
+   * eps=1e-8 (Adam/AdamW/Adagrad) and weight_decay=0.01 (AdamW, weights
+   * only) at mlp_train_rust_codegen.rs:807-813; volta_mlp_spec_default
+   * fills exactly those. */
+  float beta1;
+  float beta2;
+  float eps;
+  float weight_decay;
+} volta_mlp_spec;
+
+/* Fill *spec with the reference's constants for the given topology. */
+void volta_mlp_spec_default(volta_mlp_spec* spec, int32_t n_sizes, const int32_t* sizes,
+                            int32_t activation, int32_t optimizer, int32_t loss);
+
+/* Parse "512-1024-1024-512-256-1:relu:adam[:mse|:ce][:eps=1e-10][:wd=0.01]
+ * [:beta1=..][:beta2=..]" into *spec.  Returns 0 on success. */
+int32_t volta_mlp_spec_parse(const char* text, volta_mlp_spec* spec);
+
+/* Set the process-wide spec used by volta_train_init(batch).  Without it,
+ * volta_train_init parses the VOLTA_MLP_SPEC environment variable.
+ * Returns 0 on success. */
+int32_t volta_train_configure(const volta_mlp_spec* spec);
+
+/* Allocate a handle for an explicit spec.  Returns NULL on failure. */
+VoltaTrainHandle* volta_train_init_spec(const volta_mlp_spec* spec, int32_t batch);
+
+/* Softmax cross-entropy step: labels are B int32 class indices in
+ * [0, L[n]).  Only valid when spec.loss == VOLTA_LOSS_SOFTMAX_CE. */
+void volta_train_step_labels(VoltaTrainHandle* h, const float* X, const int32_t* labels,
+                             float lr);
+
+/* Step on inputs that are already in device memory (GPU library only; the
+ * CPU oracle treats the pointers as host pointers).  Y is float [B x Ln]
+ * for MSE or int32 [B] for softmax-CE.  When X/Y are the handle's own
+ * resident batch buffers (volta_train_batch_buffers) no copy is made.
+ * Returns 0 on success. */
+int32_t volta_train_step_device(VoltaTrainHandle* h, const float* X, const void* Y, float lr);
+
+/* Device pointers of the handle's resident batch: X [B x L0] and the
+ * target buffer (float [B x Ln] or int32 [B]).  Returns 0 on success. */
+int32_t volta_train_batch_buffers(VoltaTrainHandle* h, float** X, void** Y);
+
+/* Wait until every enqueued step has finished.  Returns 0 or an error code. */
+int32_t volta_train_sync(VoltaTrainHandle* h);
+
+/* Status bits, sticky until volta_train_clear_status. */
+#define VOLTA_STATUS_NONFINITE_LOSS 1 /* a step produced a NaN/Inf loss */
+#define VOLTA_STATUS_BAD_ARGUMENT   2 /* an entry point rejected its arguments */
+#define VOLTA_STATUS_DEVICE_ERROR   4 /* a HIP call failed */
+int32_t volta_train_status(VoltaTrainHandle* h);
+void volta_train_clear_status(VoltaTrainHandle* h);
+
+/* Last error message of the calling thread ("" when none). */
+const char* volta_train_last_error(void);
+
+/* Number of weight layers (n_sizes - 1) and the batch size of a handle. */
+int32_t volta_train_num_layers(VoltaTrainHandle* h);
+int32_t volta_train_batch(VoltaTrainHandle* h);
+
+/* Optimizer state export/import for resumable Adam/AdamW/Adagrad
+ * (the generated library has no way to save it).  The state is laid out
+ * per layer as [m_W | m_b | v_W | v_b] (Adam/AdamW) or [G_W | G_b]
+ * (Adagrad), layers in order; SGD has no state.  `step` is the Adam step
+ * counter t.  volta_train_state_size returns the float count. */
+int64_t volta_train_state_size(VoltaTrainHandle* h);
+int32_t volta_train_get_state(VoltaTrainHandle* h, float* state, int64_t* step);
+int32_t volta_train_set_state(VoltaTrainHandle* h, const float* state, int64_t step);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VOLTA_TRAIN_H */

@@ -1,0 +1,726 @@
+// ===========================================================================
+// TEST INFRASTRUCTURE -- the CPU oracle.  Not part of the product.
+//
+// A CPU restatement of the training step that Volta's `compile-train`
+// generator emits (/root/reference/src/engine/ir/codegen/
+// mlp_train_rust_codegen.rs:249-997).  It exists to check the HIP library:
+// only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load
+// it.  It exports the same C ABI (include/volta_train.h) so one harness can
+// drive either library, plus a few oracle-only entry points (volta_oracle_*)
+// for an fp64 twin and for kernel-level checks.
+//
+// Fidelity rules followed here (and why):
+//  * fp32 arithmetic in the reference's expression order, no FMA contraction
+//    (Rust never contracts; the build uses -ffp-contract=off).
+//  * GEMMs sum over k in ascending order per output element.  The reference
+//    calls the `gemm` 0.19 crate, whose blocking order is not pinned by any
+//    reference test, so bit-equality with the reference DLL is not claimed.
+//  * Loss and bias-gradient reductions are sequential, as at :792-798 and
+//    :931-933.
+//  * Adam uses host powf bias correction (:803-811) and reproduces the
+//    vector/scalar-tail split of adam_update_slice (:341-388): elements in
+//    the last (n mod 8) positions of each buffer use ((1-b2)*g)*g, the rest
+//    (1-b2)*(g*g).
+//  * The fp64 twin ("truth") runs the same algorithm in double.
+//
+// Parity status of each function is recorded next to it ("pinned by ...").
+// ===========================================================================
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#include "../include/volta_train.h"
+#include "../volta_amd/csrc/spec.h"
+
+using volta::set_last_error;
+
+namespace {
+
+// --------------------------------------------------------------------------
+// Init: reference lcg_xavier_init, mlp_train_rust_codegen.rs:629-638, called
+// with one continuing stream seeded 42 over layers 0..n-1 (:653-658).
+// Pinned by tests/test_oracle.py (range, moments, stream continuity).
+// --------------------------------------------------------------------------
+void lcg_xavier_init(float* w, size_t n, int r, int c, uint64_t* rng) {
+  const float lim = std::sqrt(6.0f / ((float)r + (float)c));
+  for (size_t i = 0; i < n; ++i) {
+    *rng = *rng * 6364136223846793005ULL + 1442695040888963407ULL;
+    const float f = (float)((*rng >> 11) & ((1ULL << 53) - 1)) / (float)(1ULL << 53);
+    w[i] = (f * 2.0f - 1.0f) * lim;
+  }
+}
+
+// --------------------------------------------------------------------------
+// Activations, mlp_train_rust_codegen.rs:563-596 (forward) and :893-916
+// (backward).  ReLU is inline at :731 / :894.  Pinned by finite differences
+// of the fp64 twin and by the torch-made goldens (tests/golden/).
+// --------------------------------------------------------------------------
+template <typename T>
+inline T sigmoid(T x) { return T(1) / (T(1) + std::exp(-x)); }
+
+template <typename T>
+inline T act_fwd(int act, T x) {
+  switch (act) {
+    case VOLTA_ACT_RELU: return x > T(0) ? x : T(0);
+    case VOLTA_ACT_SIGMOID: return sigmoid(x);
+    case VOLTA_ACT_TANH: return std::tanh(x);
+    case VOLTA_ACT_LEAKY_RELU: return x > T(0) ? x : T(0.01) * x;
+    case VOLTA_ACT_SILU: return x * sigmoid(x);
+    case VOLTA_ACT_GELU: {
+      const T c = T(0.7978845608), k = T(0.044715);
+      const T v = c * (x + k * x * x * x);
+      return T(0.5) * x * (T(1) + std::tanh(v));
+    }
+  }
+  return x;
+}
+
+// Derivative factor.  relu/leaky/silu/gelu take the pre-activation, sigmoid
+// and tanh the post-activation value y (:893-916).
+template <typename T>
+inline T act_bwd(int act, T pre, T y) {
+  switch (act) {
+    case VOLTA_ACT_RELU: return pre > T(0) ? T(1) : T(0);
+    case VOLTA_ACT_SIGMOID: return y * (T(1) - y);
+    case VOLTA_ACT_TANH: return T(1) - y * y;
+    case VOLTA_ACT_LEAKY_RELU: return pre > T(0) ? T(1) : T(0.01);
+    case VOLTA_ACT_SILU: {
+      const T s = sigmoid(pre);
+      return s * (T(1) + pre * (T(1) - s));
+    }
+    case VOLTA_ACT_GELU: {
+      const T c = T(0.7978845608), k = T(0.044715);
+      const T v = c * (pre + k * pre * pre * pre);
+      const T t = std::tanh(v);
+      const T t2 = T(1) - t * t;
+      return T(0.5) * (T(1) + t) + T(0.5) * pre * t2 * c * (T(1) + T(3) * k * pre * pre);
+    }
+  }
+  return T(1);
+}
+
+inline bool needs_pre(int act) {
+  return act == VOLTA_ACT_RELU || act == VOLTA_ACT_LEAKY_RELU || act == VOLTA_ACT_SILU ||
+         act == VOLTA_ACT_GELU;
+}
+
+// --------------------------------------------------------------------------
+// GEMMs.  C = A·B with every C element summed over k in ascending order,
+// starting from 0 (the generator calls gemm with alpha=0, beta=1 so the
+// destination is not read: :310-317).  Pinned against the reference's own C
+// GEMM (gemm_shim.c, built by oracle/Makefile into oracle/_ref/) and exactly
+// on integer-valued inputs.
+// --------------------------------------------------------------------------
+
+// C[m x n] = A[m x k] · B[k x n]
+template <typename T>
+void gemm_nn(T* C, const T* A, const T* B, int m, int k, int n) {
+  const int JB = 512;
+#pragma omp parallel for schedule(static)
+  for (int i0 = 0; i0 < m; i0 += 4) {
+    const int i1 = i0 + 4 < m ? i0 + 4 : m;
+    for (int j0 = 0; j0 < n; j0 += JB) {
+      const int j1 = j0 + JB < n ? j0 + JB : n;
+      for (int i = i0; i < i1; ++i)
+        for (int j = j0; j < j1; ++j) C[(size_t)i * n + j] = T(0);
+      for (int p = 0; p < k; ++p) {
+        const T* Bp = B + (size_t)p * n;
+        for (int i = i0; i < i1; ++i) {
+          const T a = A[(size_t)i * k + p];
+          T* Ci = C + (size_t)i * n;
+          for (int j = j0; j < j1; ++j) Ci[j] = Ci[j] + a * Bp[j];
+        }
+      }
+    }
+  }
+}
+
+// C[m x n] = A^T · B with A stored [k x m] (sgemm_tn, :315-317).  The sum
+// over k is ascending for every element.
+template <typename T>
+void gemm_tn(T* C, const T* A, const T* B, int m, int k, int n) {
+  const int JB = 512;
+#pragma omp parallel for schedule(static)
+  for (int i0 = 0; i0 < m; i0 += 4) {
+    const int i1 = i0 + 4 < m ? i0 + 4 : m;
+    for (int j0 = 0; j0 < n; j0 += JB) {
+      const int j1 = j0 + JB < n ? j0 + JB : n;
+      for (int i = i0; i < i1; ++i)
+        for (int j = j0; j < j1; ++j) C[(size_t)i * n + j] = T(0);
+      for (int p = 0; p < k; ++p) {
+        const T* Bp = B + (size_t)p * n;
+        for (int i = i0; i < i1; ++i) {
+          const T a = A[(size_t)p * m + i];
+          T* Ci = C + (size_t)i * n;
+          for (int j = j0; j < j1; ++j) Ci[j] = Ci[j] + a * Bp[j];
+        }
+      }
+    }
+  }
+}
+
+// dst[cols x rows] = src[rows x cols]^T (fast_transpose, :389-440).
+template <typename T>
+void transpose(T* dst, const T* src, int rows, int cols) {
+#pragma omp parallel for schedule(static)
+  for (int j = 0; j < cols; ++j)
+    for (int i = 0; i < rows; ++i) dst[(size_t)j * rows + i] = src[(size_t)i * cols + j];
+}
+
+// --------------------------------------------------------------------------
+// The network state (Handle, :442-560) and the step (:698-994).
+// --------------------------------------------------------------------------
+template <typename T>
+struct Net {
+  volta_mlp_spec spec;
+  int B = 0, n = 0;
+  std::vector<int> L;
+  std::vector<std::vector<T>> w, b, dw, db, mw, vw, mb, vb, gw, gb;
+  std::vector<std::vector<T>> act, pre, delta;
+  std::vector<T> wt;  // transpose scratch for dX
+  uint64_t adam_step = 0;
+  T last_loss = T(0);
+
+  void alloc(const volta_mlp_spec& s, int batch) {
+    spec = s;
+    B = batch;
+    n = s.n_sizes - 1;
+    L.assign(s.sizes, s.sizes + s.n_sizes);
+    auto sz = [](std::vector<std::vector<T>>& v, int cnt) { v.assign(cnt, {}); };
+    sz(w, n); sz(b, n); sz(dw, n); sz(db, n); sz(mw, n); sz(vw, n); sz(mb, n); sz(vb, n);
+    sz(gw, n); sz(gb, n); sz(delta, n); sz(act, n + 1); sz(pre, n);
+    size_t maxw = 0;
+    for (int i = 0; i < n; ++i) {
+      const size_t r = L[i], c = L[i + 1];
+      w[i].assign(r * c, T(0)); b[i].assign(c, T(0));
+      dw[i].assign(r * c, T(0)); db[i].assign(c, T(0));
+      if (s.optimizer == VOLTA_OPT_ADAM || s.optimizer == VOLTA_OPT_ADAMW) {
+        mw[i].assign(r * c, T(0)); vw[i].assign(r * c, T(0));
+        mb[i].assign(c, T(0)); vb[i].assign(c, T(0));
+      }
+      if (s.optimizer == VOLTA_OPT_ADAGRAD) {
+        gw[i].assign(r * c, T(0)); gb[i].assign(c, T(0));
+      }
+      delta[i].assign((size_t)B * c, T(0));
+      if (i < n - 1) pre[i].assign((size_t)B * c, T(0));
+      maxw = r * c > maxw ? r * c : maxw;
+    }
+    for (int i = 0; i <= n; ++i) act[i].assign((size_t)B * L[i], T(0));
+    wt.assign(maxw, T(0));
+  }
+
+  // Forward through the hidden layers and the output layer (:702-789).
+  void forward(const T* X) {
+    std::memcpy(act[0].data(), X, sizeof(T) * (size_t)B * L[0]);
+    for (int i = 0; i < n; ++i) {
+      const int r = L[i], c = L[i + 1];
+      const bool last = i == n - 1;
+      T* dst = last ? act[n].data() : pre[i].data();
+      gemm_nn(dst, act[i].data(), w[i].data(), B, r, c);
+      for (int bi = 0; bi < B; ++bi)
+        for (int j = 0; j < c; ++j) dst[(size_t)bi * c + j] = dst[(size_t)bi * c + j] + b[i][j];
+      if (!last) {
+        T* a = act[i + 1].data();
+        const size_t cnt = (size_t)B * c;
+        for (size_t k = 0; k < cnt; ++k) a[k] = act_fwd<T>(spec.activation, dst[k]);
+      }
+    }
+  }
+
+  // MSE loss and seed gradient, :792-798.  Pinned by torch goldens.
+  void loss_mse(const T* Y) {
+    const size_t nt = (size_t)B * L[n];
+    const T ntf = T(nt);
+    T lacc = T(0);
+    T* d_out = delta[n - 1].data();
+    const T* yhat = act[n].data();
+    for (size_t k = 0; k < nt; ++k) {
+      const T d = yhat[k] - Y[k];
+      lacc = lacc + d * d;
+      d_out[k] = T(2) * d / ntf;
+    }
+    last_loss = lacc / ntf;
+  }
+
+  // Softmax cross-entropy from logits with one-hot targets given as labels:
+  // loss per interpreter.rs:762-812 (row max, sequential exp-sum, log-sum-exp,
+  // mean over B), gradient per autograd.rs:467-534 ((softmax - t) / B with
+  // softmax per kernels/reduce.rs:203-213).  Pinned by torch goldens and the
+  // uniform-logits closed form (loss = ln C).
+  void loss_ce(const int32_t* labels) {
+    const int C = L[n];
+    const T* z = act[n].data();
+    T* d_out = delta[n - 1].data();
+    T loss_sum = T(0);
+    const T bf = T(B);
+    std::vector<T> e(C);
+    for (int bi = 0; bi < B; ++bi) {
+      const T* zr = z + (size_t)bi * C;
+      T mx = -INFINITY;
+      for (int j = 0; j < C; ++j) mx = std::fmax(mx, zr[j]);
+      T sum_exp = T(0);
+      for (int j = 0; j < C; ++j) sum_exp = sum_exp + std::exp(zr[j] - mx);
+      const T lse = mx + std::log(sum_exp);
+      const int lab = labels[bi];
+      T sample = T(0);
+      for (int j = 0; j < C; ++j) {
+        const T t = j == lab ? T(1) : T(0);
+        sample = sample - t * (zr[j] - lse);
+      }
+      loss_sum = loss_sum + sample;
+      // gradient: softmax recomputed the way reduce::softmax does it
+      T s2 = T(0);
+      for (int j = 0; j < C; ++j) {
+        e[j] = std::exp(zr[j] - mx);
+        s2 = s2 + e[j];
+      }
+      for (int j = 0; j < C; ++j) {
+        const T t = j == lab ? T(1) : T(0);
+        d_out[(size_t)bi * C + j] = (e[j] / s2 - t) / bf;
+      }
+    }
+    last_loss = loss_sum / bf;
+  }
+
+  // Adam/AdamW element update, adam_update_slice :341-388.  `tail` selects
+  // the scalar-tail expression for v.
+  static inline void adam_elem(T* w, T* m, T* v, T g, T b1, T b2, T bc1, T bc2, T lr, T eps,
+                               T wd, bool tail) {
+    const T m1 = b1 * *m + (T(1) - b1) * g;
+    const T v1 = tail ? b2 * *v + (T(1) - b2) * g * g : b2 * *v + (T(1) - b2) * (g * g);
+    *m = m1;
+    *v = v1;
+    const T w0 = *w;
+    const T mhat = m1 / bc1;
+    const T vhat = v1 / bc2;
+    const T denom = std::sqrt(vhat) + eps;
+    *w = w0 - lr * (mhat / denom + wd * w0);
+  }
+
+  static void adam_update(T* w, T* m, T* v, const T* g, size_t cnt, T b1, T b2, T bc1, T bc2,
+                          T lr, T eps, T wd) {
+    const size_t vec_end = cnt - cnt % 8;
+    for (size_t k = 0; k < cnt; ++k)
+      adam_elem(w + k, m + k, v + k, g[k], b1, b2, bc1, bc2, lr, eps, wd, k >= vec_end);
+  }
+
+  // Adagrad, :967-985.
+  static void adagrad_update(T* w, T* G, const T* g, size_t cnt, T lr, T eps) {
+    for (size_t k = 0; k < cnt; ++k) {
+      const T gk = g[k];
+      G[k] = G[k] + gk * gk;
+      w[k] = w[k] - lr * gk / (std::sqrt(G[k]) + eps);
+    }
+  }
+
+  void backward_and_update(T lr) {
+    const int act_kind = spec.activation;
+    // Adam bias correction with f32 powf on the host step counter (:803-811).
+    T bc1 = T(1), bc2 = T(1);
+    const bool adam = spec.optimizer == VOLTA_OPT_ADAM || spec.optimizer == VOLTA_OPT_ADAMW;
+    if (adam) {
+      adam_step += 1;
+      const float t = (float)adam_step;
+      bc1 = T(1.0f - powf(spec.beta1, t));
+      bc2 = T(1.0f - powf(spec.beta2, t));
+      if (sizeof(T) == sizeof(double)) {
+        bc1 = T(1) - std::pow(T(spec.beta1), T(adam_step));
+        bc2 = T(1) - std::pow(T(spec.beta2), T(adam_step));
+      }
+    }
+    // Phase 1: deltas for every layer, then db (:819-934).
+    for (int i = n - 1; i >= 0; --i) {
+      const int r = L[i], c = L[i + 1];
+      const size_t cnt = (size_t)B * c;
+      T* d = delta[i].data();
+      if (i != n - 1) {
+        const T* p = pre[i].data();
+        const T* y = act[i + 1].data();
+        for (size_t k = 0; k < cnt; ++k) d[k] = d[k] * act_bwd<T>(act_kind, p[k], y[k]);
+      }
+      if (i > 0) {
+        // delta_{i-1} = delta_i · W_i^T, computed as (W_i · delta_i^T)^T in the
+        // reference (:919-929); summing over k ascending either way.
+        transpose(wt.data(), w[i].data(), r, c);  // wt [c x r]
+        gemm_nn(delta[i - 1].data(), d, wt.data(), B, c, r);
+      }
+      T* dbi = db[i].data();
+      for (int j = 0; j < c; ++j) dbi[j] = T(0);
+      for (int bi = 0; bi < B; ++bi)
+        for (int j = 0; j < c; ++j) dbi[j] = dbi[j] + d[(size_t)bi * c + j];
+    }
+    // Phase 2: parameter updates, last layer first (:957-993).
+    const T tlr = lr;
+    for (int i = n - 1; i >= 0; --i) {
+      const int r = L[i], c = L[i + 1];
+      const size_t rc = (size_t)r * c;
+      gemm_tn(dw[i].data(), act[i].data(), delta[i].data(), r, B, c);
+      if (adam) {
+        const T wd = spec.optimizer == VOLTA_OPT_ADAMW ? T(spec.weight_decay) : T(0);
+        adam_update(w[i].data(), mw[i].data(), vw[i].data(), dw[i].data(), rc, T(spec.beta1),
+                    T(spec.beta2), bc1, bc2, tlr, T(spec.eps), wd);
+        adam_update(b[i].data(), mb[i].data(), vb[i].data(), db[i].data(), (size_t)c,
+                    T(spec.beta1), T(spec.beta2), bc1, bc2, tlr, T(spec.eps), T(0));
+      } else if (spec.optimizer == VOLTA_OPT_ADAGRAD) {
+        adagrad_update(w[i].data(), gw[i].data(), dw[i].data(), rc, tlr, T(spec.eps));
+        adagrad_update(b[i].data(), gb[i].data(), db[i].data(), (size_t)c, tlr, T(spec.eps));
+      } else {
+        // sgd_fused_tn: W = 1*W + (-lr)*(act^T delta)  (:321-324, :986-991)
+        T* wi = w[i].data();
+        const T* g = dw[i].data();
+        const T nlr = -tlr;
+        for (size_t k = 0; k < rc; ++k) wi[k] = wi[k] + nlr * g[k];
+        for (int k = 0; k < c; ++k) b[i][k] = b[i][k] - tlr * db[i][k];
+      }
+    }
+  }
+};
+
+struct Handle {
+  int precision = 32;  // 32: reference-faithful fp32; 64: fp64 twin
+  Net<float> f;
+  Net<double> d;
+  std::vector<std::vector<float>> w_mirror, b_mirror;  // fp64 twin -> fp32 view
+  int32_t status = 0;
+  std::vector<double> xbuf, ybuf;
+};
+
+Handle* make_handle(const volta_mlp_spec* spec, int32_t batch, int precision) {
+  std::string why;
+  if (!spec || !volta::validate_spec(*spec, &why)) {
+    set_last_error("oracle init: invalid spec: " + why);
+    return nullptr;
+  }
+  if (batch <= 0) {
+    set_last_error("oracle init: batch must be > 0");
+    return nullptr;
+  }
+  auto h = std::make_unique<Handle>();
+  h->precision = precision;
+  const int n = spec->n_sizes - 1;
+  // Weights from the reference LCG stream (f32) for both precisions.
+  std::vector<std::vector<float>> w0(n);
+  uint64_t rng = 42;
+  for (int i = 0; i < n; ++i) {
+    const int r = spec->sizes[i], c = spec->sizes[i + 1];
+    w0[i].assign((size_t)r * c, 0.0f);
+    lcg_xavier_init(w0[i].data(), w0[i].size(), r, c, &rng);
+  }
+  if (precision == 64) {
+    h->d.alloc(*spec, batch);
+    for (int i = 0; i < n; ++i)
+      for (size_t k = 0; k < w0[i].size(); ++k) h->d.w[i][k] = w0[i][k];
+    h->w_mirror.resize(n);
+    h->b_mirror.resize(n);
+    for (int i = 0; i < n; ++i) {
+      h->w_mirror[i].assign(w0[i].size(), 0.0f);
+      h->b_mirror[i].assign((size_t)spec->sizes[i + 1], 0.0f);
+    }
+  } else {
+    h->f.alloc(*spec, batch);
+    for (int i = 0; i < n; ++i) h->f.w[i] = w0[i];
+  }
+  return h.release();
+}
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" {
+
+VoltaTrainHandle* volta_train_init_spec(const volta_mlp_spec* spec, int32_t batch) {
+  return reinterpret_cast<VoltaTrainHandle*>(make_handle(spec, batch, 32));
+}
+
+VoltaTrainHandle* volta_train_init(int32_t batch) {
+  volta_mlp_spec s;
+  if (!volta::resolve_default_spec(&s)) return nullptr;
+  return volta_train_init_spec(&s, batch);
+}
+
+// fp64 twin of the same algorithm ("truth" for error budgets).
+VoltaTrainHandle* volta_oracle_init_f64(const volta_mlp_spec* spec, int32_t batch) {
+  return reinterpret_cast<VoltaTrainHandle*>(make_handle(spec, batch, 64));
+}
+
+static Handle* H(VoltaTrainHandle* h) { return reinterpret_cast<Handle*>(h); }
+
+static void step_impl(Handle* h, const float* X, const float* Y, const int32_t* labels, float lr) {
+  if (h->precision == 64) {
+    Net<double>& net = h->d;
+    const size_t nx = (size_t)net.B * net.L[0];
+    h->xbuf.assign(X, X + nx);
+    net.forward(h->xbuf.data());
+    if (labels) {
+      net.loss_ce(labels);
+    } else {
+      const size_t ny = (size_t)net.B * net.L[net.n];
+      h->ybuf.assign(Y, Y + ny);
+      net.loss_mse(h->ybuf.data());
+    }
+    net.backward_and_update((double)lr);
+    if (!std::isfinite(net.last_loss)) h->status |= VOLTA_STATUS_NONFINITE_LOSS;
+  } else {
+    Net<float>& net = h->f;
+    net.forward(X);
+    if (labels) net.loss_ce(labels);
+    else net.loss_mse(Y);
+    net.backward_and_update(lr);
+    if (!std::isfinite(net.last_loss)) h->status |= VOLTA_STATUS_NONFINITE_LOSS;
+  }
+}
+
+void volta_train_step(VoltaTrainHandle* vh, const float* X, const float* Y, float lr) {
+  Handle* h = H(vh);
+  if (!h) return;
+  const volta_mlp_spec& s = h->precision == 64 ? h->d.spec : h->f.spec;
+  if (!X || !Y || s.loss != VOLTA_LOSS_MSE) {
+    h->status |= VOLTA_STATUS_BAD_ARGUMENT;
+    set_last_error("volta_train_step: null input or spec loss is not MSE");
+    return;
+  }
+  step_impl(h, X, Y, nullptr, lr);
+}
+
+void volta_train_step_labels(VoltaTrainHandle* vh, const float* X, const int32_t* labels,
+                             float lr) {
+  Handle* h = H(vh);
+  if (!h) return;
+  const volta_mlp_spec& s = h->precision == 64 ? h->d.spec : h->f.spec;
+  const int B = h->precision == 64 ? h->d.B : h->f.B;
+  if (!X || !labels || s.loss != VOLTA_LOSS_SOFTMAX_CE) {
+    h->status |= VOLTA_STATUS_BAD_ARGUMENT;
+    set_last_error("volta_train_step_labels: null input or spec loss is not softmax-CE");
+    return;
+  }
+  const int C = s.sizes[s.n_sizes - 1];
+  for (int i = 0; i < B; ++i)
+    if (labels[i] < 0 || labels[i] >= C) {
+      h->status |= VOLTA_STATUS_BAD_ARGUMENT;
+      set_last_error("volta_train_step_labels: label out of range");
+      return;
+    }
+  step_impl(h, X, nullptr, labels, lr);
+}
+
+int32_t volta_train_step_device(VoltaTrainHandle* vh, const float* X, const void* Y, float lr) {
+  Handle* h = H(vh);
+  if (!h) return -1;
+  const volta_mlp_spec& s = h->precision == 64 ? h->d.spec : h->f.spec;
+  if (s.loss == VOLTA_LOSS_SOFTMAX_CE)
+    volta_train_step_labels(vh, X, static_cast<const int32_t*>(Y), lr);
+  else
+    volta_train_step(vh, X, static_cast<const float*>(Y), lr);
+  return (h->status & VOLTA_STATUS_BAD_ARGUMENT) ? -1 : 0;
+}
+
+int32_t volta_train_batch_buffers(VoltaTrainHandle*, float**, void**) {
+  set_last_error("the CPU oracle has no resident device batch");
+  return -1;
+}
+
+float volta_train_loss(VoltaTrainHandle* vh) {
+  Handle* h = H(vh);
+  if (!h) return NAN;
+  return h->precision == 64 ? (float)h->d.last_loss : h->f.last_loss;
+}
+
+double volta_oracle_loss_f64(VoltaTrainHandle* vh) {
+  Handle* h = H(vh);
+  if (!h) return NAN;
+  return h->precision == 64 ? h->d.last_loss : (double)h->f.last_loss;
+}
+
+void volta_train_get_params(VoltaTrainHandle* vh, float** wo, float** bo) {
+  Handle* h = H(vh);
+  if (!h || !wo || !bo) return;
+  if (h->precision == 64) {
+    for (int i = 0; i < h->d.n; ++i) {
+      for (size_t k = 0; k < h->w_mirror[i].size(); ++k) h->w_mirror[i][k] = (float)h->d.w[i][k];
+      for (size_t k = 0; k < h->b_mirror[i].size(); ++k) h->b_mirror[i][k] = (float)h->d.b[i][k];
+      wo[i] = h->w_mirror[i].data();
+      bo[i] = h->b_mirror[i].data();
+    }
+  } else {
+    for (int i = 0; i < h->f.n; ++i) {
+      wo[i] = h->f.w[i].data();
+      bo[i] = h->f.b[i].data();
+    }
+  }
+}
+
+// fp64 parameters of layer li (either precision).
+int32_t volta_oracle_get_params_f64(VoltaTrainHandle* vh, int32_t li, double* w, double* b) {
+  Handle* h = H(vh);
+  if (!h) return -1;
+  const int n = h->precision == 64 ? h->d.n : h->f.n;
+  if (li < 0 || li >= n) return -1;
+  if (h->precision == 64) {
+    std::copy(h->d.w[li].begin(), h->d.w[li].end(), w);
+    std::copy(h->d.b[li].begin(), h->d.b[li].end(), b);
+  } else {
+    std::copy(h->f.w[li].begin(), h->f.w[li].end(), w);
+    std::copy(h->f.b[li].begin(), h->f.b[li].end(), b);
+  }
+  return 0;
+}
+
+void volta_train_set_params(VoltaTrainHandle* vh, int32_t li, const float* w, const float* b) {
+  Handle* h = H(vh);
+  if (!h) return;
+  const int n = h->precision == 64 ? h->d.n : h->f.n;
+  if (li < 0 || li >= n || !w || !b) {
+    h->status |= VOLTA_STATUS_BAD_ARGUMENT;
+    return;
+  }
+  if (h->precision == 64) {
+    for (size_t k = 0; k < h->d.w[li].size(); ++k) h->d.w[li][k] = w[k];
+    for (size_t k = 0; k < h->d.b[li].size(); ++k) h->d.b[li][k] = b[k];
+  } else {
+    std::copy(w, w + h->f.w[li].size(), h->f.w[li].begin());
+    std::copy(b, b + h->f.b[li].size(), h->f.b[li].begin());
+  }
+}
+
+void volta_train_free(VoltaTrainHandle* vh) { delete H(vh); }
+
+int32_t volta_train_sync(VoltaTrainHandle*) { return 0; }
+
+int32_t volta_train_status(VoltaTrainHandle* vh) {
+  Handle* h = H(vh);
+  return h ? h->status : VOLTA_STATUS_BAD_ARGUMENT;
+}
+
+void volta_train_clear_status(VoltaTrainHandle* vh) {
+  if (Handle* h = H(vh)) h->status = 0;
+}
+
+int32_t volta_train_num_layers(VoltaTrainHandle* vh) {
+  Handle* h = H(vh);
+  if (!h) return -1;
+  return h->precision == 64 ? h->d.n : h->f.n;
+}
+
+int32_t volta_train_batch(VoltaTrainHandle* vh) {
+  Handle* h = H(vh);
+  if (!h) return -1;
+  return h->precision == 64 ? h->d.B : h->f.B;
+}
+
+int64_t volta_train_state_size(VoltaTrainHandle* vh) {
+  Handle* h = H(vh);
+  if (!h || h->precision != 32) return -1;
+  const Net<float>& f = h->f;
+  int64_t per = 0;
+  for (int i = 0; i < f.n; ++i) per += (int64_t)f.L[i] * f.L[i + 1] + f.L[i + 1];
+  switch (f.spec.optimizer) {
+    case VOLTA_OPT_ADAM:
+    case VOLTA_OPT_ADAMW: return 2 * per;
+    case VOLTA_OPT_ADAGRAD: return per;
+    default: return 0;
+  }
+}
+
+int32_t volta_train_get_state(VoltaTrainHandle* vh, float* state, int64_t* step) {
+  Handle* h = H(vh);
+  if (!h || h->precision != 32) return -1;
+  Net<float>& f = h->f;
+  float* p = state;
+  for (int i = 0; i < f.n; ++i) {
+    if (f.spec.optimizer == VOLTA_OPT_ADAM || f.spec.optimizer == VOLTA_OPT_ADAMW) {
+      for (auto* v : {&f.mw[i], &f.mb[i], &f.vw[i], &f.vb[i]}) {
+        std::copy(v->begin(), v->end(), p);
+        p += v->size();
+      }
+    } else if (f.spec.optimizer == VOLTA_OPT_ADAGRAD) {
+      for (auto* v : {&f.gw[i], &f.gb[i]}) {
+        std::copy(v->begin(), v->end(), p);
+        p += v->size();
+      }
+    }
+  }
+  if (step) *step = (int64_t)f.adam_step;
+  return 0;
+}
+
+int32_t volta_train_set_state(VoltaTrainHandle* vh, const float* state, int64_t step) {
+  Handle* h = H(vh);
+  if (!h || h->precision != 32 || step < 0) return -1;
+  Net<float>& f = h->f;
+  const float* p = state;
+  for (int i = 0; i < f.n; ++i) {
+    if (f.spec.optimizer == VOLTA_OPT_ADAM || f.spec.optimizer == VOLTA_OPT_ADAMW) {
+      for (auto* v : {&f.mw[i], &f.mb[i], &f.vw[i], &f.vb[i]}) {
+        std::copy(p, p + v->size(), v->begin());
+        p += v->size();
+      }
+    } else if (f.spec.optimizer == VOLTA_OPT_ADAGRAD) {
+      for (auto* v : {&f.gw[i], &f.gb[i]}) {
+        std::copy(p, p + v->size(), v->begin());
+        p += v->size();
+      }
+    }
+  }
+  f.adam_step = (uint64_t)step;
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Kernel-level oracle entry points (fp32), used to check single HIP kernels.
+// ---------------------------------------------------------------------------
+
+// C[m x n] = op(A) · op(B); ta: A stored [k x m]; tb: B stored [n x k].
+void volta_oracle_gemm(float* C, const float* A, const float* B, int32_t m, int32_t k, int32_t n,
+                       int32_t ta, int32_t tb) {
+  std::vector<float> bt;
+  const float* Bn = B;
+  if (tb) {
+    bt.resize((size_t)k * n);
+    transpose(bt.data(), B, n, k);
+    Bn = bt.data();
+  }
+  if (ta) gemm_tn(C, A, Bn, m, k, n);
+  else gemm_nn(C, A, Bn, m, k, n);
+}
+
+// Adam/AdamW update of one buffer (adam_update, :326-388).
+void volta_oracle_adam(float* w, float* m, float* v, const float* g, int64_t cnt, float b1, float b2,
+                       float bc1, float bc2, float lr, float eps, float wd) {
+  Net<float>::adam_update(w, m, v, g, (size_t)cnt, b1, b2, bc1, bc2, lr, eps, wd);
+}
+
+void volta_oracle_adagrad(float* w, float* G, const float* g, int64_t cnt, float lr, float eps) {
+  Net<float>::adagrad_update(w, G, g, (size_t)cnt, lr, eps);
+}
+
+void volta_oracle_lcg_xavier(float* w, int64_t cnt, int32_t r, int32_t c, uint64_t* rng) {
+  lcg_xavier_init(w, (size_t)cnt, r, c, rng);
+}
+
+float volta_oracle_act_fwd(int32_t act, float x) { return act_fwd<float>(act, x); }
+float volta_oracle_act_bwd(int32_t act, float pre, float y) { return act_bwd<float>(act, pre, y); }
+double volta_oracle_act_fwd_f64(int32_t act, double x) { return act_fwd<double>(act, x); }
+double volta_oracle_act_bwd_f64(int32_t act, double pre, double y) {
+  return act_bwd<double>(act, pre, y);
+}
+
+int32_t volta_oracle_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+}  // extern "C"

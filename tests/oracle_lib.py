@@ -1,0 +1,57 @@
+"""Loader for the CPU oracle (test infrastructure; see oracle/volta_oracle.cpp)."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+from volta_amd.abi import CSpec, TrainLibrary
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_DIR = os.path.join(ROOT, "oracle")
+ORACLE_SO = os.path.join(ORACLE_DIR, "liboracle_volta.so")
+REF_SHIM_SO = os.path.join(ORACLE_DIR, "_ref", "libvolta_gemm_shim.so")
+
+_F = C.POINTER(C.c_float)
+_D = C.POINTER(C.c_double)
+
+ORACLE_EXTRA = {
+    "volta_oracle_init_f64": (C.c_void_p, [C.POINTER(CSpec), C.c_int32]),
+    "volta_oracle_loss_f64": (C.c_double, [C.c_void_p]),
+    "volta_oracle_get_params_f64": (C.c_int32, [C.c_void_p, C.c_int32, _D, _D]),
+    "volta_oracle_gemm": (None, [_F, _F, _F, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32]),
+    "volta_oracle_adam": (None, [_F, _F, _F, _F, C.c_int64] + [C.c_float] * 7),
+    "volta_oracle_adagrad": (None, [_F, _F, _F, C.c_int64, C.c_float, C.c_float]),
+    "volta_oracle_lcg_xavier": (None, [_F, C.c_int64, C.c_int32, C.c_int32, C.POINTER(C.c_uint64)]),
+    "volta_oracle_act_fwd": (C.c_float, [C.c_int32, C.c_float]),
+    "volta_oracle_act_bwd": (C.c_float, [C.c_int32, C.c_float, C.c_float]),
+    "volta_oracle_act_fwd_f64": (C.c_double, [C.c_int32, C.c_double]),
+    "volta_oracle_act_bwd_f64": (C.c_double, [C.c_int32, C.c_double, C.c_double]),
+    "volta_oracle_threads": (C.c_int32, []),
+}
+
+_cache = {}
+
+
+def build_oracle() -> None:
+    subprocess.run(["make", "-s", "-C", ORACLE_DIR, "oracle"], check=True)
+
+
+def load_oracle() -> TrainLibrary:
+    if "oracle" not in _cache:
+        if not os.path.exists(ORACLE_SO):
+            build_oracle()
+        _cache["oracle"] = TrainLibrary(ORACLE_SO, extra=ORACLE_EXTRA)
+    return _cache["oracle"]
+
+
+def load_ref_shim():
+    """The reference's own C GEMM (gemm_shim.c), or None when not built."""
+    if not os.path.exists(REF_SHIM_SO):
+        return None
+    lib = C.CDLL(REF_SHIM_SO)
+    for name in ("volta_gemm_f32", "volta_gemm_tn_f32", "volta_gemm_nt_f32"):
+        fn = getattr(lib, name)
+        fn.restype = None
+        fn.argtypes = [_F, _F, _F, C.c_int64, C.c_int64, C.c_int64]
+    return lib

@@ -1,0 +1,385 @@
+"""Pins the CPU oracle (CPU only, no GPU).
+
+Each check is chosen so that a plausible mistake in the oracle (a dropped
+term, a wrong sign or index, a transposed operand) fails one of them:
+  * torch-float64 goldens (independent autograd + torch.optim), including the
+    reference's own tiny-MLP literals (tests/pytorch_parity.rs:120-243);
+  * the reference's Adam known-answer test (optimizer.rs:831-862);
+  * closed forms: Adagrad step 1, CE on uniform logits = ln C;
+  * central finite differences of the loss against the fp64 twin's gradient;
+  * the reference's own C GEMM (gemm_shim.c, built into oracle/_ref/);
+  * exact integer GEMMs;
+  * the LCG Xavier stream's range, moments and continuity across layers.
+"""
+import ctypes as C
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+from tests.oracle_lib import load_ref_shim
+from volta_amd.abi import HEADER_SYMBOLS, MlpSpec, Trainer, fptr
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+GOLDEN = json.load(open(os.path.join(HERE, "golden", "train_step_golden.json")))["cases"]
+KAT = json.load(open(os.path.join(HERE, "golden", "optimizer_kat.json")))
+
+
+def spec_of(case):
+    return MlpSpec(case["sizes"], case["activation"], case["optimizer"], case["loss"],
+                   eps=case["eps"], weight_decay=case["weight_decay"])
+
+
+def oracle_trainer(lib, spec, batch, f64=False):
+    if f64:
+        cs = spec.to_c()
+        h = lib.lib.volta_oracle_init_f64(C.byref(cs), batch)
+        return Trainer(lib, spec, batch, handle=h)
+    return Trainer(lib, spec, batch)
+
+
+def load_inputs(case):
+    inp = case["inputs"]
+    sizes = case["sizes"]
+    ws = [np.array(w, np.float32).reshape(sizes[i], sizes[i + 1]) for i, w in enumerate(inp["w"])]
+    bs = [np.array(b, np.float32) for b in inp["b"]]
+    B = case["batch"]
+    Xs = [np.array(x, np.float32).reshape(B, sizes[0]) for x in inp["X"]]
+    if case["loss"] == "ce":
+        Ys = [np.array(y, np.int32) for y in inp["Y"]]
+    else:
+        Ys = [np.array(y, np.float32).reshape(B, sizes[-1]) for y in inp["Y"]]
+    return ws, bs, Xs, Ys
+
+
+def run_oracle_case(lib, case, f64=False):
+    spec = spec_of(case)
+    ws, bs, Xs, Ys = load_inputs(case)
+    t = oracle_trainer(lib, spec, case["batch"], f64=f64)
+    t.set_all_params(ws, bs)
+    losses = []
+    for s in range(case["steps"]):
+        t.step(Xs[s % len(Xs)], Ys[s % len(Ys)], case["lr"])
+        if f64:
+            losses.append(lib.lib.volta_oracle_loss_f64(t.h))
+        else:
+            losses.append(t.loss())
+    if f64:
+        out_w, out_b = [], []
+        for i, (r, c) in enumerate(spec.shapes()):
+            w = np.zeros(r * c, np.float64)
+            b = np.zeros(c, np.float64)
+            lib.lib.volta_oracle_get_params_f64(t.h, i, w.ctypes.data_as(C.POINTER(C.c_double)),
+                                                b.ctypes.data_as(C.POINTER(C.c_double)))
+            out_w.append(w)
+            out_b.append(b)
+    else:
+        ws2, bs2 = t.get_params()
+        out_w = [w.ravel().astype(np.float64) for w in ws2]
+        out_b = [b.astype(np.float64) for b in bs2]
+    t.close()
+    return np.array(losses), out_w, out_b
+
+
+@pytest.mark.parametrize("case", GOLDEN, ids=[c["name"] for c in GOLDEN])
+def test_oracle_f64_matches_torch_golden(oracle, case):
+    """The fp64 twin must agree with torch-float64 to ~1e-9: any wrong term in
+    the forward, backward, loss or optimizer shows up far above that."""
+    losses, ws, bs = run_oracle_case(oracle, case, f64=True)
+    exp = case["expected"]
+    np.testing.assert_allclose(losses, exp["losses"], rtol=1e-8, atol=1e-10)
+    for i in range(len(ws)):
+        np.testing.assert_allclose(ws[i], exp["w"][i], rtol=1e-8, atol=1e-10, err_msg=f"W{i}")
+        np.testing.assert_allclose(bs[i], exp["b"][i], rtol=1e-8, atol=1e-10, err_msg=f"b{i}")
+
+
+@pytest.mark.parametrize("case", GOLDEN, ids=[c["name"] for c in GOLDEN])
+def test_oracle_f32_matches_torch_golden(oracle, case):
+    """The fp32 oracle (reference arithmetic) stays within fp32 rounding of the
+    float64 result."""
+    losses, ws, bs = run_oracle_case(oracle, case, f64=False)
+    exp = case["expected"]
+    np.testing.assert_allclose(losses, exp["losses"], rtol=2e-5, atol=1e-6)
+    for i in range(len(ws)):
+        np.testing.assert_allclose(ws[i], exp["w"][i], rtol=2e-5, atol=2e-6, err_msg=f"W{i}")
+        np.testing.assert_allclose(bs[i], exp["b"][i], rtol=2e-5, atol=2e-6, err_msg=f"b{i}")
+
+
+def test_tiny_fixture_single_sgd_step_gradients(oracle):
+    """Reference parity fixture, one SGD step: recover the gradient from the
+    update (g = (w0 - w1)/lr) and compare with torch's step-0 gradients."""
+    case = next(c for c in GOLDEN if c["name"] == "tiny_relu_sgd_mse")
+    spec = spec_of(case)
+    ws, bs, Xs, Ys = load_inputs(case)
+    t = oracle_trainer(oracle, spec, 2, f64=True)
+    t.set_all_params(ws, bs)
+    t.step(Xs[0], Ys[0], case["lr"])
+    lr = float(np.float32(case["lr"]))  # the ABI takes lr as float32
+    g = case["expected"]["grads_step0"]
+    for i, (r, c) in enumerate(spec.shapes()):
+        w = np.zeros(r * c)
+        b = np.zeros(c)
+        oracle.lib.volta_oracle_get_params_f64(t.h, i, w.ctypes.data_as(C.POINTER(C.c_double)),
+                                               b.ctypes.data_as(C.POINTER(C.c_double)))
+        np.testing.assert_allclose((ws[i].ravel().astype(np.float64) - w) / lr, g["w"][i], rtol=1e-8, atol=1e-10)
+        np.testing.assert_allclose((bs[i].astype(np.float64) - b) / lr, g["b"][i], rtol=1e-8, atol=1e-10)
+    t.close()
+
+
+def test_adam_reference_kat(oracle):
+    """optimizer.rs:831-862: w=0.5, g=0.1, lr=1e-3, step 1 -> 0.499000."""
+    k = KAT["adam_step1"]
+    w = np.array([k["w"]], np.float32)
+    m = np.zeros(1, np.float32)
+    v = np.zeros(1, np.float32)
+    g = np.array([k["g"]], np.float32)
+    bc1 = np.float32(1.0) - np.float32(0.9) ** 1
+    bc2 = np.float32(1.0) - np.float32(0.999) ** 1
+    oracle.lib.volta_oracle_adam(fptr(w), fptr(m), fptr(v), fptr(g), 1, 0.9, 0.999, float(bc1), float(bc2),
+                                 k["lr"], 1e-8, 0.0)
+    assert abs(float(w[0]) - k["expected"]) < k["tol"]
+
+
+def test_adagrad_step1_closed_form(oracle):
+    """Adagrad from G=0: w -= lr*g/(|g|+eps), i.e. ~lr*sign(g)."""
+    rng = np.random.default_rng(0)
+    g = rng.standard_normal(1000).astype(np.float32)
+    w = rng.standard_normal(1000).astype(np.float32)
+    G = np.zeros(1000, np.float32)
+    w0 = w.copy()
+    oracle.lib.volta_oracle_adagrad(fptr(w), fptr(G), fptr(g), 1000, 0.01, 1e-10)
+    np.testing.assert_allclose(G, g * g, rtol=1e-7)
+    np.testing.assert_allclose(w0 - w, 0.01 * np.sign(g), rtol=1e-5)
+
+
+def test_adam_vector_tail_split(oracle):
+    """adam_update_slice (mlp_train_rust_codegen.rs:341-388) computes v with
+    (1-b2)*(g*g) in its 8-wide loop and ((1-b2)*g)*g in the scalar tail; the
+    oracle follows both.  Checked against numpy float32 arithmetic."""
+    n = 13
+    rng = np.random.default_rng(1)
+    g = rng.standard_normal(n).astype(np.float32) * np.float32(3.3)
+    v = np.abs(rng.standard_normal(n)).astype(np.float32)
+    w = rng.standard_normal(n).astype(np.float32)
+    m = rng.standard_normal(n).astype(np.float32)
+    b2 = np.float32(0.999)
+    one = np.float32(1)
+    v_vec = b2 * v + (one - b2) * (g * g)
+    v_tail = b2 * v + ((one - b2) * g) * g
+    oracle.lib.volta_oracle_adam(fptr(w), fptr(m), fptr(v), fptr(g), n, 0.9, 0.999, 0.1, 0.001, 1e-3, 1e-8, 0.0)
+    np.testing.assert_array_equal(v[:8], v_vec[:8])
+    np.testing.assert_array_equal(v[8:], v_tail[8:])
+
+
+def test_ce_uniform_logits_closed_form(oracle):
+    """All-zero weights/biases give uniform logits: loss = ln C exactly in
+    float64 and the output-bias gradient is (1/C - onehot)/B summed over B."""
+    sizes = [4, 3, 5]
+    B = 4
+    spec = MlpSpec(sizes, "relu", "sgd", "ce")
+    t = oracle_trainer(oracle, spec, B, f64=True)
+    for i, (r, c) in enumerate(spec.shapes()):
+        t.set_params(i, np.zeros((r, c), np.float32), np.zeros(c, np.float32))
+    X = np.ones((B, 4), np.float32)
+    lab = np.array([0, 1, 1, 4], np.int32)
+    t.step(X, lab, 1.0)
+    assert abs(oracle.lib.volta_oracle_loss_f64(t.h) - math.log(5)) < 1e-15
+    b = np.zeros(5)
+    w = np.zeros(15)
+    oracle.lib.volta_oracle_get_params_f64(t.h, 1, w.ctypes.data_as(C.POINTER(C.c_double)),
+                                           b.ctypes.data_as(C.POINTER(C.c_double)))
+    onehot = np.eye(5)[lab]
+    expected_db = ((0.2 - onehot) / B).sum(axis=0)
+    np.testing.assert_allclose(-b, expected_db, atol=1e-15)
+    t.close()
+
+
+@pytest.mark.parametrize("act", ["relu", "sigmoid", "tanh", "leaky_relu", "silu", "gelu"])
+@pytest.mark.parametrize("loss", ["mse", "ce"])
+def test_f64_gradient_matches_finite_differences(oracle, act, loss):
+    """Gradient recovered from one SGD step (lr=1) of the fp64 twin equals the
+    central finite difference of its loss (evaluated with lr=0 steps)."""
+    sizes = [3, 5, 4, 3]
+    B = 3
+    spec = MlpSpec(sizes, act, "sgd", loss)
+    rng = np.random.default_rng(7)
+    ws = [(rng.standard_normal((r, c)) * 0.7).astype(np.float32) for r, c in spec.shapes()]
+    bs = [(rng.standard_normal(c) * 0.2).astype(np.float32) for _, c in spec.shapes()]
+    X = rng.standard_normal((B, 3)).astype(np.float32)
+    Y = rng.integers(0, 3, B).astype(np.int32) if loss == "ce" else rng.standard_normal((B, 3)).astype(np.float32)
+
+    def loss_at(wlist, blist):
+        t = oracle_trainer(oracle, spec, B, f64=True)
+        for i in range(len(wlist)):
+            t.set_params(i, wlist[i], blist[i])
+        t.step(X, Y, 0.0)
+        val = oracle.lib.volta_oracle_loss_f64(t.h)
+        t.close()
+        return val
+
+    t = oracle_trainer(oracle, spec, B, f64=True)
+    t.set_all_params(ws, bs)
+    t.step(X, Y, 1.0)
+    grads_w = []
+    for i, (r, c) in enumerate(spec.shapes()):
+        w = np.zeros(r * c)
+        b = np.zeros(c)
+        oracle.lib.volta_oracle_get_params_f64(t.h, i, w.ctypes.data_as(C.POINTER(C.c_double)),
+                                               b.ctypes.data_as(C.POINTER(C.c_double)))
+        grads_w.append((ws[i].ravel().astype(np.float64) - w, bs[i].astype(np.float64) - b))
+    t.close()
+    # Perturbations must be float32-representable (set_params takes float32):
+    # use h = 2^-10 on weights that are multiples of 2^-10 after rounding.
+    h = 2.0 ** -10
+    for li in range(len(ws)):
+        for idx in [0, ws[li].size // 2, ws[li].size - 1]:
+            wp = [w.copy() for w in ws]
+            wm = [w.copy() for w in ws]
+            wp[li].ravel()[idx] += np.float32(h)
+            wm[li].ravel()[idx] -= np.float32(h)
+            hp = float(wp[li].ravel()[idx]) - float(ws[li].ravel()[idx])
+            hm = float(ws[li].ravel()[idx]) - float(wm[li].ravel()[idx])
+            fd = (loss_at(wp, bs) - loss_at(wm, bs)) / (hp + hm)
+            g = grads_w[li][0][idx]
+            # relu/leaky kinks are avoided by the random data; tolerance is
+            # the O(h^2) truncation error.
+            assert abs(fd - g) <= 2e-5 + 1e-3 * abs(g), (li, idx, fd, g)
+        bp = [b.copy() for b in bs]
+        bm = [b.copy() for b in bs]
+        bp[li][0] += np.float32(h)
+        bm[li][0] -= np.float32(h)
+        fd = (loss_at(ws, bp) - loss_at(ws, bm)) / (float(bp[li][0]) - float(bm[li][0]))
+        g = grads_w[li][1][0]
+        assert abs(fd - g) <= 2e-5 + 1e-3 * abs(g), (li, "b", fd, g)
+
+
+@pytest.mark.parametrize("m,k,n", [(5, 7, 3), (64, 33, 17), (70, 129, 96)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1)])
+def test_oracle_gemm_integer_exact(oracle, m, k, n, ta, tb):
+    """Integer-valued operands: every summation order gives the exact result."""
+    rng = np.random.default_rng(m * 1000 + k)
+    A = rng.integers(-8, 9, (k, m) if ta else (m, k)).astype(np.float32)
+    B = rng.integers(-8, 9, (n, k) if tb else (k, n)).astype(np.float32)
+    Cm = np.zeros((m, n), np.float32)
+    oracle.lib.volta_oracle_gemm(fptr(Cm), fptr(A), fptr(B), m, k, n, ta, tb)
+    ref = (A.T if ta else A).astype(np.int64) @ (B.T if tb else B).astype(np.int64)
+    np.testing.assert_array_equal(Cm, ref.astype(np.float32))
+
+
+def test_oracle_gemm_matches_reference_gemm_shim(oracle):
+    """The reference's own C GEMM (gemm_shim.c) vs the oracle on random
+    float32 data; skipped where oracle/_ref was not built."""
+    shim = load_ref_shim()
+    if shim is None:
+        pytest.skip("oracle/_ref/libvolta_gemm_shim.so not built (reference tree absent)")
+    rng = np.random.default_rng(3)
+    m, k, n = 64, 256, 96
+    A = rng.standard_normal((m, k)).astype(np.float32)
+    B = rng.standard_normal((k, n)).astype(np.float32)
+    At = np.ascontiguousarray(A.T)
+    c_ref = np.zeros((m, n), np.float32)
+    c_or = np.zeros((m, n), np.float32)
+    shim.volta_gemm_f32(fptr(c_ref), fptr(A), fptr(B), m, k, n)
+    oracle.lib.volta_oracle_gemm(fptr(c_or), fptr(A), fptr(B), m, k, n, 0, 0)
+    exact = A.astype(np.float64) @ B.astype(np.float64)
+    bound = 2 * k * np.finfo(np.float32).eps * (np.abs(A).astype(np.float64) @ np.abs(B).astype(np.float64))
+    assert np.all(np.abs(c_ref - exact) <= bound)
+    assert np.all(np.abs(c_or - exact) <= bound)
+    np.testing.assert_allclose(c_or, c_ref, rtol=1e-4, atol=1e-4)
+    # transposed-A (dW) and transposed-B (dX) forms
+    c_ref.fill(0)
+    shim.volta_gemm_tn_f32(fptr(c_ref), fptr(At), fptr(B), m, k, n)
+    oracle.lib.volta_oracle_gemm(fptr(c_or), fptr(At), fptr(B), m, k, n, 1, 0)
+    np.testing.assert_allclose(c_or, c_ref, rtol=1e-4, atol=1e-4)
+    Bt = np.ascontiguousarray(B.T)  # [n x k]
+    shim.volta_gemm_nt_f32(fptr(c_ref), fptr(A), fptr(B), m, k, n)  # takes B^T pre-transposed = B
+    oracle.lib.volta_oracle_gemm(fptr(c_or), fptr(A), fptr(Bt), m, k, n, 0, 1)
+    np.testing.assert_allclose(c_or, c_ref, rtol=1e-4, atol=1e-4)
+
+
+def test_lcg_xavier_stream(oracle):
+    """volta_train_init draws W_i from one LCG stream seeded 42
+    (mlp_train_rust_codegen.rs:629-658): values in [-lim, lim), mean ~0,
+    variance ~lim^2/3, biases 0, and layer 1 continues layer 0's stream."""
+    sizes = [64, 128, 32]
+    spec = MlpSpec(sizes, "relu", "sgd")
+    t = Trainer(oracle, spec, 4)
+    ws, bs = t.get_params()
+    t.close()
+    for (r, c), w, b in zip(spec.shapes(), ws, bs):
+        lim = math.sqrt(6.0 / (r + c))
+        assert w.min() >= -lim and w.max() < lim
+        assert abs(w.mean()) < 0.02 * lim
+        assert abs(w.var() / (lim * lim / 3) - 1) < 0.03
+        assert not b.any()
+    rng = C.c_uint64(42)
+    w0 = np.zeros(64 * 128, np.float32)
+    oracle.lib.volta_oracle_lcg_xavier(fptr(w0), w0.size, 64, 128, C.byref(rng))
+    np.testing.assert_array_equal(w0.reshape(64, 128), ws[0])
+    # first draw from an independent big-integer evaluation of the recurrence
+    x = (42 * 6364136223846793005 + 1442695040888963407) % (1 << 64)
+    f = np.float32((x >> 11) & ((1 << 53) - 1)) / np.float32(1 << 53)
+    lim0 = np.sqrt(np.float32(6.0) / np.float32(192.0))
+    assert ws[0][0, 0] == (f * np.float32(2) - np.float32(1)) * lim0
+    w1 = np.zeros(128 * 32, np.float32)
+    oracle.lib.volta_oracle_lcg_xavier(fptr(w1), w1.size, 128, 32, C.byref(rng))
+    np.testing.assert_array_equal(w1.reshape(128, 32), ws[1])
+
+
+def test_spec_parse(oracle):
+    s = oracle.parse_spec("512-1024-1024-512-256-1:relu:adam")
+    assert s.n_sizes == 6 and list(s.sizes[:6]) == [512, 1024, 1024, 512, 256, 1]
+    assert s.optimizer == 1 and s.loss == 0
+    assert abs(s.beta1 - 0.9) < 1e-7 and abs(s.eps - 1e-8) < 1e-15 and s.weight_decay == 0.0
+    s = oracle.parse_spec("1024-4096-4096-1024-10:relu:adagrad:ce:eps=1e-10")
+    assert s.loss == 1 and abs(s.eps - 1e-10) < 1e-17
+    s = oracle.parse_spec("512-2048-2048-512-1:gelu:adamw")
+    assert abs(s.weight_decay - 0.01) < 1e-9
+    for bad in ["", "3-4", "3-4:relu", "3-0-2:relu:sgd", "3-4:swish:sgd", "3-4:relu:lamb",
+                "3-1:relu:sgd:ce", "3-4:relu:sgd:eps=0", "3-4:relu:sgd:foo=1"]:
+        with pytest.raises(ValueError):
+            oracle.parse_spec(bad)
+
+
+def test_oracle_exports_header_symbols(oracle):
+    for name in HEADER_SYMBOLS:
+        assert hasattr(oracle.lib, name), name
+
+
+def test_oracle_status_and_bad_args(oracle):
+    # tanh, because ReLU maps a NaN input to 0 (pre > 0 is false)
+    spec = MlpSpec([3, 4, 2], "tanh", "sgd")
+    t = Trainer(oracle, spec, 2)
+    t.set_params(5, np.zeros((3, 4), np.float32), np.zeros(4, np.float32))  # ignored, flagged
+    assert t.status() & 2
+    t.clear_status()
+    X = np.full((2, 3), np.nan, np.float32)
+    t.step(X, np.zeros((2, 2), np.float32), 0.1)
+    assert t.status() & 1
+    t.close()
+
+
+def test_oracle_state_roundtrip(oracle):
+    """get_state/set_state lets an Adam run resume bit-identically."""
+    spec = MlpSpec([5, 7, 3], "tanh", "adam")
+    rng = np.random.default_rng(11)
+    X = rng.standard_normal((4, 5)).astype(np.float32)
+    Y = rng.standard_normal((4, 3)).astype(np.float32)
+    a = Trainer(oracle, spec, 4)
+    for _ in range(3):
+        a.step(X, Y, 1e-2)
+    st, step = a.get_state()
+    ws, bs = a.get_params()
+    assert step == 3 and st.size == a.state_size()
+    b = Trainer(oracle, spec, 4)
+    b.set_all_params(ws, bs)
+    b.set_state(st, step)
+    for _ in range(2):
+        a.step(X, Y, 1e-2)
+        b.step(X, Y, 1e-2)
+    wa, ba = a.get_params()
+    wb, bb = b.get_params()
+    for x, y in zip(wa + ba, wb + bb):
+        np.testing.assert_array_equal(x, y)
