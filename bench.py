@@ -1,0 +1,242 @@
+#!/usr/bin/env python3
+"""Benchmark of the compile-train MLP step on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--secondary c5]
+
+Headline workload ("c2"): MLP 512-1024-1024-512-256-1,
+ReLU hidden, linear output, MSE, Adam (lr 1e-3, b1 0.9, b2 0.999, eps 1e-8),
+fp32, B=64, X,Y ~ N(0,1), He-uniform weights, zero biases, all from seed 42.
+The same resident batch is used every step (inputs in HBM before timing), as
+Volta's synthetic dataset is a single batch.  One "step" = forward, loss,
+backward and optimizer update = one replay of the captured hipGraph.
+
+Secondary workload (configs[4], "c5"): the wide classifier at B=4096, the
+fp32-MFMA-bound case, reported in the same JSON line under "secondary".
+
+The JSON line also carries:
+  roofline      the dominant kernel of the headline step: algorithmic bytes or
+                flops per launch / its average duration, timed with HIP events
+                on the handle's stream (kernel-by-kernel replay of the step);
+  cpu_baseline  the CPU oracle (C++ restatement of Volta's compile-train step,
+                OpenMP GEMMs) on this host's cores, on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+from volta_amd import data, load_hip  # noqa: E402
+from volta_amd.abi import MlpSpec, Trainer  # noqa: E402
+
+METRIC = "ms/train-step (samples/s) MLP at B=64 and B=4096; % fp32 MFMA peak"
+PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+RIDGE = PEAK_FP32_MFMA_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)  # flop/byte
+
+WORKLOADS = {
+    "c1": (MlpSpec([256, 512, 512, 256, 1], "relu", "sgd"), 64, 0.01),
+    "c2": (MlpSpec([512, 1024, 1024, 512, 256, 1], "relu", "adam"), 64, 1e-3),
+    "c3": (MlpSpec([512, 2048, 2048, 512, 1], "gelu", "adamw"), 64, 1e-3),
+    "c4_128": (MlpSpec([512, 1024, 1024, 512, 256, 1], "silu", "sgd"), 128, 0.01),
+    "c4_256": (MlpSpec([512, 1024, 1024, 512, 256, 1], "silu", "sgd"), 256, 0.01),
+    "c4_1024": (MlpSpec([512, 1024, 1024, 512, 256, 1], "silu", "sgd"), 1024, 0.01),
+    "c5": (MlpSpec([1024, 4096, 4096, 1024, 10], "relu", "adagrad", "ce", eps=1e-10), 4096, 1e-2),
+}
+
+# Reference's own published CPU figure for the headline topology with Adam
+# (docs/BENCHMARKS.md:87; 6-core x86, MKL; different input pattern).
+PUBLISHED_CPU = {"c2": {"ms_per_step": 4.259, "source": "docs/BENCHMARKS.md:87",
+                        "hardware": "Windows 11, 6-core x86-64 CPU, MKL"}}
+
+
+def gemm_flops(spec: MlpSpec, B: int) -> float:
+    """2B*sumW (fwd) + 2B*sumW (dW) + 2B*(sumW - L0*L1) (dX, none for layer 0)."""
+    sw = sum(r * c for r, c in spec.shapes())
+    l0l1 = spec.sizes[0] * spec.sizes[1]
+    return 2.0 * B * sw * 2 + 2.0 * B * (sw - l0l1)
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def profile(lib, t, reps=5):
+    fn = lib.lib.volta_hip_profile_step
+    fn.restype = C.c_int32
+    fn.argtypes = [C.c_void_p, C.c_int32, C.c_char_p, C.c_int32]
+    buf = C.create_string_buffer(1 << 16)
+    n = fn(t.h, reps, buf, len(buf))
+    if n <= 0:
+        raise RuntimeError("volta_hip_profile_step failed: " + lib.last_error())
+    rows = []
+    for line in buf.value.decode().strip().splitlines():
+        label, ms, fl, by = line.split("\t")
+        rows.append({"kernel": label, "ms": float(ms), "flops": float(fl), "bytes": float(by)})
+    return rows
+
+
+def roofline_of(row):
+    ai = row["flops"] / row["bytes"] if row["bytes"] > 0 else math.inf
+    sec = row["ms"] * 1e-3
+    if ai > RIDGE:
+        ach = row["flops"] / sec / 1e12
+        return {"kernel": row["kernel"], "bound": "mfma", "achieved": round(ach, 3),
+                "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s", "frac": round(ach / PEAK_FP32_MFMA_TFLOPS, 4),
+                "traffic": None, "avg_ms": round(row["ms"], 5), "algorithmic_flops": row["flops"],
+                "algorithmic_bytes": row["bytes"]}
+    ach = row["bytes"] / sec / 1e9
+    return {"kernel": row["kernel"], "bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBS,
+            "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None,
+            "avg_ms": round(row["ms"], 5), "algorithmic_flops": row["flops"], "algorithmic_bytes": row["bytes"]}
+
+
+def run_gpu(name, steps, warmup, want_profile=True):
+    spec, B, lr = WORKLOADS[name]
+    lib = load_hip()
+    ws, bs = data.he_uniform(42, spec.sizes)
+    X, Y = data.batch(42, spec.sizes, B, spec.loss)
+    t = Trainer(lib, spec, B)
+    t.set_all_params(ws, bs)
+    t.step(X, Y, lr)  # stages X/Y into the handle's resident buffers
+    xp, yp = t.batch_buffers()
+    for _ in range(warmup):
+        if t.step_device(xp, yp, lr) != 0:
+            raise RuntimeError(lib.last_error())
+    t.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        t.step_device(xp, yp, lr)
+    t.sync()
+    t1 = time.perf_counter()
+    loss = t.loss()
+    status = t.status()
+    if status != 0 or not math.isfinite(loss):
+        raise RuntimeError(f"{name}: bad step status {status}, loss {loss}")
+    ms = (t1 - t0) / steps * 1e3
+    out = {"ms_per_step": ms, "samples_per_s": B / (ms * 1e-3), "loss_after": loss,
+           "gemm_gflop_per_step": gemm_flops(spec, B) / 1e9}
+    out["mfma_frac_step"] = gemm_flops(spec, B) / (ms * 1e-3) / (PEAK_FP32_MFMA_TFLOPS * 1e12)
+    extra = lib.lib.volta_hip_arena_bytes
+    extra.restype = C.c_int64
+    extra.argtypes = [C.c_void_p]
+    out["arena_bytes"] = int(extra(t.h))
+    if want_profile:
+        rows = profile(lib, t)
+        out["kernels"] = rows
+        dom = max(rows, key=lambda r: r["ms"])
+        out["roofline"] = roofline_of(dom)
+        out["kernel_sum_ms"] = sum(r["ms"] for r in rows)
+    t.close()
+    return spec, B, lr, out
+
+
+def run_cpu(name, budget_s=10.0, max_steps=200):
+    """Oracle on this host's cores; bounded sample of ~budget_s seconds."""
+    from tests.oracle_lib import load_oracle
+
+    spec, B, lr = WORKLOADS[name]
+    lib = load_oracle()
+    ws, bs = data.he_uniform(42, spec.sizes)
+    X, Y = data.batch(42, spec.sizes, B, spec.loss)
+    t = Trainer(lib, spec, B)
+    t.set_all_params(ws, bs)
+    t.step(X, Y, lr)  # warm-up (page in, thread pool)
+    n = 0
+    t0 = time.perf_counter()
+    while n < max_steps:
+        t.step(X, Y, lr)
+        n += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    dt = (time.perf_counter() - t0) / n
+    t.close()
+    return {"value": round(B / dt, 2), "unit": "samples/s", "ms_per_step": round(dt * 1e3, 3),
+            "cores": int(lib.lib.volta_oracle_threads()), "kind": "port",
+            "sample": f"{n} steps of workload {name} (B={B}) after 1 warm-up step, oracle/liboracle_volta.so "
+                      f"(C++ restatement of Volta compile-train, OpenMP GEMMs)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--secondary", default="c5", help="second workload in the same line, or 'none'")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-profile", action="store_true", help="skip the per-kernel profile")
+    a = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if a.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the step would shard by data parallelism over B; see DESIGN.md).", file=sys.stderr)
+        return 2
+
+    spec, B, lr, res = run_gpu(a.config, a.steps, a.warmup, want_profile=not a.no_profile)
+    log(f"{a.config}: {res['ms_per_step']:.4f} ms/step, {res['samples_per_s']:.0f} samples/s")
+    line = {
+        "metric": METRIC,
+        "value": round(res["samples_per_s"], 2),
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(res["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: X,Y ~ N(0,1) (splitmix64 + Box-Muller, seed 42), He-uniform weights, zero biases; "
+                "one resident batch reused every step",
+        "config": {"workload": a.config, "layers": list(spec.sizes), "activation": spec.activation,
+                   "loss": spec.loss, "optimizer": spec.optimizer, "lr": lr, "batch": B,
+                   "parallelism": "single GPU"},
+        "mfma_frac_step": round(res["mfma_frac_step"], 5),
+        "gemm_gflop_per_step": round(res["gemm_gflop_per_step"], 4),
+        "loss_after": res["loss_after"],
+        "arena_bytes": res["arena_bytes"],
+    }
+    if "roofline" in res:
+        line["roofline"] = res["roofline"]
+        line["kernel_sum_ms"] = round(res["kernel_sum_ms"], 5)
+        line["kernels"] = [{k: (round(v, 5) if isinstance(v, float) else v) for k, v in r.items()}
+                           for r in res["kernels"]]
+    if a.config in PUBLISHED_CPU:
+        line["reference_published_cpu"] = PUBLISHED_CPU[a.config]
+    if not a.no_cpu:
+        line["cpu_baseline"] = run_cpu(a.config)
+        log(f"cpu baseline: {line['cpu_baseline']}")
+    if a.secondary and a.secondary != "none":
+        s_steps = max(5, a.steps // 20)
+        s_spec, s_B, s_lr, s_res = run_gpu(a.secondary, s_steps, max(2, a.warmup // 10),
+                                           want_profile=not a.no_profile)
+        log(f"{a.secondary}: {s_res['ms_per_step']:.4f} ms/step, {s_res['samples_per_s']:.0f} samples/s, "
+            f"MFMA frac {s_res['mfma_frac_step']:.3f}")
+        sec = {"workload": a.secondary, "layers": list(s_spec.sizes), "activation": s_spec.activation,
+               "loss": s_spec.loss, "optimizer": s_spec.optimizer, "lr": s_lr, "batch": s_B, "steps": s_steps,
+               "ms_per_step": round(s_res["ms_per_step"], 5), "samples_per_s": round(s_res["samples_per_s"], 2),
+               "mfma_frac_step": round(s_res["mfma_frac_step"], 5),
+               "gemm_gflop_per_step": round(s_res["gemm_gflop_per_step"], 3)}
+        if "roofline" in s_res:
+            sec["roofline"] = s_res["roofline"]
+            sec["kernels"] = [{k: (round(v, 5) if isinstance(v, float) else v) for k, v in r.items()}
+                              for r in s_res["kernels"]]
+        if not a.no_cpu:
+            sec["cpu_baseline"] = run_cpu(a.secondary, budget_s=10.0, max_steps=3)
+        line["secondary"] = sec
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

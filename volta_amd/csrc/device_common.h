@@ -1,0 +1,90 @@
+// Device-side helpers shared by the gfx950 kernels of the MLP step.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/volta_train.h"
+
+namespace volta {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kWave = 64;
+
+// Per-handle scalars the captured step reads and writes on the device, so a
+// graph replay needs no host-side argument patching.
+struct DevScalars {
+  float lr;        // learning rate of the current step (host uploads on change)
+  float bc1;       // Adam bias corrections for the current step
+  float bc2;
+  uint32_t t;      // Adam step counter (incremented once per step on device)
+  float loss;      // loss of the most recent step
+  uint32_t flags;  // sticky VOLTA_STATUS_* bits raised on the device
+  uint32_t pad[2];
+};
+
+// Hidden activations, mlp_train_rust_codegen.rs:563-596 (forward) and
+// :893-916 (derivative).  Same expression order as the reference; the
+// library is built with -ffp-contract=off so nothing is fused into FMAs.
+// kIdentity marks the linear output layer.
+constexpr int kIdentity = -1;
+
+__device__ __forceinline__ float d_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+__device__ __forceinline__ float act_forward(int act, float x) {
+  switch (act) {
+    case VOLTA_ACT_RELU: return x > 0.0f ? x : 0.0f;
+    case VOLTA_ACT_SIGMOID: return d_sigmoid(x);
+    case VOLTA_ACT_TANH: return tanhf(x);
+    case VOLTA_ACT_LEAKY_RELU: return x > 0.0f ? x : 0.01f * x;
+    case VOLTA_ACT_SILU: return x * d_sigmoid(x);
+    case VOLTA_ACT_GELU: {
+      const float c = 0.7978845608f, k = 0.044715f;
+      const float v = c * (x + k * x * x * x);
+      return 0.5f * x * (1.0f + tanhf(v));
+    }
+    default: return x;
+  }
+}
+
+// f'(.) given the pre-activation `pre` and the activation output `y`.
+// ReLU's mask uses y > 0, which equals pre > 0 because y = max(pre, 0)
+// (so ReLU layers need not keep `pre`).
+__device__ __forceinline__ float act_derivative(int act, float pre, float y) {
+  switch (act) {
+    case VOLTA_ACT_RELU: return y > 0.0f ? 1.0f : 0.0f;
+    case VOLTA_ACT_SIGMOID: return y * (1.0f - y);
+    case VOLTA_ACT_TANH: return 1.0f - y * y;
+    case VOLTA_ACT_LEAKY_RELU: return pre > 0.0f ? 1.0f : 0.01f;
+    case VOLTA_ACT_SILU: {
+      const float s = d_sigmoid(pre);
+      return s * (1.0f + pre * (1.0f - s));
+    }
+    case VOLTA_ACT_GELU: {
+      const float c = 0.7978845608f, k = 0.044715f;
+      const float v = c * (pre + k * pre * pre * pre);
+      const float t = tanhf(v);
+      const float t2 = 1.0f - t * t;
+      return 0.5f * (1.0f + t) + 0.5f * pre * t2 * c * (1.0f + 3.0f * k * pre * pre);
+    }
+    default: return 1.0f;
+  }
+}
+
+// Activations whose derivative needs the pre-activation stored.
+__host__ __device__ inline bool act_needs_pre(int act) {
+  return act == VOLTA_ACT_LEAKY_RELU || act == VOLTA_ACT_SILU || act == VOLTA_ACT_GELU;
+}
+
+// Fixed-order wavefront sum (butterfly over 64 lanes).  Every lane ends with
+// the same value and the association order depends only on lane indices,
+// so results are bit-identical run to run.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+}  // namespace volta

@@ -1,0 +1,716 @@
+// Host runtime of the gfx950 compile-train MLP step: the C ABI of
+// include/volta_train.h on top of one device arena and a fixed launch
+// sequence captured once as a hipGraph.
+//
+// Mapping onto the reference:
+//   Handle + alloc (mlp_train_rust_codegen.rs:442-560)  -> Handle, one arena
+//   LCG Xavier init, seed 42 (:629-667)                 -> lcg_xavier_init
+//   volta_train_step body (:698-994)                    -> enqueue_step()
+//   get/set_params, loss, free (:669-696)               -> host mirror + copies
+//
+// The step's launch order (a topological order of the step's dataflow):
+//   fwd_0 .. fwd_{n-1}          GEMM NN + bias + activation epilogue
+//   loss                        MSE or softmax-CE head, delta_{n-1}
+//   for i = n-1 .. 0:
+//     dX_i  (i > 0)             GEMM NT, epilogue * f'(layer i-1) -> delta_{i-1}
+//     db_i                      fixed-order column sums (+ SGD bias update)
+//     dW_i                      GEMM TN; SGD updates W_i in the epilogue
+//   Adam/AdamW/Adagrad          one flat pass over all parameters
+// dX_i reads W_i before dW_i rewrites it, and every delta is computed from
+// the pre-update weights, as in the reference's two-phase backward.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "gemm.h"
+#include "spec.h"
+#include "step_kernels.h"
+
+namespace volta {
+
+static std::string hip_msg(const char* what, hipError_t e) {
+  return std::string(what) + ": " + hipGetErrorString(e);
+}
+
+// Reference lcg_xavier_init (mlp_train_rust_codegen.rs:629-638).
+static void lcg_xavier_init(float* w, size_t n, int r, int c, uint64_t* rng) {
+  const float lim = std::sqrt(6.0f / ((float)r + (float)c));
+  for (size_t i = 0; i < n; ++i) {
+    *rng = *rng * 6364136223846793005ULL + 1442695040888963407ULL;
+    const float f = (float)((*rng >> 11) & ((1ULL << 53) - 1)) / (float)(1ULL << 53);
+    w[i] = (f * 2.0f - 1.0f) * lim;
+  }
+}
+
+static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+struct LayerPlan {
+  int r = 0, c = 0;
+  int64_t w_off = 0, b_off = 0;  // float offsets into the flat parameter buffer
+  GemmPlan fwd, dx, dw;
+};
+
+struct Handle {
+  volta_mlp_spec spec{};
+  int B = 0, n = 0;
+  std::vector<int> L;
+  int device = 0;
+  int num_cus = 256;
+  hipStream_t stream = nullptr;
+
+  // --- device arena ---------------------------------------------------------
+  char* arena = nullptr;
+  size_t arena_bytes = 0;
+  int64_t flat = 0;  // padded float count of the flat parameter buffer
+  float* params = nullptr;
+  float* grads = nullptr;
+  float* opt_a = nullptr;  // Adam m / Adagrad G
+  float* opt_b = nullptr;  // Adam v
+  std::vector<float*> act;    // act[0..n]; act[0] is the resident X
+  std::vector<float*> pre;    // pre[0..n-2]; null where the activation needs no pre
+  std::vector<float*> delta;  // delta[0..n-1]
+  void* target = nullptr;     // resident Y (float [B x Ln]) or labels (int32 [B])
+  float* gemm_ws = nullptr;
+  float* colsum_ws = nullptr;
+  DevScalars* scalars = nullptr;
+  float2* bc_table = nullptr;
+  int bc_len = 0;
+  SegTable segs{};
+  std::vector<LayerPlan> layers;
+
+  // --- launch sequence -------------------------------------------------------
+  bool use_graph = true;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+
+  // --- host side -------------------------------------------------------------
+  float* h_params = nullptr;  // pinned mirror returned by get_params
+  float* h_stage_x = nullptr;
+  void* h_stage_y = nullptr;
+  hipEvent_t stage_free = nullptr;  // staging buffers may be overwritten
+  static constexpr int kLrSlots = 64;
+  float* h_lr = nullptr;
+  hipEvent_t lr_ev[kLrSlots] = {};
+  bool lr_pending[kLrSlots] = {};
+  int lr_slot = 0;
+  bool lr_known = false;
+  float cur_lr = 0.0f;
+  int32_t status = 0;
+
+  ~Handle();
+};
+
+Handle::~Handle() {
+  // Teardown is best effort: errors here have no caller to report to.
+  if (stream) (void)hipStreamSynchronize(stream);
+  if (exec) (void)hipGraphExecDestroy(exec);
+  if (graph) (void)hipGraphDestroy(graph);
+  for (auto& e : lr_ev)
+    if (e) (void)hipEventDestroy(e);
+  if (stage_free) (void)hipEventDestroy(stage_free);
+  if (h_params) (void)hipHostFree(h_params);
+  if (h_stage_x) (void)hipHostFree(h_stage_x);
+  if (h_stage_y) (void)hipHostFree(h_stage_y);
+  if (h_lr) (void)hipHostFree(h_lr);
+  if (arena) (void)hipFree(arena);
+  if (stream) (void)hipStreamDestroy(stream);
+}
+
+#define VOLTA_CHECK(call)                                   \
+  do {                                                      \
+    hipError_t e_ = (call);                                 \
+    if (e_ != hipSuccess) {                                 \
+      set_last_error(hip_msg(#call, e_));                   \
+      return false;                                         \
+    }                                                       \
+  } while (0)
+
+// Enqueue one whole step on `st` (captured into the graph once).  With a
+// recorder attached, an event follows every kernel (profiling only).
+static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
+  const volta_mlp_spec& s = h->spec;
+  const int n = h->n, B = h->B;
+  char label[64];
+  // Forward (:702-789)
+  for (int i = 0; i < n; ++i) {
+    const LayerPlan& lp = h->layers[i];
+    GemmArgs a{};
+    a.A = h->act[i];
+    a.lda = lp.r;
+    a.B = h->params + lp.w_off;
+    a.ldb = lp.c;
+    a.M = B;
+    a.N = lp.c;
+    a.K = lp.r;
+    a.partial = h->gemm_ws;
+    a.epi.kind = EPI_BIAS_ACT;
+    a.epi.act = i < n - 1 ? s.activation : kIdentity;
+    a.epi.ldc = lp.c;
+    a.epi.out = h->act[i + 1];
+    a.epi.pre = i < n - 1 ? h->pre[i] : nullptr;
+    a.epi.bias = h->params + lp.b_off;
+    a.epi.scalars = h->scalars;
+    std::snprintf(label, sizeof label, "fwd%d", i);
+    // algorithmic bytes: 4(B*r + r*c + B*c*(2 if hidden else 1))
+    const double bytes = 4.0 * ((double)B * lp.r + (double)lp.r * lp.c + (double)B * lp.c * (i < n - 1 ? 2 : 1));
+    VOLTA_CHECK(gemm_launch(lp.fwd, a, st, rec, label, bytes));
+  }
+  // Loss head
+  const int Ln = h->L[n];
+  if (s.loss == VOLTA_LOSS_MSE) {
+    VOLTA_CHECK(launch_loss_mse(h->act[n], static_cast<const float*>(h->target), h->delta[n - 1], B * Ln,
+                                h->scalars, h->bc_table, h->bc_len, st));
+  } else {
+    VOLTA_CHECK(launch_loss_ce(h->act[n], static_cast<const int32_t*>(h->target), h->delta[n - 1], B, Ln,
+                               h->scalars, h->bc_table, h->bc_len, st));
+  }
+  VOLTA_CHECK(mark(rec, "loss", 0.0, 12.0 * B * Ln));
+  const bool sgd = s.optimizer == VOLTA_OPT_SGD;
+  // Backward (:819-993)
+  for (int i = n - 1; i >= 0; --i) {
+    const LayerPlan& lp = h->layers[i];
+    if (i > 0) {
+      GemmArgs a{};
+      a.A = h->delta[i];
+      a.lda = lp.c;
+      a.B = h->params + lp.w_off;
+      a.ldb = lp.c;
+      a.M = B;
+      a.N = lp.r;
+      a.K = lp.c;
+      a.partial = h->gemm_ws;
+      a.epi.kind = EPI_DX_ACT;
+      a.epi.act = s.activation;
+      a.epi.ldc = lp.r;
+      a.epi.out = h->delta[i - 1];
+      a.epi.aux_act = h->act[i];
+      a.epi.aux_pre = h->pre[i - 1];
+      a.epi.scalars = h->scalars;
+      std::snprintf(label, sizeof label, "dx%d", i);
+      // algorithmic bytes: 4(B*c + r*c + 2*B*r)
+      const double bytes = 4.0 * ((double)B * lp.c + (double)lp.r * lp.c + 2.0 * B * lp.r);
+      VOLTA_CHECK(gemm_launch(lp.dx, a, st, rec, label, bytes));
+    }
+    std::snprintf(label, sizeof label, "db%d", i);
+    VOLTA_CHECK(launch_colsum(h->delta[i], B, lp.c, h->grads + lp.b_off,
+                              sgd ? h->params + lp.b_off : nullptr, h->scalars, h->colsum_ws, st, rec, label));
+    GemmArgs a{};
+    a.A = h->act[i];
+    a.lda = lp.r;
+    a.B = h->delta[i];
+    a.ldb = lp.c;
+    a.M = lp.r;
+    a.N = lp.c;
+    a.K = B;
+    a.partial = h->gemm_ws;
+    a.epi.kind = sgd ? EPI_SGD : EPI_STORE;
+    a.epi.ldc = lp.c;
+    a.epi.out = sgd ? h->params + lp.w_off : h->grads + lp.w_off;
+    a.epi.scalars = h->scalars;
+    std::snprintf(label, sizeof label, "dw%d", i);
+    // algorithmic bytes: 4(B*r + B*c + r*c)
+    const double bytes = 4.0 * ((double)B * lp.r + (double)B * lp.c + (double)lp.r * lp.c);
+    VOLTA_CHECK(gemm_launch(lp.dw, a, st, rec, label, bytes));
+  }
+  double P = 0;
+  for (auto& lp : h->layers) P += (double)lp.r * lp.c + lp.c;
+  if (s.optimizer == VOLTA_OPT_ADAM || s.optimizer == VOLTA_OPT_ADAMW) {
+    VOLTA_CHECK(launch_adam(h->params, h->opt_a, h->opt_b, h->grads, h->segs, h->flat, h->scalars, s.beta1,
+                            s.beta2, s.eps, st));
+    VOLTA_CHECK(mark(rec, "adam", 0.0, 4.0 * 7.0 * P));  // w,m,v,g read; w,m,v written
+  } else if (s.optimizer == VOLTA_OPT_ADAGRAD) {
+    VOLTA_CHECK(launch_adagrad(h->params, h->opt_a, h->grads, h->segs, h->flat, h->scalars, s.eps, st));
+    VOLTA_CHECK(mark(rec, "adagrad", 0.0, 4.0 * 5.0 * P));  // w,G,g read; w,G written
+  }
+  return true;
+}
+
+static bool build(Handle* h) {
+  const volta_mlp_spec& s = h->spec;
+  const int n = h->n, B = h->B;
+  VOLTA_CHECK(hipGetDevice(&h->device));
+  VOLTA_CHECK(hipDeviceGetAttribute(&h->num_cus, hipDeviceAttributeMultiprocessorCount, h->device));
+  VOLTA_CHECK(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
+
+  // Flat parameter layout [W0 | b0 | W1 | b1 | ...], segments padded.
+  h->layers.resize(n);
+  int64_t off = 0;
+  h->segs.n = 2 * n;
+  for (int i = 0; i < n; ++i) {
+    LayerPlan& lp = h->layers[i];
+    lp.r = h->L[i];
+    lp.c = h->L[i + 1];
+    lp.w_off = off;
+    off += align_up((size_t)lp.r * lp.c, kSegAlign);
+    lp.b_off = off;
+    off += align_up((size_t)lp.c, kSegAlign);
+    h->segs.off[2 * i] = lp.w_off;
+    h->segs.count[2 * i] = (int64_t)lp.r * lp.c;
+    h->segs.wd[2 * i] = s.optimizer == VOLTA_OPT_ADAMW ? s.weight_decay : 0.0f;
+    h->segs.off[2 * i + 1] = lp.b_off;
+    h->segs.count[2 * i + 1] = lp.c;
+    h->segs.wd[2 * i + 1] = 0.0f;  // the generated step never decays biases (:966)
+  }
+  h->flat = off;
+
+  // GEMM plans.  Vector (16-byte) operand loads need the contiguous extent
+  // and leading dimension to be multiples of 4 floats.
+  size_t ws_floats = 0;
+  for (int i = 0; i < n; ++i) {
+    LayerPlan& lp = h->layers[i];
+    const bool vr = lp.r % 4 == 0, vc = lp.c % 4 == 0;
+    lp.fwd = gemm_plan(GEMM_NN, B, lp.c, lp.r, vr && vc, h->num_cus);
+    lp.dx = gemm_plan(GEMM_NT, B, lp.r, lp.c, vc, h->num_cus);
+    lp.dw = gemm_plan(GEMM_TN, lp.r, lp.c, B, vr && vc, h->num_cus);
+    ws_floats = std::max(ws_floats, lp.fwd.workspace_floats(B, lp.c));
+    if (i > 0) ws_floats = std::max(ws_floats, lp.dx.workspace_floats(B, lp.r));
+    ws_floats = std::max(ws_floats, lp.dw.workspace_floats(lp.r, lp.c));
+  }
+  int max_c = 0;
+  for (int i = 1; i <= n; ++i) max_c = std::max(max_c, h->L[i]);
+  const size_t colsum_floats = (size_t)colsum_parts(B) * max_c;
+
+  // Adam bias-correction table: entry t = (1 - b1^t, 1 - b2^t) in f32 powf,
+  // up to the first t where both round to exactly 1.0f (later steps use the
+  // last entry, which is then exact).
+  const bool adam = s.optimizer == VOLTA_OPT_ADAM || s.optimizer == VOLTA_OPT_ADAMW;
+  std::vector<float2> bc;
+  if (adam) {
+    bc.push_back(make_float2(1.0f, 1.0f));  // t = 0 is never used
+    const int kMaxTable = 1 << 24;
+    for (int t = 1; t < kMaxTable; ++t) {
+      const float b1 = 1.0f - powf(s.beta1, (float)t);
+      const float b2 = 1.0f - powf(s.beta2, (float)t);
+      bc.push_back(make_float2(b1, b2));
+      if (b1 == 1.0f && b2 == 1.0f) break;
+    }
+    h->bc_len = (int)bc.size();
+  }
+
+  // One arena, 256-byte aligned sub-buffers.
+  struct Req {
+    void** dst;
+    size_t bytes;
+  };
+  std::vector<Req> reqs;
+  auto req = [&](void** dst, size_t bytes) { reqs.push_back({dst, align_up(std::max<size_t>(bytes, 4), 256)}); };
+  req((void**)&h->scalars, sizeof(DevScalars));
+  req((void**)&h->params, (size_t)h->flat * 4);
+  req((void**)&h->grads, (size_t)h->flat * 4);
+  if (adam || s.optimizer == VOLTA_OPT_ADAGRAD) req((void**)&h->opt_a, (size_t)h->flat * 4);
+  if (adam) req((void**)&h->opt_b, (size_t)h->flat * 4);
+  h->act.assign(n + 1, nullptr);
+  h->pre.assign(n, nullptr);
+  h->delta.assign(n, nullptr);
+  for (int i = 0; i <= n; ++i) req((void**)&h->act[i], (size_t)B * h->L[i] * 4);
+  for (int i = 0; i < n - 1; ++i)
+    if (act_needs_pre(s.activation)) req((void**)&h->pre[i], (size_t)B * h->L[i + 1] * 4);
+  for (int i = 0; i < n; ++i) req((void**)&h->delta[i], (size_t)B * h->L[i + 1] * 4);
+  req(&h->target, s.loss == VOLTA_LOSS_MSE ? (size_t)B * h->L[n] * 4 : (size_t)B * 4);
+  if (ws_floats) req((void**)&h->gemm_ws, ws_floats * 4);
+  req((void**)&h->colsum_ws, colsum_floats * 4);
+  if (adam) req((void**)&h->bc_table, bc.size() * sizeof(float2));
+  size_t total = 0;
+  for (auto& r : reqs) total += r.bytes;
+  h->arena_bytes = total;
+  VOLTA_CHECK(hipMalloc((void**)&h->arena, total));
+  VOLTA_CHECK(hipMemsetAsync(h->arena, 0, total, h->stream));
+  size_t pos = 0;
+  for (auto& r : reqs) {
+    *r.dst = h->arena + pos;
+    pos += r.bytes;
+  }
+  if (adam)
+    VOLTA_CHECK(hipMemcpyAsync(h->bc_table, bc.data(), bc.size() * sizeof(float2), hipMemcpyHostToDevice,
+                               h->stream));
+
+  // Host side: pinned parameter mirror, input staging, lr slots.
+  VOLTA_CHECK(hipHostMalloc((void**)&h->h_params, (size_t)h->flat * 4, hipHostMallocDefault));
+  VOLTA_CHECK(hipHostMalloc((void**)&h->h_stage_x, (size_t)B * h->L[0] * 4, hipHostMallocDefault));
+  VOLTA_CHECK(hipHostMalloc(&h->h_stage_y, (size_t)B * std::max(h->L[n], 1) * 4, hipHostMallocDefault));
+  VOLTA_CHECK(hipHostMalloc((void**)&h->h_lr, Handle::kLrSlots * sizeof(float), hipHostMallocDefault));
+  VOLTA_CHECK(hipEventCreateWithFlags(&h->stage_free, hipEventDisableTiming));
+  for (auto& e : h->lr_ev) VOLTA_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+
+  // Reference init: LCG Xavier-uniform W from one stream seeded 42, b = 0.
+  std::memset(h->h_params, 0, (size_t)h->flat * 4);
+  uint64_t rng = 42;
+  for (int i = 0; i < n; ++i) {
+    const LayerPlan& lp = h->layers[i];
+    lcg_xavier_init(h->h_params + lp.w_off, (size_t)lp.r * lp.c, lp.r, lp.c, &rng);
+  }
+  VOLTA_CHECK(hipMemcpyAsync(h->params, h->h_params, (size_t)h->flat * 4, hipMemcpyHostToDevice, h->stream));
+  VOLTA_CHECK(hipStreamSynchronize(h->stream));
+
+  const char* ng = std::getenv("VOLTA_NO_GRAPH");
+  h->use_graph = !(ng && *ng && *ng != '0');
+  if (h->use_graph) {
+    VOLTA_CHECK(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal));
+    const bool ok = enqueue_step(h, h->stream);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(h->stream, &g);
+    if (!ok) {
+      if (g) (void)hipGraphDestroy(g);
+      return false;
+    }
+    VOLTA_CHECK(e);
+    h->graph = g;
+    VOLTA_CHECK(hipGraphInstantiate(&h->exec, h->graph, nullptr, nullptr, 0));
+  }
+  return true;
+}
+
+static void fail(Handle* h, int bits, const std::string& msg) {
+  if (h) h->status |= bits;
+  set_last_error(msg);
+}
+
+// Make the device learning rate equal `lr` for the next step.  A change is
+// uploaded from a pinned slot; a slot is reused only after its copy ran.
+static bool set_lr(Handle* h, float lr) {
+  if (h->lr_known && std::memcmp(&lr, &h->cur_lr, 4) == 0) return true;
+  const int slot = h->lr_slot;
+  h->lr_slot = (slot + 1) % Handle::kLrSlots;
+  if (h->lr_pending[slot]) VOLTA_CHECK(hipEventSynchronize(h->lr_ev[slot]));
+  h->h_lr[slot] = lr;
+  VOLTA_CHECK(hipMemcpyAsync(&h->scalars->lr, &h->h_lr[slot], sizeof(float), hipMemcpyHostToDevice, h->stream));
+  VOLTA_CHECK(hipEventRecord(h->lr_ev[slot], h->stream));
+  h->lr_pending[slot] = true;
+  h->cur_lr = lr;
+  h->lr_known = true;
+  return true;
+}
+
+static bool launch_step(Handle* h) {
+  if (h->use_graph) {
+    VOLTA_CHECK(hipGraphLaunch(h->exec, h->stream));
+    return true;
+  }
+  return enqueue_step(h, h->stream);
+}
+
+// Stage host inputs through pinned memory so the caller may reuse X/Y at once.
+static bool stage_inputs(Handle* h, const float* X, const void* Y, size_t ybytes) {
+  const size_t xbytes = (size_t)h->B * h->L[0] * 4;
+  VOLTA_CHECK(hipEventSynchronize(h->stage_free));
+  std::memcpy(h->h_stage_x, X, xbytes);
+  std::memcpy(h->h_stage_y, Y, ybytes);
+  VOLTA_CHECK(hipMemcpyAsync(h->act[0], h->h_stage_x, xbytes, hipMemcpyHostToDevice, h->stream));
+  VOLTA_CHECK(hipMemcpyAsync(h->target, h->h_stage_y, ybytes, hipMemcpyHostToDevice, h->stream));
+  VOLTA_CHECK(hipEventRecord(h->stage_free, h->stream));
+  return true;
+}
+
+static bool sync(Handle* h) {
+  VOLTA_CHECK(hipStreamSynchronize(h->stream));
+  return true;
+}
+
+}  // namespace volta
+
+using volta::Handle;
+using volta::set_last_error;
+
+static Handle* H(VoltaTrainHandle* h) { return reinterpret_cast<Handle*>(h); }
+
+extern "C" {
+
+VoltaTrainHandle* volta_train_init_spec(const volta_mlp_spec* spec, int32_t batch) {
+  std::string why;
+  if (!spec || !volta::validate_spec(*spec, &why)) {
+    set_last_error("volta_train_init_spec: invalid spec: " + why);
+    return nullptr;
+  }
+  if (batch <= 0 || batch > (1 << 24)) {
+    set_last_error("volta_train_init_spec: batch must be in [1, 16777216]");
+    return nullptr;
+  }
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0) {
+    set_last_error("volta_train_init_spec: no HIP device");
+    return nullptr;
+  }
+  std::unique_ptr<Handle> h(new (std::nothrow) Handle());
+  if (!h) {
+    set_last_error("volta_train_init_spec: out of host memory");
+    return nullptr;
+  }
+  h->spec = *spec;
+  h->B = batch;
+  h->n = spec->n_sizes - 1;
+  h->L.assign(spec->sizes, spec->sizes + spec->n_sizes);
+  if (!volta::build(h.get())) return nullptr;
+  return reinterpret_cast<VoltaTrainHandle*>(h.release());
+}
+
+VoltaTrainHandle* volta_train_init(int32_t batch) {
+  volta_mlp_spec s;
+  if (!volta::resolve_default_spec(&s)) return nullptr;
+  return volta_train_init_spec(&s, batch);
+}
+
+void volta_train_step(VoltaTrainHandle* vh, const float* X, const float* Y, float lr) {
+  Handle* h = H(vh);
+  if (!h) return;
+  if (!X || !Y || h->spec.loss != VOLTA_LOSS_MSE) {
+    volta::fail(h, VOLTA_STATUS_BAD_ARGUMENT, "volta_train_step: null input or spec loss is not MSE");
+    return;
+  }
+  if (!volta::stage_inputs(h, X, Y, (size_t)h->B * h->L[h->n] * 4) || !volta::set_lr(h, lr) ||
+      !volta::launch_step(h))
+    h->status |= VOLTA_STATUS_DEVICE_ERROR;
+}
+
+void volta_train_step_labels(VoltaTrainHandle* vh, const float* X, const int32_t* labels, float lr) {
+  Handle* h = H(vh);
+  if (!h) return;
+  if (!X || !labels || h->spec.loss != VOLTA_LOSS_SOFTMAX_CE) {
+    volta::fail(h, VOLTA_STATUS_BAD_ARGUMENT,
+                "volta_train_step_labels: null input or spec loss is not softmax-CE");
+    return;
+  }
+  const int C = h->L[h->n];
+  for (int i = 0; i < h->B; ++i)
+    if (labels[i] < 0 || labels[i] >= C) {
+      volta::fail(h, VOLTA_STATUS_BAD_ARGUMENT, "volta_train_step_labels: label out of range");
+      return;
+    }
+  if (!volta::stage_inputs(h, X, labels, (size_t)h->B * 4) || !volta::set_lr(h, lr) || !volta::launch_step(h))
+    h->status |= VOLTA_STATUS_DEVICE_ERROR;
+}
+
+int32_t volta_train_step_device(VoltaTrainHandle* vh, const float* X, const void* Y, float lr) {
+  Handle* h = H(vh);
+  if (!h) return -1;
+  if (!X || !Y) {
+    volta::fail(h, VOLTA_STATUS_BAD_ARGUMENT, "volta_train_step_device: null input");
+    return -1;
+  }
+  const size_t ybytes = h->spec.loss == VOLTA_LOSS_MSE ? (size_t)h->B * h->L[h->n] * 4 : (size_t)h->B * 4;
+  bool ok = true;
+  if (X != h->act[0])
+    ok = ok && hipMemcpyAsync(h->act[0], X, (size_t)h->B * h->L[0] * 4, hipMemcpyDeviceToDevice, h->stream) ==
+                   hipSuccess;
+  if (Y != h->target)
+    ok = ok && hipMemcpyAsync(h->target, Y, ybytes, hipMemcpyDeviceToDevice, h->stream) == hipSuccess;
+  ok = ok && volta::set_lr(h, lr) && volta::launch_step(h);
+  if (!ok) {
+    h->status |= VOLTA_STATUS_DEVICE_ERROR;
+    return -1;
+  }
+  return 0;
+}
+
+int32_t volta_train_batch_buffers(VoltaTrainHandle* vh, float** X, void** Y) {
+  Handle* h = H(vh);
+  if (!h || !X || !Y) return -1;
+  *X = h->act[0];
+  *Y = h->target;
+  return 0;
+}
+
+float volta_train_loss(VoltaTrainHandle* vh) {
+  Handle* h = H(vh);
+  if (!h) return NAN;
+  float loss = NAN;
+  if (!volta::sync(h) ||
+      hipMemcpy(&loss, &h->scalars->loss, sizeof(float), hipMemcpyDeviceToHost) != hipSuccess) {
+    h->status |= VOLTA_STATUS_DEVICE_ERROR;
+    return NAN;
+  }
+  return loss;
+}
+
+void volta_train_get_params(VoltaTrainHandle* vh, float** wo, float** bo) {
+  Handle* h = H(vh);
+  if (!h || !wo || !bo) return;
+  if (!volta::sync(h) ||
+      hipMemcpy(h->h_params, h->params, (size_t)h->flat * 4, hipMemcpyDeviceToHost) != hipSuccess)
+    h->status |= VOLTA_STATUS_DEVICE_ERROR;
+  for (int i = 0; i < h->n; ++i) {
+    wo[i] = h->h_params + h->layers[i].w_off;
+    bo[i] = h->h_params + h->layers[i].b_off;
+  }
+}
+
+void volta_train_set_params(VoltaTrainHandle* vh, int32_t li, const float* w, const float* b) {
+  Handle* h = H(vh);
+  if (!h) return;
+  if (li < 0 || li >= h->n || !w || !b) {
+    volta::fail(h, VOLTA_STATUS_BAD_ARGUMENT, "volta_train_set_params: layer index out of range");
+    return;
+  }
+  const volta::LayerPlan& lp = h->layers[li];
+  if (!volta::sync(h) ||
+      hipMemcpy(h->params + lp.w_off, w, (size_t)lp.r * lp.c * 4, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(h->params + lp.b_off, b, (size_t)lp.c * 4, hipMemcpyHostToDevice) != hipSuccess)
+    h->status |= VOLTA_STATUS_DEVICE_ERROR;
+}
+
+void volta_train_free(VoltaTrainHandle* vh) { delete H(vh); }
+
+int32_t volta_train_sync(VoltaTrainHandle* vh) {
+  Handle* h = H(vh);
+  if (!h) return -1;
+  if (!volta::sync(h)) {
+    h->status |= VOLTA_STATUS_DEVICE_ERROR;
+    return -1;
+  }
+  return 0;
+}
+
+int32_t volta_train_status(VoltaTrainHandle* vh) {
+  Handle* h = H(vh);
+  if (!h) return VOLTA_STATUS_BAD_ARGUMENT;
+  uint32_t dev_flags = 0;
+  if (!volta::sync(h) ||
+      hipMemcpy(&dev_flags, &h->scalars->flags, sizeof(uint32_t), hipMemcpyDeviceToHost) != hipSuccess)
+    h->status |= VOLTA_STATUS_DEVICE_ERROR;
+  return h->status | (int32_t)dev_flags;
+}
+
+void volta_train_clear_status(VoltaTrainHandle* vh) {
+  Handle* h = H(vh);
+  if (!h) return;
+  h->status = 0;
+  const uint32_t zero = 0;
+  if (!volta::sync(h) ||
+      hipMemcpy(&h->scalars->flags, &zero, sizeof(uint32_t), hipMemcpyHostToDevice) != hipSuccess)
+    h->status |= VOLTA_STATUS_DEVICE_ERROR;
+}
+
+// Per-kernel profile of the step: runs `reps` steps kernel by kernel on the
+// resident batch (they train the model like any other step) with an event
+// after every kernel, and writes one line per kernel to `out`:
+//   "<label>\t<avg ms>\t<algorithmic flops>\t<algorithmic bytes>\n"
+// Returns the number of kernels per step, or -1.
+int32_t volta_hip_profile_step(VoltaTrainHandle* vh, int32_t reps, char* out, int32_t out_len) {
+  Handle* h = H(vh);
+  if (!h || reps <= 0 || !out || out_len <= 0) return -1;
+  std::vector<std::string> labels;
+  std::vector<double> total_ms, flops, bytes;
+  for (int r = 0; r < reps; ++r) {
+    volta::Recorder rec;
+    rec.st = h->stream;
+    if (hipEventCreate(&rec.start) != hipSuccess || hipEventRecord(rec.start, h->stream) != hipSuccess ||
+        !volta::enqueue_step(h, h->stream, &rec) || hipStreamSynchronize(h->stream) != hipSuccess) {
+      h->status |= VOLTA_STATUS_DEVICE_ERROR;
+      return -1;
+    }
+    if (r == 0) {
+      for (auto& m : rec.marks) {
+        labels.push_back(m.label);
+        flops.push_back(m.flops);
+        bytes.push_back(m.bytes);
+      }
+      total_ms.assign(labels.size(), 0.0);
+    }
+    hipEvent_t prev = rec.start;
+    for (size_t k = 0; k < rec.marks.size() && k < labels.size(); ++k) {
+      float ms = 0.0f;
+      if (hipEventElapsedTime(&ms, prev, rec.marks[k].ev) != hipSuccess) ms = 0.0f;
+      total_ms[k] += ms;
+      prev = rec.marks[k].ev;
+    }
+  }
+  std::string text;
+  char line[256];
+  for (size_t k = 0; k < labels.size(); ++k) {
+    std::snprintf(line, sizeof line, "%s\t%.6f\t%.6g\t%.6g\n", labels[k].c_str(), total_ms[k] / reps, flops[k],
+                  bytes[k]);
+    text += line;
+  }
+  std::snprintf(out, (size_t)out_len, "%s", text.c_str());
+  return (int32_t)labels.size();
+}
+
+// Bytes of the handle's device arena (reported by the benchmark).
+int64_t volta_hip_arena_bytes(VoltaTrainHandle* vh) {
+  Handle* h = H(vh);
+  return h ? (int64_t)h->arena_bytes : -1;
+}
+
+int32_t volta_train_num_layers(VoltaTrainHandle* vh) {
+  Handle* h = H(vh);
+  return h ? h->n : -1;
+}
+
+int32_t volta_train_batch(VoltaTrainHandle* vh) {
+  Handle* h = H(vh);
+  return h ? h->B : -1;
+}
+
+int64_t volta_train_state_size(VoltaTrainHandle* vh) {
+  Handle* h = H(vh);
+  if (!h) return -1;
+  int64_t per = 0;
+  for (auto& lp : h->layers) per += (int64_t)lp.r * lp.c + lp.c;
+  switch (h->spec.optimizer) {
+    case VOLTA_OPT_ADAM:
+    case VOLTA_OPT_ADAMW: return 2 * per;
+    case VOLTA_OPT_ADAGRAD: return per;
+    default: return 0;
+  }
+}
+
+// State order per layer: [m_W | m_b | v_W | v_b] (Adam/AdamW) or [G_W | G_b].
+static bool state_copy(Handle* h, float* host, bool to_host) {
+  const bool adam = h->spec.optimizer == VOLTA_OPT_ADAM || h->spec.optimizer == VOLTA_OPT_ADAMW;
+  std::vector<float*> bufs;
+  if (adam) bufs = {h->opt_a, h->opt_b};
+  else if (h->spec.optimizer == VOLTA_OPT_ADAGRAD) bufs = {h->opt_a};
+  float* p = host;
+  for (auto& lp : h->layers) {
+    for (float* dev : bufs) {
+      const size_t nw = (size_t)lp.r * lp.c, nb = lp.c;
+      hipError_t e1, e2;
+      if (to_host) {
+        e1 = hipMemcpy(p, dev + lp.w_off, nw * 4, hipMemcpyDeviceToHost);
+        e2 = hipMemcpy(p + nw, dev + lp.b_off, nb * 4, hipMemcpyDeviceToHost);
+      } else {
+        e1 = hipMemcpy(dev + lp.w_off, p, nw * 4, hipMemcpyHostToDevice);
+        e2 = hipMemcpy(dev + lp.b_off, p + nw, nb * 4, hipMemcpyHostToDevice);
+      }
+      if (e1 != hipSuccess || e2 != hipSuccess) return false;
+      p += nw + nb;
+    }
+  }
+  return true;
+}
+
+int32_t volta_train_get_state(VoltaTrainHandle* vh, float* state, int64_t* step) {
+  Handle* h = H(vh);
+  if (!h || (!state && volta_train_state_size(vh) > 0)) return -1;
+  uint32_t t = 0;
+  if (!volta::sync(h) || !state_copy(h, state, true) ||
+      hipMemcpy(&t, &h->scalars->t, sizeof(uint32_t), hipMemcpyDeviceToHost) != hipSuccess) {
+    h->status |= VOLTA_STATUS_DEVICE_ERROR;
+    return -1;
+  }
+  if (step) *step = t;
+  return 0;
+}
+
+int32_t volta_train_set_state(VoltaTrainHandle* vh, const float* state, int64_t step) {
+  Handle* h = H(vh);
+  if (!h || step < 0 || step > 0xffffffffLL || (!state && volta_train_state_size(vh) > 0)) {
+    if (h) volta::fail(h, VOLTA_STATUS_BAD_ARGUMENT, "volta_train_set_state: bad arguments");
+    return -1;
+  }
+  const uint32_t t = (uint32_t)step;
+  if (!volta::sync(h) || !state_copy(h, const_cast<float*>(state), false) ||
+      hipMemcpy(&h->scalars->t, &t, sizeof(uint32_t), hipMemcpyHostToDevice) != hipSuccess) {
+    h->status |= VOLTA_STATUS_DEVICE_ERROR;
+    return -1;
+  }
+  return 0;
+}
+
+}  // extern "C"
