@@ -181,6 +181,22 @@ int32_t volta_train_batch(VoltaTrainHandle* h);
  * (Adagrad), layers in order; SGD has no state.  `step` is the Adam step
  * counter t.  volta_train_state_size returns the float count. */
 int64_t volta_train_state_size(VoltaTrainHandle* h);
+
+/* Copy one intermediate buffer of the most recent step to host memory
+ * `out` (for tests and debugging; the reference keeps the same buffers in
+ * its Handle, mlp_train_rust_codegen.rs:442-560):
+ *   VOLTA_BUF_ACT    act_i   [B x L[i]],   i = 0..n
+ *   VOLTA_BUF_DELTA  delta_i [B x L[i+1]], i = 0..n-1 (after the activation
+ *                    derivative has been applied)
+ *   VOLTA_BUF_GRAD_W dW_i    [L[i] x L[i+1]] (not kept for SGD, whose update
+ *                    is fused into the dW product)
+ *   VOLTA_BUF_GRAD_B db_i    [L[i+1]]
+ * Returns the number of floats written, or -1. */
+#define VOLTA_BUF_ACT 0
+#define VOLTA_BUF_DELTA 1
+#define VOLTA_BUF_GRAD_W 2
+#define VOLTA_BUF_GRAD_B 3
+int64_t volta_train_debug_buffer(VoltaTrainHandle* h, int32_t kind, int32_t layer, float* out);
 int32_t volta_train_get_state(VoltaTrainHandle* h, float* state, int64_t* step);
 int32_t volta_train_set_state(VoltaTrainHandle* h, const float* state, int64_t step);
 

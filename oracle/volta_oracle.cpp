@@ -618,62 +618,92 @@ int32_t volta_train_batch(VoltaTrainHandle* vh) {
   return h->precision == 64 ? h->d.B : h->f.B;
 }
 
+}  // extern "C"
+
+// Optimizer state in the ABI's order: per layer [m_W | m_b | v_W | v_b]
+// (Adam/AdamW) or [G_W | G_b] (Adagrad).  Either precision; the fp64 twin
+// converts from/to float so it can be started from a float state.
+template <typename T>
+static std::vector<std::vector<T>*> state_buffers(Net<T>& f, int i) {
+  if (f.spec.optimizer == VOLTA_OPT_ADAM || f.spec.optimizer == VOLTA_OPT_ADAMW)
+    return {&f.mw[i], &f.mb[i], &f.vw[i], &f.vb[i]};
+  if (f.spec.optimizer == VOLTA_OPT_ADAGRAD) return {&f.gw[i], &f.gb[i]};
+  return {};
+}
+
+template <typename T>
+static int64_t state_size(Net<T>& f) {
+  int64_t total = 0;
+  for (int i = 0; i < f.n; ++i)
+    for (auto* v : state_buffers(f, i)) total += (int64_t)v->size();
+  return total;
+}
+
+template <typename T>
+static void state_get(Net<T>& f, float* p, int64_t* step) {
+  for (int i = 0; i < f.n; ++i)
+    for (auto* v : state_buffers(f, i))
+      for (size_t k = 0; k < v->size(); ++k) *p++ = (float)(*v)[k];
+  if (step) *step = (int64_t)f.adam_step;
+}
+
+template <typename T>
+static void state_set(Net<T>& f, const float* p, int64_t step) {
+  for (int i = 0; i < f.n; ++i)
+    for (auto* v : state_buffers(f, i))
+      for (size_t k = 0; k < v->size(); ++k) (*v)[k] = T(*p++);
+  f.adam_step = (uint64_t)step;
+}
+
+extern "C" {
+
 int64_t volta_train_state_size(VoltaTrainHandle* vh) {
   Handle* h = H(vh);
-  if (!h || h->precision != 32) return -1;
-  const Net<float>& f = h->f;
-  int64_t per = 0;
-  for (int i = 0; i < f.n; ++i) per += (int64_t)f.L[i] * f.L[i + 1] + f.L[i + 1];
-  switch (f.spec.optimizer) {
-    case VOLTA_OPT_ADAM:
-    case VOLTA_OPT_ADAMW: return 2 * per;
-    case VOLTA_OPT_ADAGRAD: return per;
-    default: return 0;
-  }
+  if (!h) return -1;
+  return h->precision == 64 ? state_size(h->d) : state_size(h->f);
 }
 
 int32_t volta_train_get_state(VoltaTrainHandle* vh, float* state, int64_t* step) {
   Handle* h = H(vh);
-  if (!h || h->precision != 32) return -1;
-  Net<float>& f = h->f;
-  float* p = state;
-  for (int i = 0; i < f.n; ++i) {
-    if (f.spec.optimizer == VOLTA_OPT_ADAM || f.spec.optimizer == VOLTA_OPT_ADAMW) {
-      for (auto* v : {&f.mw[i], &f.mb[i], &f.vw[i], &f.vb[i]}) {
-        std::copy(v->begin(), v->end(), p);
-        p += v->size();
-      }
-    } else if (f.spec.optimizer == VOLTA_OPT_ADAGRAD) {
-      for (auto* v : {&f.gw[i], &f.gb[i]}) {
-        std::copy(v->begin(), v->end(), p);
-        p += v->size();
-      }
-    }
-  }
-  if (step) *step = (int64_t)f.adam_step;
+  if (!h || (!state && volta_train_state_size(vh) > 0)) return -1;
+  if (h->precision == 64) state_get(h->d, state, step);
+  else state_get(h->f, state, step);
   return 0;
 }
 
 int32_t volta_train_set_state(VoltaTrainHandle* vh, const float* state, int64_t step) {
   Handle* h = H(vh);
-  if (!h || h->precision != 32 || step < 0) return -1;
-  Net<float>& f = h->f;
-  const float* p = state;
-  for (int i = 0; i < f.n; ++i) {
-    if (f.spec.optimizer == VOLTA_OPT_ADAM || f.spec.optimizer == VOLTA_OPT_ADAMW) {
-      for (auto* v : {&f.mw[i], &f.mb[i], &f.vw[i], &f.vb[i]}) {
-        std::copy(p, p + v->size(), v->begin());
-        p += v->size();
-      }
-    } else if (f.spec.optimizer == VOLTA_OPT_ADAGRAD) {
-      for (auto* v : {&f.gw[i], &f.gb[i]}) {
-        std::copy(p, p + v->size(), v->begin());
-        p += v->size();
-      }
-    }
-  }
-  f.adam_step = (uint64_t)step;
+  if (!h || step < 0 || (!state && volta_train_state_size(vh) > 0)) return -1;
+  if (h->precision == 64) state_set(h->d, state, step);
+  else state_set(h->f, state, step);
   return 0;
+}
+
+}  // extern "C"
+
+template <typename T>
+static int64_t copy_out(const std::vector<T>& v, float* out) {
+  for (size_t k = 0; k < v.size(); ++k) out[k] = (float)v[k];
+  return (int64_t)v.size();
+}
+
+template <typename T>
+static int64_t debug_buffer(Net<T>& f, int kind, int layer, float* out) {
+  switch (kind) {
+    case VOLTA_BUF_ACT: return layer >= 0 && layer <= f.n ? copy_out(f.act[layer], out) : -1;
+    case VOLTA_BUF_DELTA: return layer >= 0 && layer < f.n ? copy_out(f.delta[layer], out) : -1;
+    case VOLTA_BUF_GRAD_W: return layer >= 0 && layer < f.n ? copy_out(f.dw[layer], out) : -1;
+    case VOLTA_BUF_GRAD_B: return layer >= 0 && layer < f.n ? copy_out(f.db[layer], out) : -1;
+  }
+  return -1;
+}
+
+extern "C" {
+
+int64_t volta_train_debug_buffer(VoltaTrainHandle* vh, int32_t kind, int32_t layer, float* out) {
+  Handle* h = H(vh);
+  if (!h || !out) return -1;
+  return h->precision == 64 ? debug_buffer(h->d, kind, layer, out) : debug_buffer(h->f, kind, layer, out);
 }
 
 // ---------------------------------------------------------------------------

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 from tests.oracle_lib import load_oracle
-from volta_amd import data, load_hip
+from volta_amd import DeviceArray, data, load_hip
 from volta_amd.abi import MlpSpec, Trainer
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -63,15 +63,12 @@ def assert_params_close(w_h, b_h, w_o, b_o, label, rtol=RTOL, atol=ATOL):
 # GEMM kernels in isolation
 # ---------------------------------------------------------------------------
 def _gemm(layout, A, B, M, N, K, tile=-1, splits=0):
-    import torch
-
     lib = load_hip()
-    dA = torch.from_numpy(A).cuda()
-    dB = torch.from_numpy(B).cuda()
-    dC = torch.zeros((M, N), dtype=torch.float32, device="cuda")
-    rc = lib.lib.volta_hip_gemm(layout, dA.data_ptr(), dB.data_ptr(), dC.data_ptr(), M, N, K, tile, splits)
+    dA, dB = DeviceArray(A), DeviceArray(B)
+    dC = DeviceArray(np.zeros((M, N), np.float32))
+    rc = lib.lib.volta_hip_gemm(layout, dA.ptr, dB.ptr, dC.ptr, M, N, K, tile, splits)
     assert rc == 0, lib.last_error()
-    return dC.cpu().numpy()
+    return dC.numpy()
 
 
 GEMM_SHAPES = [
@@ -111,6 +108,42 @@ def test_gemm_splitk_matches(splits):
     want = A.astype(np.float64) @ B.astype(np.float64)
     bound = 2 * K * np.finfo(np.float32).eps * (np.abs(A).astype(np.float64) @ np.abs(B).astype(np.float64))
     assert np.all(np.abs(got - want) <= bound)
+
+
+@pytest.mark.parametrize("kind,wd,count", [("adam", 0.0, 1000), ("adamw", 0.01, 1029), ("adam", 0.0, 5),
+                                           ("adagrad", 0.0, 3001)])
+def test_optimizer_kernel_bit_exact(kind, wd, count):
+    """Given identical gradients and state, the flat optimizer kernel equals
+    the oracle's adam_update / Adagrad loop bit for bit (IEEE division and
+    sqrt, no contraction), including the reference's 8-wide/scalar-tail
+    split of the v update."""
+    import ctypes as C
+
+    say(f"optimizer {kind} wd={wd} n={count}")
+    hip, orc = load_hip(), load_oracle()
+    rng = np.random.default_rng(count)
+    w = rng.standard_normal(count).astype(np.float32)
+    m = (0.1 * rng.standard_normal(count)).astype(np.float32)
+    v = np.abs(0.01 * rng.standard_normal(count)).astype(np.float32)
+    g = (rng.standard_normal(count) * np.exp(rng.uniform(-12, 2, count))).astype(np.float32)
+    lr, b1, b2, eps = 1e-3, 0.9, 0.999, 1e-8
+    t = 7
+    bc1 = float(np.float32(1) - np.float32(b1) ** np.float32(t))
+    bc2 = float(np.float32(1) - np.float32(b2) ** np.float32(t))
+    dw, dm, dv, dg = (DeviceArray(x.copy()) for x in (w, m, v, g))
+    okind = 1 if kind in ("adam", "adamw") else 3
+    rc = hip.lib.volta_hip_optimizer(okind, dw.ptr, dm.ptr, dv.ptr, dg.ptr, count,
+                                     lr, bc1, bc2, b1, b2, eps, wd)
+    assert rc == 0, hip.lib.last_error()
+    F = C.POINTER(C.c_float)
+    p = lambda a: a.ctypes.data_as(F)  # noqa: E731
+    if okind == 1:
+        orc.lib.volta_oracle_adam(p(w), p(m), p(v), p(g), count, b1, b2, bc1, bc2, lr, eps, wd)
+        np.testing.assert_array_equal(dv.numpy(), v)
+    else:
+        orc.lib.volta_oracle_adagrad(p(w), p(m), p(g), count, lr, eps)
+    np.testing.assert_array_equal(dm.numpy(), m)
+    np.testing.assert_array_equal(dw.numpy(), w)
 
 
 # ---------------------------------------------------------------------------
@@ -201,29 +234,62 @@ def _flat(ws, bs):
 
 
 # Adaptive optimizers turn the rounding of a near-zero gradient into a
-# +-lr sign flip (the update is lr*mhat/(sqrt(vhat)+eps)), so no fp32
-# implementation with another summation order -- the reference's DLL with
-# another BLAS included -- stays elementwise within 1e-4 of another over 50
-# steps: the fp32 oracle itself leaves that tolerance of its fp64 twin at
+# +-lr sign flip (the update is lr*mhat/(sqrt(vhat)+eps)), and ReLU turns a
+# pre-activation within rounding of zero into a full-size gradient change, so
+# no fp32 implementation with another summation order -- the reference's DLL
+# with another BLAS included -- stays elementwise within 1e-4 of another over
+# 50 steps: the fp32 oracle itself leaves that tolerance of its fp64 twin at
 # step 1 on c2 (10 of 2.2M weights) and has 953k weights outside it at step
 # 50.  For these configurations parity is therefore checked three ways:
 #   1. teacher-forced single steps: from the oracle's exact state (params,
 #      moments, step counter) at several points of its trajectory, one HIP
-#      step and one oracle step agree elementwise (rel 1e-4 / abs 1e-5) for
-#      all but a 1e-4 fraction of each layer's parameters, with layer-norm
-#      relative difference <= 1e-5;
-#   2. the loss of every step agrees within rel 1e-4 over the steps where the
-#      oracle stays within 1e-4 of fp64 (STRICT_LOSS_STEPS);
+#      step, one oracle step and one fp64-twin step: forward activations
+#      agree elementwise, ReLU masks differ only at the kink, and per layer
+#      the HIP step has no larger a fraction of parameters outside
+#      rel 1e-4 / abs 1e-5 of fp64 than the oracle (2x + 2e-5), every
+#      HIP-vs-oracle outlier being an update-direction flip (<= 8 lr);
+#   2. free-running, the loss agrees within rel 1e-4 on every step where the
+#      fp32 oracle is still within 1e-5 (relative) of its fp64 twin;
 #   3. after all steps, the HIP run is no further from the fp64 twin than
 #      3x the fp32 oracle's own distance from it (per layer RMS and loss).
-STRICT_LOSS_STEPS = {"c2_mlp512_relu_adam_b64": 8, "c3_mlp512w_gelu_adamw_b64": 8,
-                     "c5_wide_ce_adagrad_b4096": 3}
 FORCED_AT = {"c2_mlp512_relu_adam_b64": [0, 10, 25, 49], "c3_mlp512w_gelu_adamw_b64": [0, 10, 25, 49],
-             "c5_wide_ce_adagrad_b4096": [0, 2]}
+             "c5_wide_ce_adagrad_b4096": [0, 1]}
+
+
+def _check_forward_and_masks(th, to, spec, label):
+    """Forward activations agree elementwise (rel 1e-4 / abs 1e-5) and every
+    hidden unit whose ReLU-type mask differs between the two runs sits at the
+    kink (|act| <= 1e-5 in both): a value within rounding of zero, where any
+    two fp32 summation orders may fall on either side."""
+    from volta_amd.abi import BUF_ACT
+
+    for i in range(1, spec.n_layers + 1):
+        a = th.debug_buffer(BUF_ACT, i).astype(np.float64)
+        b = to.debug_buffer(BUF_ACT, i).astype(np.float64)
+        ok, mx, bad = close_enough(a, b)
+        assert ok, f"{label}: act{i} differs, {bad} elements, max {mx:.3e}"
+        if i < spec.n_layers and spec.activation in ("relu", "leaky_relu"):
+            flip = (a > 0) != (b > 0)
+            assert np.all(np.abs(a[flip]) <= 1e-5) and np.all(np.abs(b[flip]) <= 1e-5), \
+                f"{label}: act{i} mask flips away from the kink"
+
+
+def _out_of_tol(a, b):
+    err = np.abs(a - b)
+    out = err > ATOL + RTOL * np.abs(b)
+    return float(np.mean(out)), (float(err[out].max()) if out.any() else 0.0)
 
 
 @pytest.mark.parametrize("name", ADAPTIVE_CONFIGS)
 def test_adaptive_config_teacher_forced_steps(name):
+    """From the oracle's exact state at several points of its trajectory, one
+    HIP step, one fp32-oracle step and one fp64-twin step.  Per layer, the
+    HIP step has no larger a fraction of parameters outside rel 1e-4 / abs
+    1e-5 of the fp64 result than the fp32 oracle has (2x + 2e-5 slack), and
+    every HIP-vs-oracle outlier is an update-direction flip (|diff| <= 8 lr:
+    one Adam/Adagrad step moves a weight by at most a few lr)."""
+    from tests.test_oracle import oracle_trainer
+
     spec, B, lr, steps = CONFIGS[name]
     say(f"teacher-forced {name}: {spec.text()} B={B} at {FORCED_AT[name]}")
     ws, bs, batches = config_inputs(spec, B)
@@ -239,24 +305,30 @@ def test_adaptive_config_teacher_forced_steps(name):
         w0, b0 = to.get_params()
         st0, t0 = to.get_state()
         th = Trainer(hip, spec, B)
-        th.set_all_params(w0, b0)
-        th.set_state(st0, t0)
-        th.step(X, Y, lr)
-        to.step(X, Y, lr)
+        tt = oracle_trainer(orc, spec, B, f64=True)
+        for t in (th, tt):
+            t.set_all_params(w0, b0)
+            t.set_state(st0, t0)
+        for t in (th, to, tt):
+            t.step(X, Y, lr)
         done += 1
+        _check_forward_and_masks(th, to, spec, f"step {k + 1}")
         lh, lo = th.loss(), to.loss()
         assert abs(lh - lo) <= ATOL + RTOL * abs(lo), f"step {k + 1}: loss hip {lh} oracle {lo}"
-        wh, bh = th.get_params()
-        wo, bo = to.get_params()
         assert th.status() == 0
+        hipf = _flat(*th.get_params())
+        orcf = _flat(*to.get_params())
+        truth = _flat_f64(orc, tt, spec)
         th.close()
-        for i, (a, b) in enumerate(zip(_flat(wh, bh), _flat(wo, bo))):
-            err = np.abs(a - b)
-            frac = float(np.mean(err > ATOL + RTOL * np.abs(b)))
-            nrel = float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
-            say(f"  step {k + 1} layer {i}: out-of-tol fraction {frac:.2e}, norm rel {nrel:.2e}")
-            assert frac <= 1e-4, f"step {k + 1} layer {i}: {frac:.2e} of elements out of tolerance"
-            assert nrel <= 1e-5, f"step {k + 1} layer {i}: norm-relative difference {nrel:.2e}"
+        tt.close()
+        for i, (a, b, t) in enumerate(zip(hipf, orcf, truth)):
+            f_h, _ = _out_of_tol(a, t)
+            f_o, _ = _out_of_tol(b, t)
+            f_ho, worst = _out_of_tol(a, b)
+            say(f"  step {k + 1} layer {i}: out-of-tol vs fp64: hip {f_h:.2e} oracle {f_o:.2e}; "
+                f"hip vs oracle {f_ho:.2e}, worst {worst:.2e}")
+            assert f_h <= 2 * f_o + 2e-5, f"step {k + 1} layer {i}: hip {f_h:.2e} vs oracle {f_o:.2e}"
+            assert worst <= 8 * lr + ATOL, f"step {k + 1} layer {i}: outlier {worst:.3e} exceeds 8*lr"
     to.close()
 
 
@@ -282,9 +354,12 @@ def test_adaptive_config_error_budget(name):
         lo.append(to.loss())
         lt.append(orc.lib.volta_oracle_loss_f64(tt.h))
     lh, lo, lt = map(np.array, (lh, lo, lt))
-    n = STRICT_LOSS_STEPS[name]
-    ok, mx, _ = close_enough(lh[:n], lo[:n])
-    assert ok, f"losses of the first {n} steps differ: max {mx:.3e}\n hip={lh[:n]}\n ora={lo[:n]}"
+    # the leading steps on which fp32 arithmetic still tracks fp64
+    calm = np.logical_and.accumulate(np.abs(lo - lt) <= 1e-5 * np.abs(lt))
+    assert calm[0], "the oracle leaves fp64 at step 1"
+    ok, mx, _ = close_enough(lh[calm], lo[calm])
+    say(f"  loss compared on {int(calm.sum())} of {steps} steps")
+    assert ok, f"losses differ on well-conditioned steps: max {mx:.3e}\n hip={lh[calm]}\n ora={lo[calm]}"
     e_h = abs(lh[-1] - lt[-1])
     e_o = abs(lo[-1] - lt[-1])
     say(f"  final loss: hip {lh[-1]:.7g} oracle {lo[-1]:.7g} fp64 {lt[-1]:.7g}")
@@ -356,8 +431,6 @@ def test_nonfinite_and_bad_label_status():
 
 def test_resident_batch_step_device():
     """step_device on the handle's own resident buffers equals host steps."""
-    import torch
-
     say("resident batch")
     hip = load_hip()
     spec = MlpSpec([16, 32, 4], "relu", "adam")
@@ -369,9 +442,8 @@ def test_resident_batch_step_device():
     b.set_all_params(ws, bs)
     xp, yp = b.batch_buffers()
     # fill b's resident buffers through a device copy
-    dX = torch.from_numpy(X).cuda()
-    dY = torch.from_numpy(Y).cuda()
-    assert b.step_device(dX.data_ptr(), dY.data_ptr(), 1e-3) == 0
+    dX, dY = DeviceArray(X), DeviceArray(Y)
+    assert b.step_device(dX.ptr, dY.ptr, 1e-3) == 0
     a.step(X, Y, 1e-3)
     for _ in range(4):
         assert b.step_device(xp, yp, 1e-3) == 0

@@ -24,7 +24,50 @@ HIP_EXTRA = {
     "volta_hip_gemm": (C.c_int32, [C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p,
                                    C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32]),
     "volta_hip_arena_bytes": (C.c_int64, [C.c_void_p]),
+    "volta_hip_optimizer": (C.c_int32, [C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64]
+                            + [C.c_float] * 7),
+    "volta_hip_profile_step": (C.c_int32, [C.c_void_p, C.c_int32, C.c_char_p, C.c_int32]),
+    "volta_hip_device_alloc": (C.c_void_p, [C.c_int64]),
+    "volta_hip_device_free": (C.c_int32, [C.c_void_p]),
+    "volta_hip_copy": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_int64, C.c_int32]),
 }
+
+
+class DeviceArray:
+    """A float32/int32 device buffer owned through libvolta_hip.so (tests and
+    benchmarks use it instead of a second GPU runtime)."""
+
+    def __init__(self, host, lib=None):
+        import numpy as np
+
+        self.lib = lib or load_hip()
+        self.host = np.ascontiguousarray(host)
+        self.nbytes = max(int(self.host.nbytes), 4)
+        p = self.lib.lib.volta_hip_device_alloc(self.nbytes)
+        if not p:
+            raise MemoryError("volta_hip_device_alloc failed")
+        self.ptr = int(p)
+        if self.lib.lib.volta_hip_copy(self.ptr, self.host.ctypes.data, int(self.host.nbytes), 1) != 0:
+            raise RuntimeError("host->device copy failed")
+
+    def numpy(self):
+        import numpy as np
+
+        out = np.empty_like(self.host)
+        if self.lib.lib.volta_hip_copy(out.ctypes.data, self.ptr, int(out.nbytes), 2) != 0:
+            raise RuntimeError("device->host copy failed")
+        return out
+
+    def free(self):
+        if self.ptr:
+            self.lib.lib.volta_hip_device_free(self.ptr)
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
 
 _loaded = {}
 

@@ -119,7 +119,10 @@ _SIGNATURES = {
     "volta_train_state_size": (C.c_int64, [_P]),
     "volta_train_get_state": (C.c_int32, [_P, _F, C.POINTER(C.c_int64)]),
     "volta_train_set_state": (C.c_int32, [_P, _F, C.c_int64]),
+    "volta_train_debug_buffer": (C.c_int64, [_P, C.c_int32, C.c_int32, _F]),
 }
+
+BUF_ACT, BUF_DELTA, BUF_GRAD_W, BUF_GRAD_B = 0, 1, 2, 3
 
 # Every symbol include/volta_train.h declares (checked by the CPU tests).
 HEADER_SYMBOLS = tuple(_SIGNATURES)
@@ -261,6 +264,18 @@ class Trainer:
         buf = state if state.size else np.zeros(1, np.float32)
         if self.lib.lib.volta_train_set_state(self.h, fptr(buf), step) != 0:
             raise RuntimeError(self.lib.last_error())
+
+    def debug_buffer(self, kind: int, layer: int) -> np.ndarray:
+        """An intermediate buffer of the last step (see volta_train_debug_buffer)."""
+        sizes = self.spec.sizes
+        B = self.batch
+        count = {BUF_ACT: lambda i: B * sizes[i], BUF_DELTA: lambda i: B * sizes[i + 1],
+                 BUF_GRAD_W: lambda i: sizes[i] * sizes[i + 1], BUF_GRAD_B: lambda i: sizes[i + 1]}[kind](layer)
+        out = np.zeros(count, np.float32)
+        n = self.lib.lib.volta_train_debug_buffer(self.h, kind, layer, fptr(out))
+        if n != count:
+            raise RuntimeError(f"debug_buffer({kind}, {layer}) failed: {self.lib.last_error()}")
+        return out
 
     def __enter__(self):
         return self

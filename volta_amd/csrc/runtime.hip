@@ -631,6 +631,43 @@ int32_t volta_hip_profile_step(VoltaTrainHandle* vh, int32_t reps, char* out, in
   return (int32_t)labels.size();
 }
 
+int64_t volta_train_debug_buffer(VoltaTrainHandle* vh, int32_t kind, int32_t layer, float* out) {
+  Handle* h = H(vh);
+  if (!h || !out) return -1;
+  const float* src = nullptr;
+  size_t count = 0;
+  const int n = h->n, B = h->B;
+  switch (kind) {
+    case VOLTA_BUF_ACT:
+      if (layer < 0 || layer > n) return -1;
+      src = h->act[layer];
+      count = (size_t)B * h->L[layer];
+      break;
+    case VOLTA_BUF_DELTA:
+      if (layer < 0 || layer >= n) return -1;
+      src = h->delta[layer];
+      count = (size_t)B * h->L[layer + 1];
+      break;
+    case VOLTA_BUF_GRAD_W:
+      if (layer < 0 || layer >= n || h->spec.optimizer == VOLTA_OPT_SGD) return -1;
+      src = h->grads + h->layers[layer].w_off;
+      count = (size_t)h->layers[layer].r * h->layers[layer].c;
+      break;
+    case VOLTA_BUF_GRAD_B:
+      if (layer < 0 || layer >= n) return -1;
+      src = h->grads + h->layers[layer].b_off;
+      count = (size_t)h->layers[layer].c;
+      break;
+    default:
+      return -1;
+  }
+  if (!volta::sync(h) || hipMemcpy(out, src, count * sizeof(float), hipMemcpyDeviceToHost) != hipSuccess) {
+    h->status |= VOLTA_STATUS_DEVICE_ERROR;
+    return -1;
+  }
+  return (int64_t)count;
+}
+
 // Bytes of the handle's device arena (reported by the benchmark).
 int64_t volta_hip_arena_bytes(VoltaTrainHandle* vh) {
   Handle* h = H(vh);

@@ -5,6 +5,7 @@
 
 #include "gemm.h"
 #include "spec.h"
+#include "step_kernels.h"
 
 extern "C" {
 
@@ -63,6 +64,77 @@ int32_t volta_hip_gemm(int32_t layout, const float* A, const float* B, float* Cm
   if (ws) hipFree(ws);
   if (e != hipSuccess) {
     set_last_error(std::string("volta_hip_gemm: ") + hipGetErrorString(e));
+    return -1;
+  }
+  return 0;
+}
+
+// Device memory for tests, so they need no second GPU runtime in-process.
+void* volta_hip_device_alloc(int64_t bytes) {
+  void* p = nullptr;
+  if (bytes <= 0 || hipMalloc(&p, (size_t)bytes) != hipSuccess) return nullptr;
+  return p;
+}
+
+int32_t volta_hip_device_free(void* p) { return hipFree(p) == hipSuccess ? 0 : -1; }
+
+// kind: 1 host->device, 2 device->host, 3 device->device.  Synchronous.
+int32_t volta_hip_copy(void* dst, const void* src, int64_t bytes, int32_t kind) {
+  const hipMemcpyKind k = kind == 1 ? hipMemcpyHostToDevice
+                          : kind == 2 ? hipMemcpyDeviceToHost
+                                      : hipMemcpyDeviceToDevice;
+  if (bytes < 0 || kind < 1 || kind > 3) return -1;
+  return hipMemcpy(dst, src, (size_t)bytes, k) == hipSuccess ? 0 : -1;
+}
+
+// One optimizer pass over a single buffer of `count` floats, as the step
+// runs it for one parameter segment.  kind: VOLTA_OPT_ADAM (AdamW when
+// wd != 0) or VOLTA_OPT_ADAGRAD (then v is unused and m holds G).
+int32_t volta_hip_optimizer(int32_t kind, float* w, float* m, float* v, const float* g, int64_t count,
+                            float lr, float bc1, float bc2, float b1, float b2, float eps, float wd) {
+  using namespace volta;
+  if (count <= 0 || !w || !m || !g || (kind == VOLTA_OPT_ADAM && !v) ||
+      (kind != VOLTA_OPT_ADAM && kind != VOLTA_OPT_ADAGRAD)) {
+    set_last_error("volta_hip_optimizer: bad arguments");
+    return -1;
+  }
+  // The kernels walk whole kSegAlign blocks; stage through padded buffers.
+  const int64_t padded = (count + kSegAlign - 1) / kSegAlign * kSegAlign;
+  float* buf = nullptr;
+  DevScalars* sc = nullptr;
+  const size_t bytes = (size_t)padded * 4;
+  if (hipMalloc((void**)&buf, 4 * bytes) != hipSuccess) return -1;
+  if (hipMalloc((void**)&sc, sizeof(DevScalars)) != hipSuccess) {
+    (void)hipFree(buf);
+    return -1;
+  }
+  float *dw = buf, *dm = buf + padded, *dv = buf + 2 * padded, *dg = buf + 3 * padded;
+  DevScalars hs{};
+  hs.lr = lr;
+  hs.bc1 = bc1;
+  hs.bc2 = bc2;
+  SegTable segs{};
+  segs.n = 1;
+  segs.off[0] = 0;
+  segs.count[0] = count;
+  segs.wd[0] = wd;
+  hipError_t e = hipMemset(buf, 0, 4 * bytes);
+  if (e == hipSuccess) e = hipMemcpy(sc, &hs, sizeof hs, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(dw, w, count * 4, hipMemcpyDeviceToDevice);
+  if (e == hipSuccess) e = hipMemcpy(dm, m, count * 4, hipMemcpyDeviceToDevice);
+  if (e == hipSuccess && v) e = hipMemcpy(dv, v, count * 4, hipMemcpyDeviceToDevice);
+  if (e == hipSuccess) e = hipMemcpy(dg, g, count * 4, hipMemcpyDeviceToDevice);
+  if (e == hipSuccess)
+    e = kind == VOLTA_OPT_ADAM ? launch_adam(dw, dm, dv, dg, segs, padded, sc, b1, b2, eps, nullptr)
+                               : launch_adagrad(dw, dm, dg, segs, padded, sc, eps, nullptr);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemcpy(w, dw, count * 4, hipMemcpyDeviceToDevice);
+  if (e == hipSuccess) e = hipMemcpy(m, dm, count * 4, hipMemcpyDeviceToDevice);
+  if (e == hipSuccess && v) e = hipMemcpy(v, dv, count * 4, hipMemcpyDeviceToDevice);
+  (void)hipFree(buf);
+  (void)hipFree(sc);
+  if (e != hipSuccess) {
+    set_last_error(std::string("volta_hip_optimizer: ") + hipGetErrorString(e));
     return -1;
   }
   return 0;
