@@ -78,6 +78,46 @@ __host__ __device__ inline bool act_needs_pre(int act) {
   return act == VOLTA_ACT_LEAKY_RELU || act == VOLTA_ACT_SILU || act == VOLTA_ACT_GELU;
 }
 
+// One Adam/AdamW element update (adam_update_slice,
+// mlp_train_rust_codegen.rs:341-388).  `tail` marks the last (n mod 8)
+// elements of a buffer, which the reference updates in its scalar loop with
+// v = b2*v + ((1-b2)*g)*g instead of (1-b2)*(g*g).
+__device__ __forceinline__ void adam_elem(float* w, float* m, float* v, float g, bool tail, float lr,
+                                          float bc1, float bc2, float b1, float b2, float eps, float wd) {
+  const float m1 = b1 * *m + (1.0f - b1) * g;
+  const float v1 = tail ? b2 * *v + (1.0f - b2) * g * g : b2 * *v + (1.0f - b2) * (g * g);
+  *m = m1;
+  *v = v1;
+  const float w0 = *w;
+  const float mhat = m1 / bc1;
+  const float vhat = v1 / bc2;
+  const float denom = sqrtf(vhat) + eps;
+  *w = w0 - lr * (mhat / denom + wd * w0);
+}
+
+// One Adagrad element update (mlp_train_rust_codegen.rs:967-985).
+__device__ __forceinline__ void adagrad_elem(float* w, float* G, float g, float lr, float eps) {
+  const float Gk = *G + g * g;
+  *G = Gk;
+  *w = *w - lr * g / (sqrtf(Gk) + eps);
+}
+
+// Once per step, after the loss: record it, raise the non-finite flag, and
+// advance the Adam step counter and its bias corrections 1 - beta^t, read
+// from a table the host filled with the same f32 powf the reference calls
+// (mlp_train_rust_codegen.rs:803-811).  Single thread.
+__device__ __forceinline__ void step_epilogue(DevScalars* sc, const float2* bc_table, int bc_len, float loss) {
+  sc->loss = loss;
+  if (!(fabsf(loss) <= 3.402823466e38f)) atomicOr(&sc->flags, (uint32_t)VOLTA_STATUS_NONFINITE_LOSS);
+  if (bc_table) {
+    const uint32_t t = sc->t + 1u;
+    sc->t = t;
+    const float2 bc = bc_table[t < (uint32_t)bc_len ? t : (uint32_t)(bc_len - 1)];
+    sc->bc1 = bc.x;
+    sc->bc2 = bc.y;
+  }
+}
+
 // Fixed-order wavefront sum (butterfly over 64 lanes).  Every lane ends with
 // the same value and the association order depends only on lane indices,
 // so results are bit-identical run to run.

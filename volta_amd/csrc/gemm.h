@@ -20,19 +20,44 @@ enum EpiKind {
   EPI_STORE = 0,     // out = acc
   EPI_BIAS_ACT = 1,  // pre = acc + bias; out = f(pre)     (f = identity for the output layer)
   EPI_DX_ACT = 2,    // out = acc * f'(aux_pre, aux_act)
-  EPI_SGD = 3,       // out = out + (-lr) * acc            (W updated in place)
+  EPI_DW_OPT = 3,    // acc is dW: optimizer update of W (and of b from the fused column sums)
+  EPI_LOSS = 4,      // output layer + loss head: out = acc + bias, delta, loss
 };
 
 struct EpiArgs {
   int kind;
   int act;                  // enum volta_activation, or kIdentity
   int ldc;
-  float* out;
+  float* out;               // result; for EPI_DW_OPT the weights W_i (updated in place)
   float* pre;               // EPI_BIAS_ACT: where to keep the pre-activation (may be null)
-  const float* bias;        // EPI_BIAS_ACT
+  const float* bias;        // EPI_BIAS_ACT / EPI_LOSS
   const float* aux_act;     // EPI_DX_ACT: activation output of the layer below
   const float* aux_pre;     // EPI_DX_ACT: its pre-activation (null when not kept)
-  const DevScalars* scalars;  // EPI_SGD: learning rate
+  DevScalars* scalars;      // lr, bias corrections, loss, flags
+
+  // EPI_DW_OPT: optimizer over W_i (index m*ldc + n) and, when `b` is set,
+  // over b_i from the column sums of delta_i that the same kernel computes.
+  int opt;                  // enum volta_optimizer
+  float* m;                 // Adam m / Adagrad G for W_i
+  float* v;                 // Adam v for W_i
+  float* grad;              // optional copy of dW_i (debugging), may be null
+  int64_t count;            // elements of W_i (the reference's n for the tail rule)
+  float wd, b1, b2, eps;
+  float* b;                 // b_i (null: column sums not fused)
+  float* bm;                // state for b_i
+  float* bv;
+  float* bgrad;             // optional copy of db_i, may be null
+
+  // EPI_LOSS
+  int loss;                 // enum volta_loss
+  const float* y;           // MSE targets [M x N]
+  const int32_t* labels;    // CE labels [M]
+  float* delta;             // seed gradient [M x N]
+  float* loss_partials;     // one float per M-tile
+  unsigned* loss_counter;   // arrival counter (zero between launches)
+  int loss_tiles;           // number of M-tiles
+  const float2* bc_table;   // Adam bias-correction table (null without Adam)
+  int bc_len;
 };
 
 struct GemmArgs {
@@ -41,7 +66,9 @@ struct GemmArgs {
   int lda, ldb;
   int M, N, K;
   int k_per_split;
-  float* partial;  // split-K workspace: splits planes of M*N floats
+  float* partial;       // split-K workspace: splits planes of (M+1)*N floats
+  unsigned* counters;   // split-K arrival counters, one per output tile, zero between launches
+  int colsum_b;         // 1: also sum the B operand over k (dW: db = sum_b delta)
   EpiArgs epi;
 };
 
@@ -53,9 +80,15 @@ struct GemmPlan {
   int splits = 1;
   int k_per_split = 0;
   bool vec = false;
-  size_t workspace_floats(int M, int N) const { return splits > 1 ? (size_t)splits * M * N : 0; }
+  bool inkernel_reduce = false;  // split-K reduced by the last slice (else a second kernel)
+  int tiles(int M, int N) const {
+    const int t = tile == TILE_64x64 ? 64 : 128;
+    return ((M + t - 1) / t) * ((N + t - 1) / t);
+  }
+  size_t workspace_floats(int M, int N) const { return splits > 1 ? (size_t)splits * (M + 1) * N : 0; }
 };
 
+// `min_k` is the smallest K slice a split may have.
 GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus);
 // `bytes` is the caller's algorithmic HBM traffic of the product (for the
 // profiler); `rec`/`label` are optional.

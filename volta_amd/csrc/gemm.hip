@@ -1,5 +1,7 @@
 // fp32 GEMM family on CDNA4 fp32 MFMA (v_mfma_f32_32x32x2_f32), with the
-// step's elementwise work fused into the epilogue.
+// step's other work fused into the epilogue: bias + activation (forward),
+// activation derivative (dX), bias-gradient column sums + optimizer update
+// (dW), and the loss head (output layer).
 //
 //   C[M x N] = sum_k A(m,k) * B(k,n)
 //
@@ -18,9 +20,15 @@
 // k of one row -- a single 16-byte LDS read for K-contiguous tiles.  The
 // order is fixed, so results are bit-identical from run to run.
 //
-// Split-K: blockIdx.z selects a K slice; slices write partial sums to a
-// workspace that splitk_reduce adds in slice order (no atomics).
+// Split-K: blockIdx.y selects a K slice.  Each slice writes its partial tile
+// to its own workspace plane, then bumps the tile's arrival counter; the
+// last slice to arrive adds the planes in slice order (0, 1, ...) and runs
+// the epilogue.  The sum order is fixed whatever the arrival order, and the
+// counter is an integer, so results stay bit-identical; the last slice
+// resets the counter to zero for the next launch.
 #include "gemm.h"
+
+#include <cstdlib>
 
 namespace volta {
 
@@ -133,12 +141,12 @@ __device__ __forceinline__ floatx4 load_frag(const float* lds, int row, int h, i
 }
 
 // ---------------------------------------------------------------------------
-// Epilogues: called once per output element (m < M, n < N) with the fp32
-// accumulator.  They are also used by splitk_reduce.
+// Element epilogues (called once per output element m < M, n < N).
 // ---------------------------------------------------------------------------
+template <int EPI>
 __device__ __forceinline__ void apply_epilogue(const EpiArgs& e, int m, int n, float acc) {
   const size_t idx = (size_t)m * e.ldc + n;
-  switch (e.kind) {
+  switch (EPI) {
     case EPI_STORE:
       e.out[idx] = acc;
       break;
@@ -156,16 +164,203 @@ __device__ __forceinline__ void apply_epilogue(const EpiArgs& e, int m, int n, f
       e.out[idx] = acc * act_derivative(e.act, p, y);
       break;
     }
-    case EPI_SGD: {
-      // sgd_fused_tn: W = 1*W + (-lr) * (act_i^T delta_i)  (:321-324)
-      const float nlr = -e.scalars->lr;
-      e.out[idx] = e.out[idx] + nlr * acc;
+    case EPI_DW_OPT: {
+      if (e.grad) e.grad[idx] = acc;
+      const float lr = e.scalars->lr;
+      if (e.opt == VOLTA_OPT_SGD) {
+        // sgd_fused_tn: W = 1*W + (-lr) * (act_i^T delta_i)  (:321-324)
+        const float nlr = -lr;
+        e.out[idx] = e.out[idx] + nlr * acc;
+      } else if (e.opt == VOLTA_OPT_ADAGRAD) {
+        adagrad_elem(e.out + idx, e.m + idx, acc, lr, e.eps);
+      } else {
+        const bool tail = (int64_t)idx >= e.count - e.count % 8;
+        adam_elem(e.out + idx, e.m + idx, e.v + idx, acc, tail, lr, e.scalars->bc1, e.scalars->bc2, e.b1,
+                  e.b2, e.eps, e.wd);
+      }
       break;
+    }
+    default:
+      break;
+  }
+}
+
+// Epilogue for the 16 accumulators a lane holds of one 32x32 block: column n,
+// rows m_base + 8*(v/4) + (v%4).  All loads are issued before any store so
+// the memory accesses of the 16 elements overlap (the element-by-element
+// form serialises them, since the compiler cannot prove the buffers
+// disjoint).
+template <int EPI>
+__device__ __forceinline__ void block_epilogue(const EpiArgs& e, const floatx16& acc, int m_base, int n, int M,
+                                               int N) {
+  if (n >= N) return;
+  auto row = [&](int v) { return m_base + 8 * (v >> 2) + (v & 3); };
+  if constexpr (EPI == EPI_BIAS_ACT) {
+    const float b = e.bias[n];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int m = row(v);
+      if (m < M) {
+        const size_t idx = (size_t)m * e.ldc + n;
+        const float x = acc[v] + b;  // pre = act_i W_i + b_i (:716-724)
+        if (e.pre) e.pre[idx] = x;
+        e.out[idx] = act_forward(e.act, x);  // act_{i+1} = f(pre) (:725-743)
+      }
+    }
+  } else if constexpr (EPI == EPI_DX_ACT) {
+    // delta_{i-1} = (delta_i W_i^T) * f'(layer i-1)  (:893-929)
+    float y[16], p[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int m = row(v);
+      const size_t idx = (size_t)m * e.ldc + n;
+      y[v] = m < M ? e.aux_act[idx] : 0.0f;
+      p[v] = (m < M && e.aux_pre) ? e.aux_pre[idx] : y[v];
+    }
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int m = row(v);
+      if (m < M) e.out[(size_t)m * e.ldc + n] = acc[v] * act_derivative(e.act, p[v], y[v]);
+    }
+  } else if constexpr (EPI == EPI_DW_OPT) {
+    const float lr = e.scalars->lr;
+    float w[16], s1[16], s2[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int m = row(v);
+      const size_t idx = (size_t)m * e.ldc + n;
+      const bool ok = m < M;
+      w[v] = ok ? e.out[idx] : 0.0f;
+      s1[v] = ok && e.opt != VOLTA_OPT_SGD ? e.m[idx] : 0.0f;
+      s2[v] = ok && (e.opt == VOLTA_OPT_ADAM || e.opt == VOLTA_OPT_ADAMW) ? e.v[idx] : 0.0f;
+    }
+    if (e.opt == VOLTA_OPT_SGD) {
+      // sgd_fused_tn: W = 1*W + (-lr) * (act_i^T delta_i)  (:321-324)
+      const float nlr = -lr;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) w[v] = w[v] + nlr * acc[v];
+    } else if (e.opt == VOLTA_OPT_ADAGRAD) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) adagrad_elem(&w[v], &s1[v], acc[v], lr, e.eps);
+    } else {
+      const float bc1 = e.scalars->bc1, bc2 = e.scalars->bc2;
+      const int64_t vec_end = e.count - e.count % 8;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t idx = (int64_t)row(v) * e.ldc + n;
+        adam_elem(&w[v], &s1[v], &s2[v], acc[v], idx >= vec_end, lr, bc1, bc2, e.b1, e.b2, e.eps, e.wd);
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int m = row(v);
+      if (m < M) {
+        const size_t idx = (size_t)m * e.ldc + n;
+        e.out[idx] = w[v];
+        if (e.opt != VOLTA_OPT_SGD) e.m[idx] = s1[v];
+        if (e.opt == VOLTA_OPT_ADAM || e.opt == VOLTA_OPT_ADAMW) e.v[idx] = s2[v];
+        if (e.grad) e.grad[idx] = acc[v];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int m = row(v);
+      if (m < M) e.out[(size_t)m * e.ldc + n] = acc[v];
     }
   }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, bool VEC>
+// Bias update from the fused column sum db_i[n] (:931-933, :957-993).  The
+// generated step never decays biases (:966).
+__device__ __forceinline__ void apply_bias_update(const EpiArgs& e, int n, int N, float db) {
+  if (e.bgrad) e.bgrad[n] = db;
+  const float lr = e.scalars->lr;
+  if (e.opt == VOLTA_OPT_SGD) {
+    e.b[n] = e.b[n] - lr * db;  // b -= lr*db (:986-991)
+  } else if (e.opt == VOLTA_OPT_ADAGRAD) {
+    adagrad_elem(e.b + n, e.bm + n, db, lr, e.eps);
+  } else {
+    const bool tail = n >= N - N % 8;
+    adam_elem(e.b + n, e.bm + n, e.bv + n, db, tail, lr, e.scalars->bc1, e.scalars->bc2, e.b1, e.b2, e.eps,
+              0.0f);
+  }
+}
+
+// Output layer + loss head on a staged tile (z[mm][nn] = acc + bias, one
+// thread per row).  MSE (:792-798): d = z - y, loss += d^2, delta = 2d/nt.
+// Softmax-CE (interpreter.rs:762-812, autograd.rs:467-534): row max,
+// sum exp(z - max), lse, sample loss -(z_label - lse), delta = (p - onehot)/B.
+// Returns the row's loss contribution; raises BAD_ARGUMENT for a label
+// outside [0, N) (it is never used as an index).
+__device__ __forceinline__ float loss_row(const EpiArgs& e, const float* z, int m, int N, int M) {
+  float* out = e.out + (size_t)m * N;
+  float* d = e.delta + (size_t)m * N;
+  for (int j = 0; j < N; ++j) out[j] = z[j];
+  if (e.loss == VOLTA_LOSS_MSE) {
+    const float nt = (float)(M * N);
+    const float* y = e.y + (size_t)m * N;
+    float acc = 0.0f;
+    for (int j = 0; j < N; ++j) {
+      const float dj = z[j] - y[j];
+      acc = acc + dj * dj;
+      d[j] = 2.0f * dj / nt;
+    }
+    return acc;
+  }
+  const float bf = (float)M;
+  const int lab = e.labels[m];
+  float mx = -INFINITY;
+  for (int j = 0; j < N; ++j) mx = fmaxf(mx, z[j]);
+  float sum = 0.0f;
+  for (int j = 0; j < N; ++j) sum = sum + expf(z[j] - mx);
+  const float lse = mx + logf(sum);
+  float sample = __builtin_nanf("");
+  for (int j = 0; j < N; ++j) {
+    const bool on = j == lab;
+    if (on) sample = -(z[j] - lse);
+    d[j] = (expf(z[j] - mx) / sum - (on ? 1.0f : 0.0f)) / bf;
+  }
+  if (lab < 0 || lab >= N) atomicOr(&e.scalars->flags, (uint32_t)VOLTA_STATUS_BAD_ARGUMENT);
+  return sample;
+}
+
+// Loss head for one output-layer tile staged in LDS (z[mm*ZS + nn] =
+// acc + bias, rows m0.. of the batch).  One thread per row; the tile's sum
+// goes to loss_partials[tm]; with one tile it is the total, otherwise the
+// last tile to finish adds the partials in tile order.
+template <int BM>
+__device__ __forceinline__ void loss_tile(const EpiArgs& e, const float* z, int ZS, int m0, int tm, int M, int N,
+                                          float* lds_rows) {
+  const int tid = threadIdx.x;
+  if (tid < BM) lds_rows[tid] = m0 + tid < M ? loss_row(e, z + tid * ZS, m0 + tid, N, M) : 0.0f;
+  __syncthreads();
+  if (tid == 0) {
+    float s = 0.0f;
+    for (int r = 0; r < BM && m0 + r < M; ++r) s = s + lds_rows[r];
+    const float denom = e.loss == VOLTA_LOSS_MSE ? (float)(M * N) : (float)M;
+    if (e.loss_tiles == 1) {
+      step_epilogue(e.scalars, e.bc_table, e.bc_len, s / denom);
+    } else {
+      e.loss_partials[tm] = s;
+      __threadfence();
+      const unsigned ticket = atomicAdd(e.loss_counter, 1u);
+      if (ticket == (unsigned)e.loss_tiles - 1u) {
+        __threadfence();
+        float total = 0.0f;
+        for (int t = 0; t < e.loss_tiles; ++t) total = total + e.loss_partials[t];
+        step_epilogue(e.scalars, e.bc_table, e.bc_len, total / denom);
+        *e.loss_counter = 0u;
+      }
+    }
+  }
+}
+
+// EPI is the epilogue kind (compile time, so each launch carries only its
+// own epilogue).  INK selects how a split-K launch is reduced: false -- each
+// slice stores its partial plane and splitk_reduce finishes in a second
+// kernel; true -- the last slice to arrive (integer ticket) reduces.
+template <int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, bool VEC, int EPI, bool INK>
 __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
 gemm_f32_mfma(GemmArgs args) {
   using T = Tile<BM, BN, BK, WM, WN>;
@@ -174,6 +369,7 @@ gemm_f32_mfma(GemmArgs args) {
   using LB = LdsTile<BN, BK, B_KC>;
   __shared__ __attribute__((aligned(16))) float lds_a[2][LA::kFloats];
   __shared__ __attribute__((aligned(16))) float lds_b[2][LB::kFloats];
+  __shared__ float lds_small[BM + 2];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -182,16 +378,22 @@ gemm_f32_mfma(GemmArgs args) {
   const int wn = wave % T::kWavesN;
   const int h = lane >> 5;
   const int l32 = lane & 31;
+  const int M = args.M, N = args.N;
 
   // Tile coordinates.  blockIdx.x walks N fastest so neighbouring
   // workgroups share the same A rows.
-  const int tiles_n = (args.N + BN - 1) / BN;
+  const int tiles_n = (N + BN - 1) / BN;
   const int tm = blockIdx.x / tiles_n;
   const int tn = blockIdx.x % tiles_n;
   const int m0 = tm * BM, n0 = tn * BN;
 
   const int kbeg = blockIdx.y * args.k_per_split;
   const int kend = min(args.K, kbeg + args.k_per_split);
+  // Column sums of B over k (dW's db), done by the workgroups of the first
+  // row of tiles, one thread per column, in k order.
+  constexpr bool kColsum = EPI == EPI_DW_OPT && !B_KC;
+  const bool colsum = kColsum && args.colsum_b && tm == 0;
+  float csum = 0.0f;
 
   TileLoader<BM, BK, A_KC, VEC, THREADS> la;
   TileLoader<BN, BK, B_KC, VEC, THREADS> lb;
@@ -205,8 +407,8 @@ gemm_f32_mfma(GemmArgs args) {
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
   if (kbeg < kend) {
-    la.load(args.A, args.lda, args.M, kend, m0, kbeg, tid);
-    lb.load(args.B, args.ldb, args.N, kend, n0, kbeg, tid);
+    la.load(args.A, args.lda, M, kend, m0, kbeg, tid);
+    lb.load(args.B, args.ldb, N, kend, n0, kbeg, tid);
     la.store(lds_a[0], tid);
     lb.store(lds_b[0], tid);
     __syncthreads();
@@ -215,8 +417,8 @@ gemm_f32_mfma(GemmArgs args) {
     for (int k0 = kbeg; k0 < kend; k0 += BK) {
       const bool more = k0 + BK < kend;
       if (more) {
-        la.load(args.A, args.lda, args.M, kend, m0, k0 + BK, tid);
-        lb.load(args.B, args.ldb, args.N, kend, n0, k0 + BK, tid);
+        la.load(args.A, args.lda, M, kend, m0, k0 + BK, tid);
+        lb.load(args.B, args.ldb, N, kend, n0, k0 + BK, tid);
       }
       const float* a_s = lds_a[buf];
       const float* b_s = lds_b[buf];
@@ -237,6 +439,10 @@ gemm_f32_mfma(GemmArgs args) {
             for (int j = 0; j < T::TN; ++j)
               acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
       }
+      if (kColsum && colsum && tid < BN) {
+        // rows beyond kend were loaded as zeros; adding them changes nothing
+        for (int kk = 0; kk < BK; ++kk) csum = csum + b_s[kk * LB::kStride + tid];
+      }
       if (more) {
         la.store(lds_a[buf ^ 1], tid);
         lb.store(lds_b[buf ^ 1], tid);
@@ -246,56 +452,166 @@ gemm_f32_mfma(GemmArgs args) {
     }
   }
 
-  // Epilogue.  Accumulator register v of lane (h, l32) in block (i, j) holds
-  // row 8*(v/4) + 4*h + (v%4), column l32 of that 32x32 block.
-  EpiArgs e = args.epi;
-  if (gridDim.y > 1) {  // split-K partial: plain store into this slice's plane
-    e.kind = EPI_STORE;
-    e.out = args.partial + (size_t)blockIdx.y * args.M * args.N;
-    e.ldc = args.N;
-  }
+  // Accumulator register v of lane (h, l32) in block (i, j) holds row
+  // 8*(v/4) + 4*h + (v%4), column l32 of that 32x32 block.
+  if (gridDim.y > 1) {
+    // Split-K: publish this slice's partial tile (row M of each plane holds
+    // the column sums).
+    const size_t plane = (size_t)(M + 1) * N;
+    float* mine = args.partial + (size_t)blockIdx.y * plane;
 #pragma unroll
-  for (int i = 0; i < T::TM; ++i)
+    for (int i = 0; i < T::TM; ++i)
 #pragma unroll
-    for (int j = 0; j < T::TN; ++j) {
-      const int n = n0 + wn * WN + j * 32 + l32;
+      for (int j = 0; j < T::TN; ++j) {
+        const int n = n0 + wn * WN + j * 32 + l32;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int m = m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (m < args.M && n < args.N) apply_epilogue(e, m, n, acc[i][j][v]);
+        for (int v = 0; v < 16; ++v) {
+          const int m = m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+          if (m < M && n < N) mine[(size_t)m * N + n] = acc[i][j][v];
+        }
       }
+    if (kColsum && colsum && tid < BN && n0 + tid < N) mine[(size_t)M * N + n0 + tid] = csum;
+    if constexpr (!INK) {
+      return;  // splitk_reduce finishes
+    } else {
+      __threadfence();
+      __syncthreads();
+      if (tid == 0) {
+        const unsigned ticket = atomicAdd(&args.counters[blockIdx.x], 1u);
+        lds_small[BM] = ticket == gridDim.y - 1 ? 1.0f : 0.0f;
+      }
+      __syncthreads();
+      if (lds_small[BM] == 0.0f) return;
+      __threadfence();
+      const float* planes = args.partial;
+#pragma unroll
+      for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < T::TN; ++j) {
+          const int n = n0 + wn * WN + j * 32 + l32;
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int m = m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+            if (m < M && n < N) {
+              const size_t off = (size_t)m * N + n;
+              float s = planes[off];
+              for (unsigned z = 1; z < gridDim.y; ++z) s = s + planes[z * plane + off];
+              acc[i][j][v] = s;
+            }
+          }
+        }
+      if (kColsum && colsum && tid < BN && n0 + tid < N) {
+        const size_t off = (size_t)M * N + n0 + tid;
+        float s = planes[off];
+        for (unsigned z = 1; z < gridDim.y; ++z) s = s + planes[z * plane + off];
+        csum = s;
+      }
+      if (tid == 0) args.counters[blockIdx.x] = 0u;
     }
+  }
+
+  const EpiArgs& e = args.epi;
+  if constexpr (EPI == EPI_LOSS) {
+    // Output layer (N <= BN): stage z = acc + bias for the whole tile in the
+    // (now free) A buffers, then the per-row loss head.
+    static_assert(BM * (BN + 1) <= 2 * LA::kFloats, "loss staging does not fit");
+    float* z = lds_a[0];
+    constexpr int ZS = BN + 1;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < T::TN; ++j) {
+        const int nn = wn * WN + j * 32 + l32;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int mm = wm * WM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+          if (nn < N) z[mm * ZS + nn] = acc[i][j][v] + e.bias[nn];
+        }
+      }
+    __syncthreads();
+    loss_tile<BM>(e, z, ZS, m0, tm, M, N, lds_small);
+  } else {
+#pragma unroll
+    for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < T::TN; ++j)
+        block_epilogue<EPI>(e, acc[i][j], m0 + wm * WM + i * 32 + 4 * h, n0 + wn * WN + j * 32 + l32, M, N);
+    if constexpr (kColsum) {
+      if (colsum && e.b && tid < BN && n0 + tid < N) apply_bias_update(e, n0 + tid, N, csum);
+    }
+  }
 }
 
-// Sum the split-K planes in slice order, then apply the real epilogue.
-__global__ void __launch_bounds__(256) splitk_reduce(const float* __restrict__ partial, int splits,
-                                                     int M, int N, EpiArgs e) {
+// Second kernel of a split-K launch: add the planes in slice order, then the
+// epilogue (and, for dW, the bias update from the summed column sums kept in
+// row M of each plane).
+template <int EPI>
+__global__ void __launch_bounds__(256) splitk_reduce(GemmArgs a, int splits) {
+  const int M = a.M, N = a.N;
+  const size_t plane = (size_t)(M + 1) * N;
   const size_t total = (size_t)M * N;
-  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+  const size_t extra = EPI == EPI_DW_OPT && a.colsum_b ? (size_t)N : 0;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total + extra;
        idx += (size_t)gridDim.x * blockDim.x) {
-    float s = partial[idx];
-    for (int z = 1; z < splits; ++z) s = s + partial[(size_t)z * total + idx];
-    apply_epilogue(e, (int)(idx / N), (int)(idx % N), s);
+    float s = a.partial[idx];
+    for (int z = 1; z < splits; ++z) s = s + a.partial[(size_t)z * plane + idx];
+    if (idx < total) {
+      apply_epilogue<EPI>(a.epi, (int)(idx / N), (int)(idx % N), s);
+    } else if constexpr (EPI == EPI_DW_OPT) {
+      apply_bias_update(a.epi, (int)(idx - total), N, s);
+    }
   }
 }
 
 // ---------------------------------------------------------------------------
 // Host-side dispatch.
 // ---------------------------------------------------------------------------
-template <int BM, int BN, int BK, int WM, int WN>
-static hipError_t launch_cfg(const GemmArgs& a, int layout, bool vec, int splits, hipStream_t st) {
+template <int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, int EPI>
+static hipError_t launch_epi(const GemmArgs& a, bool vec, int splits, bool ink, hipStream_t st) {
   using T = Tile<BM, BN, BK, WM, WN>;
   const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   dim3 grid(tiles, splits), block(T::kThreads);
-#define VOLTA_LAUNCH(AK, BKC, V) \
-  hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WM, WN, AK, BKC, V>), grid, block, 0, st, a)
-  switch (layout) {
-    case GEMM_NN: if (vec) VOLTA_LAUNCH(true, false, true); else VOLTA_LAUNCH(true, false, false); break;
-    case GEMM_NT: if (vec) VOLTA_LAUNCH(true, true, true); else VOLTA_LAUNCH(true, true, false); break;
-    case GEMM_TN: if (vec) VOLTA_LAUNCH(false, false, true); else VOLTA_LAUNCH(false, false, false); break;
-    default: return hipErrorInvalidValue;
+  if (ink) {
+    if (vec) hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WM, WN, A_KC, B_KC, true, EPI, true>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WM, WN, A_KC, B_KC, false, EPI, true>), grid, block, 0, st, a);
+  } else {
+    if (vec) hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WM, WN, A_KC, B_KC, true, EPI, false>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WM, WN, A_KC, B_KC, false, EPI, false>), grid, block, 0, st, a);
   }
-#undef VOLTA_LAUNCH
+  return hipGetLastError();
+}
+
+// Valid (layout, epilogue) pairs of the step: NN with BIAS_ACT / LOSS /
+// STORE, NT with DX_ACT / STORE, TN with DW_OPT / STORE.
+template <int BM, int BN, int BK, int WM, int WN>
+static hipError_t launch_cfg(const GemmArgs& a, int layout, bool vec, int splits, bool ink, hipStream_t st) {
+  const int k = a.epi.kind;
+  switch (layout) {
+    case GEMM_NN:
+      if (k == EPI_BIAS_ACT) return launch_epi<BM, BN, BK, WM, WN, true, false, EPI_BIAS_ACT>(a, vec, splits, ink, st);
+      if (k == EPI_STORE) return launch_epi<BM, BN, BK, WM, WN, true, false, EPI_STORE>(a, vec, splits, ink, st);
+      if constexpr (BM * (BN + 1) <= 2 * LdsTile<BM, BK, true>::kFloats) {
+        if (k == EPI_LOSS) return launch_epi<BM, BN, BK, WM, WN, true, false, EPI_LOSS>(a, vec, splits, true, st);
+      }
+      break;
+    case GEMM_NT:
+      if (k == EPI_DX_ACT) return launch_epi<BM, BN, BK, WM, WN, true, true, EPI_DX_ACT>(a, vec, splits, ink, st);
+      if (k == EPI_STORE) return launch_epi<BM, BN, BK, WM, WN, true, true, EPI_STORE>(a, vec, splits, ink, st);
+      break;
+    case GEMM_TN:
+      if (k == EPI_DW_OPT) return launch_epi<BM, BN, BK, WM, WN, false, false, EPI_DW_OPT>(a, vec, splits, ink, st);
+      if (k == EPI_STORE) return launch_epi<BM, BN, BK, WM, WN, false, false, EPI_STORE>(a, vec, splits, ink, st);
+      break;
+  }
+  return hipErrorInvalidValue;
+}
+
+template <int EPI>
+static hipError_t launch_reduce(const GemmArgs& a, int splits, hipStream_t st) {
+  const size_t total = (size_t)a.M * a.N + a.N;
+  const int blocks = (int)std::min<size_t>((total + 255) / 256, 4096);
+  hipLaunchKernelGGL(splitk_reduce<EPI>, dim3(blocks), dim3(256), 0, st, a, splits);
   return hipGetLastError();
 }
 
@@ -303,39 +619,50 @@ hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& args_in, hipStream_t s
                        const char* label, double bytes) {
   GemmArgs a = args_in;
   a.k_per_split = p.k_per_split;
+  if (p.splits > 1 && (!a.partial || !a.counters)) return hipErrorInvalidValue;
+  if (a.epi.kind == EPI_LOSS && (p.tile != TILE_64x64 || a.N > 64)) return hipErrorInvalidValue;
+  if (a.colsum_b && p.layout != GEMM_TN) return hipErrorInvalidValue;
+  // The loss head always reduces in-kernel (it needs whole rows).
+  const bool ink = p.inkernel_reduce || a.epi.kind == EPI_LOSS;
   hipError_t err;
   switch (p.tile) {
-    case TILE_64x64: err = launch_cfg<64, 64, 32, 32, 32>(a, p.layout, p.vec, p.splits, st); break;
-    case TILE_128x128: err = launch_cfg<128, 128, 32, 64, 64>(a, p.layout, p.vec, p.splits, st); break;
+    case TILE_64x64: err = launch_cfg<64, 64, 32, 32, 32>(a, p.layout, p.vec, p.splits, ink, st); break;
+    case TILE_128x128: err = launch_cfg<128, 128, 32, 64, 64>(a, p.layout, p.vec, p.splits, ink, st); break;
     default: return hipErrorInvalidValue;
   }
   if (err != hipSuccess) return err;
   err = mark(rec, label, 2.0 * a.M * a.N * a.K, bytes);
-  if (err != hipSuccess || p.splits == 1) return err;
-  const size_t total = (size_t)a.M * a.N;
-  int blocks = (int)std::min<size_t>((total + 255) / 256, 4096);
-  hipLaunchKernelGGL(splitk_reduce, dim3(blocks), dim3(256), 0, st, a.partial, p.splits, a.M, a.N,
-                     a.epi);
-  err = hipGetLastError();
+  if (err != hipSuccess || p.splits == 1 || ink) return err;
+  switch (a.epi.kind) {
+    case EPI_STORE: err = launch_reduce<EPI_STORE>(a, p.splits, st); break;
+    case EPI_BIAS_ACT: err = launch_reduce<EPI_BIAS_ACT>(a, p.splits, st); break;
+    case EPI_DX_ACT: err = launch_reduce<EPI_DX_ACT>(a, p.splits, st); break;
+    case EPI_DW_OPT: err = launch_reduce<EPI_DW_OPT>(a, p.splits, st); break;
+    default: return hipErrorInvalidValue;
+  }
   if (err != hipSuccess) return err;
-  return mark(rec, std::string(label) + ".splitk_reduce", (double)p.splits * total,
-              4.0 * ((double)p.splits * total + 2.0 * total));
+  const double t = (double)a.M * a.N;
+  return mark(rec, std::string(label) + ".splitk_reduce", (double)p.splits * t, 4.0 * ((double)p.splits * t + 2.0 * t));
 }
-
-static int tile_bm(int t) { return t == TILE_64x64 ? 64 : 128; }
-static int tile_bn(int t) { return t == TILE_64x64 ? 64 : 128; }
 
 GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus) {
   GemmPlan p;
   p.layout = layout;
   p.vec = vec;
-  p.tile = ((size_t)M * N >= (size_t)1024 * 1024 && M >= 128 && N >= 128) ? TILE_128x128 : TILE_64x64;
-  const int tiles = ((M + tile_bm(p.tile) - 1) / tile_bm(p.tile)) * ((N + tile_bn(p.tile) - 1) / tile_bn(p.tile));
+  // 128x128 tiles only where there is enough K to amortise them; a short K
+  // (dW at small batch) is epilogue bound and wants the 4x larger grid.
+  p.tile = ((size_t)M * N >= (size_t)1024 * 1024 && M >= 128 && N >= 128 && K > 256) ? TILE_128x128
+                                                                                      : TILE_64x64;
+  const int tiles = p.tiles(M, N);
   const int bk = 32;
+  const char* mk = std::getenv("VOLTA_SPLITK_MIN_K");
+  const int min_k = mk && *mk ? std::max(32, std::atoi(mk)) : 128;
+  const char* ik = std::getenv("VOLTA_SPLITK_INKERNEL");
+  p.inkernel_reduce = ik && *ik && *ik != '0';
   int splits = 1;
   // Split K while the grid is below ~2 workgroups per CU and each slice keeps
-  // at least 256 k values.
-  while (tiles * splits * 2 <= 2 * num_cus && K / (splits * 2) >= 256 && splits < 32) splits *= 2;
+  // at least min_k values of k.
+  while (tiles * splits * 2 <= 2 * num_cus && K / (splits * 2) >= min_k && splits < 32) splits *= 2;
   int kps = (K + splits - 1) / splits;
   kps = ((kps + bk - 1) / bk) * bk;
   splits = (K + kps - 1) / kps;

@@ -9,13 +9,13 @@
 //   get/set_params, loss, free (:669-696)               -> host mirror + copies
 //
 // The step's launch order (a topological order of the step's dataflow):
-//   fwd_0 .. fwd_{n-1}          GEMM NN + bias + activation epilogue
-//   loss                        MSE or softmax-CE head, delta_{n-1}
+//   fwd_0 .. fwd_{n-1}          GEMM NN + bias + activation epilogue; the
+//                               output layer's epilogue is the MSE or
+//                               softmax-CE head (delta_{n-1}, loss, Adam t)
 //   for i = n-1 .. 0:
 //     dX_i  (i > 0)             GEMM NT, epilogue * f'(layer i-1) -> delta_{i-1}
-//     db_i                      fixed-order column sums (+ SGD bias update)
-//     dW_i                      GEMM TN; SGD updates W_i in the epilogue
-//   Adam/AdamW/Adagrad          one flat pass over all parameters
+//     dW_i                      GEMM TN + column sums (db_i); epilogue applies
+//                               SGD/Adam/AdamW/Adagrad to W_i and b_i
 // dX_i reads W_i before dW_i rewrites it, and every delta is computed from
 // the pre-update weights, as in the reference's two-phase backward.
 #include <hip/hip_runtime.h>
@@ -77,8 +77,12 @@ struct Handle {
   std::vector<float*> pre;    // pre[0..n-2]; null where the activation needs no pre
   std::vector<float*> delta;  // delta[0..n-1]
   void* target = nullptr;     // resident Y (float [B x Ln]) or labels (int32 [B])
-  float* gemm_ws = nullptr;
-  float* colsum_ws = nullptr;
+  float* gemm_ws = nullptr;   // split-K partial planes (shared: one GEMM runs at a time)
+  unsigned* counters = nullptr;   // split-K arrival counters (+1: loss counter)
+  int n_counters = 0;
+  float* loss_partials = nullptr;  // one float per output-layer M-tile
+  bool fused_loss = true;     // loss head in the output-layer GEMM (N <= 64)
+  bool keep_grads = false;    // also store dW/db in `grads` (VOLTA_KEEP_GRADS=1)
   DevScalars* scalars = nullptr;
   float2* bc_table = nullptr;
   int bc_len = 0;
@@ -137,11 +141,19 @@ Handle::~Handle() {
 static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
   const volta_mlp_spec& s = h->spec;
   const int n = h->n, B = h->B;
+  const int Ln = h->L[n];
   char label[64];
-  // Forward (:702-789)
+  auto base_args = [&](GemmArgs& a) {
+    a.partial = h->gemm_ws;
+    a.counters = h->counters;
+    a.epi.scalars = h->scalars;
+  };
+  // Forward (:702-789); the output layer also runs the loss head (:792-798).
   for (int i = 0; i < n; ++i) {
     const LayerPlan& lp = h->layers[i];
+    const bool last = i == n - 1;
     GemmArgs a{};
+    base_args(a);
     a.A = h->act[i];
     a.lda = lp.r;
     a.B = h->params + lp.w_off;
@@ -149,35 +161,44 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
     a.M = B;
     a.N = lp.c;
     a.K = lp.r;
-    a.partial = h->gemm_ws;
-    a.epi.kind = EPI_BIAS_ACT;
-    a.epi.act = i < n - 1 ? s.activation : kIdentity;
+    a.epi.kind = last && h->fused_loss ? EPI_LOSS : EPI_BIAS_ACT;
+    a.epi.act = last ? kIdentity : s.activation;
     a.epi.ldc = lp.c;
     a.epi.out = h->act[i + 1];
-    a.epi.pre = i < n - 1 ? h->pre[i] : nullptr;
+    a.epi.pre = last ? nullptr : h->pre[i];
     a.epi.bias = h->params + lp.b_off;
-    a.epi.scalars = h->scalars;
-    std::snprintf(label, sizeof label, "fwd%d", i);
-    // algorithmic bytes: 4(B*r + r*c + B*c*(2 if hidden else 1))
-    const double bytes = 4.0 * ((double)B * lp.r + (double)lp.r * lp.c + (double)B * lp.c * (i < n - 1 ? 2 : 1));
+    if (last) {
+      a.epi.loss = s.loss;
+      a.epi.y = static_cast<const float*>(h->target);
+      a.epi.labels = static_cast<const int32_t*>(h->target);
+      a.epi.delta = h->delta[n - 1];
+      a.epi.loss_partials = h->loss_partials;
+      a.epi.loss_counter = h->counters + h->n_counters - 1;
+      a.epi.loss_tiles = (B + 63) / 64;
+      a.epi.bc_table = h->bc_table;
+      a.epi.bc_len = h->bc_len;
+    }
+    std::snprintf(label, sizeof label, last && h->fused_loss ? "fwd%d+loss" : "fwd%d", i);
+    // algorithmic bytes: 4(B*r + r*c + B*c*(2 if hidden else 1)) (+ loss head)
+    const double bytes = 4.0 * ((double)B * lp.r + (double)lp.r * lp.c + (double)B * lp.c * (last ? 1 : 2)) +
+                         (last && h->fused_loss ? 8.0 * B * Ln : 0.0);
     VOLTA_CHECK(gemm_launch(lp.fwd, a, st, rec, label, bytes));
   }
-  // Loss head
-  const int Ln = h->L[n];
-  if (s.loss == VOLTA_LOSS_MSE) {
-    VOLTA_CHECK(launch_loss_mse(h->act[n], static_cast<const float*>(h->target), h->delta[n - 1], B * Ln,
-                                h->scalars, h->bc_table, h->bc_len, st));
-  } else {
-    VOLTA_CHECK(launch_loss_ce(h->act[n], static_cast<const int32_t*>(h->target), h->delta[n - 1], B, Ln,
-                               h->scalars, h->bc_table, h->bc_len, st));
+  if (!h->fused_loss) {  // output layer wider than one tile: stand-alone loss head
+    if (s.loss == VOLTA_LOSS_MSE)
+      VOLTA_CHECK(launch_loss_mse(h->act[n], static_cast<const float*>(h->target), h->delta[n - 1], B * Ln,
+                                  h->scalars, h->bc_table, h->bc_len, st));
+    else
+      VOLTA_CHECK(launch_loss_ce(h->act[n], static_cast<const int32_t*>(h->target), h->delta[n - 1], B, Ln,
+                                 h->scalars, h->bc_table, h->bc_len, st));
+    VOLTA_CHECK(mark(rec, "loss", 0.0, 12.0 * B * Ln));
   }
-  VOLTA_CHECK(mark(rec, "loss", 0.0, 12.0 * B * Ln));
-  const bool sgd = s.optimizer == VOLTA_OPT_SGD;
-  // Backward (:819-993)
+  // Backward (:819-993).  dX_i reads W_i before dW_i updates it in place.
   for (int i = n - 1; i >= 0; --i) {
     const LayerPlan& lp = h->layers[i];
     if (i > 0) {
       GemmArgs a{};
+      base_args(a);
       a.A = h->delta[i];
       a.lda = lp.c;
       a.B = h->params + lp.w_off;
@@ -185,23 +206,21 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
       a.M = B;
       a.N = lp.r;
       a.K = lp.c;
-      a.partial = h->gemm_ws;
       a.epi.kind = EPI_DX_ACT;
       a.epi.act = s.activation;
       a.epi.ldc = lp.r;
       a.epi.out = h->delta[i - 1];
       a.epi.aux_act = h->act[i];
       a.epi.aux_pre = h->pre[i - 1];
-      a.epi.scalars = h->scalars;
       std::snprintf(label, sizeof label, "dx%d", i);
       // algorithmic bytes: 4(B*c + r*c + 2*B*r)
       const double bytes = 4.0 * ((double)B * lp.c + (double)lp.r * lp.c + 2.0 * B * lp.r);
       VOLTA_CHECK(gemm_launch(lp.dx, a, st, rec, label, bytes));
     }
-    std::snprintf(label, sizeof label, "db%d", i);
-    VOLTA_CHECK(launch_colsum(h->delta[i], B, lp.c, h->grads + lp.b_off,
-                              sgd ? h->params + lp.b_off : nullptr, h->scalars, h->colsum_ws, st, rec, label));
+    // dW_i = act_i^T delta_i with db_i = column sums of delta_i and the
+    // optimizer update of W_i and b_i in the epilogue.
     GemmArgs a{};
+    base_args(a);
     a.A = h->act[i];
     a.lda = lp.r;
     a.B = h->delta[i];
@@ -209,25 +228,33 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
     a.M = lp.r;
     a.N = lp.c;
     a.K = B;
-    a.partial = h->gemm_ws;
-    a.epi.kind = sgd ? EPI_SGD : EPI_STORE;
-    a.epi.ldc = lp.c;
-    a.epi.out = sgd ? h->params + lp.w_off : h->grads + lp.w_off;
-    a.epi.scalars = h->scalars;
-    std::snprintf(label, sizeof label, "dw%d", i);
-    // algorithmic bytes: 4(B*r + B*c + r*c)
-    const double bytes = 4.0 * ((double)B * lp.r + (double)B * lp.c + (double)lp.r * lp.c);
+    a.colsum_b = 1;
+    EpiArgs& e = a.epi;
+    e.kind = EPI_DW_OPT;
+    e.ldc = lp.c;
+    e.opt = s.optimizer == VOLTA_OPT_ADAMW ? VOLTA_OPT_ADAM : s.optimizer;
+    e.out = h->params + lp.w_off;
+    e.b = h->params + lp.b_off;
+    e.m = h->opt_a ? h->opt_a + lp.w_off : nullptr;
+    e.v = h->opt_b ? h->opt_b + lp.w_off : nullptr;
+    e.bm = h->opt_a ? h->opt_a + lp.b_off : nullptr;
+    e.bv = h->opt_b ? h->opt_b + lp.b_off : nullptr;
+    e.grad = h->keep_grads ? h->grads + lp.w_off : nullptr;
+    e.bgrad = h->keep_grads ? h->grads + lp.b_off : nullptr;
+    e.count = (int64_t)lp.r * lp.c;
+    e.wd = s.optimizer == VOLTA_OPT_ADAMW ? s.weight_decay : 0.0f;
+    e.b1 = s.beta1;
+    e.b2 = s.beta2;
+    e.eps = s.eps;
+    std::snprintf(label, sizeof label, "dw%d+db+opt", i);
+    // algorithmic bytes: dW 4(B*r + B*c + r*c), db 4(B*c + c), and the
+    // optimizer's 4*s per parameter minus the gradient round trip it saves:
+    // SGD reads+writes W (s=2 beyond dW), Adam w,m,v read+write (6),
+    // Adagrad w,G read+write (4).
+    const double P_i = (double)lp.r * lp.c + lp.c;
+    const int sopt = s.optimizer == VOLTA_OPT_SGD ? 2 : s.optimizer == VOLTA_OPT_ADAGRAD ? 4 : 6;
+    const double bytes = 4.0 * ((double)B * lp.r + (double)B * lp.c) + 4.0 * sopt * P_i;
     VOLTA_CHECK(gemm_launch(lp.dw, a, st, rec, label, bytes));
-  }
-  double P = 0;
-  for (auto& lp : h->layers) P += (double)lp.r * lp.c + lp.c;
-  if (s.optimizer == VOLTA_OPT_ADAM || s.optimizer == VOLTA_OPT_ADAMW) {
-    VOLTA_CHECK(launch_adam(h->params, h->opt_a, h->opt_b, h->grads, h->segs, h->flat, h->scalars, s.beta1,
-                            s.beta2, s.eps, st));
-    VOLTA_CHECK(mark(rec, "adam", 0.0, 4.0 * 7.0 * P));  // w,m,v,g read; w,m,v written
-  } else if (s.optimizer == VOLTA_OPT_ADAGRAD) {
-    VOLTA_CHECK(launch_adagrad(h->params, h->opt_a, h->grads, h->segs, h->flat, h->scalars, s.eps, st));
-    VOLTA_CHECK(mark(rec, "adagrad", 0.0, 4.0 * 5.0 * P));  // w,G,g read; w,G written
   }
   return true;
 }
@@ -238,6 +265,8 @@ static bool build(Handle* h) {
   VOLTA_CHECK(hipGetDevice(&h->device));
   VOLTA_CHECK(hipDeviceGetAttribute(&h->num_cus, hipDeviceAttributeMultiprocessorCount, h->device));
   VOLTA_CHECK(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
+  const char* kg = std::getenv("VOLTA_KEEP_GRADS");
+  h->keep_grads = kg && *kg && *kg != '0';
 
   // Flat parameter layout [W0 | b0 | W1 | b1 | ...], segments padded.
   h->layers.resize(n);
@@ -261,21 +290,26 @@ static bool build(Handle* h) {
   h->flat = off;
 
   // GEMM plans.  Vector (16-byte) operand loads need the contiguous extent
-  // and leading dimension to be multiples of 4 floats.
+  // and leading dimension to be multiples of 4 floats.  The output layer's
+  // loss head runs in its GEMM when the layer fits one 64-wide tile.
+  h->fused_loss = h->L[n] <= 64;
   size_t ws_floats = 0;
+  int max_tiles = 1;
   for (int i = 0; i < n; ++i) {
     LayerPlan& lp = h->layers[i];
     const bool vr = lp.r % 4 == 0, vc = lp.c % 4 == 0;
     lp.fwd = gemm_plan(GEMM_NN, B, lp.c, lp.r, vr && vc, h->num_cus);
+    if (i == n - 1 && h->fused_loss) lp.fwd.tile = TILE_64x64;
     lp.dx = gemm_plan(GEMM_NT, B, lp.r, lp.c, vc, h->num_cus);
     lp.dw = gemm_plan(GEMM_TN, lp.r, lp.c, B, vr && vc, h->num_cus);
     ws_floats = std::max(ws_floats, lp.fwd.workspace_floats(B, lp.c));
     if (i > 0) ws_floats = std::max(ws_floats, lp.dx.workspace_floats(B, lp.r));
     ws_floats = std::max(ws_floats, lp.dw.workspace_floats(lp.r, lp.c));
+    max_tiles = std::max(max_tiles, lp.fwd.tiles(B, lp.c));
+    max_tiles = std::max(max_tiles, lp.dx.tiles(B, lp.r));
+    max_tiles = std::max(max_tiles, lp.dw.tiles(lp.r, lp.c));
   }
-  int max_c = 0;
-  for (int i = 1; i <= n; ++i) max_c = std::max(max_c, h->L[i]);
-  const size_t colsum_floats = (size_t)colsum_parts(B) * max_c;
+  h->n_counters = max_tiles + 1;  // last one: the loss head's tile counter
 
   // Adam bias-correction table: entry t = (1 - b1^t, 1 - b2^t) in f32 powf,
   // up to the first t where both round to exactly 1.0f (later steps use the
@@ -303,7 +337,7 @@ static bool build(Handle* h) {
   auto req = [&](void** dst, size_t bytes) { reqs.push_back({dst, align_up(std::max<size_t>(bytes, 4), 256)}); };
   req((void**)&h->scalars, sizeof(DevScalars));
   req((void**)&h->params, (size_t)h->flat * 4);
-  req((void**)&h->grads, (size_t)h->flat * 4);
+  if (h->keep_grads) req((void**)&h->grads, (size_t)h->flat * 4);
   if (adam || s.optimizer == VOLTA_OPT_ADAGRAD) req((void**)&h->opt_a, (size_t)h->flat * 4);
   if (adam) req((void**)&h->opt_b, (size_t)h->flat * 4);
   h->act.assign(n + 1, nullptr);
@@ -315,7 +349,8 @@ static bool build(Handle* h) {
   for (int i = 0; i < n; ++i) req((void**)&h->delta[i], (size_t)B * h->L[i + 1] * 4);
   req(&h->target, s.loss == VOLTA_LOSS_MSE ? (size_t)B * h->L[n] * 4 : (size_t)B * 4);
   if (ws_floats) req((void**)&h->gemm_ws, ws_floats * 4);
-  req((void**)&h->colsum_ws, colsum_floats * 4);
+  req((void**)&h->counters, (size_t)h->n_counters * sizeof(unsigned));
+  req((void**)&h->loss_partials, (size_t)((B + 63) / 64) * 4);
   if (adam) req((void**)&h->bc_table, bc.size() * sizeof(float2));
   size_t total = 0;
   for (auto& r : reqs) total += r.bytes;
@@ -649,12 +684,12 @@ int64_t volta_train_debug_buffer(VoltaTrainHandle* vh, int32_t kind, int32_t lay
       count = (size_t)B * h->L[layer + 1];
       break;
     case VOLTA_BUF_GRAD_W:
-      if (layer < 0 || layer >= n || h->spec.optimizer == VOLTA_OPT_SGD) return -1;
+      if (layer < 0 || layer >= n || !h->keep_grads) return -1;
       src = h->grads + h->layers[layer].w_off;
       count = (size_t)h->layers[layer].r * h->layers[layer].c;
       break;
     case VOLTA_BUF_GRAD_B:
-      if (layer < 0 || layer >= n) return -1;
+      if (layer < 0 || layer >= n || !h->keep_grads) return -1;
       src = h->grads + h->layers[layer].b_off;
       count = (size_t)h->layers[layer].c;
       break;

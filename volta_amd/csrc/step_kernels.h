@@ -25,10 +25,6 @@ hipError_t launch_loss_mse(const float* yhat, const float* y, float* delta, int 
                            const float2* bc_table, int bc_len, hipStream_t st);
 hipError_t launch_loss_ce(const float* z, const int32_t* labels, float* delta, int B, int C,
                           DevScalars* sc, const float2* bc_table, int bc_len, hipStream_t st);
-int colsum_parts(int B);
-hipError_t launch_colsum(const float* delta, int B, int c, float* db, float* bias, const DevScalars* sc,
-                         float* workspace, hipStream_t st, Recorder* rec = nullptr,
-                         const char* label = "colsum");
 hipError_t launch_adam(float* w, float* m, float* v, const float* g, const SegTable& segs,
                        int64_t total, const DevScalars* sc, float b1, float b2, float eps,
                        hipStream_t st);

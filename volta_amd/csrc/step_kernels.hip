@@ -1,6 +1,8 @@
-// Non-GEMM kernels of the MLP step: loss heads, bias-gradient column sums,
-// flat optimizer passes.  All reductions use a fixed association order and
-// no atomics, so two runs on the same inputs are bit-identical.
+// Non-GEMM kernels of the MLP step: the stand-alone loss heads (used when the
+// output layer is wider than one GEMM tile) and flat optimizer passes (the
+// step fuses the optimizer into the dW epilogue; these run the same element
+// functions over whole buffers for checks).  All reductions use a fixed
+// association order and no floating-point atomics.
 #include "step_kernels.h"
 
 namespace volta {
@@ -19,22 +21,6 @@ __device__ __forceinline__ float block_sum_fixed(float v, float* lds) {
     for (int w = 1; w < THREADS / kWave; ++w) s = s + lds[w];
   }
   return s;
-}
-
-// Once per step, after the loss: advance the Adam step counter and publish
-// the bias corrections 1 - beta^t, looked up in a table the host filled with
-// the same f32 powf the reference calls (mlp_train_rust_codegen.rs:803-811).
-__device__ __forceinline__ void step_epilogue(DevScalars* sc, const float2* bc_table, int bc_len,
-                                              float loss) {
-  sc->loss = loss;
-  if (!(fabsf(loss) <= 3.402823466e38f)) sc->flags |= VOLTA_STATUS_NONFINITE_LOSS;
-  if (bc_table) {
-    const uint32_t t = sc->t + 1u;
-    sc->t = t;
-    const float2 bc = bc_table[t < (uint32_t)bc_len ? t : (uint32_t)(bc_len - 1)];
-    sc->bc1 = bc.x;
-    sc->bc2 = bc.y;
-  }
 }
 
 // MSE head (mlp_train_rust_codegen.rs:792-798): d = yhat - y,
@@ -78,59 +64,21 @@ loss_ce_kernel(const float* __restrict__ z, const int32_t* __restrict__ labels,
     float sum = 0.0f;
     for (int j = 0; j < C; ++j) sum = sum + expf(zr[j] - mx);
     const float lse = mx + logf(sum);
-    float sample = 0.0f;
-    bool hit = false;
+    float sample = __builtin_nanf("");
     for (int j = 0; j < C; ++j) {
       const bool on = j == lab;
-      hit |= on;
       if (on) sample = -(zr[j] - lse);
       dr[j] = (expf(zr[j] - mx) / sum - (on ? 1.0f : 0.0f)) / bf;
     }
-    if (!hit) {
-      bad = true;
-      sample = __builtin_nanf("");
-    }
+    bad |= lab < 0 || lab >= C;
     acc = acc + sample;
   }
   const int any_bad = __syncthreads_or(bad ? 1 : 0);
   const float s = block_sum_fixed<1024>(acc, lds);
   if (threadIdx.x == 0) {
-    if (any_bad) sc->flags |= VOLTA_STATUS_BAD_ARGUMENT;
+    if (any_bad) atomicOr(&sc->flags, (uint32_t)VOLTA_STATUS_BAD_ARGUMENT);
     step_epilogue(sc, bc_table, bc_len, s / bf);
   }
-}
-
-// Bias gradient db[j] = sum_b delta[b, j] (mlp_train_rust_codegen.rs:931-933).
-// Stage 1: block (x, y) sums rows [y*rows_per_part, ...) of 256 columns in
-// row order.  With one part it writes db directly (and, for SGD, applies
-// b -= lr*db, :986-991); otherwise it writes partial[y][j].
-__global__ void __launch_bounds__(256)
-colsum_kernel(const float* __restrict__ delta, int B, int c, int rows_per_part,
-              float* __restrict__ out, float* __restrict__ bias, const DevScalars* sc) {
-  const int j = blockIdx.x * 256 + threadIdx.x;
-  if (j >= c) return;
-  const int r0 = blockIdx.y * rows_per_part;
-  const int r1 = min(B, r0 + rows_per_part);
-  float s = 0.0f;
-  for (int r = r0; r < r1; ++r) s = s + delta[(size_t)r * c + j];
-  if (gridDim.y == 1) {
-    out[j] = s;
-    if (bias) bias[j] = bias[j] - sc->lr * s;
-  } else {
-    out[(size_t)blockIdx.y * c + j] = s;
-  }
-}
-
-// Stage 2: db[j] = sum over parts in part order (+ SGD bias update).
-__global__ void __launch_bounds__(256)
-colsum_final_kernel(const float* __restrict__ partial, int parts, int c, float* __restrict__ db,
-                    float* __restrict__ bias, const DevScalars* sc) {
-  const int j = blockIdx.x * 256 + threadIdx.x;
-  if (j >= c) return;
-  float s = partial[j];
-  for (int p = 1; p < parts; ++p) s = s + partial[(size_t)p * c + j];
-  db[j] = s;
-  if (bias) bias[j] = bias[j] - sc->lr * s;
 }
 
 // Find the segment holding flat element `base` (segments are padded to
@@ -142,11 +90,8 @@ __device__ __forceinline__ int find_segment(const SegTable& t, int64_t base) {
   return s;
 }
 
-// Adam / AdamW over the flat parameter buffer, one element per thread
-// (adam_update_slice, mlp_train_rust_codegen.rs:341-388; AdamW decays
-// weights only, :960-966).  The reference computes v with (1-b2)*(g*g) in
-// its 8-wide loop and ((1-b2)*g)*g in the scalar tail (last n%8 elements of
-// each buffer); the same split is kept per segment.
+// Adam / AdamW over a flat segmented buffer (adam_update,
+// mlp_train_rust_codegen.rs:326-388; the tail rule is per segment).
 __global__ void __launch_bounds__(256)
 adam_kernel(float* __restrict__ w, float* __restrict__ m, float* __restrict__ v,
             const float* __restrict__ g, SegTable segs, const DevScalars* __restrict__ sc,
@@ -157,25 +102,15 @@ adam_kernel(float* __restrict__ w, float* __restrict__ m, float* __restrict__ v,
   const float wd = segs.wd[s];
   const int64_t count = segs.count[s];
   const int64_t vec_end = count - count % 8;
-  const float omb1 = 1.0f - b1, omb2 = 1.0f - b2;
   for (int e = threadIdx.x; e < kSegAlign; e += 256) {
     const int64_t local = base - segs.off[s] + e;
     if (local >= count) continue;
     const int64_t k = base + e;
-    const float gk = g[k];
-    const float m1 = b1 * m[k] + omb1 * gk;
-    const float v1 = local >= vec_end ? b2 * v[k] + omb2 * gk * gk : b2 * v[k] + omb2 * (gk * gk);
-    m[k] = m1;
-    v[k] = v1;
-    const float w0 = w[k];
-    const float mhat = m1 / bc1;
-    const float vhat = v1 / bc2;
-    const float denom = sqrtf(vhat) + eps;
-    w[k] = w0 - lr * (mhat / denom + wd * w0);
+    adam_elem(w + k, m + k, v + k, g[k], local >= vec_end, lr, bc1, bc2, b1, b2, eps, wd);
   }
 }
 
-// Adagrad (mlp_train_rust_codegen.rs:967-985): G += g^2; w -= lr*g/(sqrt(G)+eps).
+// Adagrad over a flat segmented buffer (mlp_train_rust_codegen.rs:967-985).
 __global__ void __launch_bounds__(256)
 adagrad_kernel(float* __restrict__ w, float* __restrict__ G, const float* __restrict__ g,
                SegTable segs, const DevScalars* __restrict__ sc, float eps) {
@@ -187,10 +122,7 @@ adagrad_kernel(float* __restrict__ w, float* __restrict__ G, const float* __rest
     const int64_t local = base - segs.off[s] + e;
     if (local >= count) continue;
     const int64_t k = base + e;
-    const float gk = g[k];
-    const float Gk = G[k] + gk * gk;
-    G[k] = Gk;
-    w[k] = w[k] - lr * gk / (sqrtf(Gk) + eps);
+    adagrad_elem(w + k, G + k, g[k], lr, eps);
   }
 }
 
@@ -207,35 +139,6 @@ hipError_t launch_loss_ce(const float* z, const int32_t* labels, float* delta, i
   hipLaunchKernelGGL(loss_ce_kernel, dim3(1), dim3(1024), 0, st, z, labels, delta, B, C, sc, bc_table,
                      bc_len);
   return hipGetLastError();
-}
-
-int colsum_parts(int B) {
-  if (B <= 256) return 1;
-  int parts = B / 128;
-  return parts > 32 ? 32 : parts;
-}
-
-hipError_t launch_colsum(const float* delta, int B, int c, float* db, float* bias, const DevScalars* sc,
-                         float* workspace, hipStream_t st, Recorder* rec, const char* label) {
-  const int parts = colsum_parts(B);
-  const int rpp = (B + parts - 1) / parts;
-  dim3 grid((c + 255) / 256, parts);
-  // algorithmic traffic of db = colsum(delta): 4(B*c + c) bytes
-  const double bytes = 4.0 * ((double)B * c + c);
-  if (parts == 1) {
-    hipLaunchKernelGGL(colsum_kernel, grid, dim3(256), 0, st, delta, B, c, rpp, db, bias, sc);
-    hipError_t e = hipGetLastError();
-    return e != hipSuccess ? e : mark(rec, label, (double)B * c, bytes);
-  }
-  hipLaunchKernelGGL(colsum_kernel, grid, dim3(256), 0, st, delta, B, c, rpp, workspace,
-                     (float*)nullptr, sc);
-  hipError_t e = hipGetLastError();
-  if (e == hipSuccess) e = mark(rec, label, (double)B * c, bytes);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(colsum_final_kernel, dim3((c + 255) / 256), dim3(256), 0, st, workspace, parts, c,
-                     db, bias, sc);
-  e = hipGetLastError();
-  return e != hipSuccess ? e : mark(rec, std::string(label) + ".final", (double)parts * c, 4.0 * ((double)parts * c + c));
 }
 
 hipError_t launch_adam(float* w, float* m, float* v, const float* g, const SegTable& segs,

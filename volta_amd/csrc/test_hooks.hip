@@ -43,9 +43,16 @@ int32_t volta_hip_gemm(int32_t layout, const float* A, const float* B, float* Cm
     p.splits = (K + kps - 1) / kps;
   }
   float* ws = nullptr;
-  if (p.splits > 1 && hipMalloc((void**)&ws, p.workspace_floats(M, N) * sizeof(float)) != hipSuccess) {
-    set_last_error("volta_hip_gemm: workspace allocation failed");
-    return -1;
+  unsigned* counters = nullptr;
+  if (p.splits > 1) {
+    const size_t cbytes = (size_t)p.tiles(M, N) * sizeof(unsigned);
+    if (hipMalloc((void**)&ws, p.workspace_floats(M, N) * sizeof(float)) != hipSuccess ||
+        hipMalloc((void**)&counters, cbytes) != hipSuccess || hipMemset(counters, 0, cbytes) != hipSuccess) {
+      if (ws) (void)hipFree(ws);
+      if (counters) (void)hipFree(counters);
+      set_last_error("volta_hip_gemm: workspace allocation failed");
+      return -1;
+    }
   }
   GemmArgs a{};
   a.A = A;
@@ -56,12 +63,14 @@ int32_t volta_hip_gemm(int32_t layout, const float* A, const float* B, float* Cm
   a.N = N;
   a.K = K;
   a.partial = ws;
+  a.counters = counters;
   a.epi.kind = EPI_STORE;
   a.epi.ldc = N;
   a.epi.out = Cm;
   hipError_t e = gemm_launch(p, a, nullptr);
   if (e == hipSuccess) e = hipDeviceSynchronize();
-  if (ws) hipFree(ws);
+  if (ws) (void)hipFree(ws);
+  if (counters) (void)hipFree(counters);
   if (e != hipSuccess) {
     set_last_error(std::string("volta_hip_gemm: ") + hipGetErrorString(e));
     return -1;
