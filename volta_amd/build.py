@@ -24,8 +24,8 @@ CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libvolta_hip.so")
 
-SOURCES = ["gemm.hip", "step_kernels.hip", "runtime.hip", "test_hooks.hip", "spec.cpp"]
-HEADERS = ["gemm.h", "step_kernels.h", "device_common.h", "spec.h"]
+SOURCES = ["gemm.hip", "skinny.hip", "step_kernels.hip", "runtime.hip", "test_hooks.hip", "spec.cpp"]
+HEADERS = ["gemm.h", "skinny.h", "step_kernels.h", "device_common.h", "recorder.h", "spec.h"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("VOLTA_OFFLOAD_ARCH", "gfx950")

@@ -30,10 +30,18 @@
 #include <vector>
 
 #include "gemm.h"
+#include "skinny.h"
 #include "spec.h"
 #include "step_kernels.h"
 
 namespace volta {
+
+// How the output layer and the loss head run.
+enum OutMode {
+  OUT_NARROW = 0,     // L[n] <= 16: out_layer_kernel (dot products + loss head)
+  OUT_GEMM_LOSS = 1,  // L[n] <= 64: MFMA GEMM with the loss head in its epilogue
+  OUT_GEMM = 2,       // wider: MFMA GEMM, then a stand-alone loss kernel
+};
 
 static std::string hip_msg(const char* what, hipError_t e) {
   return std::string(what) + ": " + hipGetErrorString(e);
@@ -81,7 +89,9 @@ struct Handle {
   unsigned* counters = nullptr;   // split-K arrival counters (+1: loss counter)
   int n_counters = 0;
   float* loss_partials = nullptr;  // one float per output-layer M-tile
-  bool fused_loss = true;     // loss head in the output-layer GEMM (N <= 64)
+  int out_mode = 0;           // OUT_NARROW / OUT_GEMM_LOSS / OUT_GEMM (output layer + loss head)
+  bool narrow_dx = false;     // dX of the output layer as an outer product (L[n] <= 16)
+  bool narrow_dw = false;     // dW of the output layer by narrow_dw_kernel
   bool keep_grads = false;    // also store dW/db in `grads` (VOLTA_KEEP_GRADS=1)
   DevScalars* scalars = nullptr;
   float2* bc_table = nullptr;
@@ -152,6 +162,30 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
   for (int i = 0; i < n; ++i) {
     const LayerPlan& lp = h->layers[i];
     const bool last = i == n - 1;
+    if (last && h->out_mode == OUT_NARROW) {
+      OutLayerArgs o{};
+      o.act = h->act[i];
+      o.W = h->params + lp.w_off;
+      o.bias = h->params + lp.b_off;
+      o.B = B;
+      o.K = lp.r;
+      o.N = lp.c;
+      o.loss = s.loss;
+      o.y = static_cast<const float*>(h->target);
+      o.labels = static_cast<const int32_t*>(h->target);
+      o.out = h->act[n];
+      o.delta = h->delta[n - 1];
+      o.partials = h->loss_partials;
+      o.scalars = h->scalars;
+      o.bc_table = h->bc_table;
+      o.bc_len = h->bc_len;
+      VOLTA_CHECK(launch_out_layer(o, st));
+      // algorithmic bytes: 4(B*r + r*c + B*c) + loss head 8*B*c
+      std::snprintf(label, sizeof label, "fwd%d+loss", i);
+      VOLTA_CHECK(mark(rec, label, 2.0 * B * lp.r * lp.c,
+                       4.0 * ((double)B * lp.r + (double)lp.r * lp.c + (double)B * lp.c) + 8.0 * B * lp.c));
+      continue;
+    }
     GemmArgs a{};
     base_args(a);
     a.A = h->act[i];
@@ -161,7 +195,7 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
     a.M = B;
     a.N = lp.c;
     a.K = lp.r;
-    a.epi.kind = last && h->fused_loss ? EPI_LOSS : EPI_BIAS_ACT;
+    a.epi.kind = last && h->out_mode == OUT_GEMM_LOSS ? EPI_LOSS : EPI_BIAS_ACT;
     a.epi.act = last ? kIdentity : s.activation;
     a.epi.ldc = lp.c;
     a.epi.out = h->act[i + 1];
@@ -178,13 +212,13 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
       a.epi.bc_table = h->bc_table;
       a.epi.bc_len = h->bc_len;
     }
-    std::snprintf(label, sizeof label, last && h->fused_loss ? "fwd%d+loss" : "fwd%d", i);
+    std::snprintf(label, sizeof label, last && h->out_mode == OUT_GEMM_LOSS ? "fwd%d+loss" : "fwd%d", i);
     // algorithmic bytes: 4(B*r + r*c + B*c*(2 if hidden else 1)) (+ loss head)
     const double bytes = 4.0 * ((double)B * lp.r + (double)lp.r * lp.c + (double)B * lp.c * (last ? 1 : 2)) +
-                         (last && h->fused_loss ? 8.0 * B * Ln : 0.0);
+                         (last && h->out_mode == OUT_GEMM_LOSS ? 8.0 * B * Ln : 0.0);
     VOLTA_CHECK(gemm_launch(lp.fwd, a, st, rec, label, bytes));
   }
-  if (!h->fused_loss) {  // output layer wider than one tile: stand-alone loss head
+  if (h->out_mode == OUT_GEMM) {  // output layer wider than one tile: stand-alone loss head
     if (s.loss == VOLTA_LOSS_MSE)
       VOLTA_CHECK(launch_loss_mse(h->act[n], static_cast<const float*>(h->target), h->delta[n - 1], B * Ln,
                                   h->scalars, h->bc_table, h->bc_len, st));
@@ -196,7 +230,14 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
   // Backward (:819-993).  dX_i reads W_i before dW_i updates it in place.
   for (int i = n - 1; i >= 0; --i) {
     const LayerPlan& lp = h->layers[i];
-    if (i > 0) {
+    const bool out_layer = i == n - 1;
+    if (i > 0 && out_layer && h->narrow_dx) {
+      VOLTA_CHECK(launch_outer_dx(h->delta[i], h->params + lp.w_off, B, lp.r, lp.c, s.activation, h->act[i],
+                                  h->pre[i - 1], h->delta[i - 1], st));
+      std::snprintf(label, sizeof label, "dx%d", i);
+      VOLTA_CHECK(mark(rec, label, 2.0 * B * lp.r * lp.c,
+                       4.0 * ((double)B * lp.c + (double)lp.r * lp.c + 2.0 * B * lp.r)));
+    } else if (i > 0) {
       GemmArgs a{};
       base_args(a);
       a.A = h->delta[i];
@@ -216,6 +257,35 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
       // algorithmic bytes: 4(B*c + r*c + 2*B*r)
       const double bytes = 4.0 * ((double)B * lp.c + (double)lp.r * lp.c + 2.0 * B * lp.r);
       VOLTA_CHECK(gemm_launch(lp.dx, a, st, rec, label, bytes));
+    }
+    const double P_i = (double)lp.r * lp.c + lp.c;
+    const int sopt = s.optimizer == VOLTA_OPT_SGD ? 2 : s.optimizer == VOLTA_OPT_ADAGRAD ? 4 : 6;
+    if (out_layer && h->narrow_dw) {
+      NarrowDwArgs d{};
+      d.act = h->act[i];
+      d.delta = h->delta[i];
+      d.B = B;
+      d.R = lp.r;
+      d.N = lp.c;
+      d.opt = s.optimizer == VOLTA_OPT_ADAMW ? VOLTA_OPT_ADAM : s.optimizer;
+      d.w = h->params + lp.w_off;
+      d.b = h->params + lp.b_off;
+      d.m = h->opt_a ? h->opt_a + lp.w_off : nullptr;
+      d.v = h->opt_b ? h->opt_b + lp.w_off : nullptr;
+      d.bm = h->opt_a ? h->opt_a + lp.b_off : nullptr;
+      d.bv = h->opt_b ? h->opt_b + lp.b_off : nullptr;
+      d.grad = h->keep_grads ? h->grads + lp.w_off : nullptr;
+      d.bgrad = h->keep_grads ? h->grads + lp.b_off : nullptr;
+      d.wd = s.optimizer == VOLTA_OPT_ADAMW ? s.weight_decay : 0.0f;
+      d.b1 = s.beta1;
+      d.b2 = s.beta2;
+      d.eps = s.eps;
+      d.scalars = h->scalars;
+      VOLTA_CHECK(launch_narrow_dw(d, st));
+      std::snprintf(label, sizeof label, "dw%d+db+opt", i);
+      VOLTA_CHECK(mark(rec, label, 2.0 * B * lp.r * lp.c,
+                       4.0 * ((double)B * lp.r + (double)B * lp.c) + 4.0 * sopt * P_i));
+      continue;
     }
     // dW_i = act_i^T delta_i with db_i = column sums of delta_i and the
     // optimizer update of W_i and b_i in the epilogue.
@@ -251,8 +321,6 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
     // optimizer's 4*s per parameter minus the gradient round trip it saves:
     // SGD reads+writes W (s=2 beyond dW), Adam w,m,v read+write (6),
     // Adagrad w,G read+write (4).
-    const double P_i = (double)lp.r * lp.c + lp.c;
-    const int sopt = s.optimizer == VOLTA_OPT_SGD ? 2 : s.optimizer == VOLTA_OPT_ADAGRAD ? 4 : 6;
     const double bytes = 4.0 * ((double)B * lp.r + (double)B * lp.c) + 4.0 * sopt * P_i;
     VOLTA_CHECK(gemm_launch(lp.dw, a, st, rec, label, bytes));
   }
@@ -292,14 +360,17 @@ static bool build(Handle* h) {
   // GEMM plans.  Vector (16-byte) operand loads need the contiguous extent
   // and leading dimension to be multiples of 4 floats.  The output layer's
   // loss head runs in its GEMM when the layer fits one 64-wide tile.
-  h->fused_loss = h->L[n] <= 64;
+  const int Ln = h->L[n];
+  h->out_mode = Ln <= 16 ? OUT_NARROW : Ln <= 64 ? OUT_GEMM_LOSS : OUT_GEMM;
+  h->narrow_dx = Ln <= 16 && n > 1;
+  h->narrow_dw = Ln <= 16 && (size_t)B * Ln * sizeof(float) <= kNarrowDwLdsBytes;
   size_t ws_floats = 0;
   int max_tiles = 1;
   for (int i = 0; i < n; ++i) {
     LayerPlan& lp = h->layers[i];
     const bool vr = lp.r % 4 == 0, vc = lp.c % 4 == 0;
     lp.fwd = gemm_plan(GEMM_NN, B, lp.c, lp.r, vr && vc, h->num_cus);
-    if (i == n - 1 && h->fused_loss) lp.fwd.tile = TILE_64x64;
+    if (i == n - 1 && h->out_mode == OUT_GEMM_LOSS) lp.fwd.tile = TILE_64x64;
     lp.dx = gemm_plan(GEMM_NT, B, lp.r, lp.c, vc, h->num_cus);
     lp.dw = gemm_plan(GEMM_TN, lp.r, lp.c, B, vr && vc, h->num_cus);
     ws_floats = std::max(ws_floats, lp.fwd.workspace_floats(B, lp.c));
@@ -350,7 +421,7 @@ static bool build(Handle* h) {
   req(&h->target, s.loss == VOLTA_LOSS_MSE ? (size_t)B * h->L[n] * 4 : (size_t)B * 4);
   if (ws_floats) req((void**)&h->gemm_ws, ws_floats * 4);
   req((void**)&h->counters, (size_t)h->n_counters * sizeof(unsigned));
-  req((void**)&h->loss_partials, (size_t)((B + 63) / 64) * 4);
+  req((void**)&h->loss_partials, (size_t)std::max((B + 63) / 64, out_layer_blocks(B)) * 4);
   if (adam) req((void**)&h->bc_table, bc.size() * sizeof(float2));
   size_t total = 0;
   for (auto& r : reqs) total += r.bytes;

@@ -1,0 +1,53 @@
+// Host interface of the narrow output-layer kernels (skinny.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "device_common.h"
+
+namespace volta {
+
+struct OutLayerArgs {
+  const float* act;   // act_{n-1} [B x K]
+  const float* W;     // W_{n-1} [K x N]
+  const float* bias;  // b_{n-1} [N]
+  int B, K, N;
+  int loss;           // enum volta_loss
+  const float* y;     // MSE targets [B x N]
+  const int32_t* labels;  // CE labels [B]
+  float* out;         // act_n = z [B x N]
+  float* delta;       // delta_{n-1} [B x N]
+  float* partials;    // per-block loss (when more than one block)
+  DevScalars* scalars;
+  const float2* bc_table;
+  int bc_len;
+};
+
+struct NarrowDwArgs {
+  const float* act;    // act_i [B x R]
+  const float* delta;  // delta_i [B x N]
+  int B, R, N;
+  int opt;             // enum volta_optimizer (AdamW as Adam with wd)
+  float* w;            // W_i [R x N], updated in place
+  float* m;            // Adam m / Adagrad G for W_i
+  float* v;            // Adam v for W_i
+  float* b;            // b_i [N]
+  float* bm;
+  float* bv;
+  float* grad;         // optional dW copy
+  float* bgrad;        // optional db copy
+  float wd, b1, b2, eps;
+  DevScalars* scalars;
+};
+
+constexpr size_t kNarrowDwLdsBytes = 64 * 1024;
+
+int out_layer_blocks(int B);
+hipError_t launch_out_layer(const OutLayerArgs& p, hipStream_t st);
+hipError_t launch_outer_dx(const float* delta, const float* W, int B, int R, int K, int act, const float* aux_act,
+                           const float* aux_pre, float* out, hipStream_t st);
+hipError_t launch_narrow_dw(const NarrowDwArgs& p, hipStream_t st);
+
+}  // namespace volta
