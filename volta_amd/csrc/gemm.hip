@@ -389,11 +389,15 @@ gemm_f32_mfma(GemmArgs args) {
 
   const int kbeg = blockIdx.y * args.k_per_split;
   const int kend = min(args.K, kbeg + args.k_per_split);
-  // Column sums of B over k (dW's db), done by the workgroups of the first
-  // row of tiles, one thread per column, in k order.
+  // Column sums of B over k (dW's db = sum_b delta), taken from the MFMA B
+  // fragments the waves already hold: the first row of waves (wm == 0) of
+  // the first row of tiles adds its fragments in k order per lane half,
+  // then the two halves are added.  Fixed order, no extra LDS traffic.
   constexpr bool kColsum = EPI == EPI_DW_OPT && !B_KC;
-  const bool colsum = kColsum && args.colsum_b && tm == 0;
-  float csum = 0.0f;
+  const bool colsum = kColsum && args.colsum_b && tm == 0 && wm == 0;
+  float cs[T::TN];
+#pragma unroll
+  for (int j = 0; j < T::TN; ++j) cs[j] = 0.0f;
 
   TileLoader<BM, BK, A_KC, VEC, THREADS> la;
   TileLoader<BN, BK, B_KC, VEC, THREADS> lb;
@@ -438,10 +442,13 @@ gemm_f32_mfma(GemmArgs args) {
 #pragma unroll
             for (int j = 0; j < T::TN; ++j)
               acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
-      }
-      if (kColsum && colsum && tid < BN) {
-        // rows beyond kend were loaded as zeros; adding them changes nothing
-        for (int kk = 0; kk < BK; ++kk) csum = csum + b_s[kk * LB::kStride + tid];
+        if (kColsum && colsum) {
+          // rows beyond kend were loaded as zeros; adding them changes nothing
+#pragma unroll
+          for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) cs[j] = cs[j] + fb[j][s];
+        }
       }
       if (more) {
         la.store(lds_a[buf ^ 1], tid);
@@ -451,6 +458,14 @@ gemm_f32_mfma(GemmArgs args) {
       buf ^= 1;
     }
   }
+
+  // Column sums: add the two lane halves (same value in both lanes); lanes
+  // of half 0 own column n0 + wn*WN + j*32 + l32.
+  if (kColsum && colsum) {
+#pragma unroll
+    for (int j = 0; j < T::TN; ++j) cs[j] = cs[j] + __shfl_xor(cs[j], 32, kWave);
+  }
+  const bool cs_owner = kColsum && colsum && h == 0;
 
   // Accumulator register v of lane (h, l32) in block (i, j) holds row
   // 8*(v/4) + 4*h + (v%4), column l32 of that 32x32 block.
@@ -470,7 +485,13 @@ gemm_f32_mfma(GemmArgs args) {
           if (m < M && n < N) mine[(size_t)m * N + n] = acc[i][j][v];
         }
       }
-    if (kColsum && colsum && tid < BN && n0 + tid < N) mine[(size_t)M * N + n0 + tid] = csum;
+    if (cs_owner) {
+#pragma unroll
+      for (int j = 0; j < T::TN; ++j) {
+        const int n = n0 + wn * WN + j * 32 + l32;
+        if (n < N) mine[(size_t)M * N + n] = cs[j];
+      }
+    }
     if constexpr (!INK) {
       return;  // splitk_reduce finishes
     } else {
@@ -500,11 +521,17 @@ gemm_f32_mfma(GemmArgs args) {
             }
           }
         }
-      if (kColsum && colsum && tid < BN && n0 + tid < N) {
-        const size_t off = (size_t)M * N + n0 + tid;
-        float s = planes[off];
-        for (unsigned z = 1; z < gridDim.y; ++z) s = s + planes[z * plane + off];
-        csum = s;
+      if (cs_owner) {
+#pragma unroll
+        for (int j = 0; j < T::TN; ++j) {
+          const int n = n0 + wn * WN + j * 32 + l32;
+          if (n < N) {
+            const size_t off = (size_t)M * N + n;
+            float s = planes[off];
+            for (unsigned z = 1; z < gridDim.y; ++z) s = s + planes[z * plane + off];
+            cs[j] = s;
+          }
+        }
       }
       if (tid == 0) args.counters[blockIdx.x] = 0u;
     }
@@ -538,7 +565,13 @@ gemm_f32_mfma(GemmArgs args) {
       for (int j = 0; j < T::TN; ++j)
         block_epilogue<EPI>(e, acc[i][j], m0 + wm * WM + i * 32 + 4 * h, n0 + wn * WN + j * 32 + l32, M, N);
     if constexpr (kColsum) {
-      if (colsum && e.b && tid < BN && n0 + tid < N) apply_bias_update(e, n0 + tid, N, csum);
+      if (cs_owner && e.b) {
+#pragma unroll
+        for (int j = 0; j < T::TN; ++j) {
+          const int n = n0 + wn * WN + j * 32 + l32;
+          if (n < N) apply_bias_update(e, n, N, cs[j]);
+        }
+      }
     }
   }
 }
@@ -620,7 +653,7 @@ hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& args_in, hipStream_t s
   GemmArgs a = args_in;
   a.k_per_split = p.k_per_split;
   if (p.splits > 1 && (!a.partial || !a.counters)) return hipErrorInvalidValue;
-  if (a.epi.kind == EPI_LOSS && (p.tile != TILE_64x64 || a.N > 64)) return hipErrorInvalidValue;
+  if (a.epi.kind == EPI_LOSS && (p.tile == TILE_128x128 || a.N > 64)) return hipErrorInvalidValue;
   if (a.colsum_b && p.layout != GEMM_TN) return hipErrorInvalidValue;
   // The loss head always reduces in-kernel (it needs whole rows).
   const bool ink = p.inkernel_reduce || a.epi.kind == EPI_LOSS;
@@ -628,6 +661,7 @@ hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& args_in, hipStream_t s
   switch (p.tile) {
     case TILE_64x64: err = launch_cfg<64, 64, 32, 32, 32>(a, p.layout, p.vec, p.splits, ink, st); break;
     case TILE_128x128: err = launch_cfg<128, 128, 32, 64, 64>(a, p.layout, p.vec, p.splits, ink, st); break;
+    case TILE_64x64_K64: err = launch_cfg<64, 64, 64, 32, 32>(a, p.layout, p.vec, p.splits, ink, st); break;
     default: return hipErrorInvalidValue;
   }
   if (err != hipSuccess) return err;
@@ -653,16 +687,20 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus) {
   // (dW at small batch) is epilogue bound and wants the 4x larger grid.
   p.tile = ((size_t)M * N >= (size_t)1024 * 1024 && M >= 128 && N >= 128 && K > 256) ? TILE_128x128
                                                                                       : TILE_64x64;
+  const char* sb = std::getenv("VOLTA_SMALL_BK");
+  if (p.tile == TILE_64x64 && sb && std::atoi(sb) == 64) p.tile = TILE_64x64_K64;
   const int tiles = p.tiles(M, N);
-  const int bk = 32;
+  const int bk = p.tile == TILE_64x64_K64 ? 64 : 32;
   const char* mk = std::getenv("VOLTA_SPLITK_MIN_K");
   const int min_k = mk && *mk ? std::max(32, std::atoi(mk)) : 128;
   const char* ik = std::getenv("VOLTA_SPLITK_INKERNEL");
   p.inkernel_reduce = ik && *ik && *ik != '0';
+  const char* sw = std::getenv("VOLTA_SPLITK_WGS_PER_CU");
+  const int wgs_per_cu = sw && *sw ? std::max(1, std::atoi(sw)) : 1;
   int splits = 1;
-  // Split K while the grid is below ~2 workgroups per CU and each slice keeps
-  // at least min_k values of k.
-  while (tiles * splits * 2 <= 2 * num_cus && K / (splits * 2) >= min_k && splits < 32) splits *= 2;
+  // Split K while the grid is below ~wgs_per_cu workgroups per CU and each
+  // slice keeps at least min_k values of k.
+  while (tiles * splits * 2 <= wgs_per_cu * num_cus && K / (splits * 2) >= min_k && splits < 32) splits *= 2;
   int kps = (K + splits - 1) / splits;
   kps = ((kps + bk - 1) / bk) * bk;
   splits = (K + kps - 1) / kps;

@@ -31,7 +31,7 @@ int32_t volta_hip_gemm(int32_t layout, const float* A, const float* B, float* Cm
   const int contig_b = layout == GEMM_NT ? K : N;
   const bool vec = contig_a % 4 == 0 && contig_b % 4 == 0;
   GemmPlan p = gemm_plan(layout, M, N, K, vec, cus);
-  if (force_tile > TILE_128x128) {
+  if (force_tile > TILE_64x64_K64) {
     set_last_error("volta_hip_gemm: unknown tile");
     return -1;
   }
