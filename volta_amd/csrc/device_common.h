@@ -118,6 +118,34 @@ __device__ __forceinline__ void step_epilogue(DevScalars* sc, const float2* bc_t
   }
 }
 
+// step_epilogue split in two so its loads (step counter, then the table
+// entry) overlap the kernel's main work: step_prefetch at kernel start,
+// step_finish at the end (same stores as step_epilogue).  Single thread;
+// nothing else may change the counter in between.
+struct StepNext {
+  uint32_t t;
+  float2 bc;
+};
+
+__device__ __forceinline__ StepNext step_prefetch(const DevScalars* sc, const float2* bc_table, int bc_len) {
+  StepNext s{};
+  if (bc_table) {
+    s.t = sc->t + 1u;
+    s.bc = bc_table[s.t < (uint32_t)bc_len ? s.t : (uint32_t)(bc_len - 1)];
+  }
+  return s;
+}
+
+__device__ __forceinline__ void step_finish(DevScalars* sc, const StepNext& s, bool has_table, float loss) {
+  sc->loss = loss;
+  if (!(fabsf(loss) <= 3.402823466e38f)) atomicOr(&sc->flags, (uint32_t)VOLTA_STATUS_NONFINITE_LOSS);
+  if (has_table) {
+    sc->t = s.t;
+    sc->bc1 = s.bc.x;
+    sc->bc2 = s.bc.y;
+  }
+}
+
 // Fixed-order wavefront sum (butterfly over 64 lanes).  Every lane ends with
 // the same value and the association order depends only on lane indices,
 // so results are bit-identical run to run.

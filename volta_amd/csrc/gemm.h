@@ -60,32 +60,6 @@ struct EpiArgs {
   int bc_len;
 };
 
-// An operand that its producer left as split-K partial planes: the value at
-// (row, col) of the producer's [rows x ld] output is
-//   T( sum_{z = 0..splits-1} planes[z*stride + row*ld + col] )   (z in order)
-// with T the producer's epilogue, applied by the consumer while it loads its
-// tile.  This replaces a separate reduction kernel; the arithmetic is the
-// same as that kernel's (planes in slice order, then the epilogue).
-enum DeferKind {
-  DEFER_NONE = 0,
-  DEFER_BIAS_ACT = 1,  // T(x) = f(x + bias[col])       (forward output)
-  DEFER_DX_ACT = 2,    // T(x) = x * f'(pre, act)[row][col]  (dX output)
-};
-
-struct DeferredOperand {
-  int kind;              // DeferKind
-  int splits;
-  int ld;                // row length of the producer output
-  size_t stride;         // floats between planes
-  const float* planes;
-  int act;               // activation of T (kIdentity for none)
-  const float* bias;     // DEFER_BIAS_ACT
-  const float* aux_act;  // DEFER_DX_ACT: activation output at (row, col)
-  const float* aux_pre;  // DEFER_DX_ACT: pre-activation (null when not kept)
-  float* mat_out;        // if set, the designated workgroups also store T(...) here
-  float* mat_pre;        // DEFER_BIAS_ACT: and the pre-activation here
-};
-
 struct GemmArgs {
   const float* A;
   const float* B;
@@ -95,8 +69,6 @@ struct GemmArgs {
   float* partial;       // split-K workspace: splits planes of (M+1)*N floats
   unsigned* counters;   // split-K arrival counters, one per output tile, zero between launches
   int colsum_b;         // 1: also sum the B operand over k (dW: db = sum_b delta)
-  DeferredOperand da;   // A operand still in partial planes (kind DEFER_NONE: read A)
-  DeferredOperand db;   // B operand still in partial planes (kind DEFER_NONE: read B)
   EpiArgs epi;
 };
 
@@ -109,7 +81,6 @@ struct GemmPlan {
   int k_per_split = 0;
   bool vec = false;
   bool inkernel_reduce = false;  // split-K reduced by the last slice (else a second kernel)
-  bool defer_out = false;        // leave the partial planes to the consumer (no reduce kernel)
   int tiles(int M, int N) const {
     const int t = tile == TILE_128x128 ? 128 : 64;
     return ((M + t - 1) / t) * ((N + t - 1) / t);
@@ -120,56 +91,6 @@ struct GemmPlan {
 // `min_k` is the smallest K slice a split may have.
 GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus);
 
-// Value of a deferred operand at (row, col..col+3), the four columns at once
-// (col % 4 == 0); optionally stores T(...) (and the pre-activation).
-__device__ __forceinline__ floatx4 deferred_load4(const DeferredOperand& d, int row, int col, bool mat) {
-  const size_t off = (size_t)row * d.ld + col;
-  floatx4 s = *reinterpret_cast<const floatx4*>(d.planes + off);
-  for (int z = 1; z < d.splits; ++z) {
-    const floatx4 p = *reinterpret_cast<const floatx4*>(d.planes + (size_t)z * d.stride + off);
-    s[0] = s[0] + p[0];
-    s[1] = s[1] + p[1];
-    s[2] = s[2] + p[2];
-    s[3] = s[3] + p[3];
-  }
-  floatx4 out;
-  if (d.kind == DEFER_BIAS_ACT) {
-    const floatx4 b = *reinterpret_cast<const floatx4*>(d.bias + col);
-    floatx4 pre;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      pre[e] = s[e] + b[e];
-      out[e] = act_forward(d.act, pre[e]);
-    }
-    if (mat && d.mat_pre) *reinterpret_cast<floatx4*>(d.mat_pre + off) = pre;
-  } else {
-    const floatx4 y = *reinterpret_cast<const floatx4*>(d.aux_act + off);
-    const floatx4 p = d.aux_pre ? *reinterpret_cast<const floatx4*>(d.aux_pre + off) : y;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) out[e] = s[e] * act_derivative(d.act, p[e], y[e]);
-  }
-  if (mat && d.mat_out) *reinterpret_cast<floatx4*>(d.mat_out + off) = out;
-  return out;
-}
-
-// Scalar form (used by the narrow output-layer kernel).
-__device__ __forceinline__ float deferred_load1(const DeferredOperand& d, int row, int col, bool mat) {
-  const size_t off = (size_t)row * d.ld + col;
-  float s = d.planes[off];
-  for (int z = 1; z < d.splits; ++z) s = s + d.planes[(size_t)z * d.stride + off];
-  float out;
-  if (d.kind == DEFER_BIAS_ACT) {
-    const float pre = s + d.bias[col];
-    out = act_forward(d.act, pre);
-    if (mat && d.mat_pre) d.mat_pre[off] = pre;
-  } else {
-    const float y = d.aux_act[off];
-    const float p = d.aux_pre ? d.aux_pre[off] : y;
-    out = s * act_derivative(d.act, p, y);
-  }
-  if (mat && d.mat_out) d.mat_out[off] = out;
-  return out;
-}
 // `bytes` is the caller's algorithmic HBM traffic of the product (for the
 // profiler); `rec`/`label` are optional.
 hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& a, hipStream_t st, Recorder* rec = nullptr,

@@ -209,13 +209,14 @@ __device__ __forceinline__ void block_epilogue(const EpiArgs& e, const floatx16&
     }
   } else if constexpr (EPI == EPI_DX_ACT) {
     // delta_{i-1} = (delta_i W_i^T) * f'(layer i-1)  (:893-929)
+    const float* pp = e.aux_pre ? e.aux_pre : e.aux_act;
     float y[16], p[16];
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int m = row(v);
       const size_t idx = (size_t)m * e.ldc + n;
       y[v] = m < M ? e.aux_act[idx] : 0.0f;
-      p[v] = (m < M && e.aux_pre) ? e.aux_pre[idx] : y[v];
+      p[v] = m < M ? pp[idx] : 0.0f;
     }
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
@@ -576,23 +577,85 @@ gemm_f32_mfma(GemmArgs args) {
   }
 }
 
+// Planes whose loads splitk_reduce issues together (more planes: a loop).
+constexpr int kReduceUnroll = 8;
+
 // Second kernel of a split-K launch: add the planes in slice order, then the
 // epilogue (and, for dW, the bias update from the summed column sums kept in
-// row M of each plane).
-template <int EPI>
+// row M of each plane).  One thread per W consecutive elements of a row;
+// every load a thread needs (all planes, bias or activation operands) is
+// issued before the first use, so the kernel waits one memory latency.
+template <int EPI, int W>
 __global__ void __launch_bounds__(256) splitk_reduce(GemmArgs a, int splits) {
   const int M = a.M, N = a.N;
   const size_t plane = (size_t)(M + 1) * N;
   const size_t total = (size_t)M * N;
   const size_t extra = EPI == EPI_DW_OPT && a.colsum_b ? (size_t)N : 0;
-  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total + extra;
-       idx += (size_t)gridDim.x * blockDim.x) {
-    float s = a.partial[idx];
-    for (int z = 1; z < splits; ++z) s = s + a.partial[(size_t)z * plane + idx];
+  const size_t items = (total + extra) / W;  // W divides N
+  const EpiArgs& e = a.epi;
+  for (size_t it = (size_t)blockIdx.x * blockDim.x + threadIdx.x; it < items;
+       it += (size_t)gridDim.x * blockDim.x) {
+    const size_t idx = it * W;
+    float s[W];
+    if (splits <= kReduceUnroll) {
+      float p[kReduceUnroll][W];
+#pragma unroll
+      for (int z = 0; z < kReduceUnroll; ++z)
+        if (z < splits) {
+          const float* src = a.partial + (size_t)z * plane + idx;
+          if constexpr (W == 4) {
+            const floatx4 v = *reinterpret_cast<const floatx4*>(src);
+#pragma unroll
+            for (int q = 0; q < W; ++q) p[z][q] = v[q];
+          } else {
+            p[z][0] = src[0];
+          }
+        }
+#pragma unroll
+      for (int q = 0; q < W; ++q) s[q] = p[0][q];
+#pragma unroll
+      for (int z = 1; z < kReduceUnroll; ++z)
+        if (z < splits) {
+#pragma unroll
+          for (int q = 0; q < W; ++q) s[q] = s[q] + p[z][q];
+        }
+    } else {
+#pragma unroll
+      for (int q = 0; q < W; ++q) s[q] = a.partial[idx + q];
+      for (int z = 1; z < splits; ++z)
+#pragma unroll
+        for (int q = 0; q < W; ++q) s[q] = s[q] + a.partial[(size_t)z * plane + idx + q];
+    }
     if (idx < total) {
-      apply_epilogue<EPI>(a.epi, (int)(idx / N), (int)(idx % N), s);
+      const int m = (int)(idx / N), n = (int)(idx % N);
+      const size_t o = (size_t)m * e.ldc + n;
+      if constexpr (EPI == EPI_BIAS_ACT) {
+        float b[W];
+#pragma unroll
+        for (int q = 0; q < W; ++q) b[q] = e.bias[n + q];
+#pragma unroll
+        for (int q = 0; q < W; ++q) {
+          const float v = s[q] + b[q];  // pre = act_i W_i + b_i (:716-724)
+          if (e.pre) e.pre[o + q] = v;
+          e.out[o + q] = act_forward(e.act, v);
+        }
+      } else if constexpr (EPI == EPI_DX_ACT) {
+        const float* pp = e.aux_pre ? e.aux_pre : e.aux_act;
+        float y[W], pr[W];
+#pragma unroll
+        for (int q = 0; q < W; ++q) {
+          y[q] = e.aux_act[o + q];
+          pr[q] = pp[o + q];
+        }
+#pragma unroll
+        for (int q = 0; q < W; ++q) e.out[o + q] = s[q] * act_derivative(e.act, pr[q], y[q]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < W; ++q) apply_epilogue<EPI>(e, m, n + q, s[q]);
+      }
     } else if constexpr (EPI == EPI_DW_OPT) {
-      apply_bias_update(a.epi, (int)(idx - total), N, s);
+#pragma unroll
+      for (int q = 0; q < W; ++q) apply_bias_update(e, (int)(idx + q - total), N, s[q]);
     }
   }
 }
@@ -642,9 +705,12 @@ static hipError_t launch_cfg(const GemmArgs& a, int layout, bool vec, int splits
 
 template <int EPI>
 static hipError_t launch_reduce(const GemmArgs& a, int splits, hipStream_t st) {
-  const size_t total = (size_t)a.M * a.N + a.N;
-  const int blocks = (int)std::min<size_t>((total + 255) / 256, 4096);
-  hipLaunchKernelGGL(splitk_reduce<EPI>, dim3(blocks), dim3(256), 0, st, a, splits);
+  const size_t total = (size_t)a.M * a.N + (EPI == EPI_DW_OPT && a.colsum_b ? a.N : 0);
+  const bool v4 = a.N % 4 == 0 && a.epi.ldc % 4 == 0;
+  const size_t items = v4 ? total / 4 : total;
+  const int blocks = (int)std::min<size_t>((items + 255) / 256, 1 << 20);
+  if (v4) hipLaunchKernelGGL((splitk_reduce<EPI, 4>), dim3(blocks), dim3(256), 0, st, a, splits);
+  else hipLaunchKernelGGL((splitk_reduce<EPI, 1>), dim3(blocks), dim3(256), 0, st, a, splits);
   return hipGetLastError();
 }
 

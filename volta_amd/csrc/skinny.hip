@@ -14,32 +14,56 @@
 
 namespace volta {
 
-// One output row z[0..N) of the output layer, computed by a whole wave:
-// lane l sums k = l, l+64, ..., then a fixed butterfly adds the lanes.
-template <int NMAX>
-__device__ __forceinline__ void wave_row(const float* __restrict__ a, const float* __restrict__ W, int K, int N,
-                                         float* z) {
+// Output rows z[g][0..N) of RG rows (rows[g], valid where rows[g] >= 0),
+// computed by a whole wave: lane l sums k = l, l+64, ... in ascending order,
+// then a fixed butterfly adds the lanes.  The k loop runs in chunks of C
+// values per lane whose loads (activations of all RG rows and the matching
+// rows of W) are all issued before the chunk's first multiply, so a chunk
+// costs one memory latency.
+template <int NMAX, int RG, int C>
+__device__ __forceinline__ void wave_rows(const OutLayerArgs& p, const int* rows, float (*z)[NMAX]) {
   const int lane = threadIdx.x & 63;
-  float acc[NMAX];
+  const int K = p.K, N = p.N;
+  float acc[RG][NMAX];
 #pragma unroll
-  for (int j = 0; j < NMAX; ++j) acc[j] = 0.0f;
-  for (int k = lane; k < K; k += 64) {
-    const float x = a[k];
-    const float* w = W + (size_t)k * N;
+  for (int g = 0; g < RG; ++g)
 #pragma unroll
-    for (int j = 0; j < NMAX; ++j)
-      if (j < N) acc[j] = acc[j] + x * w[j];
+    for (int j = 0; j < NMAX; ++j) acc[g][j] = 0.0f;
+  for (int k0 = lane; k0 < K; k0 += 64 * C) {
+    float x[RG][C], wv[C][NMAX];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int k = k0 + 64 * c;
+#pragma unroll
+      for (int j = 0; j < NMAX; ++j) wv[c][j] = k < K && j < N ? p.W[(size_t)k * N + j] : 0.0f;
+#pragma unroll
+      for (int g = 0; g < RG; ++g) x[g][c] = k < K && rows[g] >= 0 ? p.act[(size_t)rows[g] * K + k] : 0.0f;
+    }
+#pragma unroll
+    for (int g = 0; g < RG; ++g)
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        if (k0 + 64 * c < K) {
+#pragma unroll
+          for (int j = 0; j < NMAX; ++j)
+            if (j < N) acc[g][j] = acc[g][j] + x[g][c] * wv[c][j];
+        }
+      }
   }
 #pragma unroll
-  for (int j = 0; j < NMAX; ++j) z[j] = wave_sum(acc[j]);
+  for (int g = 0; g < RG; ++g)
+#pragma unroll
+    for (int j = 0; j < NMAX; ++j) z[g][j] = wave_sum(acc[g][j]);
 }
 
 // Loss head of one row (same definitions as the MFMA path's loss epilogue):
 // MSE (:792-798) d = z - y, loss += d^2, delta = 2d/nt; softmax-CE
 // (interpreter.rs:762-812, autograd.rs:467-534).  Returns the row's loss.
-// (Loops run to NMAX with a j < N guard so z stays in registers.)
+// `y` holds the row's targets (MSE), `lab` its label (CE), both loaded
+// before z was computed.  (Loops run to NMAX with a j < N guard so z stays
+// in registers.)
 template <int NMAX>
-__device__ __forceinline__ float head_row(const OutLayerArgs& p, const float* z, int m) {
+__device__ __forceinline__ float head_row(const OutLayerArgs& p, const float* z, const float* y, int lab, int m) {
   const int N = p.N;
   float* out = p.out + (size_t)m * N;
   float* d = p.delta + (size_t)m * N;
@@ -48,7 +72,6 @@ __device__ __forceinline__ float head_row(const OutLayerArgs& p, const float* z,
     if (j < N) out[j] = z[j];
   if (p.loss == VOLTA_LOSS_MSE) {
     const float nt = (float)(p.B * N);
-    const float* y = p.y + (size_t)m * N;
     float acc = 0.0f;
 #pragma unroll
     for (int j = 0; j < NMAX; ++j) {
@@ -61,7 +84,6 @@ __device__ __forceinline__ float head_row(const OutLayerArgs& p, const float* z,
     return acc;
   }
   const float bf = (float)p.B;
-  const int lab = p.labels[m];
   float mx = -INFINITY;
 #pragma unroll
   for (int j = 0; j < NMAX; ++j)
@@ -85,25 +107,59 @@ __device__ __forceinline__ float head_row(const OutLayerArgs& p, const float* z,
 }
 
 // Block b handles rows [b*rows_per_block, ...): wave w takes every
-// (waves)-th row.  The block's loss is the sum of its waves' row sums in
-// wave order; with one block it finishes the step's loss directly,
-// otherwise it lands in partials[b] for loss_finish_kernel.
+// (waves)-th row, RG rows at a time (in increasing row order).  The block's
+// loss is the sum of its waves' row sums in wave order; with one block it
+// finishes the step's loss directly, otherwise it lands in partials[b] for
+// loss_finish_kernel.  Lane 0 loads the bias, the targets/labels of its
+// rows and the next step counter before the dot products.
 template <int NMAX>
 __global__ void __launch_bounds__(1024) out_layer_kernel(OutLayerArgs p, int rows_per_block) {
+  // rows per group and k per lane per chunk, sized to stay within the 128
+  // registers a 1024-thread block allows
+  constexpr int RG = NMAX >= 16 ? 1 : 4;
+  constexpr int C = NMAX >= 16 ? 2 : 4;
   __shared__ float wave_loss[16];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int waves = blockDim.x >> 6;
   const int r0 = blockIdx.x * rows_per_block;
   const int r1 = min(p.B, r0 + rows_per_block);
+  const int N = p.N;
+  const bool single = gridDim.x == 1;
+  StepNext next{};
+  if (single && threadIdx.x == 0) next = step_prefetch(p.scalars, p.bc_table, p.bc_len);
+  float bias[NMAX];
+#pragma unroll
+  for (int j = 0; j < NMAX; ++j) bias[j] = lane == 0 && j < N ? p.bias[j] : 0.0f;
   float wl = 0.0f;
-  for (int m = r0 + wave; m < r1; m += waves) {
-    float z[NMAX];
-    wave_row<NMAX>(p.act + (size_t)m * p.K, p.W, p.K, p.N, z);
+  for (int m0 = r0 + wave; m0 < r1; m0 += waves * RG) {
+    int rows[RG];
+    float y[RG][NMAX];
+    int lab[RG];
+#pragma unroll
+    for (int g = 0; g < RG; ++g) {
+      const int m = m0 + g * waves;
+      rows[g] = m < r1 ? m : -1;
+      lab[g] = 0;
+      if (lane == 0 && rows[g] >= 0) {
+        if (p.loss == VOLTA_LOSS_MSE) {
+#pragma unroll
+          for (int j = 0; j < NMAX; ++j) y[g][j] = j < N ? p.y[(size_t)m * N + j] : 0.0f;
+        } else {
+          lab[g] = p.labels[m];
+        }
+      }
+    }
+    float z[RG][NMAX];
+    wave_rows<NMAX, RG, C>(p, rows, z);
     if (lane == 0) {
 #pragma unroll
-      for (int j = 0; j < NMAX; ++j)
-        if (j < p.N) z[j] = z[j] + p.bias[j];
-      wl = wl + head_row<NMAX>(p, z, m);
+      for (int g = 0; g < RG; ++g) {
+        if (rows[g] < 0) continue;
+#pragma unroll
+        for (int j = 0; j < NMAX; ++j)
+          if (j < N) z[g][j] = z[g][j] + bias[j];
+        wl = wl + head_row<NMAX>(p, z[g], y[g], lab[g], rows[g]);
+      }
     }
   }
   if (lane == 0) wave_loss[wave] = wl;
@@ -111,9 +167,9 @@ __global__ void __launch_bounds__(1024) out_layer_kernel(OutLayerArgs p, int row
   if (threadIdx.x == 0) {
     float s = wave_loss[0];
     for (int w = 1; w < waves; ++w) s = s + wave_loss[w];
-    if (gridDim.x == 1) {
+    if (single) {
       const float denom = p.loss == VOLTA_LOSS_MSE ? (float)(p.B * p.N) : (float)p.B;
-      step_epilogue(p.scalars, p.bc_table, p.bc_len, s / denom);
+      step_finish(p.scalars, next, p.bc_table != nullptr, s / denom);
     } else {
       p.partials[blockIdx.x] = s;
     }
@@ -140,67 +196,111 @@ outer_dx_kernel(const float* __restrict__ delta, const float* __restrict__ W, in
     const int b = (int)(idx / R), j = (int)(idx % R);
     const float* d = delta + (size_t)b * K;
     const float* w = W + (size_t)j * K;
+    const float y = aux_act[idx];
+    const float pre = (aux_pre ? aux_pre : aux_act)[idx];
     float s = 0.0f;
     for (int k = 0; k < K; ++k) s = s + d[k] * w[k];
-    const float y = aux_act[idx];
-    const float pre = aux_pre ? aux_pre[idx] : y;
     out[idx] = s * act_derivative(act, pre, y);
   }
 }
 
 // dW[j][k] = sum_b act[b][j] * delta[b][k] (b ascending, as sgemm_tn sums),
-// one thread per row j of W; delta is staged in LDS.  Block 0 also forms
-// db[k] = sum_b delta[b][k] (:931-933).  Then the optimizer update of W and
-// b (same element functions as the MFMA path).
+// one thread per row j of W (one wave per block, so R/64 CUs share the
+// loads); delta is staged in LDS.  Block 0 also forms db[k] = sum_b
+// delta[b][k] (:931-933).  Then the optimizer update of W and b (same
+// element functions as the MFMA path).  Latency: the optimizer state, the
+// scalars and the first chunk of act are loaded before the LDS staging
+// barrier, and act is read in chunks of kChunk rows whose loads are all
+// issued before the chunk's first multiply.
 template <int NMAX>
-__global__ void __launch_bounds__(256) narrow_dw_kernel(NarrowDwArgs p) {
+__global__ void __launch_bounds__(64) narrow_dw_kernel(NarrowDwArgs p) {
+  constexpr int kChunk = 32;
   extern __shared__ float sdelta[];  // [B x N]
   const int B = p.B, N = p.N, R = p.R;
-  for (int i = threadIdx.x; i < B * N; i += blockDim.x) sdelta[i] = p.delta[i];
-  __syncthreads();
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  const bool own = j < R;
+  const bool sgd = p.opt == VOLTA_OPT_SGD, adam = p.opt == VOLTA_OPT_ADAM;
   const float lr = p.scalars->lr;
   const float bc1 = p.scalars->bc1, bc2 = p.scalars->bc2;
-  const int j = blockIdx.x * blockDim.x + threadIdx.x;
-  if (j < R) {
-    float acc[NMAX];
+  float w[NMAX], s1[NMAX], s2[NMAX];
 #pragma unroll
-    for (int k = 0; k < NMAX; ++k) acc[k] = 0.0f;
-    for (int b = 0; b < B; ++b) {
-      const float a = p.act[(size_t)b * R + j];
+  for (int k = 0; k < NMAX; ++k) {
+    const size_t idx = (size_t)j * N + k;
+    const bool ok = own && k < N;
+    w[k] = ok ? p.w[idx] : 0.0f;
+    s1[k] = ok && !sgd ? p.m[idx] : 0.0f;
+    s2[k] = ok && adam ? p.v[idx] : 0.0f;
+  }
+  // bias state (block 0, threads k < N)
+  const bool bown = blockIdx.x == 0 && (int)threadIdx.x < N;
+  const float bw = bown ? p.b[threadIdx.x] : 0.0f;
+  const float bs1 = bown && !sgd ? p.bm[threadIdx.x] : 0.0f;
+  const float bs2 = bown && adam ? p.bv[threadIdx.x] : 0.0f;
+  float a[kChunk];
 #pragma unroll
-      for (int k = 0; k < NMAX; ++k)
-        if (k < N) acc[k] = acc[k] + a * sdelta[b * N + k];
+  for (int c = 0; c < kChunk; ++c) a[c] = own && c < B ? p.act[(size_t)c * R + j] : 0.0f;
+  for (int i = threadIdx.x; i < B * N; i += blockDim.x) sdelta[i] = p.delta[i];
+  __syncthreads();
+
+  float acc[NMAX];
+#pragma unroll
+  for (int k = 0; k < NMAX; ++k) acc[k] = 0.0f;
+  for (int b0 = 0; b0 < B; b0 += kChunk) {
+    if (b0 > 0) {
+#pragma unroll
+      for (int c = 0; c < kChunk; ++c) a[c] = own && b0 + c < B ? p.act[(size_t)(b0 + c) * R + j] : 0.0f;
     }
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c) {
+      if (b0 + c < B) {
+#pragma unroll
+        for (int k = 0; k < NMAX; ++k)
+          if (k < N) acc[k] = acc[k] + a[c] * sdelta[(b0 + c) * N + k];
+      }
+    }
+  }
+  if (own) {
     const int64_t count = (int64_t)R * N;
     const int64_t vec_end = count - count % 8;
 #pragma unroll
     for (int k = 0; k < NMAX; ++k) {
       if (k >= N) break;
       const int64_t idx = (int64_t)j * N + k;
-      if (p.grad) p.grad[idx] = acc[k];
-      if (p.opt == VOLTA_OPT_SGD) {
+      if (sgd) {
         const float nlr = -lr;
-        p.w[idx] = p.w[idx] + nlr * acc[k];
+        w[k] = w[k] + nlr * acc[k];
       } else if (p.opt == VOLTA_OPT_ADAGRAD) {
-        adagrad_elem(p.w + idx, p.m + idx, acc[k], lr, p.eps);
+        adagrad_elem(&w[k], &s1[k], acc[k], lr, p.eps);
       } else {
-        adam_elem(p.w + idx, p.m + idx, p.v + idx, acc[k], idx >= vec_end, lr, bc1, bc2, p.b1, p.b2, p.eps,
-                  p.wd);
+        adam_elem(&w[k], &s1[k], &s2[k], acc[k], idx >= vec_end, lr, bc1, bc2, p.b1, p.b2, p.eps, p.wd);
       }
     }
+#pragma unroll
+    for (int k = 0; k < NMAX; ++k) {
+      if (k >= N) break;
+      const size_t idx = (size_t)j * N + k;
+      if (p.grad) p.grad[idx] = acc[k];
+      p.w[idx] = w[k];
+      if (!sgd) p.m[idx] = s1[k];
+      if (adam) p.v[idx] = s2[k];
+    }
   }
-  if (blockIdx.x == 0 && threadIdx.x < N) {
+  if (bown) {
     const int k = threadIdx.x;
     float db = 0.0f;
     for (int b = 0; b < B; ++b) db = db + sdelta[b * N + k];
     if (p.bgrad) p.bgrad[k] = db;
-    if (p.opt == VOLTA_OPT_SGD) {
-      p.b[k] = p.b[k] - lr * db;
+    float x = bw, y1 = bs1, y2 = bs2;
+    if (sgd) {
+      x = x - lr * db;
     } else if (p.opt == VOLTA_OPT_ADAGRAD) {
-      adagrad_elem(p.b + k, p.bm + k, db, lr, p.eps);
+      adagrad_elem(&x, &y1, db, lr, p.eps);
     } else {
-      adam_elem(p.b + k, p.bm + k, p.bv + k, db, k >= N - N % 8, lr, bc1, bc2, p.b1, p.b2, p.eps, 0.0f);
+      adam_elem(&x, &y1, &y2, db, k >= N - N % 8, lr, bc1, bc2, p.b1, p.b2, p.eps, 0.0f);
     }
+    p.b[k] = x;
+    if (!sgd) p.bm[k] = y1;
+    if (adam) p.bv[k] = y2;
   }
 }
 
@@ -236,14 +336,15 @@ hipError_t launch_outer_dx(const float* delta, const float* W, int B, int R, int
 
 hipError_t launch_narrow_dw(const NarrowDwArgs& p, hipStream_t st) {
   if (p.N > 16 || p.N < 1 || (size_t)p.B * p.N * sizeof(float) > kNarrowDwLdsBytes) return hipErrorInvalidValue;
-  const int blocks = (p.R + 255) / 256;
+  if (p.opt != VOLTA_OPT_SGD && p.opt != VOLTA_OPT_ADAM && p.opt != VOLTA_OPT_ADAGRAD) return hipErrorInvalidValue;
+  const int blocks = (p.R + 63) / 64;
   const size_t lds = (size_t)p.B * p.N * sizeof(float);
   if (p.N <= 1)
-    hipLaunchKernelGGL(narrow_dw_kernel<1>, dim3(blocks), dim3(256), lds, st, p);
+    hipLaunchKernelGGL(narrow_dw_kernel<1>, dim3(blocks), dim3(64), lds, st, p);
   else if (p.N <= 4)
-    hipLaunchKernelGGL(narrow_dw_kernel<4>, dim3(blocks), dim3(256), lds, st, p);
+    hipLaunchKernelGGL(narrow_dw_kernel<4>, dim3(blocks), dim3(64), lds, st, p);
   else
-    hipLaunchKernelGGL(narrow_dw_kernel<16>, dim3(blocks), dim3(256), lds, st, p);
+    hipLaunchKernelGGL(narrow_dw_kernel<16>, dim3(blocks), dim3(64), lds, st, p);
   return hipGetLastError();
 }
 
