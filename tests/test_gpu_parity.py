@@ -388,6 +388,65 @@ def test_two_runs_bit_identical(name):
         np.testing.assert_array_equal(a, b)
 
 
+PAIR_CASES = {
+    # narrow dW_4 beside dX_3, GEMM pairs (dX_i, dW_{i+1}), (dW_1, dW_0)
+    "c2": (MlpSpec([512, 1024, 1024, 512, 256, 1], "relu", "adam"), 64, 1e-3),
+    # gelu keeps pre-activations for the dX epilogue
+    "c3": (MlpSpec([512, 2048, 2048, 512, 1], "gelu", "adamw"), 64, 1e-3),
+    # loss-head GEMM; split-K dW on both sides of the (dW_1, dW_0) pair
+    "ce40": (MlpSpec([256, 512, 512, 40], "leaky_relu", "sgd", "ce"), 256, 0.05),
+    # narrow dW with 8 outputs beside a dX GEMM
+    "silu": (MlpSpec([128, 512, 256, 8], "silu", "adagrad"), 32, 1e-2),
+    # two layers: (narrow dW_1, dW_0)
+    "two": (MlpSpec([64, 128, 4], "tanh", "adam"), 16, 1e-3),
+}
+
+
+def _run_with_env(env, spec, B, lr, steps):
+    from volta_amd.abi import BUF_ACT, BUF_DELTA
+
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        hip = load_hip()
+        ws, bs, batches = config_inputs(spec, B, seed=11)
+        t = Trainer(hip, spec, B)
+        t.set_all_params(ws, bs)
+        losses = []
+        for s in range(steps):
+            X, Y = batches[s % len(batches)]
+            t.step(X, Y, lr)
+            losses.append(t.loss())
+        bufs = [t.debug_buffer(BUF_ACT, i) for i in range(1, len(spec.sizes))]
+        bufs += [t.debug_buffer(BUF_DELTA, i) for i in range(len(spec.sizes) - 1)]
+        w, b = t.get_params()
+        assert t.status() == 0
+        t.close()
+        return np.array(losses, np.float32), w + b, bufs
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+@pytest.mark.parametrize("name", sorted(PAIR_CASES))
+def test_paired_backward_launches_bit_identical(name):
+    """dX_i and dW_{i+1} (and dW_1, dW_0) in one launch give the same bits as
+    separate launches: losses, parameters, activations and deltas after 4
+    steps."""
+    spec, B, lr = PAIR_CASES[name]
+    say(f"paired backward {name}")
+    l1, p1, b1 = _run_with_env({"VOLTA_NO_PAIR": "1"}, spec, B, lr, 4)
+    l2, p2, b2 = _run_with_env({"VOLTA_NO_PAIR": "0"}, spec, B, lr, 4)
+    np.testing.assert_array_equal(l1, l2)
+    for a, b in zip(p1, p2):
+        np.testing.assert_array_equal(a, b)
+    for a, b in zip(b1, b2):
+        np.testing.assert_array_equal(a, b)
+
+
 # ---------------------------------------------------------------------------
 # ABI behaviour
 # ---------------------------------------------------------------------------

@@ -7,6 +7,7 @@
 
 #include "device_common.h"
 #include "recorder.h"
+#include "skinny.h"
 
 namespace volta {
 
@@ -95,5 +96,27 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus);
 // profiler); `rec`/`label` are optional.
 hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& a, hipStream_t st, Recorder* rec = nullptr,
                        const char* label = "gemm", double bytes = 0.0);
+
+// One operation of a paired launch (two independent operations of the
+// backward pass in one kernel launch: no buffer one writes is touched by the
+// other).
+enum PairKind { PAIR_NONE = 0, PAIR_GEMM = 1, PAIR_NARROW_DW = 2 };
+
+struct PairOp {
+  int kind = PAIR_NONE;
+  GemmPlan plan;        // PAIR_GEMM
+  GemmArgs args{};      // PAIR_GEMM (args.partial: this operation's own workspace)
+  NarrowDwArgs nd{};    // PAIR_NARROW_DW
+};
+
+// Whether a and b can share one launch: dX (NT, activation-derivative
+// epilogue) or dW (TN, optimizer epilogue) products on 64x64 tiles with
+// 16-byte rows, or the narrow output-layer dW whose staged delta fits the
+// launch's LDS.
+bool pair_supported(const PairOp& a, const PairOp& b);
+
+// Both operations in one launch, then the split-K reductions either needs.
+hipError_t pair_launch(const PairOp& a, const PairOp& b, hipStream_t st, Recorder* rec, const char* label,
+                       double flops, double bytes);
 
 }  // namespace volta

@@ -27,6 +27,7 @@
 // counter is an integer, so results stay bit-identical; the last slice
 // resets the counter to zero for the next launch.
 #include "gemm.h"
+#include "narrow_dw.h"
 
 #include <cstdlib>
 
@@ -361,16 +362,19 @@ __device__ __forceinline__ void loss_tile(const EpiArgs& e, const float* z, int 
 // own epilogue).  INK selects how a split-K launch is reduced: false -- each
 // slice stores its partial plane and splitk_reduce finishes in a second
 // kernel; true -- the last slice to arrive (integer ticket) reduces.
+//
+// The tile body is a device function of the block coordinates (bx = output
+// tile, by = K slice of gy) and of its LDS (two A buffers, two B buffers,
+// BM + 2 floats), so a launch may also run it beside another operation.
 template <int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, bool VEC, int EPI, bool INK>
-__global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
-gemm_f32_mfma(GemmArgs args) {
+__device__ __forceinline__ void gemm_tile(const GemmArgs& args, int bx, int by, int gy, float* lds_a0,
+                                          float* lds_b0, float* lds_small) {
   using T = Tile<BM, BN, BK, WM, WN>;
   constexpr int THREADS = T::kThreads;
   using LA = LdsTile<BM, BK, A_KC>;
   using LB = LdsTile<BN, BK, B_KC>;
-  __shared__ __attribute__((aligned(16))) float lds_a[2][LA::kFloats];
-  __shared__ __attribute__((aligned(16))) float lds_b[2][LB::kFloats];
-  __shared__ float lds_small[BM + 2];
+  auto lds_a = [&](int i) { return lds_a0 + i * LA::kFloats; };
+  auto lds_b = [&](int i) { return lds_b0 + i * LB::kFloats; };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -381,14 +385,14 @@ gemm_f32_mfma(GemmArgs args) {
   const int l32 = lane & 31;
   const int M = args.M, N = args.N;
 
-  // Tile coordinates.  blockIdx.x walks N fastest so neighbouring
+  // Tile coordinates.  bx walks N fastest so neighbouring
   // workgroups share the same A rows.
   const int tiles_n = (N + BN - 1) / BN;
-  const int tm = blockIdx.x / tiles_n;
-  const int tn = blockIdx.x % tiles_n;
+  const int tm = bx / tiles_n;
+  const int tn = bx % tiles_n;
   const int m0 = tm * BM, n0 = tn * BN;
 
-  const int kbeg = blockIdx.y * args.k_per_split;
+  const int kbeg = by * args.k_per_split;
   const int kend = min(args.K, kbeg + args.k_per_split);
   // Column sums of B over k (dW's db = sum_b delta), taken from the MFMA B
   // fragments the waves already hold: the first row of waves (wm == 0) of
@@ -414,8 +418,8 @@ gemm_f32_mfma(GemmArgs args) {
   if (kbeg < kend) {
     la.load(args.A, args.lda, M, kend, m0, kbeg, tid);
     lb.load(args.B, args.ldb, N, kend, n0, kbeg, tid);
-    la.store(lds_a[0], tid);
-    lb.store(lds_b[0], tid);
+    la.store(lds_a(0), tid);
+    lb.store(lds_b(0), tid);
     __syncthreads();
 
     int buf = 0;
@@ -425,8 +429,8 @@ gemm_f32_mfma(GemmArgs args) {
         la.load(args.A, args.lda, M, kend, m0, k0 + BK, tid);
         lb.load(args.B, args.ldb, N, kend, n0, k0 + BK, tid);
       }
-      const float* a_s = lds_a[buf];
-      const float* b_s = lds_b[buf];
+      const float* a_s = lds_a(buf);
+      const float* b_s = lds_b(buf);
 #pragma unroll
       for (int g = 0; g < BK / 8; ++g) {
         floatx4 fa[T::TM], fb[T::TN];
@@ -452,8 +456,8 @@ gemm_f32_mfma(GemmArgs args) {
         }
       }
       if (more) {
-        la.store(lds_a[buf ^ 1], tid);
-        lb.store(lds_b[buf ^ 1], tid);
+        la.store(lds_a(buf ^ 1), tid);
+        lb.store(lds_b(buf ^ 1), tid);
       }
       __syncthreads();
       buf ^= 1;
@@ -470,11 +474,11 @@ gemm_f32_mfma(GemmArgs args) {
 
   // Accumulator register v of lane (h, l32) in block (i, j) holds row
   // 8*(v/4) + 4*h + (v%4), column l32 of that 32x32 block.
-  if (gridDim.y > 1) {
+  if (gy > 1) {
     // Split-K: publish this slice's partial tile (row M of each plane holds
     // the column sums).
     const size_t plane = (size_t)(M + 1) * N;
-    float* mine = args.partial + (size_t)blockIdx.y * plane;
+    float* mine = args.partial + (size_t)by * plane;
 #pragma unroll
     for (int i = 0; i < T::TM; ++i)
 #pragma unroll
@@ -499,8 +503,8 @@ gemm_f32_mfma(GemmArgs args) {
       __threadfence();
       __syncthreads();
       if (tid == 0) {
-        const unsigned ticket = atomicAdd(&args.counters[blockIdx.x], 1u);
-        lds_small[BM] = ticket == gridDim.y - 1 ? 1.0f : 0.0f;
+        const unsigned ticket = atomicAdd(&args.counters[bx], 1u);
+        lds_small[BM] = ticket == (unsigned)gy - 1u ? 1.0f : 0.0f;
       }
       __syncthreads();
       if (lds_small[BM] == 0.0f) return;
@@ -517,7 +521,7 @@ gemm_f32_mfma(GemmArgs args) {
             if (m < M && n < N) {
               const size_t off = (size_t)m * N + n;
               float s = planes[off];
-              for (unsigned z = 1; z < gridDim.y; ++z) s = s + planes[z * plane + off];
+              for (int z = 1; z < gy; ++z) s = s + planes[z * plane + off];
               acc[i][j][v] = s;
             }
           }
@@ -529,12 +533,12 @@ gemm_f32_mfma(GemmArgs args) {
           if (n < N) {
             const size_t off = (size_t)M * N + n;
             float s = planes[off];
-            for (unsigned z = 1; z < gridDim.y; ++z) s = s + planes[z * plane + off];
+            for (int z = 1; z < gy; ++z) s = s + planes[z * plane + off];
             cs[j] = s;
           }
         }
       }
-      if (tid == 0) args.counters[blockIdx.x] = 0u;
+      if (tid == 0) args.counters[bx] = 0u;
     }
   }
 
@@ -543,7 +547,7 @@ gemm_f32_mfma(GemmArgs args) {
     // Output layer (N <= BN): stage z = acc + bias for the whole tile in the
     // (now free) A buffers, then the per-row loss head.
     static_assert(BM * (BN + 1) <= 2 * LA::kFloats, "loss staging does not fit");
-    float* z = lds_a[0];
+    float* z = lds_a(0);
     constexpr int ZS = BN + 1;
     __syncthreads();
 #pragma unroll
@@ -575,6 +579,16 @@ gemm_f32_mfma(GemmArgs args) {
       }
     }
   }
+}
+
+template <int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, bool VEC, int EPI, bool INK>
+__global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
+gemm_f32_mfma(GemmArgs args) {
+  __shared__ __attribute__((aligned(16))) float lds_a[2 * LdsTile<BM, BK, A_KC>::kFloats];
+  __shared__ __attribute__((aligned(16))) float lds_b[2 * LdsTile<BN, BK, B_KC>::kFloats];
+  __shared__ float lds_small[BM + 2];
+  gemm_tile<BM, BN, BK, WM, WN, A_KC, B_KC, VEC, EPI, INK>(args, blockIdx.x, blockIdx.y, gridDim.y, lds_a, lds_b,
+                                                          lds_small);
 }
 
 // Planes whose loads splitk_reduce issues together (more planes: a loop).
@@ -743,6 +757,144 @@ hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& args_in, hipStream_t s
   if (err != hipSuccess) return err;
   const double t = (double)a.M * a.N;
   return mark(rec, std::string(label) + ".splitk_reduce", (double)p.splits * t, 4.0 * ((double)p.splits * t + 2.0 * t));
+}
+
+// ---------------------------------------------------------------------------
+// Paired launches: blocks [0, na) run operation A, the rest operation B.
+// ---------------------------------------------------------------------------
+template <int EPI, bool A_KC, bool B_KC>
+struct GemmOp64 {  // 64x64 tiles, BK 32, 16-byte rows, split-K by a separate reduction
+  using Args = GemmArgs;
+  static constexpr int kLa = LdsTile<64, 32, A_KC>::kFloats;
+  static constexpr int kLb = LdsTile<64, 32, B_KC>::kFloats;
+  static constexpr int kLds = 2 * kLa + 2 * kLb + 64 + 2;
+  static __device__ __forceinline__ void run(const GemmArgs& a, int blk, float* lds) {
+    const int tiles = ((a.M + 63) / 64) * ((a.N + 63) / 64);
+    const int gy = (a.K + a.k_per_split - 1) / a.k_per_split;
+    gemm_tile<64, 64, 32, 32, 32, A_KC, B_KC, true, EPI, false>(a, blk % tiles, blk / tiles, gy, lds,
+                                                                lds + 2 * kLa, lds + 2 * kLa + 2 * kLb);
+  }
+};
+
+template <int NMAX>
+struct NarrowDwOp {  // staged delta in the launch's LDS
+  using Args = NarrowDwArgs;
+  static constexpr int kLds = 0;
+  static __device__ __forceinline__ void run(const NarrowDwArgs& p, int blk, float* lds) {
+    narrow_dw_block<NMAX>(p, blk, lds);
+  }
+};
+
+template <class OA, class OB>
+struct PairLds {
+  static constexpr int kFloats = OA::kLds > OB::kLds ? OA::kLds : (OB::kLds > 0 ? OB::kLds : 1);
+};
+
+template <class OA, class OB>
+__global__ void __launch_bounds__(256) pair_kernel(typename OA::Args a, typename OB::Args b, int na) {
+  __shared__ __attribute__((aligned(16))) float lds[PairLds<OA, OB>::kFloats];
+  if ((int)blockIdx.x < na) OA::run(a, blockIdx.x, lds);
+  else OB::run(b, blockIdx.x - na, lds);
+}
+
+using DxOp = GemmOp64<EPI_DX_ACT, true, true>;
+using DwOp = GemmOp64<EPI_DW_OPT, false, false>;
+
+static int op_blocks(const PairOp& o) {
+  if (o.kind == PAIR_GEMM) return o.plan.tiles(o.args.M, o.args.N) * o.plan.splits;
+  return (o.nd.R + 255) / 256;
+}
+
+static int op_lds_floats(const PairOp& o) {
+  if (o.kind != PAIR_GEMM) return 0;
+  return o.plan.layout == GEMM_NT ? DxOp::kLds : DwOp::kLds;
+}
+
+bool pair_supported(const PairOp& a, const PairOp& b) {
+  auto gemm_ok = [](const PairOp& o) {
+    return o.plan.tile == TILE_64x64 && o.plan.vec && !o.plan.inkernel_reduce &&
+           ((o.plan.layout == GEMM_NT && o.args.epi.kind == EPI_DX_ACT) ||
+            (o.plan.layout == GEMM_TN && o.args.epi.kind == EPI_DW_OPT)) &&
+           (o.plan.splits == 1 || o.args.partial);
+  };
+  auto narrow_ok = [](const PairOp& o) {
+    return o.nd.N >= 1 && o.nd.N <= 16 &&
+           (o.nd.opt == VOLTA_OPT_SGD || o.nd.opt == VOLTA_OPT_ADAM || o.nd.opt == VOLTA_OPT_ADAGRAD);
+  };
+  const PairOp* ops[2] = {&a, &b};
+  int lds = 0;
+  for (const PairOp* o : ops) {
+    if (o->kind == PAIR_GEMM && !gemm_ok(*o)) return false;
+    if (o->kind == PAIR_NARROW_DW && !narrow_ok(*o)) return false;
+    if (o->kind == PAIR_NONE) return false;
+    lds = std::max(lds, op_lds_floats(*o));
+  }
+  // the pairs of the backward order: (dX, dW), (dX, narrow dW), (dW, dW), (narrow dW, dW)
+  const bool a_dx = a.kind == PAIR_GEMM && a.plan.layout == GEMM_NT;
+  const bool b_dw = b.kind == PAIR_GEMM && b.plan.layout == GEMM_TN;
+  if (!((a_dx && (b_dw || b.kind == PAIR_NARROW_DW)) || (!a_dx && b_dw))) return false;
+  for (const PairOp* o : ops)  // the narrow dW stages B x N floats of delta in the GEMM's LDS
+    if (o->kind == PAIR_NARROW_DW && (size_t)o->nd.B * o->nd.N > (size_t)lds) return false;
+  // no split product in the pair may share the other's workspace
+  if (a.kind == PAIR_GEMM && b.kind == PAIR_GEMM && a.plan.splits > 1 && b.plan.splits > 1 &&
+      a.args.partial == b.args.partial)
+    return false;
+  return true;
+}
+
+template <class OA, class OB>
+static hipError_t launch_pair_t(const typename OA::Args& a, int na, const typename OB::Args& b, int nb,
+                                hipStream_t st) {
+  hipLaunchKernelGGL((pair_kernel<OA, OB>), dim3(na + nb), dim3(256), 0, st, a, b, na);
+  return hipGetLastError();
+}
+
+template <class OA>
+static hipError_t launch_with_narrow(const typename OA::Args& aa, int na, const PairOp& b, hipStream_t st) {
+  const int nb = op_blocks(b);
+  if (b.nd.N <= 1) return launch_pair_t<OA, NarrowDwOp<1>>(aa, na, b.nd, nb, st);
+  if (b.nd.N <= 4) return launch_pair_t<OA, NarrowDwOp<4>>(aa, na, b.nd, nb, st);
+  return launch_pair_t<OA, NarrowDwOp<16>>(aa, na, b.nd, nb, st);
+}
+
+static hipError_t reduce_after(const PairOp& o, hipStream_t st) {
+  if (o.kind != PAIR_GEMM || o.plan.splits == 1) return hipSuccess;
+  GemmArgs a = o.args;
+  a.k_per_split = o.plan.k_per_split;
+  if (o.args.epi.kind == EPI_DX_ACT) return launch_reduce<EPI_DX_ACT>(a, o.plan.splits, st);
+  return launch_reduce<EPI_DW_OPT>(a, o.plan.splits, st);
+}
+
+hipError_t pair_launch(const PairOp& a, const PairOp& b, hipStream_t st, Recorder* rec, const char* label,
+                       double flops, double bytes) {
+  if (!pair_supported(a, b)) return hipErrorInvalidValue;
+  const int na = op_blocks(a), nb = op_blocks(b);
+  GemmArgs aa = a.args, bb = b.args;
+  aa.k_per_split = a.plan.k_per_split;
+  bb.k_per_split = b.plan.k_per_split;
+  hipError_t err;
+  if (a.kind == PAIR_GEMM && a.plan.layout == GEMM_NT) {
+    err = b.kind == PAIR_GEMM ? launch_pair_t<DxOp, DwOp>(aa, na, bb, nb, st) : launch_with_narrow<DxOp>(aa, na, b, st);
+  } else if (a.kind == PAIR_GEMM) {
+    err = launch_pair_t<DwOp, DwOp>(aa, na, bb, nb, st);
+  } else if (a.nd.N <= 1) {
+    err = launch_pair_t<NarrowDwOp<1>, DwOp>(a.nd, na, bb, nb, st);
+  } else if (a.nd.N <= 4) {
+    err = launch_pair_t<NarrowDwOp<4>, DwOp>(a.nd, na, bb, nb, st);
+  } else {
+    err = launch_pair_t<NarrowDwOp<16>, DwOp>(a.nd, na, bb, nb, st);
+  }
+  if (err != hipSuccess) return err;
+  if ((err = mark(rec, label, flops, bytes)) != hipSuccess) return err;
+  for (const PairOp* o : {&a, &b}) {
+    if (o->kind != PAIR_GEMM || o->plan.splits == 1) continue;
+    if ((err = reduce_after(*o, st)) != hipSuccess) return err;
+    const double t = (double)o->args.M * o->args.N;
+    if ((err = mark(rec, std::string(label) + ".splitk_reduce", (double)o->plan.splits * t,
+                    4.0 * ((double)o->plan.splits * t + 2.0 * t))) != hipSuccess)
+      return err;
+  }
+  return hipSuccess;
 }
 
 GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus) {

@@ -85,7 +85,10 @@ struct Handle {
   std::vector<float*> pre;    // pre[0..n-2]; null where the activation needs no pre
   std::vector<float*> delta;  // delta[0..n-1]
   void* target = nullptr;     // resident Y (float [B x Ln]) or labels (int32 [B])
-  float* gemm_ws = nullptr;   // split-K partial planes (shared: one GEMM runs at a time)
+  float* gemm_ws = nullptr;   // split-K partial planes: [0, ws_half) and [ws_half, 2*ws_half), one
+                              // region per operation of a paired launch
+  size_t ws_half = 0;         // floats
+  bool pair_backward = true;  // dX_i and dW_{i+1} in one launch (VOLTA_NO_PAIR=1: separate)
   unsigned* counters = nullptr;   // split-K arrival counters (+1: loss counter)
   int n_counters = 0;
   float* loss_partials = nullptr;  // one float per output-layer M-tile
@@ -227,47 +230,57 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
                                  h->scalars, h->bc_table, h->bc_len, st));
     VOLTA_CHECK(mark(rec, "loss", 0.0, 12.0 * B * Ln));
   }
-  // Backward (:819-993).  dX_i reads W_i before dW_i updates it in place.
-  for (int i = n - 1; i >= 0; --i) {
+  // Backward (:819-993).  dX_i reads W_i before dW_i updates it in place,
+  // so every delta comes from the pre-update weights.
+  //
+  // Launch order: dX_{n-1}; then (dX_i with dW_{i+1}) for i = n-2 .. 1; then
+  // (dW_1 with dW_0).  The two operations of a pair touch disjoint buffers
+  // (dX_i reads W_i, delta_i; dW_{i+1} rewrites W_{i+1}, b_{i+1} and their
+  // optimizer state), and each pair runs after the launch that produced its
+  // inputs (delta_i from dX_{i+1}, delta_{i+1} from dX_{i+2}).  A pair the
+  // paired kernel does not cover runs as two launches in the same order.
+  const int sopt = s.optimizer == VOLTA_OPT_SGD ? 2 : s.optimizer == VOLTA_OPT_ADAGRAD ? 4 : 6;
+  // dX_i as a GEMM (i > 0 and not the narrow output layer)
+  auto make_dx = [&](int i, float* ws) {
     const LayerPlan& lp = h->layers[i];
-    const bool out_layer = i == n - 1;
-    if (i > 0 && out_layer && h->narrow_dx) {
-      VOLTA_CHECK(launch_outer_dx(h->delta[i], h->params + lp.w_off, B, lp.r, lp.c, s.activation, h->act[i],
-                                  h->pre[i - 1], h->delta[i - 1], st));
-      std::snprintf(label, sizeof label, "dx%d", i);
-      VOLTA_CHECK(mark(rec, label, 2.0 * B * lp.r * lp.c,
-                       4.0 * ((double)B * lp.c + (double)lp.r * lp.c + 2.0 * B * lp.r)));
-    } else if (i > 0) {
-      GemmArgs a{};
-      base_args(a);
-      a.A = h->delta[i];
-      a.lda = lp.c;
-      a.B = h->params + lp.w_off;
-      a.ldb = lp.c;
-      a.M = B;
-      a.N = lp.r;
-      a.K = lp.c;
-      a.epi.kind = EPI_DX_ACT;
-      a.epi.act = s.activation;
-      a.epi.ldc = lp.r;
-      a.epi.out = h->delta[i - 1];
-      a.epi.aux_act = h->act[i];
-      a.epi.aux_pre = h->pre[i - 1];
-      std::snprintf(label, sizeof label, "dx%d", i);
-      // algorithmic bytes: 4(B*c + r*c + 2*B*r)
-      const double bytes = 4.0 * ((double)B * lp.c + (double)lp.r * lp.c + 2.0 * B * lp.r);
-      VOLTA_CHECK(gemm_launch(lp.dx, a, st, rec, label, bytes));
-    }
-    const double P_i = (double)lp.r * lp.c + lp.c;
-    const int sopt = s.optimizer == VOLTA_OPT_SGD ? 2 : s.optimizer == VOLTA_OPT_ADAGRAD ? 4 : 6;
-    if (out_layer && h->narrow_dw) {
-      NarrowDwArgs d{};
+    PairOp o;
+    o.kind = PAIR_GEMM;
+    o.plan = lp.dx;
+    GemmArgs& a = o.args;
+    base_args(a);
+    a.partial = ws;
+    a.A = h->delta[i];
+    a.lda = lp.c;
+    a.B = h->params + lp.w_off;
+    a.ldb = lp.c;
+    a.M = B;
+    a.N = lp.r;
+    a.K = lp.c;
+    a.epi.kind = EPI_DX_ACT;
+    a.epi.act = s.activation;
+    a.epi.ldc = lp.r;
+    a.epi.out = h->delta[i - 1];
+    a.epi.aux_act = h->act[i];
+    a.epi.aux_pre = h->pre[i - 1];
+    return o;
+  };
+  // dW_i = act_i^T delta_i with db_i = column sums of delta_i and the
+  // optimizer update of W_i and b_i (GEMM epilogue, or the narrow kernel for
+  // the output layer).
+  auto make_dw = [&](int i, float* ws) {
+    const LayerPlan& lp = h->layers[i];
+    PairOp o;
+    const int opt = s.optimizer == VOLTA_OPT_ADAMW ? VOLTA_OPT_ADAM : s.optimizer;
+    const float wd = s.optimizer == VOLTA_OPT_ADAMW ? s.weight_decay : 0.0f;
+    if (i == n - 1 && h->narrow_dw) {
+      o.kind = PAIR_NARROW_DW;
+      NarrowDwArgs& d = o.nd;
       d.act = h->act[i];
       d.delta = h->delta[i];
       d.B = B;
       d.R = lp.r;
       d.N = lp.c;
-      d.opt = s.optimizer == VOLTA_OPT_ADAMW ? VOLTA_OPT_ADAM : s.optimizer;
+      d.opt = opt;
       d.w = h->params + lp.w_off;
       d.b = h->params + lp.b_off;
       d.m = h->opt_a ? h->opt_a + lp.w_off : nullptr;
@@ -276,21 +289,18 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
       d.bv = h->opt_b ? h->opt_b + lp.b_off : nullptr;
       d.grad = h->keep_grads ? h->grads + lp.w_off : nullptr;
       d.bgrad = h->keep_grads ? h->grads + lp.b_off : nullptr;
-      d.wd = s.optimizer == VOLTA_OPT_ADAMW ? s.weight_decay : 0.0f;
+      d.wd = wd;
       d.b1 = s.beta1;
       d.b2 = s.beta2;
       d.eps = s.eps;
       d.scalars = h->scalars;
-      VOLTA_CHECK(launch_narrow_dw(d, st));
-      std::snprintf(label, sizeof label, "dw%d+db+opt", i);
-      VOLTA_CHECK(mark(rec, label, 2.0 * B * lp.r * lp.c,
-                       4.0 * ((double)B * lp.r + (double)B * lp.c) + 4.0 * sopt * P_i));
-      continue;
+      return o;
     }
-    // dW_i = act_i^T delta_i with db_i = column sums of delta_i and the
-    // optimizer update of W_i and b_i in the epilogue.
-    GemmArgs a{};
+    o.kind = PAIR_GEMM;
+    o.plan = lp.dw;
+    GemmArgs& a = o.args;
     base_args(a);
+    a.partial = ws;
     a.A = h->act[i];
     a.lda = lp.r;
     a.B = h->delta[i];
@@ -302,7 +312,7 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
     EpiArgs& e = a.epi;
     e.kind = EPI_DW_OPT;
     e.ldc = lp.c;
-    e.opt = s.optimizer == VOLTA_OPT_ADAMW ? VOLTA_OPT_ADAM : s.optimizer;
+    e.opt = opt;
     e.out = h->params + lp.w_off;
     e.b = h->params + lp.b_off;
     e.m = h->opt_a ? h->opt_a + lp.w_off : nullptr;
@@ -312,17 +322,69 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
     e.grad = h->keep_grads ? h->grads + lp.w_off : nullptr;
     e.bgrad = h->keep_grads ? h->grads + lp.b_off : nullptr;
     e.count = (int64_t)lp.r * lp.c;
-    e.wd = s.optimizer == VOLTA_OPT_ADAMW ? s.weight_decay : 0.0f;
+    e.wd = wd;
     e.b1 = s.beta1;
     e.b2 = s.beta2;
     e.eps = s.eps;
-    std::snprintf(label, sizeof label, "dw%d+db+opt", i);
-    // algorithmic bytes: dW 4(B*r + B*c + r*c), db 4(B*c + c), and the
-    // optimizer's 4*s per parameter minus the gradient round trip it saves:
-    // SGD reads+writes W (s=2 beyond dW), Adam w,m,v read+write (6),
-    // Adagrad w,G read+write (4).
-    const double bytes = 4.0 * ((double)B * lp.r + (double)B * lp.c) + 4.0 * sopt * P_i;
-    VOLTA_CHECK(gemm_launch(lp.dw, a, st, rec, label, bytes));
+    return o;
+  };
+  // algorithmic figures (flops, bytes) of dX_i and dW_i:
+  //   dX: 4(B*c + r*c + 2*B*r); dW + db + optimizer: 4(B*r + B*c) + 4*s*(r*c + c)
+  //   with s = 2 (SGD), 4 (Adagrad), 6 (Adam/AdamW) beyond the gradient.
+  auto dx_cost = [&](int i) {
+    const LayerPlan& lp = h->layers[i];
+    return std::make_pair(2.0 * B * lp.r * lp.c, 4.0 * ((double)B * lp.c + (double)lp.r * lp.c + 2.0 * B * lp.r));
+  };
+  auto dw_cost = [&](int i) {
+    const LayerPlan& lp = h->layers[i];
+    return std::make_pair(2.0 * B * lp.r * lp.c,
+                          4.0 * ((double)B * lp.r + (double)B * lp.c) + 4.0 * sopt * ((double)lp.r * lp.c + lp.c));
+  };
+  auto run_single = [&](const PairOp& o, const char* lbl, std::pair<double, double> cost) -> bool {
+    if (o.kind == PAIR_NARROW_DW) {
+      VOLTA_CHECK(launch_narrow_dw(o.nd, st));
+      VOLTA_CHECK(mark(rec, lbl, cost.first, cost.second));
+      return true;
+    }
+    VOLTA_CHECK(gemm_launch(o.plan, o.args, st, rec, lbl, cost.second));
+    return true;
+  };
+  auto run_pair = [&](const PairOp& x, const char* lx, std::pair<double, double> cx, const PairOp& y,
+                      const char* ly, std::pair<double, double> cy) -> bool {
+    if (h->pair_backward && pair_supported(x, y)) {
+      std::snprintf(label, sizeof label, "%s|%s", lx, ly);
+      VOLTA_CHECK(pair_launch(x, y, st, rec, label, cx.first + cy.first, cx.second + cy.second));
+      return true;
+    }
+    return run_single(x, lx, cx) && run_single(y, ly, cy);
+  };
+  char lx[32], ly[32];
+  float* ws0 = h->gemm_ws;
+  float* ws1 = h->gemm_ws ? h->gemm_ws + h->ws_half : nullptr;
+  // dX_{n-1}
+  if (n > 1) {
+    const int i = n - 1;
+    const LayerPlan& lp = h->layers[i];
+    std::snprintf(lx, sizeof lx, "dx%d", i);
+    if (h->narrow_dx) {
+      VOLTA_CHECK(launch_outer_dx(h->delta[i], h->params + lp.w_off, B, lp.r, lp.c, s.activation, h->act[i],
+                                  h->pre[i - 1], h->delta[i - 1], st));
+      VOLTA_CHECK(mark(rec, lx, dx_cost(i).first, dx_cost(i).second));
+    } else if (!run_single(make_dx(i, ws0), lx, dx_cost(i))) {
+      return false;
+    }
+  }
+  for (int i = n - 2; i >= 1; --i) {
+    std::snprintf(lx, sizeof lx, "dx%d", i);
+    std::snprintf(ly, sizeof ly, "dw%d+db+opt", i + 1);
+    if (!run_pair(make_dx(i, ws0), lx, dx_cost(i), make_dw(i + 1, ws1), ly, dw_cost(i + 1))) return false;
+  }
+  if (n > 1) {
+    std::snprintf(lx, sizeof lx, "dw%d+db+opt", 1);
+    std::snprintf(ly, sizeof ly, "dw%d+db+opt", 0);
+    if (!run_pair(make_dw(1, ws0), lx, dw_cost(1), make_dw(0, ws1), ly, dw_cost(0))) return false;
+  } else {
+    if (!run_single(make_dw(0, ws0), "dw0+db+opt", dw_cost(0))) return false;
   }
   return true;
 }
@@ -381,6 +443,11 @@ static bool build(Handle* h) {
     max_tiles = std::max(max_tiles, lp.dw.tiles(lp.r, lp.c));
   }
   h->n_counters = max_tiles + 1;  // last one: the loss head's tile counter
+  const char* np = std::getenv("VOLTA_NO_PAIR");
+  h->pair_backward = !(np && *np && *np != '0');
+  ws_floats = align_up(ws_floats, 64);
+  h->ws_half = ws_floats;
+  ws_floats *= 2;
 
   // Adam bias-correction table: entry t = (1 - b1^t, 1 - b2^t) in f32 powf,
   // up to the first t where both round to exactly 1.0f (later steps use the
