@@ -70,19 +70,45 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def profile(lib, t, reps=5):
+def launches(lib, t):
+    """The step's launch sequence: label and algorithmic flops/bytes of each
+    launch (volta_hip_profile_step, one kernel-by-kernel replay)."""
     fn = lib.lib.volta_hip_profile_step
     fn.restype = C.c_int32
     fn.argtypes = [C.c_void_p, C.c_int32, C.c_char_p, C.c_int32]
     buf = C.create_string_buffer(1 << 16)
-    n = fn(t.h, reps, buf, len(buf))
+    n = fn(t.h, 1, buf, len(buf))
     if n <= 0:
         raise RuntimeError("volta_hip_profile_step failed: " + lib.last_error())
     rows = []
     for line in buf.value.decode().strip().splitlines():
         label, ms, fl, by = line.split("\t")
-        rows.append({"kernel": label, "ms": float(ms), "flops": float(fl), "bytes": float(by)})
+        rows.append({"kernel": label, "flops": float(fl), "bytes": float(by)})
     return rows
+
+
+def profile(lib, t, step_ms):
+    """Per-launch duration inside whole steps (time_in_step for every launch);
+    about 0.5 s of steps per launch, 5..50 repetitions."""
+    rows = launches(lib, t)
+    reps = int(max(5, min(50, 500.0 / max(step_ms, 1e-3))))
+    for i, r in enumerate(rows):
+        ms, label = time_in_step(lib, t, i, reps)
+        if label != r["kernel"]:
+            raise RuntimeError(f"launch order mismatch: {label} vs {r['kernel']}")
+        r["ms"] = ms
+    return rows
+
+
+def time_in_step(lib, t, index, reps=50):
+    """Average duration of launch `index` inside whole steps (HIP events on
+    the library's stream around that launch only; the other launches run
+    back to back)."""
+    avg = C.c_float(0.0)
+    lab = C.create_string_buffer(128)
+    if lib.lib.volta_hip_time_kernel(t.h, index, reps, C.byref(avg), lab, len(lab)) != 0:
+        raise RuntimeError("volta_hip_time_kernel failed: " + lib.last_error())
+    return float(avg.value), lab.value.decode()
 
 
 def roofline_of(row):
@@ -131,10 +157,9 @@ def run_gpu(name, steps, warmup, want_profile=True):
     extra.argtypes = [C.c_void_p]
     out["arena_bytes"] = int(extra(t.h))
     if want_profile:
-        rows = profile(lib, t)
+        rows = profile(lib, t, ms)
         out["kernels"] = rows
-        dom = max(rows, key=lambda r: r["ms"])
-        out["roofline"] = roofline_of(dom)
+        out["roofline"] = roofline_of(max(rows, key=lambda r: r["ms"]))
         out["kernel_sum_ms"] = sum(r["ms"] for r in rows)
     t.close()
     return spec, B, lr, out

@@ -431,15 +431,31 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& args, int bx, int by, 
       }
       const float* a_s = lds_a(buf);
       const float* b_s = lds_b(buf);
+      // Fragments are double-buffered in registers: those of group g + 1
+      // are read from LDS before the MFMAs of group g are issued, so the LDS
+      // latency hides behind the matrix work.
+      floatx4 fa_n[T::TM], fb_n[T::TN];
+#pragma unroll
+      for (int i = 0; i < T::TM; ++i) fa_n[i] = load_frag<BM, BK, A_KC>(a_s, wm * WM + i * 32 + l32, h, 0);
+#pragma unroll
+      for (int j = 0; j < T::TN; ++j) fb_n[j] = load_frag<BN, BK, B_KC>(b_s, wn * WN + j * 32 + l32, h, 0);
 #pragma unroll
       for (int g = 0; g < BK / 8; ++g) {
         floatx4 fa[T::TM], fb[T::TN];
 #pragma unroll
-        for (int i = 0; i < T::TM; ++i)
-          fa[i] = load_frag<BM, BK, A_KC>(a_s, wm * WM + i * 32 + l32, h, g);
+        for (int i = 0; i < T::TM; ++i) fa[i] = fa_n[i];
 #pragma unroll
-        for (int j = 0; j < T::TN; ++j)
-          fb[j] = load_frag<BN, BK, B_KC>(b_s, wn * WN + j * 32 + l32, h, g);
+        for (int j = 0; j < T::TN; ++j) fb[j] = fb_n[j];
+        if (g + 1 < BK / 8) {
+#pragma unroll
+          for (int i = 0; i < T::TM; ++i)
+            fa_n[i] = load_frag<BM, BK, A_KC>(a_s, wm * WM + i * 32 + l32, h, g + 1);
+#pragma unroll
+          for (int j = 0; j < T::TN; ++j)
+            fb_n[j] = load_frag<BN, BK, B_KC>(b_s, wn * WN + j * 32 + l32, h, g + 1);
+        }
+        // keep the scheduler from sinking those reads below the MFMAs
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -447,6 +463,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& args, int bx, int by, 
 #pragma unroll
             for (int j = 0; j < T::TN; ++j)
               acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
         if (kColsum && colsum) {
           // rows beyond kend were loaded as zeros; adding them changes nothing
 #pragma unroll

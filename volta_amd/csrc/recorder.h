@@ -17,12 +17,30 @@ struct KernelMark {
   hipEvent_t ev;
 };
 
+// Two modes: every kernel (target < 0: an event after each launch), or one
+// kernel bracketed (target = k: events `before` and `after` launch k only,
+// so a captured graph of the step carries just two extra nodes).
 struct Recorder {
   hipStream_t st = nullptr;
   hipEvent_t start = nullptr;
   std::vector<KernelMark> marks;
+  int target = -1;
+  int count = 0;
+  hipEvent_t before = nullptr;  // recorded by the caller when target == 0
+  hipEvent_t after = nullptr;
+  std::string target_label;
 
   hipError_t mark(const std::string& label, double flops, double bytes) {
+    if (target >= 0) {
+      const int k = count++;
+      hipError_t err = hipSuccess;
+      if (k == target - 1) err = hipEventRecord(before, st);
+      if (k == target) {
+        target_label = label;
+        err = hipEventRecord(after, st);
+      }
+      return err;
+    }
     hipEvent_t e = nullptr;
     hipError_t err = hipEventCreate(&e);
     if (err != hipSuccess) return err;
@@ -34,6 +52,8 @@ struct Recorder {
     for (auto& m : marks)
       if (m.ev) (void)hipEventDestroy(m.ev);
     if (start) (void)hipEventDestroy(start);
+    if (before) (void)hipEventDestroy(before);
+    if (after) (void)hipEventDestroy(after);
   }
 };
 
