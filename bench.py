@@ -160,6 +160,10 @@ def run_gpu(name, steps, warmup, want_profile=True):
         rows = profile(lib, t, ms)
         out["kernels"] = rows
         out["roofline"] = roofline_of(max(rows, key=lambda r: r["ms"]))
+        tr = measured_traffic(name, out["roofline"]["kernel"])
+        if tr:
+            out["roofline"]["traffic"] = tr["bytes"]
+            out["roofline"]["traffic_detail"] = tr
         out["kernel_sum_ms"] = sum(r["ms"] for r in rows)
     t.close()
     return spec, B, lr, out
@@ -191,6 +195,45 @@ def run_cpu(name, budget_s=10.0, max_steps=200):
                       f"(C++ restatement of Volta compile-train, OpenMP GEMMs)"}
 
 
+def calibration_copy(mib, reps=10):
+    """A copy kernel over a known byte count, for scaling FETCH_SIZE and
+    WRITE_SIZE: each dispatch reads and writes exactly mib MiB."""
+    lib = load_hip()
+    n = mib << 20
+    f = lib.lib
+    src, dst = f.volta_hip_device_alloc(n), f.volta_hip_device_alloc(n)
+    if not src or not dst:
+        raise RuntimeError("device allocation failed")
+    try:
+        if f.volta_hip_calibration_copy(dst, src, n, reps) != 0:
+            raise RuntimeError("calibration copy failed")
+    finally:
+        f.volta_hip_device_free(src)
+        f.volta_hip_device_free(dst)
+    log(f"calibration copy: {reps} dispatches of {mib} MiB read + {mib} MiB written")
+    return 0
+
+
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.txt")
+
+
+def measured_traffic(workload, label):
+    """HBM bytes per launch of `label` from the committed rocprofv3 counter
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy calibration), or None."""
+    try:
+        lines = open(TRAFFIC_FILE).read().splitlines()
+    except OSError:
+        return None
+    for line in lines:
+        if line.startswith("#") or not line.strip():
+            continue
+        f = line.split("\t")
+        if len(f) >= 4 and f[0] == workload and f[1] == label:
+            return {"bytes": float(f[2]) + float(f[3]), "fetch": float(f[2]), "write": float(f[3]),
+                    "source": "profiles/hbm_traffic.txt"}
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -200,7 +243,11 @@ def main():
     ap.add_argument("--secondary", default="c5", help="second workload in the same line, or 'none'")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-profile", action="store_true", help="skip the per-kernel profile")
+    ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB 10 times (scales rocprofv3 HBM counters)")
     a = ap.parse_args()
+    if a.calibration_copy:
+        return calibration_copy(a.calibration_copy)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "

@@ -29,6 +29,7 @@ HIP_EXTRA = {
     "volta_hip_profile_step": (C.c_int32, [C.c_void_p, C.c_int32, C.c_char_p, C.c_int32]),
     "volta_hip_time_kernel": (C.c_int32, [C.c_void_p, C.c_int32, C.c_int32, C.POINTER(C.c_float), C.c_char_p,
                                           C.c_int32]),
+    "volta_hip_calibration_copy": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_int64, C.c_int32]),
     "volta_hip_device_alloc": (C.c_void_p, [C.c_int64]),
     "volta_hip_device_free": (C.c_int32, [C.c_void_p]),
     "volta_hip_copy": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_int64, C.c_int32]),

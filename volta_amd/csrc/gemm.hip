@@ -225,16 +225,18 @@ __device__ __forceinline__ void block_epilogue(const EpiArgs& e, const floatx16&
       if (m < M) e.out[(size_t)m * e.ldc + n] = acc[v] * act_derivative(e.act, p[v], y[v]);
     }
   } else if constexpr (EPI == EPI_DW_OPT) {
+    // 32-bit element offsets (W_i has fewer than 2^30 elements, checked at
+    // launch): one offset register per element serves W, m and v alike.
     const float lr = e.scalars->lr;
+    const uint32_t n32 = (uint32_t)n, ldc = (uint32_t)e.ldc;
+    auto off = [&](int v) { return (uint32_t)row(v) * ldc + n32; };
     float w[16], s1[16], s2[16];
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const int m = row(v);
-      const size_t idx = (size_t)m * e.ldc + n;
-      const bool ok = m < M;
-      w[v] = ok ? e.out[idx] : 0.0f;
-      s1[v] = ok && e.opt != VOLTA_OPT_SGD ? e.m[idx] : 0.0f;
-      s2[v] = ok && (e.opt == VOLTA_OPT_ADAM || e.opt == VOLTA_OPT_ADAMW) ? e.v[idx] : 0.0f;
+      const bool ok = row(v) < M;
+      w[v] = ok ? e.out[off(v)] : 0.0f;
+      s1[v] = ok && e.opt != VOLTA_OPT_SGD ? e.m[off(v)] : 0.0f;
+      s2[v] = ok && (e.opt == VOLTA_OPT_ADAM || e.opt == VOLTA_OPT_ADAMW) ? e.v[off(v)] : 0.0f;
     }
     if (e.opt == VOLTA_OPT_SGD) {
       // sgd_fused_tn: W = 1*W + (-lr) * (act_i^T delta_i)  (:321-324)
@@ -246,22 +248,18 @@ __device__ __forceinline__ void block_epilogue(const EpiArgs& e, const floatx16&
       for (int v = 0; v < 16; ++v) adagrad_elem(&w[v], &s1[v], acc[v], lr, e.eps);
     } else {
       const float bc1 = e.scalars->bc1, bc2 = e.scalars->bc2;
-      const int64_t vec_end = e.count - e.count % 8;
+      const uint32_t vec_end = (uint32_t)(e.count - e.count % 8);
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t idx = (int64_t)row(v) * e.ldc + n;
-        adam_elem(&w[v], &s1[v], &s2[v], acc[v], idx >= vec_end, lr, bc1, bc2, e.b1, e.b2, e.eps, e.wd);
-      }
+      for (int v = 0; v < 16; ++v)
+        adam_elem(&w[v], &s1[v], &s2[v], acc[v], off(v) >= vec_end, lr, bc1, bc2, e.b1, e.b2, e.eps, e.wd);
     }
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const int m = row(v);
-      if (m < M) {
-        const size_t idx = (size_t)m * e.ldc + n;
-        e.out[idx] = w[v];
-        if (e.opt != VOLTA_OPT_SGD) e.m[idx] = s1[v];
-        if (e.opt == VOLTA_OPT_ADAM || e.opt == VOLTA_OPT_ADAMW) e.v[idx] = s2[v];
-        if (e.grad) e.grad[idx] = acc[v];
+      if (row(v) < M) {
+        e.out[off(v)] = w[v];
+        if (e.opt != VOLTA_OPT_SGD) e.m[off(v)] = s1[v];
+        if (e.opt == VOLTA_OPT_ADAM || e.opt == VOLTA_OPT_ADAMW) e.v[off(v)] = s2[v];
+        if (e.grad) e.grad[off(v)] = acc[v];
       }
     }
   } else {
@@ -584,8 +582,13 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& args, int bx, int by, 
 #pragma unroll
     for (int i = 0; i < T::TM; ++i)
 #pragma unroll
-      for (int j = 0; j < T::TN; ++j)
+      for (int j = 0; j < T::TN; ++j) {
         block_epilogue<EPI>(e, acc[i][j], m0 + wm * WM + i * 32 + 4 * h, n0 + wn * WN + j * 32 + l32, M, N);
+        // one block's loads at a time: hoisting the next block's loads
+        // above these stores would raise the register count (occupancy)
+        // of the whole kernel
+        __builtin_amdgcn_sched_barrier(0);
+      }
     if constexpr (kColsum) {
       if (cs_owner && e.b) {
 #pragma unroll
@@ -752,6 +755,8 @@ hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& args_in, hipStream_t s
   if (p.splits > 1 && (!a.partial || !a.counters)) return hipErrorInvalidValue;
   if (a.epi.kind == EPI_LOSS && (p.tile == TILE_128x128 || a.N > 64)) return hipErrorInvalidValue;
   if (a.colsum_b && p.layout != GEMM_TN) return hipErrorInvalidValue;
+  // the optimizer epilogue indexes W_i with 32-bit element offsets
+  if (a.epi.kind == EPI_DW_OPT && (size_t)a.M * a.epi.ldc >= ((size_t)1 << 30)) return hipErrorInvalidValue;
   // The loss head always reduces in-kernel (it needs whole rows).
   const bool ink = p.inkernel_reduce || a.epi.kind == EPI_LOSS;
   hipError_t err;
@@ -832,7 +837,8 @@ bool pair_supported(const PairOp& a, const PairOp& b) {
     return o.plan.tile == TILE_64x64 && o.plan.vec && !o.plan.inkernel_reduce &&
            ((o.plan.layout == GEMM_NT && o.args.epi.kind == EPI_DX_ACT) ||
             (o.plan.layout == GEMM_TN && o.args.epi.kind == EPI_DW_OPT)) &&
-           (o.plan.splits == 1 || o.args.partial);
+           (o.plan.splits == 1 || o.args.partial) &&
+           (o.args.epi.kind != EPI_DW_OPT || (size_t)o.args.M * o.args.epi.ldc < ((size_t)1 << 30));
   };
   auto narrow_ok = [](const PairOp& o) {
     return o.nd.N >= 1 && o.nd.N <= 16 &&

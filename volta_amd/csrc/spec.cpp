@@ -53,6 +53,9 @@ bool validate_spec(const volta_mlp_spec& s, std::string* why) {
   for (int i = 0; i < s.n_sizes; ++i)
     if (s.sizes[i] <= 0 || s.sizes[i] > (1 << 20))
       return fail("layer size " + std::to_string(i) + " out of range (1..1048576)");
+  for (int i = 0; i + 1 < s.n_sizes; ++i)
+    if ((int64_t)s.sizes[i] * s.sizes[i + 1] >= ((int64_t)1 << 30))
+      return fail("layer " + std::to_string(i) + " has 2^30 or more weights");
   if (s.activation < VOLTA_ACT_RELU || s.activation > VOLTA_ACT_GELU)
     return fail("unknown activation");
   if (s.optimizer < VOLTA_OPT_SGD || s.optimizer > VOLTA_OPT_ADAGRAD)

@@ -3,11 +3,35 @@
 // isolation.  Not part of the reference ABI.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "gemm.h"
 #include "spec.h"
 #include "step_kernels.h"
 
+namespace {
+// Plain 16-byte copy: the reference kernel for scaling HBM counters
+// (FETCH_SIZE / WRITE_SIZE read for a known number of bytes).
+__global__ void __launch_bounds__(256) calibration_copy_kernel(const float4* __restrict__ src,
+                                                               float4* __restrict__ dst, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
+}  // namespace
+
 extern "C" {
+
+// Copy `bytes` (a multiple of 16) from src to dst with calibration_copy_kernel,
+// `reps` times, synchronously.  Used to scale HBM counter readings.
+int32_t volta_hip_calibration_copy(void* dst, const void* src, int64_t bytes, int32_t reps) {
+  if (!dst || !src || bytes <= 0 || bytes % 16 != 0 || reps <= 0) return -1;
+  const size_t n = (size_t)bytes / 16;
+  const int blocks = (int)std::min<size_t>((n + 255) / 256, 8192);
+  for (int r = 0; r < reps; ++r)
+    hipLaunchKernelGGL(calibration_copy_kernel, dim3(blocks), dim3(256), 0, 0, static_cast<const float4*>(src),
+                       static_cast<float4*>(dst), n);
+  return hipGetLastError() == hipSuccess && hipDeviceSynchronize() == hipSuccess ? 0 : -1;
+}
 
 // C[M x N] = op(A) op(B) for layout GEMM_NN / GEMM_NT / GEMM_TN (see gemm.h).
 // force_tile < 0 and force_splits <= 0 select the runtime's own plan.
