@@ -937,9 +937,10 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus) {
   const char* ik = std::getenv("VOLTA_SPLITK_INKERNEL");
   p.inkernel_reduce = ik && *ik && *ik != '0';
   const char* sw = std::getenv("VOLTA_SPLITK_WGS_PER_CU");
-  const int wgs_per_cu = sw && *sw ? std::max(1, std::atoi(sw)) : 1;
+  const int wgs_per_cu = sw && *sw ? std::max(1, std::atoi(sw)) : 2;
   int splits = 1;
-  // Split K while the grid is below ~wgs_per_cu workgroups per CU and each
+  // Split K while the grid is below ~wgs_per_cu workgroups per CU (two: a
+  // second wave per SIMD hides the first one's memory latency) and each
   // slice keeps at least min_k values of k.
   while (tiles * splits * 2 <= wgs_per_cu * num_cus && K / (splits * 2) >= min_k && splits < 32) splits *= 2;
   int kps = (K + splits - 1) / splits;
