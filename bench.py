@@ -89,26 +89,29 @@ def launches(lib, t):
 
 def profile(lib, t, step_ms):
     """Per-launch duration inside whole steps (time_in_step for every launch);
-    about 0.5 s of steps per launch, 5..50 repetitions."""
+    about 0.4 s of steps per launch, 3..50 repetitions."""
     rows = launches(lib, t)
-    reps = int(max(5, min(50, 500.0 / max(step_ms, 1e-3))))
+    reps = int(max(3, min(50, 200.0 / max(step_ms, 1e-3))))
     for i, r in enumerate(rows):
-        ms, label = time_in_step(lib, t, i, reps)
+        ms, bracket, marker, label = time_in_step(lib, t, i, reps)
         if label != r["kernel"]:
             raise RuntimeError(f"launch order mismatch: {label} vs {r['kernel']}")
         r["ms"] = ms
+        r["bracket_ms"] = round(bracket, 5)
+        r["marker_ms"] = round(marker, 5)
     return rows
 
 
 def time_in_step(lib, t, index, reps=50):
-    """Average duration of launch `index` inside whole steps (HIP events on
-    the library's stream around that launch only; the other launches run
-    back to back)."""
-    avg = C.c_float(0.0)
+    """Duration of launch `index` inside whole steps: HIP events on the
+    library's stream around that launch only (the other launches run back to
+    back), minus the same two events recorded back to back at that position
+    (the markers' own cost).  Returns (ms, bracket_ms, marker_ms, label)."""
+    avg = (C.c_float * 2)()
     lab = C.create_string_buffer(128)
-    if lib.lib.volta_hip_time_kernel(t.h, index, reps, C.byref(avg), lab, len(lab)) != 0:
+    if lib.lib.volta_hip_time_kernel(t.h, index, reps, avg, lab, len(lab)) != 0:
         raise RuntimeError("volta_hip_time_kernel failed: " + lib.last_error())
-    return float(avg.value), lab.value.decode()
+    return max(avg[0] - avg[1], 0.0), float(avg[0]), float(avg[1]), lab.value.decode()
 
 
 def roofline_of(row):
@@ -234,6 +237,114 @@ def measured_traffic(workload, label):
     return None
 
 
+def _bench_labels(bench_json):
+    """Launch labels per workload, in launch order, from a bench JSON line."""
+    for line in open(bench_json):
+        if line.startswith("{"):
+            b = json.loads(line)
+    labels = {b["config"]["workload"]: [k["kernel"] for k in b["kernels"]]}
+    if b.get("secondary"):
+        labels[b["secondary"]["workload"]] = [k["kernel"] for k in b["secondary"]["kernels"]]
+    return b, labels
+
+
+def _per_launch(rows, labels, value):
+    """Split a profiler's dispatch rows (one bench process: primary workload,
+    then secondary) into whole steps and map each step position to its launch
+    label.  Returns {workload: [(kernel, workgroups, [values...]) per launch]}
+    over every whole step of that workload."""
+    import re
+
+    seq = []
+    for r in sorted(rows, key=lambda r: int(r["Dispatch_Id"])):
+        if "__amd_rocclr" in r["Kernel_Name"]:
+            continue
+        nm = re.sub(r"\(.*", "", r["Kernel_Name"].replace("volta::", "").replace("void ", ""))
+        v = value(r)
+        if nm.startswith("loss_finish_kernel") and seq:  # second kernel of the output-layer launch
+            seq[-1][2] += v
+            continue
+        if "Grid_Size" in r:  # counter collection: total threads
+            wg = int(r["Grid_Size"]) // int(r["Workgroup_Size"])
+        else:  # kernel trace: per dimension
+            wg = int(r["Grid_Size_X"]) // int(r["Workgroup_Size_X"]) * int(r["Grid_Size_Y"])
+        seq.append([nm, wg, v])
+    order = list(labels)
+    regions = [seq]
+    if len(order) > 1:  # the secondary's first launch is a 128x128 tile kernel (B=4096)
+        i2 = next(i for i, x in enumerate(seq) if "128, 128" in x[0])
+        regions = [seq[:i2], seq[i2:]]
+    out = {}
+    for wl, reg in zip(order, regions):
+        n = len(labels[wl])
+        reg = reg[len(reg) - (len(reg) // n) * n:]
+        steps = [reg[k * n:(k + 1) * n] for k in range(len(reg) // n)]
+        out[wl] = [(steps[-1][p][0], steps[-1][p][1], [s[p][2] for s in steps]) for p in range(n)]
+    return out
+
+
+def traffic_table(pmc_dir, bench_json):
+    """Text table of HBM bytes per launch from four rocprofv3 --pmc passes
+    (FETCH_SIZE and WRITE_SIZE over `--calibration-copy 256` into
+    pmc_dir/cal_<COUNTER>/ and over `--no-cpu --no-profile` into
+    pmc_dir/bench_<COUNTER>/), each counter scaled by what it reads for the
+    copy's known 256 MiB; launches are named from a bench JSON line of the
+    same build (same launch order); averages over the last 10 steps."""
+    import csv
+
+    cal = {}
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        rows = [r for r in csv.DictReader(open(f"{pmc_dir}/cal_{c}/cal_counter_collection.csv"))
+                if "calibration_copy" in r["Kernel_Name"]]
+        cal[c] = 256 * 1024 / (sum(float(r["Counter_Value"]) for r in rows) / len(rows))
+    _, labels = _bench_labels(bench_json)
+    per = {}
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        rows = list(csv.DictReader(open(f"{pmc_dir}/bench_{c}/bench_counter_collection.csv")))
+        for wl, lst in _per_launch(rows, labels, lambda r, c=c: float(r["Counter_Value"]) * 1024 * cal[c]).items():
+            per[(wl, c)] = [(k, w, sum(v[-10:]) / len(v[-10:])) for k, w, v in lst]
+    out = [f"# calibration (plain copy, 256 MiB read and written per dispatch): "
+           f"FETCH_SIZE x{cal['FETCH_SIZE']:.3f}, WRITE_SIZE x{cal['WRITE_SIZE']:.3f}",
+           "# workload\tlaunch\tfetch_bytes\twrite_bytes\tkernel (workgroups)"]
+    for wl in labels:
+        for p, lab in enumerate(labels[wl]):
+            f, w = per[(wl, "FETCH_SIZE")][p], per[(wl, "WRITE_SIZE")][p]
+            out.append(f"{wl}\t{lab}\t{f[2]:.0f}\t{w[2]:.0f}\t{f[0]} ({f[1]})")
+    print("\n".join(out))
+    return 0
+
+
+def trace_summary(trace_csv, bench_json):
+    """Per-launch kernel durations from a rocprofv3 --kernel-trace of one
+    bench run, averaged over every whole step the run executed, beside the
+    bench's own in-step figure for the same launch."""
+    import csv
+
+    b, labels = _bench_labels(bench_json)
+    rows = [r for r in csv.DictReader(open(trace_csv)) if r["Kind"] == "KERNEL_DISPATCH"]
+    per = _per_launch(rows, labels, lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
+    res = {b["config"]["workload"]: b}
+    if b.get("secondary"):
+        res[b["secondary"]["workload"]] = b["secondary"]
+    out = []
+    for wl in labels:
+        r = res[wl]
+        bench_ms = {k["kernel"]: k["ms"] for k in r["kernels"]}
+        lst = per[wl]
+        tot = sum(sum(v) / len(v) for _, _, v in lst)
+        rf = r["roofline"]
+        out += [f"## workload {wl}: step {r['ms_per_step'] * 1000:.1f} us (bench wall clock, graph replay); "
+                f"sum of kernel durations per step {tot:.1f} us over {len(lst[0][2])} steps",
+                f"## roofline launch {rf['kernel']}: bench {rf['avg_ms'] * 1000:.2f} us (events around it inside "
+                f"whole steps), {rf['achieved']} {rf['unit']} = {rf['frac'] * 100:.1f}% of {rf['peak']}",
+                f"{'avg_us':>9} {'min_us':>9} {'bench_us':>9}  launch  [kernel (workgroups)]"]
+        for (k, w, v), lab in zip(lst, labels[wl]):
+            out.append(f"{sum(v) / len(v):9.2f} {min(v):9.2f} {bench_ms[lab] * 1000:9.2f}  {lab}  [{k} ({w})]")
+        out.append("")
+    print("\n".join(out))
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -245,7 +356,15 @@ def main():
     ap.add_argument("--no-profile", action="store_true", help="skip the per-kernel profile")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB 10 times (scales rocprofv3 HBM counters)")
+    ap.add_argument("--traffic-table", nargs=2, metavar=("PMC_DIR", "BENCH_JSON"),
+                    help="only print HBM bytes per launch from rocprofv3 counter passes (no GPU)")
+    ap.add_argument("--trace-summary", nargs=2, metavar=("TRACE_CSV", "BENCH_JSON"),
+                    help="only print per-launch durations from a rocprofv3 kernel trace of a bench run (no GPU)")
     a = ap.parse_args()
+    if a.traffic_table:
+        return traffic_table(*a.traffic_table)
+    if a.trace_summary:
+        return trace_summary(*a.trace_summary)
     if a.calibration_copy:
         return calibration_copy(a.calibration_copy)
     world = int(os.environ.get("WORLD_SIZE", "1"))

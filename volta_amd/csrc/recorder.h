@@ -25,6 +25,7 @@ struct Recorder {
   hipEvent_t start = nullptr;
   std::vector<KernelMark> marks;
   int target = -1;
+  bool empty = false;  // record `after` right behind `before` (the markers' own cost)
   int count = 0;
   hipEvent_t before = nullptr;  // recorded by the caller when target == 0
   hipEvent_t after = nullptr;
@@ -34,10 +35,13 @@ struct Recorder {
     if (target >= 0) {
       const int k = count++;
       hipError_t err = hipSuccess;
-      if (k == target - 1) err = hipEventRecord(before, st);
+      if (k == target - 1) {
+        err = hipEventRecord(before, st);
+        if (empty && err == hipSuccess) err = hipEventRecord(after, st);
+      }
       if (k == target) {
         target_label = label;
-        err = hipEventRecord(after, st);
+        if (!empty) err = hipEventRecord(after, st);
       }
       return err;
     }

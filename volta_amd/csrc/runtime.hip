@@ -804,24 +804,29 @@ int32_t volta_hip_profile_step(VoltaTrainHandle* vh, int32_t reps, char* out, in
   return (int32_t)labels.size();
 }
 
-// Average duration (ms) of launch `index` of the step: the step's launch
-// sequence is enqueued `reps` times on the handle's stream with an event
-// before and after that launch only (the other launches run back to back as
-// in the graph).  Writes the launch's label to `label` (label_len bytes).
-// Test and benchmark use.
+// Duration of launch `index` of the step: the step's launch sequence is
+// enqueued on the handle's stream with an event before and after that
+// launch only (the other launches run back to back as in the graph), `reps`
+// times; the same is done with the two events recorded back to back at that
+// position.  Writes the mean bracketed time to avg_ms[0], the mean
+// back-to-back (marker) time to avg_ms[1], and the launch's label to
+// `label`.  Test and benchmark use.
 int32_t volta_hip_time_kernel(VoltaTrainHandle* vh, int32_t index, int32_t reps, float* avg_ms, char* label,
                               int32_t label_len) {
   Handle* h = H(vh);
   if (!h || index < 0 || reps <= 0 || !avg_ms) return -1;
-  double total = 0.0;
+  double total[2] = {0.0, 0.0};
   std::string lab;
-  for (int r = 0; r < reps; ++r) {
+  for (int r = 0; r < 2 * reps; ++r) {
+    const bool empty = r % 2 == 1;
     volta::Recorder rec;
     rec.st = h->stream;
     rec.target = index;
+    rec.empty = empty;
     float ms = 0.0f;
     if (hipEventCreate(&rec.before) != hipSuccess || hipEventCreate(&rec.after) != hipSuccess ||
-        (index == 0 && hipEventRecord(rec.before, h->stream) != hipSuccess)) {
+        (index == 0 && hipEventRecord(rec.before, h->stream) != hipSuccess) ||
+        (index == 0 && empty && hipEventRecord(rec.after, h->stream) != hipSuccess)) {
       volta::set_last_error("volta_hip_time_kernel: event setup failed");
       return -1;
     }
@@ -830,16 +835,17 @@ int32_t volta_hip_time_kernel(VoltaTrainHandle* vh, int32_t index, int32_t reps,
       volta::set_last_error("volta_hip_time_kernel: index beyond the step's launches");
       return -1;
     }
-    const hipError_t e1 = hipEventSynchronize(rec.after);
-    const hipError_t e2 = e1 == hipSuccess ? hipEventElapsedTime(&ms, rec.before, rec.after) : e1;
+    const hipError_t e0 = hipStreamSynchronize(h->stream);
+    const hipError_t e2 = e0 == hipSuccess ? hipEventElapsedTime(&ms, rec.before, rec.after) : e0;
     if (e2 != hipSuccess) {
       volta::set_last_error(std::string("volta_hip_time_kernel: ") + hipGetErrorString(e2));
       return -1;
     }
-    total += ms;
-    lab = rec.target_label;
+    total[empty ? 1 : 0] += ms;
+    if (!empty) lab = rec.target_label;
   }
-  *avg_ms = (float)(total / reps);
+  avg_ms[0] = (float)(total[0] / reps);
+  avg_ms[1] = (float)(total[1] / reps);
   if (label && label_len > 0) std::snprintf(label, (size_t)label_len, "%s", lab.c_str());
   return 0;
 }
