@@ -9,15 +9,19 @@
 //   get/set_params, loss, free (:669-696)               -> host mirror + copies
 //
 // The step's launch order (a topological order of the step's dataflow):
-//   fwd_0 .. fwd_{n-1}          GEMM NN + bias + activation epilogue; the
-//                               output layer's epilogue is the MSE or
-//                               softmax-CE head (delta_{n-1}, loss, Adam t)
-//   for i = n-1 .. 0:
-//     dX_i  (i > 0)             GEMM NT, epilogue * f'(layer i-1) -> delta_{i-1}
-//     dW_i                      GEMM TN + column sums (db_i); epilogue applies
-//                               SGD/Adam/AdamW/Adagrad to W_i and b_i
-// dX_i reads W_i before dW_i rewrites it, and every delta is computed from
-// the pre-update weights, as in the reference's two-phase backward.
+//   fwd_0 .. fwd_{n-2}          GEMM NN + bias + activation (in the split-K
+//                               reduction when K is split)
+//   fwd_{n-1} + loss            narrow output kernel (L_n <= 16), GEMM with the
+//                               loss head in its epilogue (<= 64), or GEMM +
+//                               loss kernel: delta_{n-1}, loss, Adam t
+//   dX_{n-1}                    outer product (L_n <= 16) or GEMM NT
+//   dX_i | dW_{i+1}             one paired launch, i = n-2 .. 1
+//   dW_1 | dW_0                 one paired launch
+// dX_i: GEMM NT with epilogue * f'(layer i-1) -> delta_{i-1}.  dW_i: GEMM TN
+// whose epilogue applies SGD/Adam/AdamW/Adagrad to W_i, and to b_i from the
+// column sums of delta_i (db_i) the same kernel forms.  dX_i reads W_i before
+// dW_i rewrites it (a later launch), so every delta comes from the pre-update
+// weights, as in the reference's two-phase backward.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
