@@ -188,9 +188,10 @@ int64_t volta_train_state_size(VoltaTrainHandle* h);
  *   VOLTA_BUF_ACT    act_i   [B x L[i]],   i = 0..n
  *   VOLTA_BUF_DELTA  delta_i [B x L[i+1]], i = 0..n-1 (after the activation
  *                    derivative has been applied)
- *   VOLTA_BUF_GRAD_W dW_i    [L[i] x L[i+1]] (not kept for SGD, whose update
- *                    is fused into the dW product)
- *   VOLTA_BUF_GRAD_B db_i    [L[i+1]]
+ *   VOLTA_BUF_GRAD_W dW_i    [L[i] x L[i+1]] (GPU library: only when the
+ *                    handle was created with VOLTA_KEEP_GRADS=1, since the
+ *                    optimizer update is fused into the dW product)
+ *   VOLTA_BUF_GRAD_B db_i    [L[i+1]] (same condition)
  * Returns the number of floats written, or -1. */
 #define VOLTA_BUF_ACT 0
 #define VOLTA_BUF_DELTA 1
@@ -199,6 +200,31 @@ int64_t volta_train_state_size(VoltaTrainHandle* h);
 int64_t volta_train_debug_buffer(VoltaTrainHandle* h, int32_t kind, int32_t layer, float* out);
 int32_t volta_train_get_state(VoltaTrainHandle* h, float* state, int64_t* step);
 int32_t volta_train_set_state(VoltaTrainHandle* h, const float* state, int64_t step);
+
+/* Change the optimizer hyperparameters of a live handle (the generated
+ * library bakes them in, mlp_train_rust_codegen.rs:803-811, :957-993):
+ * Adam/AdamW beta1 and beta2, eps (Adam/AdamW/Adagrad), AdamW weight decay
+ * (weights only).  The step counter and optimizer state are kept; the next
+ * step uses the new values.  Waits for enqueued steps.  Returns 0, or -1
+ * (volta_train_last_error) for values outside the ranges the spec accepts. */
+int32_t volta_train_set_hparams(VoltaTrainHandle* h, float beta1, float beta2, float eps, float weight_decay);
+
+/* Forward pass only, with the handle's current parameters: out [rows x Ln]
+ * = the output layer's pre-activation (no loss, no softmax) for host input
+ * X [rows x L0]; any rows > 0 (run B rows at a time).  Synchronous.  Uses
+ * the handle's activation buffers, which the next step recomputes.
+ * Returns 0 on success. */
+int32_t volta_train_infer(VoltaTrainHandle* h, const float* X, int64_t rows, float* out);
+
+/* The inference library's entry point (codegen/inner.rs:198; contract
+ * docs/ARCHITECTURE.md:125-141): output = forward(input) for in_n = rows*L0
+ * input floats, writing rows*Ln floats (out_n must be at least that).  The
+ * reference embeds trained weights in the inference library; here the model
+ * is the handle given to volta_infer_bind (null unbinds; the binding is
+ * process-wide).  On an error `output` is left untouched and
+ * volta_train_last_error() says why. */
+int32_t volta_infer_bind(VoltaTrainHandle* h);
+void volta_infer(const float* input, int64_t in_n, float* output, int64_t out_n);
 
 #ifdef __cplusplus
 }

@@ -25,12 +25,14 @@
 //
 // Parity status of each function is recorded next to it ("pinned by ...").
 // ===========================================================================
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -751,6 +753,85 @@ int32_t volta_oracle_threads(void) {
 #else
   return 1;
 #endif
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Hyperparameters of a live handle, and the forward-only entry points
+// (same contract as include/volta_train.h).
+// ---------------------------------------------------------------------------
+template <typename T>
+static void infer_rows(Net<T>& net, const float* X, int64_t rows, float* out) {
+  const int B = net.B, L0 = net.L[0], Ln = net.L[net.n];
+  std::vector<T> xb((size_t)B * L0, T(0));
+  for (int64_t r0 = 0; r0 < rows; r0 += B) {
+    const int64_t m = std::min<int64_t>(B, rows - r0);
+    std::fill(xb.begin(), xb.end(), T(0));
+    for (int64_t k = 0; k < m * L0; ++k) xb[(size_t)k] = (T)X[r0 * L0 + k];
+    net.forward(xb.data());
+    for (int64_t k = 0; k < m * Ln; ++k) out[r0 * Ln + k] = (float)net.act[net.n][(size_t)k];
+  }
+}
+
+static std::mutex g_infer_mu;
+static VoltaTrainHandle* g_infer_model = nullptr;
+
+extern "C" {
+
+int32_t volta_train_set_hparams(VoltaTrainHandle* vh, float beta1, float beta2, float eps, float weight_decay) {
+  Handle* h = H(vh);
+  if (!h) return -1;
+  volta_mlp_spec s = h->precision == 64 ? h->d.spec : h->f.spec;
+  s.beta1 = beta1;
+  s.beta2 = beta2;
+  s.eps = eps;
+  s.weight_decay = weight_decay;
+  std::string why;
+  if (!volta::validate_spec(s, &why)) {
+    h->status |= VOLTA_STATUS_BAD_ARGUMENT;
+    set_last_error("volta_train_set_hparams: " + why);
+    return -1;
+  }
+  if (h->precision == 64) h->d.spec = s;
+  else h->f.spec = s;
+  return 0;
+}
+
+int32_t volta_train_infer(VoltaTrainHandle* vh, const float* X, int64_t rows, float* out) {
+  Handle* h = H(vh);
+  if (!h) return -1;
+  if (!X || !out || rows <= 0) {
+    h->status |= VOLTA_STATUS_BAD_ARGUMENT;
+    set_last_error("volta_train_infer: bad arguments");
+    return -1;
+  }
+  if (h->precision == 64) infer_rows(h->d, X, rows, out);
+  else infer_rows(h->f, X, rows, out);
+  return 0;
+}
+
+int32_t volta_infer_bind(VoltaTrainHandle* vh) {
+  std::lock_guard<std::mutex> lock(g_infer_mu);
+  g_infer_model = vh;
+  return 0;
+}
+
+void volta_infer(const float* input, int64_t in_n, float* output, int64_t out_n) {
+  std::lock_guard<std::mutex> lock(g_infer_mu);
+  Handle* h = H(g_infer_model);
+  if (!h) {
+    set_last_error("volta_infer: no model bound (volta_infer_bind)");
+    return;
+  }
+  const std::vector<int>& L = h->precision == 64 ? h->d.L : h->f.L;
+  const int L0 = L.front(), Ln = L.back();
+  if (!input || !output || in_n <= 0 || in_n % L0 != 0 || out_n < in_n / L0 * Ln) {
+    h->status |= VOLTA_STATUS_BAD_ARGUMENT;
+    set_last_error("volta_infer: in_n must be rows*L0 and out_n >= rows*Ln");
+    return;
+  }
+  (void)volta_train_infer(g_infer_model, input, in_n / L0, output);
 }
 
 }  // extern "C"

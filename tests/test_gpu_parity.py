@@ -5,6 +5,7 @@ rel 1e-4 / abs 1e-5 of the oracle on the same seeded inputs, and two GPU runs
 bit-identical.  Kernel-level GEMM checks compare with the oracle GEMM and are
 exact on integer-valued operands.
 """
+import ctypes
 import json
 import os
 import sys
@@ -15,6 +16,8 @@ import pytest
 from tests.oracle_lib import load_oracle
 from volta_amd import DeviceArray, data, load_hip
 from volta_amd.abi import MlpSpec, Trainer
+
+C_F = ctypes.POINTER(ctypes.c_float)
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 GOLDEN = json.load(open(os.path.join(HERE, "golden", "train_step_golden.json")))["cases"]
@@ -564,3 +567,105 @@ def test_lr_change_between_steps():
     assert_params_close(wh, bh, wo, bo, "lr schedule")
     th.close()
     to.close()
+
+
+# ---------------------------------------------------------------------------
+# Forward-only entry points and live hyperparameters
+# ---------------------------------------------------------------------------
+INFER_CASES = [
+    (MlpSpec([512, 1024, 1024, 512, 256, 1], "relu", "adam"), 64, (64, 17, 200)),
+    (MlpSpec([64, 96, 40], "gelu", "sgd", "ce"), 32, (32, 5, 70)),
+    (MlpSpec([1024, 4096, 10], "silu", "adagrad", "ce"), 256, (256, 3, 300)),
+]
+
+
+@pytest.mark.parametrize("k", range(len(INFER_CASES)))
+def test_infer_matches_oracle(k):
+    """volta_train_infer (forward GEMMs only, any row count, chunked by B)
+    against the oracle's forward on the same weights: rel 1e-4 / abs 1e-5."""
+    spec, B, row_counts = INFER_CASES[k]
+    say(f"infer {spec.sizes} {spec.activation} B={B}")
+    hip, orc = load_hip(), load_oracle()
+    ws, bs = data.he_uniform(21, spec.sizes)
+    th, to = Trainer(hip, spec, B), Trainer(orc, spec, B)
+    th.set_all_params(ws, bs)
+    to.set_all_params(ws, bs)
+    rng = np.random.default_rng(k)
+    for rows in row_counts:
+        X = rng.standard_normal((rows, spec.sizes[0])).astype(np.float32)
+        got, want = th.infer(X), to.infer(X)
+        ok, mx, bad = close_enough(got, want)
+        assert ok, f"rows={rows}: {bad} outputs differ, max {mx:.3e}"
+    th.close()
+    to.close()
+
+
+def test_volta_infer_symbol_and_training_unaffected():
+    """volta_infer on the bound handle equals Trainer.infer bit for bit, and
+    an inference between steps does not change what training computes."""
+    say("volta_infer symbol")
+    hip = load_hip()
+    spec = MlpSpec([32, 64, 48, 4], "tanh", "adam")
+    ws, bs, batches = config_inputs(spec, 16)
+    X, Y = batches[0]
+    a, b = Trainer(hip, spec, 16), Trainer(hip, spec, 16)
+    a.set_all_params(ws, bs)
+    b.set_all_params(ws, bs)
+    Xi = np.random.default_rng(2).standard_normal((23, 32)).astype(np.float32)
+    for s in range(3):
+        a.step(X, Y, 1e-3)
+        b.step(X, Y, 1e-3)
+        want = a.infer(Xi)
+        out = np.zeros(23 * 4, np.float32)
+        assert hip.lib.volta_infer_bind(a.h) == 0
+        hip.lib.volta_infer(Xi.ctypes.data_as(C_F), Xi.size, out.ctypes.data_as(C_F), out.size)
+        np.testing.assert_array_equal(out.reshape(23, 4), want)
+    hip.lib.volta_infer_bind(None)
+    assert a.loss() == b.loss()
+    wa, ba = a.get_params()
+    wb, bb = b.get_params()
+    for p, q in zip(wa + ba, wb + bb):
+        np.testing.assert_array_equal(p, q)
+    assert a.status() == 0
+    a.close()
+    b.close()
+
+
+def test_set_hparams_matches_handle_built_with_them():
+    """set_hparams on a live handle (bias-correction table rebuilt, graph
+    re-captured) gives the bits of a handle created with those values, and
+    the oracle agrees within tolerance."""
+    say("set_hparams")
+    hip, orc = load_hip(), load_oracle()
+    base = MlpSpec([64, 128, 64, 8], "relu", "adamw")
+    new = MlpSpec([64, 128, 64, 8], "relu", "adamw", beta1=0.8, beta2=0.99, eps=1e-6, weight_decay=0.05)
+    ws, bs, batches = config_inputs(base, 32)
+    X, Y = batches[0]
+    a, b, o = Trainer(hip, base, 32), Trainer(hip, new, 32), Trainer(orc, new, 32)
+    for t in (a, b, o):
+        t.set_all_params(ws, bs)
+    a.step(X, Y, 1e-3)
+    b.step(X, Y, 1e-3)
+    o.step(X, Y, 1e-3)
+    # change the base handle after one step with the default values: the
+    # other two ran step 1 with the new values, so compare from a common state
+    st, step = b.get_state()
+    w, bb_ = b.get_params()
+    a.set_all_params(w, bb_)
+    a.set_state(st, step)
+    a.set_hparams(0.8, 0.99, 1e-6, 0.05)
+    for _ in range(4):
+        a.step(X, Y, 1e-3)
+        b.step(X, Y, 1e-3)
+        o.step(X, Y, 1e-3)
+    assert a.loss() == b.loss()
+    wa, ba = a.get_params()
+    wb, bb2 = b.get_params()
+    for p, q in zip(wa + ba, wb + bb2):
+        np.testing.assert_array_equal(p, q)
+    wo, bo = o.get_params()
+    assert_params_close(wb, bb2, wo, bo, "set_hparams vs oracle")
+    with pytest.raises(ValueError):
+        a.set_hparams(0.9, 1.0, 1e-8, 0.0)
+    for t in (a, b, o):
+        t.close()

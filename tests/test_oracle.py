@@ -383,3 +383,95 @@ def test_oracle_state_roundtrip(oracle):
     wb, bb = b.get_params()
     for x, y in zip(wa + ba, wb + bb):
         np.testing.assert_array_equal(x, y)
+
+
+# ---------------------------------------------------------------------------
+# Forward-only entry points and live hyperparameters
+# ---------------------------------------------------------------------------
+def _np_act(name, x):
+    """Activation closed forms (mlp_train_rust_codegen.rs:563-596), float64."""
+    if name == "relu":
+        return np.maximum(x, 0.0)
+    if name == "leaky_relu":
+        return np.where(x > 0, x, 0.01 * x)
+    if name == "sigmoid":
+        return 1.0 / (1.0 + np.exp(-x))
+    if name == "tanh":
+        return np.tanh(x)
+    if name == "silu":
+        return x / (1.0 + np.exp(-x))
+    if name == "gelu":
+        return 0.5 * x * (1.0 + np.tanh(0.7978845608 * (x + 0.044715 * x ** 3)))
+    raise ValueError(name)
+
+
+def _np_forward(ws, bs, X, act):
+    a = X.astype(np.float64)
+    for i, (w, b) in enumerate(zip(ws, bs)):
+        z = a @ w.astype(np.float64) + b.astype(np.float64)
+        a = z if i == len(ws) - 1 else _np_act(act, z)
+    return a
+
+
+@pytest.mark.parametrize("act", ["relu", "sigmoid", "tanh", "leaky_relu", "silu", "gelu"])
+def test_oracle_infer_matches_closed_form_forward(oracle, act):
+    """volta_train_infer = the model's forward (output pre-activation) for any
+    row count: the fp64 twin equals a numpy float64 forward, the fp32 oracle
+    is within fp32 rounding; rows below, at and above the batch (chunks)."""
+    spec = MlpSpec([12, 20, 16, 5], act, "adam")
+    rng = np.random.default_rng(3)
+    ws = [rng.uniform(-0.5, 0.5, (r, c)).astype(np.float32) for r, c in spec.shapes()]
+    bs = [rng.uniform(-0.1, 0.1, c).astype(np.float32) for _, c in spec.shapes()]
+    for rows in (3, 8, 21):
+        X = rng.standard_normal((rows, 12)).astype(np.float32)
+        want = _np_forward(ws, bs, X, act)
+        for f64, tol in ((True, 1e-6), (False, 1e-5)):
+            t = oracle_trainer(oracle, spec, 8, f64=f64)
+            t.set_all_params(ws, bs)
+            got = t.infer(X)
+            np.testing.assert_allclose(got, want, rtol=tol, atol=tol)
+            t.close()
+
+
+def test_oracle_volta_infer_symbol(oracle):
+    """The reference's inference signature volta_infer(in, in_n, out, out_n)
+    runs the bound model; bad sizes and an unbound model leave out alone."""
+    spec = MlpSpec([6, 10, 3], "tanh", "sgd")
+    t = Trainer(oracle, spec, 4)
+    X = np.random.default_rng(1).standard_normal((7, 6)).astype(np.float32)
+    want = t.infer(X)
+    f = oracle.lib
+    out = np.full(7 * 3, -7.0, np.float32)
+    f.volta_infer_bind(None)
+    f.volta_infer(fptr(X), X.size, fptr(out), out.size)
+    assert (out == -7.0).all() and b"bound" in f.volta_train_last_error()
+    f.volta_infer_bind(t.h)
+    f.volta_infer(fptr(X), X.size - 1, fptr(out), out.size)
+    assert (out == -7.0).all()
+    f.volta_infer(fptr(X), X.size, fptr(out), out.size)
+    np.testing.assert_array_equal(out.reshape(7, 3), want)
+    f.volta_infer_bind(None)
+    t.close()
+
+
+def test_oracle_set_hparams_equals_spec_from_start(oracle):
+    """set_hparams before the first step gives the same bits as a handle
+    created with those hyperparameters; out-of-range values are rejected."""
+    base = MlpSpec([8, 16, 4], "relu", "adamw")
+    new = MlpSpec([8, 16, 4], "relu", "adamw", beta1=0.8, beta2=0.99, eps=1e-6, weight_decay=0.05)
+    rng = np.random.default_rng(5)
+    X = rng.standard_normal((4, 8)).astype(np.float32)
+    Y = rng.standard_normal((4, 4)).astype(np.float32)
+    a, b = Trainer(oracle, base, 4), Trainer(oracle, new, 4)
+    a.set_hparams(0.8, 0.99, 1e-6, 0.05)
+    for _ in range(3):
+        a.step(X, Y, 1e-2)
+        b.step(X, Y, 1e-2)
+    wa, ba = a.get_params()
+    wb, bb = b.get_params()
+    for p, q in zip(wa + ba, wb + bb):
+        np.testing.assert_array_equal(p, q)
+    with pytest.raises(ValueError):
+        a.set_hparams(1.5, 0.99, 1e-6, 0.0)
+    a.close()
+    b.close()

@@ -120,6 +120,10 @@ _SIGNATURES = {
     "volta_train_get_state": (C.c_int32, [_P, _F, C.POINTER(C.c_int64)]),
     "volta_train_set_state": (C.c_int32, [_P, _F, C.c_int64]),
     "volta_train_debug_buffer": (C.c_int64, [_P, C.c_int32, C.c_int32, _F]),
+    "volta_train_set_hparams": (C.c_int32, [_P, C.c_float, C.c_float, C.c_float, C.c_float]),
+    "volta_train_infer": (C.c_int32, [_P, _F, C.c_int64, _F]),
+    "volta_infer_bind": (C.c_int32, [_P]),
+    "volta_infer": (None, [_F, C.c_int64, _F, C.c_int64]),
 }
 
 BUF_ACT, BUF_DELTA, BUF_GRAD_W, BUF_GRAD_B = 0, 1, 2, 3
@@ -264,6 +268,21 @@ class Trainer:
         buf = state if state.size else np.zeros(1, np.float32)
         if self.lib.lib.volta_train_set_state(self.h, fptr(buf), step) != 0:
             raise RuntimeError(self.lib.last_error())
+
+    def set_hparams(self, beta1: float, beta2: float, eps: float, weight_decay: float) -> None:
+        if self.lib.lib.volta_train_set_hparams(self.h, beta1, beta2, eps, weight_decay) != 0:
+            raise ValueError(self.lib.last_error())
+
+    def infer(self, X: np.ndarray) -> np.ndarray:
+        """Forward pass only: the output layer's pre-activation for X [rows x L0]."""
+        X = np.ascontiguousarray(X, dtype=np.float32)
+        rows = X.shape[0]
+        if X.ndim != 2 or X.shape[1] != self.spec.sizes[0] or rows == 0:
+            raise ValueError(f"X must be [rows x {self.spec.sizes[0]}]")
+        out = np.zeros((rows, self.spec.sizes[-1]), np.float32)
+        if self.lib.lib.volta_train_infer(self.h, fptr(X), rows, fptr(out)) != 0:
+            raise RuntimeError(self.lib.last_error())
+        return out
 
     def debug_buffer(self, kind: int, layer: int) -> np.ndarray:
         """An intermediate buffer of the last step (see volta_train_debug_buffer)."""

@@ -29,6 +29,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -101,8 +102,11 @@ struct Handle {
   bool narrow_dw = false;     // dW of the output layer by narrow_dw_kernel
   bool keep_grads = false;    // also store dW/db in `grads` (VOLTA_KEEP_GRADS=1)
   DevScalars* scalars = nullptr;
-  float2* bc_table = nullptr;
+  float2* bc_table = nullptr;  // own allocation (its length depends on beta1/beta2)
   int bc_len = 0;
+  float* infer_x = nullptr;    // inference input rows (allocated on first use)
+  float* infer_ws = nullptr;   // split-K workspace of inference plans (grown on demand)
+  size_t infer_ws_floats = 0;
   SegTable segs{};
   std::vector<LayerPlan> layers;
 
@@ -140,6 +144,9 @@ Handle::~Handle() {
   if (h_stage_x) (void)hipHostFree(h_stage_x);
   if (h_stage_y) (void)hipHostFree(h_stage_y);
   if (h_lr) (void)hipHostFree(h_lr);
+  if (bc_table) (void)hipFree(bc_table);
+  if (infer_x) (void)hipFree(infer_x);
+  if (infer_ws) (void)hipFree(infer_ws);
   if (arena) (void)hipFree(arena);
   if (stream) (void)hipStreamDestroy(stream);
 }
@@ -393,6 +400,59 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
   return true;
 }
 
+// Adam bias-correction table: entry t = (1 - b1^t, 1 - b2^t) in f32 powf,
+// up to the first t where both round to exactly 1.0f (later steps use the
+// last entry, which is then exact).  (Re)allocated whenever beta1/beta2 are
+// set; the caller has synchronized the stream.
+static bool make_bc_table(Handle* h) {
+  const volta_mlp_spec& s = h->spec;
+  if (h->bc_table) {
+    VOLTA_CHECK(hipFree(h->bc_table));
+    h->bc_table = nullptr;
+    h->bc_len = 0;
+  }
+  if (s.optimizer != VOLTA_OPT_ADAM && s.optimizer != VOLTA_OPT_ADAMW) return true;
+  std::vector<float2> bc;
+  bc.push_back(make_float2(1.0f, 1.0f));  // t = 0 is never used
+  const int kMaxTable = 1 << 24;
+  for (int t = 1; t < kMaxTable; ++t) {
+    const float b1 = 1.0f - powf(s.beta1, (float)t);
+    const float b2 = 1.0f - powf(s.beta2, (float)t);
+    bc.push_back(make_float2(b1, b2));
+    if (b1 == 1.0f && b2 == 1.0f) break;
+  }
+  VOLTA_CHECK(hipMalloc((void**)&h->bc_table, bc.size() * sizeof(float2)));
+  VOLTA_CHECK(hipMemcpy(h->bc_table, bc.data(), bc.size() * sizeof(float2), hipMemcpyHostToDevice));
+  h->bc_len = (int)bc.size();
+  return true;
+}
+
+// Capture the step into a fresh graph (hyperparameters are kernel
+// arguments, so a change of them is a new capture).
+static bool capture(Handle* h) {
+  if (h->exec) {
+    VOLTA_CHECK(hipGraphExecDestroy(h->exec));
+    h->exec = nullptr;
+  }
+  if (h->graph) {
+    VOLTA_CHECK(hipGraphDestroy(h->graph));
+    h->graph = nullptr;
+  }
+  if (!h->use_graph) return true;
+  VOLTA_CHECK(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal));
+  const bool ok = enqueue_step(h, h->stream);
+  hipGraph_t g = nullptr;
+  const hipError_t e = hipStreamEndCapture(h->stream, &g);
+  if (!ok) {
+    if (g) (void)hipGraphDestroy(g);
+    return false;
+  }
+  VOLTA_CHECK(e);
+  h->graph = g;
+  VOLTA_CHECK(hipGraphInstantiate(&h->exec, h->graph, nullptr, nullptr, 0));
+  return true;
+}
+
 static bool build(Handle* h) {
   const volta_mlp_spec& s = h->spec;
   const int n = h->n, B = h->B;
@@ -453,22 +513,7 @@ static bool build(Handle* h) {
   h->ws_half = ws_floats;
   ws_floats *= 2;
 
-  // Adam bias-correction table: entry t = (1 - b1^t, 1 - b2^t) in f32 powf,
-  // up to the first t where both round to exactly 1.0f (later steps use the
-  // last entry, which is then exact).
   const bool adam = s.optimizer == VOLTA_OPT_ADAM || s.optimizer == VOLTA_OPT_ADAMW;
-  std::vector<float2> bc;
-  if (adam) {
-    bc.push_back(make_float2(1.0f, 1.0f));  // t = 0 is never used
-    const int kMaxTable = 1 << 24;
-    for (int t = 1; t < kMaxTable; ++t) {
-      const float b1 = 1.0f - powf(s.beta1, (float)t);
-      const float b2 = 1.0f - powf(s.beta2, (float)t);
-      bc.push_back(make_float2(b1, b2));
-      if (b1 == 1.0f && b2 == 1.0f) break;
-    }
-    h->bc_len = (int)bc.size();
-  }
 
   // One arena, 256-byte aligned sub-buffers.
   struct Req {
@@ -493,7 +538,6 @@ static bool build(Handle* h) {
   if (ws_floats) req((void**)&h->gemm_ws, ws_floats * 4);
   req((void**)&h->counters, (size_t)h->n_counters * sizeof(unsigned));
   req((void**)&h->loss_partials, (size_t)std::max((B + 63) / 64, out_layer_blocks(B)) * 4);
-  if (adam) req((void**)&h->bc_table, bc.size() * sizeof(float2));
   size_t total = 0;
   for (auto& r : reqs) total += r.bytes;
   h->arena_bytes = total;
@@ -504,9 +548,7 @@ static bool build(Handle* h) {
     *r.dst = h->arena + pos;
     pos += r.bytes;
   }
-  if (adam)
-    VOLTA_CHECK(hipMemcpyAsync(h->bc_table, bc.data(), bc.size() * sizeof(float2), hipMemcpyHostToDevice,
-                               h->stream));
+  if (!make_bc_table(h)) return false;
 
   // Host side: pinned parameter mirror, input staging, lr slots.
   VOLTA_CHECK(hipHostMalloc((void**)&h->h_params, (size_t)h->flat * 4, hipHostMallocDefault));
@@ -528,18 +570,52 @@ static bool build(Handle* h) {
 
   const char* ng = std::getenv("VOLTA_NO_GRAPH");
   h->use_graph = !(ng && *ng && *ng != '0');
-  if (h->use_graph) {
-    VOLTA_CHECK(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal));
-    const bool ok = enqueue_step(h, h->stream);
-    hipGraph_t g = nullptr;
-    const hipError_t e = hipStreamEndCapture(h->stream, &g);
-    if (!ok) {
-      if (g) (void)hipGraphDestroy(g);
-      return false;
-    }
-    VOLTA_CHECK(e);
-    h->graph = g;
-    VOLTA_CHECK(hipGraphInstantiate(&h->exec, h->graph, nullptr, nullptr, 0));
+  return capture(h);
+}
+
+// Forward pass only for `rows` <= B rows already in h->infer_x: hidden
+// layers as in the step (bias + activation epilogue, or the split-K
+// reduction), the output layer with the identity; result in act[n].
+static bool enqueue_forward(Handle* h, int rows, hipStream_t st) {
+  const volta_mlp_spec& s = h->spec;
+  const int n = h->n;
+  // plans for `rows` (a smaller M may split K where the step's plan did not)
+  std::vector<GemmPlan> plans(n);
+  size_t ws = 0;
+  for (int i = 0; i < n; ++i) {
+    const LayerPlan& lp = h->layers[i];
+    plans[i] = gemm_plan(GEMM_NN, rows, lp.c, lp.r, lp.fwd.vec, h->num_cus);
+    plans[i].inkernel_reduce = false;
+    ws = std::max(ws, plans[i].workspace_floats(rows, lp.c));
+  }
+  if (ws > h->infer_ws_floats) {
+    VOLTA_CHECK(hipStreamSynchronize(st));
+    if (h->infer_ws) VOLTA_CHECK(hipFree(h->infer_ws));
+    h->infer_ws = nullptr;
+    h->infer_ws_floats = 0;
+    VOLTA_CHECK(hipMalloc((void**)&h->infer_ws, ws * sizeof(float)));
+    h->infer_ws_floats = ws;
+  }
+  for (int i = 0; i < n; ++i) {
+    const LayerPlan& lp = h->layers[i];
+    const bool last = i == n - 1;
+    GemmArgs a{};
+    a.partial = h->infer_ws;
+    a.counters = h->counters;
+    a.epi.scalars = h->scalars;
+    a.A = i == 0 ? h->infer_x : h->act[i];
+    a.lda = lp.r;
+    a.B = h->params + lp.w_off;
+    a.ldb = lp.c;
+    a.M = rows;
+    a.N = lp.c;
+    a.K = lp.r;
+    a.epi.kind = EPI_BIAS_ACT;
+    a.epi.act = last ? kIdentity : s.activation;
+    a.epi.ldc = lp.c;
+    a.epi.out = h->act[i + 1];
+    a.epi.bias = h->params + lp.b_off;
+    VOLTA_CHECK(gemm_launch(plans[i], a, st));
   }
   return true;
 }
@@ -956,6 +1032,83 @@ int32_t volta_train_get_state(VoltaTrainHandle* vh, float* state, int64_t* step)
   }
   if (step) *step = t;
   return 0;
+}
+
+int32_t volta_train_set_hparams(VoltaTrainHandle* vh, float beta1, float beta2, float eps, float weight_decay) {
+  Handle* h = H(vh);
+  if (!h) return -1;
+  volta_mlp_spec s = h->spec;
+  s.beta1 = beta1;
+  s.beta2 = beta2;
+  s.eps = eps;
+  s.weight_decay = weight_decay;
+  std::string why;
+  if (!volta::validate_spec(s, &why)) {
+    volta::fail(h, VOLTA_STATUS_BAD_ARGUMENT, "volta_train_set_hparams: " + why);
+    return -1;
+  }
+  if (!volta::sync(h)) {
+    h->status |= VOLTA_STATUS_DEVICE_ERROR;
+    return -1;
+  }
+  h->spec = s;
+  for (int i = 0; i < h->n; ++i) h->segs.wd[2 * i] = s.optimizer == VOLTA_OPT_ADAMW ? s.weight_decay : 0.0f;
+  if (!volta::make_bc_table(h) || !volta::capture(h)) {
+    h->status |= VOLTA_STATUS_DEVICE_ERROR;
+    return -1;
+  }
+  return 0;
+}
+
+int32_t volta_train_infer(VoltaTrainHandle* vh, const float* X, int64_t rows, float* out) {
+  Handle* h = H(vh);
+  if (!h) return -1;
+  if (!X || !out || rows <= 0) {
+    volta::fail(h, VOLTA_STATUS_BAD_ARGUMENT, "volta_train_infer: bad arguments");
+    return -1;
+  }
+  const int B = h->B, L0 = h->L[0], Ln = h->L[h->n];
+  if (!h->infer_x && hipMalloc((void**)&h->infer_x, (size_t)B * L0 * sizeof(float)) != hipSuccess) {
+    volta::fail(h, VOLTA_STATUS_DEVICE_ERROR, "volta_train_infer: device allocation failed");
+    return -1;
+  }
+  for (int64_t r0 = 0; r0 < rows; r0 += B) {
+    const int m = (int)std::min<int64_t>(B, rows - r0);
+    if (hipMemcpyAsync(h->infer_x, X + r0 * L0, (size_t)m * L0 * sizeof(float), hipMemcpyHostToDevice,
+                       h->stream) != hipSuccess ||
+        !volta::enqueue_forward(h, m, h->stream) ||
+        hipMemcpyAsync(out + r0 * Ln, h->act[h->n], (size_t)m * Ln * sizeof(float), hipMemcpyDeviceToHost,
+                       h->stream) != hipSuccess ||
+        hipStreamSynchronize(h->stream) != hipSuccess) {
+      volta::fail(h, VOLTA_STATUS_DEVICE_ERROR, "volta_train_infer: device error");
+      return -1;
+    }
+  }
+  return 0;
+}
+
+static std::mutex g_infer_mu;
+static VoltaTrainHandle* g_infer_model = nullptr;
+
+int32_t volta_infer_bind(VoltaTrainHandle* vh) {
+  std::lock_guard<std::mutex> lock(g_infer_mu);
+  g_infer_model = vh;
+  return 0;
+}
+
+void volta_infer(const float* input, int64_t in_n, float* output, int64_t out_n) {
+  std::lock_guard<std::mutex> lock(g_infer_mu);
+  Handle* h = H(g_infer_model);
+  if (!h) {
+    set_last_error("volta_infer: no model bound (volta_infer_bind)");
+    return;
+  }
+  const int L0 = h->L[0], Ln = h->L[h->n];
+  if (!input || !output || in_n <= 0 || in_n % L0 != 0 || out_n < in_n / L0 * Ln) {
+    volta::fail(h, VOLTA_STATUS_BAD_ARGUMENT, "volta_infer: in_n must be rows*L0 and out_n >= rows*Ln");
+    return;
+  }
+  (void)volta_train_infer(g_infer_model, input, in_n / L0, output);
 }
 
 int32_t volta_train_set_state(VoltaTrainHandle* vh, const float* state, int64_t step) {
