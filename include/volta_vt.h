@@ -1,0 +1,34 @@
+/* .vt front end of the MI355X training library: what `volta compile-train
+ * --rust model.vt` takes from a Volta source (executor.rs:1806-1863).
+ *
+ * Reads the MLP subset of the language (model / dataset / train
+ * statements, frontend/parser.rs:136-181; top-level numeric variables and
+ * print are accepted), resolves the first model declared the way
+ * compile-train does (layers and activation from the model block; the
+ * optimizer from the last train statement naming the model, else the
+ * model's own, else SGD; autopilot rules when a train statement names
+ * none, autopilot.rs:143-160) and applies the compile-train guards
+ * (executor.rs:3147-3189) plus this library's limits (no dropout,
+ * LayerNorm, gradient clipping or hidden softmax yet). */
+#ifndef VOLTA_VT_H
+#define VOLTA_VT_H
+
+#include "volta_train.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Fill *spec for the first model of `source` (NUL-terminated .vt text).
+ * `summary` (optional) receives a one-line description followed by
+ * "note: ..." lines for what the reference would do that this library does
+ * not (e.g. the interpreter's pre-training epochs).  Returns 0, or -1 with
+ * the reason (line:column: message) in volta_train_last_error(). */
+int32_t volta_vt_compile_train_spec(const char* source, volta_mlp_spec* spec, char* summary,
+                                    int32_t summary_len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VOLTA_VT_H */

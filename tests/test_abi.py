@@ -12,8 +12,8 @@ from volta_amd.abi import HEADER_SYMBOLS
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def header_functions():
-    text = open(os.path.join(ROOT, "include", "volta_train.h")).read()
+def header_functions(name="volta_train.h"):
+    text = open(os.path.join(ROOT, "include", name)).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(volta_\w+)\s*\(", text)))
 
@@ -32,6 +32,16 @@ def test_reference_six_symbols_declared():
 def test_hip_library_exports_header_symbols():
     lib = load_hip()
     for name in header_functions():
+        assert hasattr(lib.lib, name), name
+
+
+@pytest.mark.skipif(not os.path.exists(HIP_LIB), reason="libvolta_hip.so not built")
+def test_hip_library_exports_vt_front_end():
+    from volta_amd.abi import VT_SIGNATURES
+
+    assert sorted(VT_SIGNATURES) == header_functions("volta_vt.h")
+    lib = load_hip()
+    for name in header_functions("volta_vt.h"):
         assert hasattr(lib.lib, name), name
 
 

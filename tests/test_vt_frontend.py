@@ -1,0 +1,136 @@
+"""The .vt front end of compile-train (include/volta_vt.h) and the volta-hip
+command line, on the CPU: what spec each source resolves to, the guards,
+and the generated per-model library's exports.  The sources are written
+here in the language's MLP subset (model / dataset / train blocks)."""
+import ctypes as C
+import os
+import subprocess
+
+import pytest
+
+from volta_amd import HIP_LIB, load_hip
+from volta_amd.abi import ACTIVATIONS, OPTIMIZERS, CSpec
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CLI = os.path.join(ROOT, "volta_amd", "volta-hip")
+pytestmark = pytest.mark.skipif(not (os.path.exists(HIP_LIB) and os.path.exists(CLI)),
+                                reason="library / CLI not built")
+
+HEADLINE = """# the headline topology with Adam
+model net
+    layers 512 1024 1024 512 256 1
+    activation relu
+
+dataset data
+    type synthetic
+    batch 64
+
+train net on data
+    epochs 50
+    optimizer adam
+    lr 0.001
+    device cpu
+"""
+
+
+def resolve(source):
+    lib = load_hip()
+    spec = CSpec()
+    buf = C.create_string_buffer(4096)
+    rc = lib.lib.volta_vt_compile_train_spec(source.encode(), C.byref(spec), buf, len(buf))
+    if rc != 0:
+        raise ValueError(lib.last_error())
+    return spec, buf.value.decode()
+
+
+def names(spec):
+    act = {v: k for k, v in ACTIVATIONS.items()}[spec.activation]
+    opt = {v: k for k, v in OPTIMIZERS.items()}[spec.optimizer]
+    return list(spec.sizes[:spec.n_sizes]), act, opt
+
+
+def test_headline_source():
+    spec, summary = resolve(HEADLINE)
+    assert names(spec) == ([512, 1024, 1024, 512, 256, 1], "relu", "adam")
+    assert spec.loss == 0 and abs(spec.beta1 - 0.9) < 1e-7 and abs(spec.eps - 1e-8) < 1e-12
+    assert "lr=0.001 epochs=50 batch=64" in summary
+    assert "note: the reference trains the model in its interpreter for 50 epoch(s)" in summary
+
+
+@pytest.mark.parametrize("src,want", [
+    # no train statement: the model's own optimizer, else SGD (executor.rs:1834-1837)
+    ("model m\n    layers 4 8 2\n", ([4, 8, 2], "relu", "sgd")),
+    ("model m\n    layers 4 8 2\n    activation tanh\n    optimizer adagrad 0.01\n", ([4, 8, 2], "tanh", "adagrad")),
+    # train without optimizer: autopilot rule, adam up to 6 layers, adamw above
+    ("model m\n    layers 4 8 2\ndataset d\ntrain m on d\n", ([4, 8, 2], "relu", "adam")),
+    ("model m\n    layers 4 8 8 8 8 8 8 2\ndataset d\ntrain m on d\n", ([4, 8, 8, 8, 8, 8, 8, 2], "relu", "adamw")),
+    # train optimizer beats the model's; the last train statement decides
+    ("model m\n    layers 4 8 2\n    optimizer sgd\ndataset d\ntrain m on d\n    optimizer adamw\n"
+     "train m on d\n    optimizer Adagrad\n", ([4, 8, 2], "relu", "adagrad")),
+    # aliases, variables, comments, strings and negative numbers
+    ("width 16  # a variable\nmodel m  # comment\n    layers 4 width 2\n    activation leakyrelu\n"
+     "    seed -3\ndataset d\n    source \"x.csv\"\ntrain m on d\n    optimizer sgd\n",
+     ([4, 16, 2], "leaky_relu", "sgd")),
+    # the first model is the one compiled
+    ("model a\n    layers 3 5 1\n    activation gelu\nmodel b\n    layers 9 9 9\n", ([3, 5, 1], "gelu", "sgd")),
+])
+def test_resolution(src, want):
+    spec, _ = resolve(src)
+    assert names(spec) == want
+
+
+@pytest.mark.parametrize("src,msg", [
+    ("model m\n    layers 4 8 2\ndataset d\ntrain m on d\n    optimizer rmsprop\n",
+     "supports only SGD, Adam, AdamW, and Adagrad"),
+    ("model m\n    layers 4 8 2\n    use block\n", "is MLP-only"),
+    ("model m\n    layers 4 8 2\n    layernorm yes\n", "layernorm is not supported"),
+    ("model m\n    layers 4 8 2\n    dropout 0.1\n", "dropout is not supported"),
+    ("model m\n    layers 4 8 2\ndataset d\ntrain m on d\n    clip_grad 1.0\n", "clip_grad is not supported"),
+    ("model m\n    layers 4 8 2\n    activation softmax\n", "softmax"),
+    ("model m\n    layers 4 8 2\n    activation swish\n", "invalid value 'swish'"),
+    ("model m\n    layers 4\n", "at least 2 values"),
+    ("model m\n    layers 4 0 2\n", "must be > 0"),
+    ("model m\n    activation relu\n", "missing required property 'layers'"),
+    ("model m\n    layers 4 8 2\n    layers 4 8 2\n", "duplicate 'layers'"),
+    ("model m\n\tlayers 4 8 2\n", "tabs are not allowed"),
+    ("model m\n  layers 4 8 2\n", "inconsistent indentation"),
+    ("model m\n    layers 4 8 2\ntrain m on nowhere\n", "Undefined dataset: 'nowhere'"),
+    ("dataset d\n", "No models found"),
+    ("model m\n    layers 4 8 2\nloop 3\n    print 1\n", "not part of the compile-train subset"),
+])
+def test_guards(src, msg):
+    with pytest.raises(ValueError) as e:
+        resolve(src)
+    assert msg in str(e.value), str(e.value)
+
+
+def test_cli_check_and_compile_train(tmp_path):
+    vt = tmp_path / "net.vt"
+    vt.write_text(HEADLINE)
+    r = subprocess.run([CLI, "check", str(vt)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    assert r.stdout.startswith("model=net layers=512-1024-1024-512-256-1 activation=relu optimizer=adam")
+    bad = tmp_path / "bad.vt"
+    bad.write_text("model m\n    layers 4 8 2\ndataset d\ntrain m on d\n    optimizer rmsprop\n")
+    r = subprocess.run([CLI, "compile-train", str(bad)], capture_output=True, text=True)
+    assert r.returncode == 1 and "rmsprop" in r.stderr
+    r = subprocess.run([CLI, "compile-train", str(vt)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    out = tmp_path / "net.train_hip.so"
+    assert out.exists() and not (tmp_path / "net.train_hip.so.c").exists()
+    lib = C.CDLL(str(out))
+    for sym in ("volta_train_init", "volta_train_step", "volta_train_loss", "volta_train_get_params",
+                "volta_train_set_params", "volta_train_free", "volta_train_step_labels"):
+        assert hasattr(lib, sym), sym
+    lib.volta_train_init.restype = C.c_void_p
+    lib.volta_train_last_error.restype = C.c_char_p
+    h = lib.volta_train_init(8)  # no GPU here: NULL with the library's reason
+    if h:
+        lib.volta_train_free.argtypes = [C.c_void_p]
+        lib.volta_train_free(h)
+    else:
+        assert b"HIP" in lib.volta_train_last_error()
+    r = subprocess.run([CLI, "compile-train", str(vt), "-o", str(tmp_path / "x.so"), "--keep-source"],
+                       capture_output=True, text=True)
+    assert r.returncode == 0 and (tmp_path / "x.so.c").exists()
+    assert subprocess.run([CLI, "frobnicate", str(vt)], capture_output=True).returncode == 2

@@ -85,5 +85,7 @@ def load_hip(path: str = HIP_LIB) -> TrainLibrary:
         if not os.path.exists(path):
             raise HipLibraryMissing(
                 f"{path} is not built; run `python -m volta_amd.build` (or __graft_entry__.build())")
-        _loaded[path] = TrainLibrary(path, extra=HIP_EXTRA)
+        from .abi import VT_SIGNATURES
+
+        _loaded[path] = TrainLibrary(path, extra={**HIP_EXTRA, **VT_SIGNATURES})
     return _loaded[path]

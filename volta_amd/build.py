@@ -24,8 +24,13 @@ CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libvolta_hip.so")
 
-SOURCES = ["gemm.hip", "skinny.hip", "step_kernels.hip", "runtime.hip", "test_hooks.hip", "spec.cpp"]
-HEADERS = ["gemm.h", "skinny.h", "step_kernels.h", "device_common.h", "recorder.h", "spec.h"]
+SOURCES = ["gemm.hip", "skinny.hip", "step_kernels.hip", "runtime.hip", "test_hooks.hip", "spec.cpp",
+           "vt_frontend.cpp"]
+HEADERS = ["gemm.h", "skinny.h", "step_kernels.h", "device_common.h", "recorder.h", "spec.h", "narrow_dw.h",
+           "vt_frontend.h"]
+CLI = os.path.join(PKG, "volta-hip")
+CLI_SOURCES = ["volta_hip_cli.cpp", "vt_frontend.cpp", "spec.cpp"]
+CXX = os.environ.get("CXX", "g++")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("VOLTA_OFFLOAD_ARCH", "gfx950")
@@ -77,6 +82,13 @@ def build(verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stderr}")
     shutil.move(LIB + ".tmp", LIB)
+    # the command line (host code only; finds libvolta_hip.so beside itself)
+    cmd = [CXX, "-O2", "-std=c++17", "-Wall", "-I", os.path.join(ROOT, "include"), "-o", CLI + ".tmp"] + \
+        [os.path.join(CSRC, s) for s in CLI_SOURCES]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"CLI build failed: {' '.join(cmd)}\n{r.stderr}")
+    shutil.move(CLI + ".tmp", CLI)
     return LIB
 
 

@@ -1,0 +1,527 @@
+// .vt front end for compile-train: lexes the indentation-structured Volta
+// source (frontend/lexer.rs: 4-space indents, '#' comments, no tabs), parses
+// the model / dataset / train statements (frontend/parser.rs:136-181) and
+// resolves the first model the way `volta compile-train --rust` does
+// (executor.rs:1806-1863): layers and activation from the model block, the
+// optimizer from the last `train` statement naming the model (autopilot
+// precedence train > model > rule, autopilot.rs:143-160) or, with no train
+// statement, the model's own optimizer or SGD; then the compile-train guards
+// (executor.rs:3147-3189) and this library's own limits.
+#include "vt_frontend.h"
+
+#include "../../include/volta_vt.h"
+
+#include <algorithm>
+#include <cctype>
+#include <cmath>
+#include <cstdio>
+#include <map>
+#include <sstream>
+
+#include "spec.h"
+
+namespace volta {
+namespace {
+
+enum TokKind { T_IDENT, T_INT, T_FLOAT, T_STR, T_SYM };
+
+struct Tok {
+  TokKind kind;
+  std::string text;
+  double num = 0.0;
+  int line = 0, col = 0;
+};
+
+struct Line {
+  int indent = 0;  // columns of leading spaces
+  int number = 0;
+  std::vector<Tok> toks;
+};
+
+struct Fail {
+  std::string msg;
+};
+
+[[noreturn]] void fail_at(int line, int col, const std::string& m) {
+  throw Fail{std::to_string(line) + ":" + std::to_string(col) + ": " + m};
+}
+
+// Split the source into non-blank logical lines of tokens.
+std::vector<Line> lex(const std::string& src) {
+  std::vector<Line> out;
+  std::istringstream in(src);
+  std::string raw;
+  int number = 0;
+  while (std::getline(in, raw)) {
+    ++number;
+    if (!raw.empty() && raw.back() == '\r') raw.pop_back();
+    size_t i = 0;
+    while (i < raw.size() && (raw[i] == ' ' || raw[i] == '\t')) {
+      if (raw[i] == '\t') fail_at(number, (int)i + 1, "tabs are not allowed for indentation; use 4 spaces");
+      ++i;
+    }
+    Line ln;
+    ln.indent = (int)i;
+    ln.number = number;
+    while (i < raw.size()) {
+      const char c = raw[i];
+      const int col = (int)i + 1;
+      if (c == ' ' || c == '\t') {
+        ++i;
+      } else if (c == '#') {
+        break;
+      } else if (std::isdigit((unsigned char)c)) {
+        size_t j = i;
+        while (j < raw.size() && std::isdigit((unsigned char)raw[j])) ++j;
+        bool flt = false;
+        if (j + 1 < raw.size() && raw[j] == '.' && std::isdigit((unsigned char)raw[j + 1])) {
+          flt = true;
+          ++j;
+          while (j < raw.size() && std::isdigit((unsigned char)raw[j])) ++j;
+        }
+        Tok t{flt ? T_FLOAT : T_INT, raw.substr(i, j - i), 0.0, number, col};
+        t.num = std::strtod(t.text.c_str(), nullptr);
+        ln.toks.push_back(t);
+        i = j;
+      } else if (std::isalpha((unsigned char)c) || c == '_') {
+        size_t j = i;
+        while (j < raw.size() && (std::isalnum((unsigned char)raw[j]) || raw[j] == '_')) ++j;
+        ln.toks.push_back({T_IDENT, raw.substr(i, j - i), 0.0, number, col});
+        i = j;
+      } else if (c == '"') {
+        std::string s;
+        size_t j = i + 1;
+        bool closed = false;
+        while (j < raw.size()) {
+          if (raw[j] == '"') {
+            closed = true;
+            ++j;
+            break;
+          }
+          if (raw[j] == '\\' && j + 1 < raw.size()) {
+            const char e = raw[j + 1];
+            s += e == 'n' ? '\n' : e == 't' ? '\t' : e == 'r' ? '\r' : e;
+            j += 2;
+            continue;
+          }
+          s += raw[j++];
+        }
+        if (!closed) fail_at(number, col, "unclosed string literal");
+        ln.toks.push_back({T_STR, s, 0.0, number, col});
+        i = j;
+      } else {
+        static const char* two[] = {"==", "!=", ">=", "<=", "->", ".."};
+        std::string sym(1, c);
+        for (const char* t : two)
+          if (raw.compare(i, 2, t) == 0) sym = t;
+        ln.toks.push_back({T_SYM, sym, 0.0, number, col});
+        i += sym.size();
+      }
+    }
+    if (!ln.toks.empty()) out.push_back(ln);
+  }
+  return out;
+}
+
+// A property value after '-' folding: number, symbol (identifier or
+// keyword), string or bool.
+struct Value {
+  enum Kind { NUM, INT, SYM, STR } kind;
+  double num = 0.0;
+  std::string text;
+  int line = 0, col = 0;
+};
+
+struct Property {
+  std::string key;
+  std::vector<Value> values;
+  int line = 0, col = 0;
+};
+
+struct Block {
+  std::vector<Property> props;
+};
+
+Property parse_property(const Line& ln, const std::map<std::string, double>& vars) {
+  Property p;
+  const auto& t = ln.toks;
+  if (t[0].kind != T_IDENT) fail_at(ln.number, t[0].col, "invalid property: missing property key");
+  p.key = t[0].text;
+  p.line = ln.number;
+  p.col = t[0].col;
+  for (size_t k = 1; k < t.size(); ++k) {
+    Value v;
+    v.line = ln.number;
+    v.col = t[k].col;
+    if (t[k].kind == T_SYM && t[k].text == "-") {
+      if (k + 1 >= t.size() || (t[k + 1].kind != T_INT && t[k + 1].kind != T_FLOAT))
+        fail_at(ln.number, t[k].col, "invalid property value; '-' must be followed by a number");
+      ++k;
+      v.kind = t[k].kind == T_INT ? Value::INT : Value::NUM;
+      v.num = -t[k].num;
+    } else if (t[k].kind == T_INT || t[k].kind == T_FLOAT) {
+      v.kind = t[k].kind == T_INT ? Value::INT : Value::NUM;
+      v.num = t[k].num;
+    } else if (t[k].kind == T_STR) {
+      v.kind = Value::STR;
+      v.text = t[k].text;
+    } else if (t[k].kind == T_IDENT) {
+      auto it = vars.find(t[k].text);
+      if (it != vars.end()) {  // a top-level numeric variable
+        v.kind = std::floor(it->second) == it->second ? Value::INT : Value::NUM;
+        v.num = it->second;
+      } else {
+        v.kind = Value::SYM;
+        v.text = t[k].text;
+      }
+    } else {
+      fail_at(ln.number, t[k].col, "invalid property value '" + t[k].text + "'");
+    }
+    p.values.push_back(v);
+  }
+  if (p.values.empty()) fail_at(ln.number, t[0].col, "invalid property structure: missing property value");
+  return p;
+}
+
+const Property* find(const Block& b, const char* key) {
+  for (const auto& p : b.props)
+    if (p.key == key) return &p;
+  return nullptr;
+}
+
+void check_unique(const Block& b, const char* ctx) {
+  for (size_t i = 0; i < b.props.size(); ++i)
+    for (size_t j = 0; j < i; ++j)
+      if (b.props[i].key == b.props[j].key)
+        fail_at(b.props[i].line, b.props[i].col, "duplicate '" + b.props[i].key + "' in " + ctx + " block");
+}
+
+void warn_unknown(const Block& b, const char* ctx, std::initializer_list<const char*> known,
+                  std::vector<std::string>* notes) {
+  for (const auto& p : b.props) {
+    bool ok = false;
+    for (const char* k : known) ok = ok || p.key == k;
+    if (!ok) notes->push_back("unknown property '" + p.key + "' in " + ctx + " block (ignored)");
+  }
+}
+
+const Value& single(const Property& p, const std::string& label) {
+  if (p.values.size() != 1) fail_at(p.line, p.col, label + " expects exactly one value");
+  return p.values[0];
+}
+
+int64_t int_of(const Value& v, const std::string& label) {
+  if (v.kind != Value::INT) fail_at(v.line, v.col, label + " expects an integer");
+  return (int64_t)v.num;
+}
+
+double num_of(const Value& v, const std::string& label) {
+  if (v.kind != Value::INT && v.kind != Value::NUM) fail_at(v.line, v.col, label + " expects a number");
+  return v.num;
+}
+
+std::string sym_of(const Value& v, const std::string& label) {
+  if (v.kind != Value::SYM && v.kind != Value::STR) fail_at(v.line, v.col, label + " expects a name");
+  std::string s = v.text;
+  std::transform(s.begin(), s.end(), s.begin(), [](unsigned char c) { return (char)std::tolower(c); });
+  return s;
+}
+
+void allowed(const Value& v, const std::string& label, const std::string& s,
+             std::initializer_list<const char*> names) {
+  for (const char* n : names)
+    if (s == n) return;
+  std::string all;
+  for (const char* n : names) all += std::string(all.empty() ? "" : ", ") + n;
+  fail_at(v.line, v.col, "invalid property: " + label + " has invalid value '" + s + "'; allowed: " + all);
+}
+
+// language-level names (rules.rs:39-49)
+const std::initializer_list<const char*> kActivations = {"relu", "sigmoid", "tanh", "softmax", "leaky_relu",
+                                                         "leakyrelu", "silu", "gelu"};
+const std::initializer_list<const char*> kOptimizers = {"adam", "adamw", "sgd", "rmsprop", "rms_prop", "adagrad"};
+const std::initializer_list<const char*> kDevices = {"cpu", "gpu", "cuda", "auto"};
+
+struct Statement {
+  std::string kind;  // model / dataset / train
+  std::string name, data;
+  Block block;
+  int line = 0;
+};
+
+}  // namespace
+
+bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::string* error) {
+  try {
+    const std::vector<Line> lines = lex(source);
+    std::vector<Statement> stmts;
+    std::map<std::string, double> vars;
+    std::vector<std::string> notes;
+    for (size_t li = 0; li < lines.size();) {
+      const Line& ln = lines[li];
+      if (ln.indent != 0) fail_at(ln.number, 1, "unexpected indentation");
+      const Tok& head = ln.toks[0];
+      Statement st;
+      st.line = ln.number;
+      const std::string kw = head.kind == T_IDENT ? head.text : "";
+      if (kw == "model" || kw == "dataset") {
+        if (ln.toks.size() != 2 || ln.toks[1].kind != T_IDENT)
+          fail_at(ln.number, head.col, "use: " + kw + " <name>");
+        st.kind = kw;
+        st.name = ln.toks[1].text;
+      } else if (kw == "train") {
+        if (ln.toks.size() != 4 || ln.toks[1].kind != T_IDENT || ln.toks[2].text != "on" ||
+            ln.toks[3].kind != T_IDENT)
+          fail_at(ln.number, head.col, "invalid train syntax; use: train <model_name> on <dataset_name>");
+        st.kind = kw;
+        st.name = ln.toks[1].text;
+        st.data = ln.toks[3].text;
+      } else if (kw == "print") {
+        notes.push_back("line " + std::to_string(ln.number) + ": print skipped");
+        ++li;
+        continue;
+      } else if (head.kind == T_IDENT && ln.toks.size() >= 2 &&
+                 !(kw == "save" || kw == "load" || kw == "infer" || kw == "fn" || kw == "struct" ||
+                   kw == "loop" || kw == "for" || kw == "if" || kw == "elif" || kw == "else" ||
+                   kw == "return")) {
+        // top-level variable: `name <number>` or `name = <number>`
+        size_t k = 1;
+        if (ln.toks[k].kind == T_SYM && ln.toks[k].text == "=") ++k;
+        double sign = 1.0;
+        if (k < ln.toks.size() && ln.toks[k].kind == T_SYM && ln.toks[k].text == "-") {
+          sign = -1.0;
+          ++k;
+        }
+        if (k + 1 == ln.toks.size() && (ln.toks[k].kind == T_INT || ln.toks[k].kind == T_FLOAT)) {
+          vars[head.text] = sign * ln.toks[k].num;
+        } else {
+          notes.push_back("line " + std::to_string(ln.number) + ": non-numeric variable '" + head.text +
+                          "' skipped");
+        }
+        ++li;
+        continue;
+      } else {
+        fail_at(ln.number, head.col,
+                "statement '" + head.text + "' is not part of the compile-train subset (model, dataset, train)");
+      }
+      ++li;
+      // property block: the following lines indented by exactly 4
+      if (li < lines.size() && lines[li].indent > 0) {
+        if (lines[li].indent != 4) fail_at(lines[li].number, 1, "inconsistent indentation (use 4 spaces)");
+        while (li < lines.size() && lines[li].indent > 0) {
+          if (lines[li].indent != 4) fail_at(lines[li].number, 1, "inconsistent indentation (use 4 spaces)");
+          st.block.props.push_back(parse_property(lines[li], vars));
+          ++li;
+        }
+      } else if (st.kind == "model") {
+        fail_at(st.line, 1, "missing indent for property block");
+      }
+      stmts.push_back(st);
+    }
+
+    // the first model declared
+    const Statement* model = nullptr;
+    for (const auto& s : stmts)
+      if (s.kind == "model") {
+        model = &s;
+        break;
+      }
+    if (!model) throw Fail{"No models found — declare a model first"};
+    const Block& mb = model->block;
+    check_unique(mb, "model");
+    warn_unknown(mb, "model", {"layers", "activation", "optimizer", "precision", "memory", "seed", "use",
+                               "dropout", "layernorm"}, &notes);
+    const Property* layers = find(mb, "layers");
+    if (!layers) fail_at(model->line, 1, "invalid property: missing required property 'layers' in model");
+    if (layers->values.size() < 2) fail_at(layers->line, layers->col, "model.layers must have at least 2 values");
+    if ((int)layers->values.size() > VOLTA_MAX_LAYER_SIZES)
+      fail_at(layers->line, layers->col, "model.layers has more than " + std::to_string(VOLTA_MAX_LAYER_SIZES) +
+                                             " values (this library's limit)");
+    std::vector<int> sizes;
+    for (const auto& v : layers->values) {
+      const int64_t x = int_of(v, "model.layers");
+      if (x <= 0) fail_at(v.line, v.col, "model.layers values must be > 0, found " + std::to_string(x));
+      if (x > (1 << 20)) fail_at(v.line, v.col, "model.layers value above this library's limit 1048576");
+      sizes.push_back((int)x);
+    }
+    std::string activation = "relu";  // AUTOPILOT_DEFAULT_ACTIVATION
+    if (const Property* p = find(mb, "activation")) {
+      const Value& v = single(*p, "model.activation");
+      activation = sym_of(v, "model.activation");
+      allowed(v, "model.activation", activation, kActivations);
+    }
+    std::string model_opt;
+    double model_lr = 0.0;
+    if (const Property* p = find(mb, "optimizer")) {
+      if (p->values.empty() || p->values.size() > 2) fail_at(p->line, p->col, "model.optimizer expects 1 or 2 values");
+      model_opt = sym_of(p->values[0], "model.optimizer");
+      allowed(p->values[0], "model.optimizer", model_opt, kOptimizers);
+      if (p->values.size() == 2) {
+        model_lr = num_of(p->values[1], "model.optimizer learning rate");
+        if (!(model_lr > 0.0)) fail_at(p->values[1].line, p->values[1].col, "model.optimizer learning rate must be > 0");
+      }
+    }
+    if (const Property* p = find(mb, "use"))
+      fail_at(p->line, p->col,
+              "Model '" + model->name + "' uses template '" + sym_of(single(*p, "model.use"), "model.use") +
+                  "'. `compile-train` is MLP-only and does not support function-backed/custom training graphs.");
+    if (const Property* p = find(mb, "dropout")) {
+      const double d = num_of(single(*p, "model.dropout"), "model.dropout");
+      if (!(d >= 0.0 && d < 1.0)) fail_at(p->line, p->col, "model.dropout must be in [0, 1)");
+      if (d > 0.0) fail_at(p->line, p->col, "model.dropout is not supported by this MI355X training library yet");
+    }
+    if (const Property* p = find(mb, "layernorm")) {
+      const Value& v = single(*p, "model.layernorm");
+      const std::string s = sym_of(v, "model.layernorm");
+      if (s == "yes" || s == "true" || s == "on")
+        fail_at(p->line, p->col, "model.layernorm is not supported by this MI355X training library yet");
+    }
+
+    // every train statement needs a declared model and an earlier dataset
+    // (executor.rs:930-957)
+    for (const auto& s : stmts) {
+      if (s.kind != "train") continue;
+      bool have_model = false, have_data = false;
+      for (const auto& d : stmts) {
+        have_model = have_model || (d.kind == "model" && d.name == s.name && d.line < s.line);
+        have_data = have_data || (d.kind == "dataset" && d.name == s.data && d.line < s.line);
+      }
+      if (!have_data) fail_at(s.line, 1, "Undefined dataset: '" + s.data + "'");
+      if (!have_model) fail_at(s.line, 1, "Undefined model: '" + s.name + "'");
+    }
+    // train statements naming the model; the last one decides (each run
+    // overwrites the model's optimizer, executor.rs:1294-1301)
+    const int nlayers = (int)sizes.size();
+    const Statement* train = nullptr;
+    for (const auto& s : stmts) {
+      if (s.kind == "train" && s.name == model->name) train = &s;
+    }
+    std::string optimizer;
+    VtTrainPlan out;
+    if (train) {
+      const Block& tb = train->block;
+      check_unique(tb, "train");
+      warn_unknown(tb, "train", {"epochs", "device", "optimizer", "lr", "batch", "precision", "clip_grad",
+                                 "weight_decay", "warmup_steps", "lr_schedule", "early_stopping",
+                                 "gradient_accumulation"}, &notes);
+      // autopilot precedence (autopilot.rs:130-196)
+      out.epochs = 10;  // AUTOPILOT_DEFAULT_EPOCHS
+      if (const Property* p = find(tb, "epochs")) {
+        out.epochs = int_of(single(*p, "train.epochs"), "train.epochs");
+        if (out.epochs < 0) fail_at(p->line, p->col, "train.epochs must be non-negative");
+      }
+      if (const Property* p = find(tb, "device")) {
+        const Value& v = single(*p, "train.device");
+        allowed(v, "train.device", sym_of(v, "train.device"), kDevices);
+      }
+      if (const Property* p = find(tb, "optimizer")) {
+        const Value& v = single(*p, "train.optimizer");
+        optimizer = sym_of(v, "train.optimizer");
+        allowed(v, "train.optimizer", optimizer, kOptimizers);
+      } else if (!model_opt.empty()) {
+        optimizer = model_opt;
+      } else {
+        optimizer = nlayers <= 6 ? "adam" : "adamw";  // small/medium vs large model rule
+      }
+      out.lr = nlayers <= 3 ? 0.001 : nlayers <= 6 ? 0.0007 : 0.0003;
+      if (model_lr > 0.0) out.lr = model_lr;
+      if (const Property* p = find(tb, "lr")) {
+        out.lr = num_of(single(*p, "train.lr"), "train.lr");
+        if (!(out.lr > 0.0)) fail_at(p->line, p->col, "train.lr must be > 0");
+      }
+      out.batch = 32;  // AUTOPILOT_DEFAULT_BATCH
+      for (const auto& d : stmts)
+        if (d.kind == "dataset" && d.name == train->data)
+          if (const Property* p = find(d.block, "batch")) out.batch = int_of(single(*p, "dataset.batch"), "dataset.batch");
+      if (const Property* p = find(tb, "batch")) {
+        out.batch = int_of(single(*p, "train.batch"), "train.batch");
+        if (out.batch <= 0) fail_at(p->line, p->col, "train.batch must be > 0");
+      }
+      if (const Property* p = find(tb, "clip_grad")) {
+        const double c = num_of(single(*p, "train.clip_grad"), "train.clip_grad");
+        if (c > 0.0) fail_at(p->line, p->col, "train.clip_grad is not supported by this MI355X training library yet");
+      }
+      if (find(tb, "weight_decay"))
+        notes.push_back("train.weight_decay shapes the interpreter's training only; the generated step "
+                        "uses the compile-train constant (AdamW 0.01 on weights)");
+      if (out.epochs > 0)
+        notes.push_back("the reference trains the model in its interpreter for " + std::to_string(out.epochs) +
+                        " epoch(s) before generating the library and starts the library from those weights; "
+                        "this library starts from the LCG Xavier init (seed 42) — load trained weights with "
+                        "volta_train_set_params");
+      out.trained = true;
+    } else {
+      optimizer = model_opt.empty() ? "sgd" : model_opt;
+    }
+    // compile-train --rust guard (executor.rs:3172-3189)
+    if (!(optimizer == "sgd" || optimizer == "adam" || optimizer == "adamw" || optimizer == "adagrad"))
+      throw Fail{"Model '" + model->name + "' requests optimizer '" + optimizer +
+                 "', but `compile-train --rust` supports only SGD, Adam, AdamW, and Adagrad today. "
+                 "Use runtime `train` for RMSProp or other optimizers."};
+    if (activation == "softmax")
+      throw Fail{"activation softmax (as a hidden activation) is not supported by this MI355X training library yet"};
+
+    const int act = activation == "relu" ? VOLTA_ACT_RELU
+                    : activation == "sigmoid" ? VOLTA_ACT_SIGMOID
+                    : activation == "tanh" ? VOLTA_ACT_TANH
+                    : (activation == "leaky_relu" || activation == "leakyrelu") ? VOLTA_ACT_LEAKY_RELU
+                    : activation == "silu" ? VOLTA_ACT_SILU
+                                           : VOLTA_ACT_GELU;
+    const int opt = optimizer == "sgd" ? VOLTA_OPT_SGD
+                    : optimizer == "adam" ? VOLTA_OPT_ADAM
+                    : optimizer == "adamw" ? VOLTA_OPT_ADAMW
+                                           : VOLTA_OPT_ADAGRAD;
+    volta_mlp_spec_default(&out.spec, (int32_t)sizes.size(), sizes.data(), act, opt, VOLTA_LOSS_MSE);
+    std::string why;
+    if (!validate_spec(out.spec, &why)) throw Fail{"model '" + model->name + "': " + why};
+    out.model = model->name;
+    out.notes = notes;
+    *plan = out;
+    return true;
+  } catch (const Fail& f) {
+    if (error) *error = f.msg;
+    return false;
+  }
+}
+
+std::string vt_plan_summary(const VtTrainPlan& p) {
+  static const char* acts[] = {"relu", "sigmoid", "tanh", "leaky_relu", "silu", "gelu"};
+  static const char* opts[] = {"sgd", "adam", "adamw", "adagrad"};
+  std::string layers;
+  for (int i = 0; i < p.spec.n_sizes; ++i) layers += (i ? "-" : "") + std::to_string(p.spec.sizes[i]);
+  char buf[512];
+  std::snprintf(buf, sizeof buf, "model=%s layers=%s activation=%s optimizer=%s loss=mse", p.model.c_str(),
+                layers.c_str(), acts[p.spec.activation], opts[p.spec.optimizer]);
+  std::string s = buf;
+  if (p.trained) {
+    std::snprintf(buf, sizeof buf, " lr=%g epochs=%lld batch=%lld", p.lr, (long long)p.epochs, (long long)p.batch);
+    s += buf;
+  }
+  return s;
+}
+
+}  // namespace volta
+
+// ---------------------------------------------------------------------------
+// C entry point (include/volta_vt.h)
+// ---------------------------------------------------------------------------
+extern "C" int32_t volta_vt_compile_train_spec(const char* source, volta_mlp_spec* spec, char* summary,
+                                                int32_t summary_len) {
+  if (!source || !spec) {
+    volta::set_last_error("volta_vt_compile_train_spec: null argument");
+    return -1;
+  }
+  volta::VtTrainPlan plan;
+  std::string err;
+  if (!volta::vt_compile_train_plan(source, &plan, &err)) {
+    volta::set_last_error(err);
+    return -1;
+  }
+  *spec = plan.spec;
+  if (summary && summary_len > 0) {
+    std::string s = volta::vt_plan_summary(plan);
+    for (const auto& n : plan.notes) s += "\nnote: " + n;
+    std::snprintf(summary, (size_t)summary_len, "%s", s.c_str());
+  }
+  return 0;
+}

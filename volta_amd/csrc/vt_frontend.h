@@ -1,0 +1,31 @@
+// Front end for `compile-train`: the MLP subset of the Volta language (.vt),
+// reduced to the spec of the training library.
+#pragma once
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "../../include/volta_train.h"
+
+namespace volta {
+
+struct VtTrainPlan {
+  volta_mlp_spec spec{};
+  std::string model;          // first model declared (the one compile-train builds)
+  bool trained = false;       // a `train <model> on <dataset>` statement names it
+  double lr = 0.0;            // resolved learning rate of the last such statement (0: none)
+  int64_t epochs = 0;         // its resolved epochs
+  int64_t batch = 0;          // its resolved batch
+  std::vector<std::string> notes;  // what the reference would do that this build does not
+};
+
+// Parse `source` and resolve the first model as `volta compile-train --rust`
+// does (executor.rs:1806-1863, guards :3147-3189).  Returns false with a
+// message (line:column: text) on a parse error or an unsupported model.
+bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::string* error);
+
+// One-line description of a plan ("model=... layers=a-b-c activation=...").
+std::string vt_plan_summary(const VtTrainPlan& plan);
+
+}  // namespace volta
