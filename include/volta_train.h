@@ -124,6 +124,18 @@ typedef struct volta_mlp_spec {
   float beta2;
   float eps;
   float weight_decay;
+  /* Codegen extras of the generated step (0 = off, the default):
+   *   clip_grad  > 0: after the backward deltas, scale every delta by
+   *              clip/||deltas|| when the norm over all layers' deltas
+   *              exceeds clip (:936-955; db_i keeps the unscaled deltas).
+   *   dropout_p  in [0, 1): inverted dropout after each hidden activation,
+   *              mask from the LCG stream seeded 12345678 (:774-788).
+   *   layernorm  1: LayerNorm (eps 1e-5) after each hidden activation,
+   *              gamma=1/beta=0 at init, updated by plain SGD (:745-772,
+   *              :829-887). */
+  float clip_grad;
+  float dropout_p;
+  int32_t layernorm;
 } volta_mlp_spec;
 
 /* Fill *spec with the reference's constants for the given topology. */

@@ -189,6 +189,10 @@ struct Net {
   std::vector<std::vector<T>> w, b, dw, db, mw, vw, mb, vb, gw, gb;
   std::vector<std::vector<T>> act, pre, delta;
   std::vector<T> wt;  // transpose scratch for dX
+  // codegen extras (:745-788, :829-892, :936-955)
+  std::vector<std::vector<T>> ln_g, ln_b, ln_mu, ln_is, ln_dg, ln_db;
+  std::vector<std::vector<uint8_t>> mask;
+  uint64_t dropout_rng = 12345678ULL;  // alloc: dropout_rng: 12345678u64 (:553)
   uint64_t adam_step = 0;
   T last_loss = T(0);
 
@@ -200,6 +204,8 @@ struct Net {
     auto sz = [](std::vector<std::vector<T>>& v, int cnt) { v.assign(cnt, {}); };
     sz(w, n); sz(b, n); sz(dw, n); sz(db, n); sz(mw, n); sz(vw, n); sz(mb, n); sz(vb, n);
     sz(gw, n); sz(gb, n); sz(delta, n); sz(act, n + 1); sz(pre, n);
+    sz(ln_g, n); sz(ln_b, n); sz(ln_mu, n); sz(ln_is, n); sz(ln_dg, n); sz(ln_db, n);
+    mask.assign(n, {});
     size_t maxw = 0;
     for (int i = 0; i < n; ++i) {
       const size_t r = L[i], c = L[i + 1];
@@ -214,6 +220,12 @@ struct Net {
       }
       delta[i].assign((size_t)B * c, T(0));
       if (i < n - 1) pre[i].assign((size_t)B * c, T(0));
+      if (i < n - 1 && s.layernorm) {
+        ln_g[i].assign(c, T(1)); ln_b[i].assign(c, T(0));  // gamma = 1, beta = 0 (:660-668)
+        ln_mu[i].assign(B, T(0)); ln_is[i].assign(B, T(0));
+        ln_dg[i].assign(c, T(0)); ln_db[i].assign(c, T(0));
+      }
+      if (i < n - 1 && s.dropout_p > 0.0f) mask[i].assign((size_t)B * c, 0);
       maxw = r * c > maxw ? r * c : maxw;
     }
     for (int i = 0; i <= n; ++i) act[i].assign((size_t)B * L[i], T(0));
@@ -234,8 +246,89 @@ struct Net {
         T* a = act[i + 1].data();
         const size_t cnt = (size_t)B * c;
         for (size_t k = 0; k < cnt; ++k) a[k] = act_fwd<T>(spec.activation, dst[k]);
+        if (spec.layernorm) layernorm_fwd(i);
+        if (spec.dropout_p > 0.0f) dropout_fwd(i);
       }
     }
+  }
+
+  // LayerNorm after the activation (:745-772): per row, sequential f32
+  // mean and biased variance, eps 1e-5, then xhat * gamma + beta.
+  void layernorm_fwd(int i) {
+    const int c = L[i + 1];
+    T* a = act[i + 1].data();
+    for (int bi = 0; bi < B; ++bi) {
+      T* r = a + (size_t)bi * c;
+      T mu = T(0);
+      for (int j = 0; j < c; ++j) mu = mu + r[j];
+      mu = mu / T(c);
+      ln_mu[i][bi] = mu;
+      T var = T(0);
+      for (int j = 0; j < c; ++j) {
+        const T d = r[j] - mu;
+        var = var + d * d;
+      }
+      var = var / T(c);
+      const T is = T(1) / std::sqrt(var + T(1e-5f));
+      ln_is[i][bi] = is;
+      for (int j = 0; j < c; ++j) {
+        const T xhat = (r[j] - mu) * is;
+        r[j] = xhat * ln_g[i][j] + ln_b[i][j];
+      }
+    }
+  }
+
+  // Inverted dropout (:774-788): one LCG draw per element in row-major
+  // order, r = (rng >> 33) / 2^31 in f32, keep when r >= p.
+  void dropout_fwd(int i) {
+    const size_t cnt = (size_t)B * L[i + 1];
+    const float p = spec.dropout_p;
+    const float keep_scale = 1.0f / (1.0f - p);
+    T* a = act[i + 1].data();
+    for (size_t k = 0; k < cnt; ++k) {
+      dropout_rng = dropout_rng * 6364136223846793005ULL + 1442695040888963407ULL;
+      const float r = (float)(dropout_rng >> 33) / 2147483648.0f;
+      const uint8_t keep = r >= p ? 1 : 0;
+      mask[i][k] = keep;
+      a[k] = a[k] * (T((float)keep) * T(keep_scale));
+    }
+  }
+
+  // LayerNorm backward and its SGD update of gamma/beta (:829-887), in the
+  // reference's order: xhat recomputed from the stored output as
+  // (y - beta) / (gamma + 1e-12), per-row means of d_xhat and d_xhat*xhat.
+  void layernorm_bwd(int i, T lr) {
+    const int c = L[i + 1];
+    T* d = delta[i].data();
+    const T* y = act[i + 1].data();
+    std::vector<T>& g = ln_g[i];
+    std::vector<T>& be = ln_b[i];
+    std::vector<T>& dg = ln_dg[i];
+    std::vector<T>& dbe = ln_db[i];
+    std::fill(dg.begin(), dg.end(), T(0));
+    std::fill(dbe.begin(), dbe.end(), T(0));
+    for (int bi = 0; bi < B; ++bi) {
+      const size_t base = (size_t)bi * c;
+      const T is = ln_is[i][bi];
+      T sum_d = T(0), sum_dxh = T(0);
+      for (int j = 0; j < c; ++j) {
+        const T xh = (y[base + j] - be[j]) / (g[j] + T(1e-12f));
+        const T dout = d[base + j];
+        dg[j] = dg[j] + dout * xh;
+        dbe[j] = dbe[j] + dout;
+        sum_d = sum_d + dout * g[j];
+        sum_dxh = sum_dxh + dout * g[j] * xh;
+      }
+      sum_d = sum_d / T(c);
+      sum_dxh = sum_dxh / T(c);
+      for (int j = 0; j < c; ++j) {
+        const T xh = (y[base + j] - be[j]) / (g[j] + T(1e-12f));
+        const T d_xhat = d[base + j] * g[j];
+        d[base + j] = is * (d_xhat - sum_d - xh * sum_dxh);
+      }
+    }
+    for (int j = 0; j < c; ++j) g[j] = g[j] - lr * dg[j];
+    for (int j = 0; j < c; ++j) be[j] = be[j] - lr * dbe[j];
   }
 
   // MSE loss and seed gradient, :792-798.  Pinned by torch goldens.
@@ -345,6 +438,14 @@ struct Net {
       const size_t cnt = (size_t)B * c;
       T* d = delta[i].data();
       if (i != n - 1) {
+        // LayerNorm backward, then the dropout mask, then the activation
+        // derivative (:824-916); sigmoid/tanh take act_{i+1}, which holds
+        // the LayerNorm/dropout output when those are on (:908-914).
+        if (spec.layernorm) layernorm_bwd(i, lr);
+        if (spec.dropout_p > 0.0f) {
+          const float keep_scale = 1.0f / (1.0f - spec.dropout_p);
+          for (size_t k = 0; k < cnt; ++k) d[k] = d[k] * (T((float)mask[i][k]) * T(keep_scale));
+        }
         const T* p = pre[i].data();
         const T* y = act[i + 1].data();
         for (size_t k = 0; k < cnt; ++k) d[k] = d[k] * act_bwd<T>(act_kind, p[k], y[k]);
@@ -359,6 +460,19 @@ struct Net {
       for (int j = 0; j < c; ++j) dbi[j] = T(0);
       for (int bi = 0; bi < B; ++bi)
         for (int j = 0; j < c; ++j) dbi[j] = dbi[j] + d[(size_t)bi * c + j];
+    }
+    // Gradient clipping by the global norm of the deltas (:936-955), after
+    // db was formed from the unscaled deltas.
+    if (spec.clip_grad > 0.0f) {
+      T gsq = T(0);
+      for (int i = 0; i < n; ++i)
+        for (const T v : delta[i]) gsq = gsq + v * v;
+      const T gnorm = std::sqrt(gsq);
+      const T cv = T(spec.clip_grad);
+      const T scale = gnorm > cv ? cv / gnorm : T(1);
+      if (scale < T(1))
+        for (int i = 0; i < n; ++i)
+          for (T& v : delta[i]) v = v * scale;
     }
     // Phase 2: parameter updates, last layer first (:957-993).
     const T tlr = lr;

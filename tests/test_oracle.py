@@ -475,3 +475,141 @@ def test_oracle_set_hparams_equals_spec_from_start(oracle):
         a.set_hparams(1.5, 0.99, 1e-6, 0.0)
     a.close()
     b.close()
+
+
+# ---------------------------------------------------------------------------
+# Codegen extras: dropout, LayerNorm, gradient clipping
+# ---------------------------------------------------------------------------
+def _lcg_keep(n, p, state=12345678):
+    """The dropout stream written out with Python integers: state' = state*A
+    + C mod 2^64, r = f32(state >> 33) / 2^31, keep when r >= p."""
+    A, Cc, M = 6364136223846793005, 1442695040888963407, 1 << 64
+    keep = np.zeros(n, bool)
+    for k in range(n):
+        state = (state * A + Cc) % M
+        r = np.float32(state >> 33) / np.float32(2147483648.0)
+        keep[k] = r >= np.float32(p)
+    return keep, state
+
+
+def test_oracle_dropout_mask_follows_the_lcg_stream(oracle):
+    """act_1 after a zero-lr step = relu(pre_0) * mask / (1 - p), with the
+    mask drawn from the reference's LCG in row-major order; the stream
+    continues across layers and steps."""
+    spec = MlpSpec([5, 12, 9, 2], "relu", "sgd", dropout_p=0.3)
+    B = 4
+    t = Trainer(oracle, spec, B)
+    rng = np.random.default_rng(9)
+    X = rng.standard_normal((B, 5)).astype(np.float32)
+    Y = rng.standard_normal((B, 2)).astype(np.float32)
+    keep_scale = np.float32(1.0) / (np.float32(1.0) - np.float32(0.3))
+    state = 12345678
+    from volta_amd.abi import BUF_ACT
+    for step in range(2):
+        t.step(X, Y, 0.0)
+        k1, state = _lcg_keep(B * 12, 0.3, state)
+        k2, state = _lcg_keep(B * 9, 0.3, state)
+        a1 = t.debug_buffer(BUF_ACT, 1).reshape(B, 12)
+        ws, bs = t.get_params()
+        pre0 = X @ ws[0] + bs[0]
+        want1 = np.maximum(pre0, 0) * (k1.reshape(B, 12).astype(np.float32) * keep_scale)
+        np.testing.assert_allclose(a1, want1, rtol=1e-5, atol=1e-6)
+        assert ((a1 == 0) | k1.reshape(B, 12)).all()
+        a2 = t.debug_buffer(BUF_ACT, 2).reshape(B, 9)
+        assert (a2[~k2.reshape(B, 9)] == 0).all()
+    t.close()
+
+
+def test_oracle_layernorm_forward_closed_form(oracle):
+    """With gamma = 1 and beta = 0 (init), each row of act_1 is the
+    standardised relu(pre_0): mean 0 and variance v/(v + 1e-5)."""
+    spec = MlpSpec([6, 32, 3], "relu", "sgd", layernorm=True)
+    B = 5
+    t = oracle_trainer(oracle, spec, B, f64=True)
+    rng = np.random.default_rng(4)
+    X = rng.standard_normal((B, 6)).astype(np.float32)
+    t.step(X, np.zeros((B, 3), np.float32), 0.0)
+    from volta_amd.abi import BUF_ACT
+    ws, bs = t.get_params()
+    h = np.maximum(X.astype(np.float64) @ ws[0].astype(np.float64) + bs[0], 0)
+    mu = h.mean(axis=1, keepdims=True)
+    var = ((h - mu) ** 2).mean(axis=1, keepdims=True)
+    want = (h - mu) / np.sqrt(var + np.float64(np.float32(1e-5)))
+    np.testing.assert_allclose(t.debug_buffer(BUF_ACT, 1).reshape(B, 32), want, rtol=1e-6, atol=1e-6)
+    t.close()
+
+
+@pytest.mark.parametrize("act", ["relu", "gelu", "silu"])
+def test_f64_layernorm_gradient_matches_finite_differences(oracle, act):
+    """dW through the LayerNorm backward equals the finite-difference
+    gradient of the fp64 twin's loss (derivatives that use the
+    pre-activation; sigmoid/tanh with LayerNorm use the reference's own
+    post-LayerNorm derivative, :908-914, which is not the true gradient)."""
+    spec = MlpSpec([4, 7, 6, 2], act, "sgd", layernorm=True)
+    B = 3
+    rng = np.random.default_rng(12)
+    ws = [rng.uniform(-0.6, 0.6, (r, c)).astype(np.float32) for r, c in spec.shapes()]
+    bs = [rng.uniform(-0.2, 0.2, c).astype(np.float32) for _, c in spec.shapes()]
+    X = rng.standard_normal((B, 4)).astype(np.float32)
+    Y = rng.standard_normal((B, 2)).astype(np.float32)
+    lr = 1e-3
+
+    def loss_at(wsx):
+        t = oracle_trainer(oracle, spec, B, f64=True)
+        t.set_all_params(wsx, bs)
+        t.step(X, Y, 0.0)
+        v = float(oracle.lib.volta_oracle_loss_f64(t.h))
+        t.close()
+        return v
+
+    t = oracle_trainer(oracle, spec, B, f64=True)
+    t.set_all_params(ws, bs)
+    t.step(X, Y, lr)
+    w_after, _ = t.get_params()
+    t.close()
+    for li in range(3):
+        grad = (ws[li].astype(np.float64) - w_after[li].astype(np.float64)) / lr
+        for (a, b) in [(0, 0), (ws[li].shape[0] - 1, ws[li].shape[1] - 1), (1, 1)]:
+            h = 1e-3
+            wp = [w.copy() for w in ws]
+            wm = [w.copy() for w in ws]
+            wp[li][a, b] += h
+            wm[li][a, b] -= h
+            fd = (loss_at(wp) - loss_at(wm)) / (2 * (np.float64(wp[li][a, b]) - np.float64(ws[li][a, b])))
+            assert abs(fd - grad[a, b]) <= 2e-3 * max(1.0, abs(fd)), (li, a, b, fd, grad[a, b])
+
+
+def test_oracle_clip_scales_dw_but_not_db(oracle):
+    """With clipping the weight step shrinks by clip/||deltas|| (norm over
+    every layer's deltas) while the bias step keeps the unscaled deltas
+    (db is formed before the clip, :931-955)."""
+    base = MlpSpec([6, 10, 8, 3], "tanh", "sgd")
+    B = 4
+    rng = np.random.default_rng(21)
+    ws = [rng.uniform(-0.5, 0.5, (r, c)).astype(np.float32) for r, c in base.shapes()]
+    bs = [rng.uniform(-0.1, 0.1, c).astype(np.float32) for _, c in base.shapes()]
+    X = rng.standard_normal((B, 6)).astype(np.float32)
+    Y = rng.standard_normal((B, 3)).astype(np.float32)
+    from volta_amd.abi import BUF_DELTA
+    out = {}
+
+    def run(name, spec):
+        t = oracle_trainer(oracle, spec, B, f64=True)
+        t.set_all_params(ws, bs)
+        t.step(X, Y, 0.5)
+        out[name] = t.get_params() + ([t.debug_buffer(BUF_DELTA, i) for i in range(3)],)
+        t.close()
+
+    run("base", base)
+    deltas = out["base"][2]
+    gnorm = np.sqrt(sum(float((d.astype(np.float64) ** 2).sum()) for d in deltas))
+    clip_val = float(np.float32(0.4 * gnorm))
+    run("clip", MlpSpec([6, 10, 8, 3], "tanh", "sgd", clip_grad=clip_val))
+    scale = clip_val / gnorm
+    assert scale < 1
+    for i in range(3):
+        dw_base = ws[i].astype(np.float64) - out["base"][0][i]
+        dw_clip = ws[i].astype(np.float64) - out["clip"][0][i]
+        # weights come back as float32: allow their rounding
+        np.testing.assert_allclose(dw_clip, dw_base * scale, rtol=1e-4, atol=2e-7)
+        np.testing.assert_array_equal(out["clip"][1][i], out["base"][1][i])  # bias step unscaled

@@ -45,6 +45,9 @@ class CSpec(C.Structure):
         ("beta2", C.c_float),
         ("eps", C.c_float),
         ("weight_decay", C.c_float),
+        ("clip_grad", C.c_float),
+        ("dropout_p", C.c_float),
+        ("layernorm", C.c_int32),
     ]
 
 
@@ -61,6 +64,9 @@ class MlpSpec:
     beta2: float = 0.999
     eps: float = 1e-8
     weight_decay: Optional[float] = None  # None -> 0.01 for adamw, else 0
+    clip_grad: float = 0.0    # codegen extras (0 / False: off)
+    dropout_p: float = 0.0
+    layernorm: bool = False
 
     def to_c(self) -> CSpec:
         s = CSpec()
@@ -79,7 +85,14 @@ class MlpSpec:
         if wd is None:
             wd = 0.01 if self.optimizer == "adamw" else 0.0
         s.weight_decay = wd
+        s.clip_grad = self.clip_grad
+        s.dropout_p = self.dropout_p
+        s.layernorm = 1 if self.layernorm else 0
         return s
+
+    @property
+    def has_extras(self) -> bool:
+        return self.clip_grad > 0 or self.dropout_p > 0 or bool(self.layernorm)
 
     @property
     def n_layers(self) -> int:
@@ -89,7 +102,14 @@ class MlpSpec:
         return [(self.sizes[i], self.sizes[i + 1]) for i in range(self.n_layers)]
 
     def text(self) -> str:
-        return "-".join(str(s) for s in self.sizes) + f":{self.activation}:{self.optimizer}:{self.loss}"
+        t = "-".join(str(s) for s in self.sizes) + f":{self.activation}:{self.optimizer}:{self.loss}"
+        if self.clip_grad > 0:
+            t += f":clip={self.clip_grad!r}"
+        if self.dropout_p > 0:
+            t += f":dropout={self.dropout_p!r}"
+        if self.layernorm:
+            t += ":ln"
+        return t
 
 
 _P = C.c_void_p

@@ -10,6 +10,7 @@
 #include <cerrno>
 #include <cstdio>
 #include <cstdlib>
+#include <cmath>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -67,6 +68,9 @@ bool validate_spec(const volta_mlp_spec& s, std::string* why) {
   if (!(s.beta1 >= 0.0f && s.beta1 < 1.0f)) return fail("beta1 must be in [0, 1)");
   if (!(s.beta2 >= 0.0f && s.beta2 < 1.0f)) return fail("beta2 must be in [0, 1)");
   if (!(s.weight_decay >= 0.0f)) return fail("weight_decay must be >= 0");
+  if (!(s.clip_grad >= 0.0f) || std::isinf(s.clip_grad)) return fail("clip_grad must be finite and >= 0");
+  if (!(s.dropout_p >= 0.0f && s.dropout_p < 1.0f)) return fail("dropout_p must be in [0, 1)");
+  if (s.layernorm != 0 && s.layernorm != 1) return fail("layernorm must be 0 or 1");
   return true;
 }
 
@@ -175,6 +179,10 @@ extern "C" int32_t volta_mlp_spec_parse(const char* text, volta_mlp_spec* spec) 
       s.loss = VOLTA_LOSS_SOFTMAX_CE;
       continue;
     }
+    if (f == "ln" || f == "layernorm") {
+      s.layernorm = 1;
+      continue;
+    }
     size_t eq = f.find('=');
     if (eq == std::string::npos) {
       set_last_error("unknown spec field '" + f + "'");
@@ -190,6 +198,8 @@ extern "C" int32_t volta_mlp_spec_parse(const char* text, volta_mlp_spec* spec) 
     else if (key == "wd" || key == "weight_decay") s.weight_decay = v;
     else if (key == "beta1" || key == "b1") s.beta1 = v;
     else if (key == "beta2" || key == "b2") s.beta2 = v;
+    else if (key == "clip" || key == "clip_grad") s.clip_grad = v;
+    else if (key == "dropout") s.dropout_p = v;
     else {
       set_last_error("unknown spec key '" + key + "'");
       return -1;
