@@ -187,11 +187,13 @@ const char* volta_train_last_error(void);
 int32_t volta_train_num_layers(VoltaTrainHandle* h);
 int32_t volta_train_batch(VoltaTrainHandle* h);
 
-/* Optimizer state export/import for resumable Adam/AdamW/Adagrad
- * (the generated library has no way to save it).  The state is laid out
- * per layer as [m_W | m_b | v_W | v_b] (Adam/AdamW) or [G_W | G_b]
- * (Adagrad), layers in order; SGD has no state.  `step` is the Adam step
- * counter t.  volta_train_state_size returns the float count. */
+/* Training state export/import for resumable training (the generated
+ * library has no way to save it).  The state is laid out per layer as
+ * [m_W | m_b | v_W | v_b] (Adam/AdamW) or [G_W | G_b] (Adagrad), layers in
+ * order (SGD has no optimizer state), followed, when the spec has
+ * LayerNorm, by [gamma_i | beta_i] for each hidden layer i = 0..n-2.
+ * `step` is the Adam step counter t.  volta_train_state_size returns the
+ * float count.  The dropout stream has its own pair of calls below. */
 int64_t volta_train_state_size(VoltaTrainHandle* h);
 
 /* Copy one intermediate buffer of the most recent step to host memory
@@ -209,9 +211,22 @@ int64_t volta_train_state_size(VoltaTrainHandle* h);
 #define VOLTA_BUF_DELTA 1
 #define VOLTA_BUF_GRAD_W 2
 #define VOLTA_BUF_GRAD_B 3
+/*   VOLTA_BUF_LN_GAMMA   gamma_i [L[i+1]], i = 0..n-2 (spec.layernorm)
+ *   VOLTA_BUF_LN_BETA    beta_i  [L[i+1]]
+ *   VOLTA_BUF_DROPOUT_MASK keep mask of hidden layer i as 0.0/1.0
+ *                        [B x L[i+1]] (spec.dropout_p > 0) */
+#define VOLTA_BUF_LN_GAMMA 4
+#define VOLTA_BUF_LN_BETA 5
+#define VOLTA_BUF_DROPOUT_MASK 6
 int64_t volta_train_debug_buffer(VoltaTrainHandle* h, int32_t kind, int32_t layer, float* out);
 int32_t volta_train_get_state(VoltaTrainHandle* h, float* state, int64_t* step);
 int32_t volta_train_set_state(VoltaTrainHandle* h, const float* state, int64_t step);
+
+/* The dropout LCG state (the reference Handle's dropout_rng, seeded
+ * 12345678 at alloc, :553, and advanced once per hidden element per
+ * step, :777), for resuming a run with dropout.  Return 0, or -1. */
+int32_t volta_train_get_dropout_rng(VoltaTrainHandle* h, uint64_t* rng);
+int32_t volta_train_set_dropout_rng(VoltaTrainHandle* h, uint64_t rng);
 
 /* Change the optimizer hyperparameters of a live handle (the generated
  * library bakes them in, mlp_train_rust_codegen.rs:803-811, :957-993):

@@ -233,7 +233,7 @@ struct Net {
   }
 
   // Forward through the hidden layers and the output layer (:702-789).
-  void forward(const T* X) {
+  void forward(const T* X, bool train = true) {
     std::memcpy(act[0].data(), X, sizeof(T) * (size_t)B * L[0]);
     for (int i = 0; i < n; ++i) {
       const int r = L[i], c = L[i + 1];
@@ -247,7 +247,7 @@ struct Net {
         const size_t cnt = (size_t)B * c;
         for (size_t k = 0; k < cnt; ++k) a[k] = act_fwd<T>(spec.activation, dst[k]);
         if (spec.layernorm) layernorm_fwd(i);
-        if (spec.dropout_p > 0.0f) dropout_fwd(i);
+        if (train && spec.dropout_p > 0.0f) dropout_fwd(i);
       }
     }
   }
@@ -736,38 +736,43 @@ int32_t volta_train_batch(VoltaTrainHandle* vh) {
 
 }  // extern "C"
 
-// Optimizer state in the ABI's order: per layer [m_W | m_b | v_W | v_b]
-// (Adam/AdamW) or [G_W | G_b] (Adagrad).  Either precision; the fp64 twin
-// converts from/to float so it can be started from a float state.
+// Training state in the ABI's order: per layer [m_W | m_b | v_W | v_b]
+// (Adam/AdamW) or [G_W | G_b] (Adagrad), then, with LayerNorm, [gamma_i |
+// beta_i] per hidden layer.  Either precision; the fp64 twin converts
+// from/to float so it can be started from a float state.
 template <typename T>
-static std::vector<std::vector<T>*> state_buffers(Net<T>& f, int i) {
-  if (f.spec.optimizer == VOLTA_OPT_ADAM || f.spec.optimizer == VOLTA_OPT_ADAMW)
-    return {&f.mw[i], &f.mb[i], &f.vw[i], &f.vb[i]};
-  if (f.spec.optimizer == VOLTA_OPT_ADAGRAD) return {&f.gw[i], &f.gb[i]};
-  return {};
+static std::vector<std::vector<T>*> state_buffers(Net<T>& f) {
+  std::vector<std::vector<T>*> v;
+  for (int i = 0; i < f.n; ++i) {
+    if (f.spec.optimizer == VOLTA_OPT_ADAM || f.spec.optimizer == VOLTA_OPT_ADAMW) {
+      v.insert(v.end(), {&f.mw[i], &f.mb[i], &f.vw[i], &f.vb[i]});
+    } else if (f.spec.optimizer == VOLTA_OPT_ADAGRAD) {
+      v.insert(v.end(), {&f.gw[i], &f.gb[i]});
+    }
+  }
+  if (f.spec.layernorm)
+    for (int i = 0; i < f.n - 1; ++i) v.insert(v.end(), {&f.ln_g[i], &f.ln_b[i]});
+  return v;
 }
 
 template <typename T>
 static int64_t state_size(Net<T>& f) {
   int64_t total = 0;
-  for (int i = 0; i < f.n; ++i)
-    for (auto* v : state_buffers(f, i)) total += (int64_t)v->size();
+  for (auto* v : state_buffers(f)) total += (int64_t)v->size();
   return total;
 }
 
 template <typename T>
 static void state_get(Net<T>& f, float* p, int64_t* step) {
-  for (int i = 0; i < f.n; ++i)
-    for (auto* v : state_buffers(f, i))
-      for (size_t k = 0; k < v->size(); ++k) *p++ = (float)(*v)[k];
+  for (auto* v : state_buffers(f))
+    for (size_t k = 0; k < v->size(); ++k) *p++ = (float)(*v)[k];
   if (step) *step = (int64_t)f.adam_step;
 }
 
 template <typename T>
 static void state_set(Net<T>& f, const float* p, int64_t step) {
-  for (int i = 0; i < f.n; ++i)
-    for (auto* v : state_buffers(f, i))
-      for (size_t k = 0; k < v->size(); ++k) (*v)[k] = T(*p++);
+  for (auto* v : state_buffers(f))
+    for (size_t k = 0; k < v->size(); ++k) (*v)[k] = T(*p++);
   f.adam_step = (uint64_t)step;
 }
 
@@ -795,6 +800,21 @@ int32_t volta_train_set_state(VoltaTrainHandle* vh, const float* state, int64_t 
   return 0;
 }
 
+int32_t volta_train_get_dropout_rng(VoltaTrainHandle* vh, uint64_t* rng) {
+  Handle* h = H(vh);
+  if (!h || !rng) return -1;
+  *rng = h->precision == 64 ? h->d.dropout_rng : h->f.dropout_rng;
+  return 0;
+}
+
+int32_t volta_train_set_dropout_rng(VoltaTrainHandle* vh, uint64_t rng) {
+  Handle* h = H(vh);
+  if (!h) return -1;
+  h->d.dropout_rng = rng;
+  h->f.dropout_rng = rng;
+  return 0;
+}
+
 }  // extern "C"
 
 template <typename T>
@@ -810,6 +830,14 @@ static int64_t debug_buffer(Net<T>& f, int kind, int layer, float* out) {
     case VOLTA_BUF_DELTA: return layer >= 0 && layer < f.n ? copy_out(f.delta[layer], out) : -1;
     case VOLTA_BUF_GRAD_W: return layer >= 0 && layer < f.n ? copy_out(f.dw[layer], out) : -1;
     case VOLTA_BUF_GRAD_B: return layer >= 0 && layer < f.n ? copy_out(f.db[layer], out) : -1;
+    case VOLTA_BUF_LN_GAMMA:
+      return f.spec.layernorm && layer >= 0 && layer < f.n - 1 ? copy_out(f.ln_g[layer], out) : -1;
+    case VOLTA_BUF_LN_BETA:
+      return f.spec.layernorm && layer >= 0 && layer < f.n - 1 ? copy_out(f.ln_b[layer], out) : -1;
+    case VOLTA_BUF_DROPOUT_MASK:
+      if (!(f.spec.dropout_p > 0.0f) || layer < 0 || layer >= f.n - 1) return -1;
+      for (size_t k = 0; k < f.mask[layer].size(); ++k) out[k] = (float)f.mask[layer][k];
+      return (int64_t)f.mask[layer].size();
   }
   return -1;
 }
@@ -883,7 +911,7 @@ static void infer_rows(Net<T>& net, const float* X, int64_t rows, float* out) {
     const int64_t m = std::min<int64_t>(B, rows - r0);
     std::fill(xb.begin(), xb.end(), T(0));
     for (int64_t k = 0; k < m * L0; ++k) xb[(size_t)k] = (T)X[r0 * L0 + k];
-    net.forward(xb.data());
+    net.forward(xb.data(), false);  // inference: LayerNorm, no dropout
     for (int64_t k = 0; k < m * Ln; ++k) out[r0 * Ln + k] = (float)net.act[net.n][(size_t)k];
   }
 }

@@ -83,9 +83,8 @@ def test_resolution(src, want):
     ("model m\n    layers 4 8 2\ndataset d\ntrain m on d\n    optimizer rmsprop\n",
      "supports only SGD, Adam, AdamW, and Adagrad"),
     ("model m\n    layers 4 8 2\n    use block\n", "is MLP-only"),
-    ("model m\n    layers 4 8 2\n    layernorm yes\n", "layernorm is not supported"),
-    ("model m\n    layers 4 8 2\n    dropout 0.1\n", "dropout is not supported"),
-    ("model m\n    layers 4 8 2\ndataset d\ntrain m on d\n    clip_grad 1.0\n", "clip_grad is not supported"),
+    ("model m\n    layers 4 8 2\n    dropout 1.0\n", "model.dropout must be in [0, 1)"),
+    ("model m\n    layers 4 8 2\ndataset d\ntrain m on d\n    clip_grad 0\n", "clip_grad must be positive"),
     ("model m\n    layers 4 8 2\n    activation softmax\n", "softmax"),
     ("model m\n    layers 4 8 2\n    activation swish\n", "invalid value 'swish'"),
     ("model m\n    layers 4\n", "at least 2 values"),
@@ -102,6 +101,24 @@ def test_guards(src, msg):
     with pytest.raises(ValueError) as e:
         resolve(src)
     assert msg in str(e.value), str(e.value)
+
+
+@pytest.mark.parametrize("src,want", [
+    # model.dropout / model.layernorm (executor.rs:1930-1971)
+    ("model m\n    layers 4 8 2\n    dropout 0.25\n    layernorm yes\n", (0.0, 0.25, 1)),
+    ("model m\n    layers 4 8 2\n    layernorm no\n    dropout 0\n", (0.0, 0.0, 0)),
+    ("model m\n    layers 4 8 2\n    layernorm on\n", (0.0, 0.0, 1)),
+    # the last run of the model that sets clip_grad keeps it (executor.rs:1299)
+    ("model m\n    layers 4 8 2\ndataset d\ntrain m on d\n    clip_grad 2.5\ntrain m on d\n    epochs 1\n",
+     (2.5, 0.0, 0)),
+    ("model m\n    layers 4 8 2\nmodel k\n    layers 2 2\ndataset d\ntrain m on d\n    clip_grad 2.5\n"
+     "train m on d\n    clip_grad 0.5\ntrain k on d\n    clip_grad 9\n", (0.5, 0.0, 0)),
+])
+def test_codegen_extras(src, want):
+    spec, summary = resolve(src)
+    assert (round(spec.clip_grad, 6), round(spec.dropout_p, 6), spec.layernorm) == want
+    if want[2]:
+        assert "layernorm=yes" in summary
 
 
 def test_cli_check_and_compile_train(tmp_path):

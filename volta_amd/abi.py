@@ -139,6 +139,8 @@ _SIGNATURES = {
     "volta_train_state_size": (C.c_int64, [_P]),
     "volta_train_get_state": (C.c_int32, [_P, _F, C.POINTER(C.c_int64)]),
     "volta_train_set_state": (C.c_int32, [_P, _F, C.c_int64]),
+    "volta_train_get_dropout_rng": (C.c_int32, [_P, C.POINTER(C.c_uint64)]),
+    "volta_train_set_dropout_rng": (C.c_int32, [_P, C.c_uint64]),
     "volta_train_debug_buffer": (C.c_int64, [_P, C.c_int32, C.c_int32, _F]),
     "volta_train_set_hparams": (C.c_int32, [_P, C.c_float, C.c_float, C.c_float, C.c_float]),
     "volta_train_infer": (C.c_int32, [_P, _F, C.c_int64, _F]),
@@ -152,6 +154,7 @@ VT_SIGNATURES = {
 }
 
 BUF_ACT, BUF_DELTA, BUF_GRAD_W, BUF_GRAD_B = 0, 1, 2, 3
+BUF_LN_GAMMA, BUF_LN_BETA, BUF_DROPOUT_MASK = 4, 5, 6
 
 # Every symbol include/volta_train.h declares (checked by the CPU tests).
 HEADER_SYMBOLS = tuple(_SIGNATURES)
@@ -294,6 +297,16 @@ class Trainer:
         if self.lib.lib.volta_train_set_state(self.h, fptr(buf), step) != 0:
             raise RuntimeError(self.lib.last_error())
 
+    def get_dropout_rng(self) -> int:
+        v = C.c_uint64()
+        if self.lib.lib.volta_train_get_dropout_rng(self.h, C.byref(v)) != 0:
+            raise RuntimeError(self.lib.last_error())
+        return int(v.value)
+
+    def set_dropout_rng(self, rng: int) -> None:
+        if self.lib.lib.volta_train_set_dropout_rng(self.h, C.c_uint64(rng)) != 0:
+            raise RuntimeError(self.lib.last_error())
+
     def set_hparams(self, beta1: float, beta2: float, eps: float, weight_decay: float) -> None:
         if self.lib.lib.volta_train_set_hparams(self.h, beta1, beta2, eps, weight_decay) != 0:
             raise ValueError(self.lib.last_error())
@@ -314,7 +327,9 @@ class Trainer:
         sizes = self.spec.sizes
         B = self.batch
         count = {BUF_ACT: lambda i: B * sizes[i], BUF_DELTA: lambda i: B * sizes[i + 1],
-                 BUF_GRAD_W: lambda i: sizes[i] * sizes[i + 1], BUF_GRAD_B: lambda i: sizes[i + 1]}[kind](layer)
+                 BUF_GRAD_W: lambda i: sizes[i] * sizes[i + 1], BUF_GRAD_B: lambda i: sizes[i + 1],
+                 BUF_LN_GAMMA: lambda i: sizes[i + 1], BUF_LN_BETA: lambda i: sizes[i + 1],
+                 BUF_DROPOUT_MASK: lambda i: B * sizes[i + 1]}[kind](layer)
         out = np.zeros(count, np.float32)
         n = self.lib.lib.volta_train_debug_buffer(self.h, kind, layer, fptr(out))
         if n != count:

@@ -24,10 +24,10 @@ CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libvolta_hip.so")
 
-SOURCES = ["gemm.hip", "skinny.hip", "step_kernels.hip", "runtime.hip", "test_hooks.hip", "spec.cpp",
-           "vt_frontend.cpp"]
-HEADERS = ["gemm.h", "skinny.h", "step_kernels.h", "device_common.h", "recorder.h", "spec.h", "narrow_dw.h",
-           "vt_frontend.h"]
+SOURCES = ["gemm.hip", "skinny.hip", "step_kernels.hip", "extras.hip", "runtime.hip", "test_hooks.hip",
+           "spec.cpp", "vt_frontend.cpp"]
+HEADERS = ["gemm.h", "skinny.h", "step_kernels.h", "extras.h", "device_common.h", "recorder.h", "spec.h",
+           "narrow_dw.h", "vt_frontend.h"]
 CLI = os.path.join(PKG, "volta-hip")
 CLI_SOURCES = ["volta_hip_cli.cpp", "vt_frontend.cpp", "spec.cpp"]
 CXX = os.environ.get("CXX", "g++")

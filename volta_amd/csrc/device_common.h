@@ -22,7 +22,8 @@ struct DevScalars {
   uint32_t t;      // Adam step counter (incremented once per step on device)
   float loss;      // loss of the most recent step
   uint32_t flags;  // sticky VOLTA_STATUS_* bits raised on the device
-  uint32_t pad[2];
+  float clip_scale;  // gradient clipping: factor applied to the deltas of this step
+  uint64_t rng;      // dropout LCG state at the start of the step's forward
 };
 
 // Hidden activations, mlp_train_rust_codegen.rs:563-596 (forward) and

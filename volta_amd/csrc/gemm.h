@@ -97,6 +97,10 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus);
 hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& a, hipStream_t st, Recorder* rec = nullptr,
                        const char* label = "gemm", double bytes = 0.0);
 
+// b_i update (optimizer of EpiArgs: opt, b, bm, bv, bgrad, b1, b2, eps,
+// scalars) from db_i = the column sums of delta_i [B x N], b ascending.
+hipError_t launch_bias_update(const EpiArgs& e, const float* delta, int B, int N, hipStream_t st);
+
 // One operation of a paired launch (two independent operations of the
 // backward pass in one kernel launch: no buffer one writes is touched by the
 // other).

@@ -951,4 +951,22 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus) {
   return p;
 }
 
+// Bias update from db[n] = sum_b delta[b][n], b ascending (:931-933), for
+// steps whose dW launches run without the fused column sums (gradient
+// clipping forms db from the deltas before they are scaled, :936-955).
+__global__ void __launch_bounds__(256) bias_update_kernel(EpiArgs e, const float* __restrict__ delta, int B, int N) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  float db = 0.0f;
+  for (int b = 0; b < B; ++b) db = db + delta[(size_t)b * N + n];
+  apply_bias_update(e, n, N, db);
+}
+
+hipError_t launch_bias_update(const EpiArgs& e, const float* delta, int B, int N, hipStream_t st) {
+  if (!e.b || !e.scalars || !delta || B < 1 || N < 1) return hipErrorInvalidValue;
+  if (e.opt != VOLTA_OPT_SGD && (!e.bm || (e.opt == VOLTA_OPT_ADAM && !e.bv))) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(bias_update_kernel, dim3((N + 255) / 256), dim3(256), 0, st, e, delta, B, N);
+  return hipGetLastError();
+}
+
 }  // namespace volta

@@ -35,8 +35,8 @@ __device__ __forceinline__ void narrow_dw_block(const NarrowDwArgs& p, int block
     s1[k] = ok && !sgd ? p.m[idx] : 0.0f;
     s2[k] = ok && adam ? p.v[idx] : 0.0f;
   }
-  // bias state (block 0, threads k < N)
-  const bool bown = block == 0 && (int)threadIdx.x < N;
+  // bias state (block 0, threads k < N; no bias work when p.b is null)
+  const bool bown = block == 0 && (int)threadIdx.x < N && p.b;
   const float bw = bown ? p.b[threadIdx.x] : 0.0f;
   const float bs1 = bown && !sgd ? p.bm[threadIdx.x] : 0.0f;
   const float bs2 = bown && adam ? p.bv[threadIdx.x] : 0.0f;

@@ -34,6 +34,7 @@
 #include <string>
 #include <vector>
 
+#include "extras.h"
 #include "gemm.h"
 #include "skinny.h"
 #include "spec.h"
@@ -110,6 +111,16 @@ struct Handle {
   SegTable segs{};
   std::vector<LayerPlan> layers;
 
+  // --- codegen extras (spec.layernorm / dropout_p / clip_grad) --------------
+  bool ext_ln = false, ext_drop = false, ext_clip = false;
+  std::vector<float*> ln_g, ln_b;    // gamma, beta [L[i+1]] per hidden layer i < n-1
+  std::vector<float*> ln_mu, ln_is;  // row statistics [B]
+  std::vector<float*> ln_dg, ln_db;  // gradients [L[i+1]]
+  std::vector<uint8_t*> mask;        // dropout keep mask [B x L[i+1]]
+  float* clip_partials = nullptr;    // [kClipBlocks]
+  bool hidden_ext() const { return ext_ln || ext_drop; }
+  bool extras() const { return ext_ln || ext_drop || ext_clip; }
+
   // --- launch sequence -------------------------------------------------------
   bool use_graph = true;
   hipGraph_t graph = nullptr;
@@ -159,6 +170,31 @@ Handle::~Handle() {
       return false;                                         \
     }                                                       \
   } while (0)
+
+// LayerNorm / dropout of hidden layer i over `rows` rows of act_{i+1}
+// (training: statistics kept and dropout drawn; inference: LayerNorm only).
+static HiddenFwdArgs hidden_fwd_args(const Handle* h, int i, int rows, bool train) {
+  HiddenFwdArgs f{};
+  f.act = h->act[i + 1];
+  f.B = rows;
+  f.c = h->L[i + 1];
+  if (h->ext_ln) {
+    f.gamma = h->ln_g[i];
+    f.beta = h->ln_b[i];
+    f.mu = train ? h->ln_mu[i] : nullptr;
+    f.inv_std = train ? h->ln_is[i] : nullptr;
+  }
+  if (train && h->ext_drop) {
+    f.mask = h->mask[i];
+    f.p = h->spec.dropout_p;
+    f.keep_scale = 1.0f / (1.0f - h->spec.dropout_p);
+    uint64_t off = 0;
+    for (int k = 0; k < i; ++k) off += (uint64_t)h->B * h->L[k + 1];
+    f.rng_offset = off;
+  }
+  f.scalars = h->scalars;
+  return f;
+}
 
 // Enqueue one whole step on `st` (captured into the graph once).  With a
 // recorder attached, an event follows every kernel (profiling only).
@@ -231,6 +267,17 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
     const double bytes = 4.0 * ((double)B * lp.r + (double)lp.r * lp.c + (double)B * lp.c * (last ? 1 : 2)) +
                          (last && h->out_mode == OUT_GEMM_LOSS ? 8.0 * B * Ln : 0.0);
     VOLTA_CHECK(gemm_launch(lp.fwd, a, st, rec, label, bytes));
+    if (!last && h->hidden_ext()) {
+      VOLTA_CHECK(launch_hidden_fwd(hidden_fwd_args(h, i, B, true), st));
+      std::snprintf(label, sizeof label, "fwd%d.ln_dropout", i);
+      VOLTA_CHECK(mark(rec, label, 0.0, 4.0 * 3.0 * B * lp.c));
+      if (h->ext_drop && i == n - 2) {
+        uint64_t draws = 0;
+        for (int k = 0; k < n - 1; ++k) draws += (uint64_t)B * h->L[k + 1];
+        VOLTA_CHECK(launch_rng_advance(h->scalars, draws, st));
+        VOLTA_CHECK(mark(rec, "rng_advance", 0.0, 0.0));
+      }
+    }
   }
   if (h->out_mode == OUT_GEMM) {  // output layer wider than one tile: stand-alone loss head
     if (s.loss == VOLTA_LOSS_MSE)
@@ -372,6 +419,94 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
   char lx[32], ly[32];
   float* ws0 = h->gemm_ws;
   float* ws1 = h->gemm_ws ? h->gemm_ws + h->ws_half : nullptr;
+  if (h->extras()) {
+    // Codegen extras (:824-892, :936-955).  Phase 1, i = n-1 .. 0: the
+    // hidden layer's LayerNorm backward, dropout mask and f' (its dX ran
+    // with the identity derivative), b_i from db_i when clipping (db comes
+    // from the unscaled deltas), dX_i.  Then the clip scales every delta,
+    // and phase 2 runs dW_i (W_i only when clipping).  No paired launches:
+    // the clip needs every delta before the first dW.
+    const int dx_act = h->hidden_ext() ? kIdentity : s.activation;
+    for (int i = n - 1; i >= 0; --i) {
+      const LayerPlan& lp = h->layers[i];
+      if (i != n - 1 && h->hidden_ext()) {
+        HiddenBwdArgs a{};
+        a.delta = h->delta[i];
+        a.act = h->act[i + 1];
+        a.pre = h->pre[i];
+        a.B = B;
+        a.c = lp.c;
+        a.act_kind = s.activation;
+        if (h->ext_ln) {
+          a.gamma = h->ln_g[i];
+          a.beta = h->ln_b[i];
+          a.inv_std = h->ln_is[i];
+          a.dgamma = h->ln_dg[i];
+          a.dbeta = h->ln_db[i];
+        }
+        if (h->ext_drop) {
+          a.mask = h->mask[i];
+          a.keep_scale = 1.0f / (1.0f - s.dropout_p);
+        }
+        VOLTA_CHECK(launch_hidden_bwd(a, h->ext_ln ? h->ln_g[i] : nullptr, h->ext_ln ? h->ln_b[i] : nullptr,
+                                      h->scalars, st));
+        std::snprintf(lx, sizeof lx, "bwd%d.ln_dropout", i);
+        VOLTA_CHECK(mark(rec, lx, 0.0, 4.0 * 5.0 * B * lp.c));
+      }
+      if (h->ext_clip) {
+        EpiArgs e{};
+        e.opt = s.optimizer == VOLTA_OPT_ADAMW ? VOLTA_OPT_ADAM : s.optimizer;
+        e.b = h->params + lp.b_off;
+        e.bm = h->opt_a ? h->opt_a + lp.b_off : nullptr;
+        e.bv = h->opt_b ? h->opt_b + lp.b_off : nullptr;
+        e.bgrad = h->keep_grads ? h->grads + lp.b_off : nullptr;
+        e.b1 = s.beta1;
+        e.b2 = s.beta2;
+        e.eps = s.eps;
+        e.scalars = h->scalars;
+        VOLTA_CHECK(launch_bias_update(e, h->delta[i], B, lp.c, st));
+        std::snprintf(lx, sizeof lx, "db%d+opt", i);
+        VOLTA_CHECK(mark(rec, lx, (double)B * lp.c, 4.0 * B * lp.c));
+      }
+      if (i == 0) break;
+      std::snprintf(lx, sizeof lx, "dx%d", i);
+      if (i == n - 1 && h->narrow_dx) {
+        VOLTA_CHECK(launch_outer_dx(h->delta[i], h->params + lp.w_off, B, lp.r, lp.c, dx_act, h->act[i],
+                                    h->pre[i - 1], h->delta[i - 1], st));
+        VOLTA_CHECK(mark(rec, lx, dx_cost(i).first, dx_cost(i).second));
+      } else {
+        PairOp o = make_dx(i, ws0);
+        o.args.epi.act = dx_act;
+        if (!run_single(o, lx, dx_cost(i))) return false;
+      }
+    }
+    if (h->ext_clip) {
+      ClipArgs c{};
+      c.n = n;
+      for (int i = 0; i < n; ++i) {
+        c.delta[i] = h->delta[i];
+        c.count[i] = (int64_t)B * h->L[i + 1];
+      }
+      c.clip = s.clip_grad;
+      c.partials = h->clip_partials;
+      c.scalars = h->scalars;
+      VOLTA_CHECK(launch_clip(c, st));
+      double cnt = 0.0;
+      for (int i = 0; i < n; ++i) cnt += (double)B * h->L[i + 1];
+      VOLTA_CHECK(mark(rec, "clip", 3.0 * cnt, 12.0 * cnt));
+    }
+    for (int i = n - 1; i >= 0; --i) {
+      PairOp o = make_dw(i, ws0);
+      if (h->ext_clip) {
+        o.args.colsum_b = 0;
+        o.args.epi.b = nullptr;
+        o.nd.b = nullptr;
+      }
+      std::snprintf(lx, sizeof lx, h->ext_clip ? "dw%d+opt" : "dw%d+db+opt", i);
+      if (!run_single(o, lx, dw_cost(i))) return false;
+    }
+    return true;
+  }
   // dX_{n-1}
   if (n > 1) {
     const int i = n - 1;
@@ -461,6 +596,9 @@ static bool build(Handle* h) {
   VOLTA_CHECK(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
   const char* kg = std::getenv("VOLTA_KEEP_GRADS");
   h->keep_grads = kg && *kg && *kg != '0';
+  h->ext_ln = s.layernorm != 0 && n > 1;
+  h->ext_drop = s.dropout_p > 0.0f && n > 1;
+  h->ext_clip = s.clip_grad > 0.0f;
 
   // Flat parameter layout [W0 | b0 | W1 | b1 | ...], segments padded.
   h->layers.resize(n);
@@ -508,7 +646,7 @@ static bool build(Handle* h) {
   }
   h->n_counters = max_tiles + 1;  // last one: the loss head's tile counter
   const char* np = std::getenv("VOLTA_NO_PAIR");
-  h->pair_backward = !(np && *np && *np != '0');
+  h->pair_backward = !(np && *np && *np != '0') && !h->extras();
   ws_floats = align_up(ws_floats, 64);
   h->ws_half = ws_floats;
   ws_floats *= 2;
@@ -532,7 +670,27 @@ static bool build(Handle* h) {
   h->delta.assign(n, nullptr);
   for (int i = 0; i <= n; ++i) req((void**)&h->act[i], (size_t)B * h->L[i] * 4);
   for (int i = 0; i < n - 1; ++i)
-    if (act_needs_pre(s.activation)) req((void**)&h->pre[i], (size_t)B * h->L[i + 1] * 4);
+    if (act_needs_pre(s.activation) || h->hidden_ext()) req((void**)&h->pre[i], (size_t)B * h->L[i + 1] * 4);
+  h->ln_g.assign(n, nullptr);
+  h->ln_b.assign(n, nullptr);
+  h->ln_mu.assign(n, nullptr);
+  h->ln_is.assign(n, nullptr);
+  h->ln_dg.assign(n, nullptr);
+  h->ln_db.assign(n, nullptr);
+  h->mask.assign(n, nullptr);
+  for (int i = 0; i < n - 1; ++i) {
+    const size_t c = h->L[i + 1];
+    if (h->ext_ln) {
+      req((void**)&h->ln_g[i], c * 4);
+      req((void**)&h->ln_b[i], c * 4);
+      req((void**)&h->ln_mu[i], (size_t)B * 4);
+      req((void**)&h->ln_is[i], (size_t)B * 4);
+      req((void**)&h->ln_dg[i], c * 4);
+      req((void**)&h->ln_db[i], c * 4);
+    }
+    if (h->ext_drop) req((void**)&h->mask[i], (size_t)B * c);
+  }
+  if (h->ext_clip) req((void**)&h->clip_partials, kClipBlocks * 4);
   for (int i = 0; i < n; ++i) req((void**)&h->delta[i], (size_t)B * h->L[i + 1] * 4);
   req(&h->target, s.loss == VOLTA_LOSS_MSE ? (size_t)B * h->L[n] * 4 : (size_t)B * 4);
   if (ws_floats) req((void**)&h->gemm_ws, ws_floats * 4);
@@ -566,6 +724,12 @@ static bool build(Handle* h) {
     lcg_xavier_init(h->h_params + lp.w_off, (size_t)lp.r * lp.c, lp.r, lp.c, &rng);
   }
   VOLTA_CHECK(hipMemcpyAsync(h->params, h->h_params, (size_t)h->flat * 4, hipMemcpyHostToDevice, h->stream));
+  // Extras state: gamma = 1, beta = 0 (:660-668); dropout LCG seed (:553).
+  std::vector<float> ones(h->ext_ln ? (size_t)*std::max_element(h->L.begin(), h->L.end()) : 0, 1.0f);
+  const uint64_t seed = 12345678ULL;
+  for (int i = 0; i < n - 1 && h->ext_ln; ++i)
+    VOLTA_CHECK(hipMemcpyAsync(h->ln_g[i], ones.data(), (size_t)h->L[i + 1] * 4, hipMemcpyHostToDevice, h->stream));
+  VOLTA_CHECK(hipMemcpyAsync(&h->scalars->rng, &seed, sizeof seed, hipMemcpyHostToDevice, h->stream));
   VOLTA_CHECK(hipStreamSynchronize(h->stream));
 
   const char* ng = std::getenv("VOLTA_NO_GRAPH");
@@ -575,7 +739,8 @@ static bool build(Handle* h) {
 
 // Forward pass only for `rows` <= B rows already in h->infer_x: hidden
 // layers as in the step (bias + activation epilogue, or the split-K
-// reduction), the output layer with the identity; result in act[n].
+// reduction, then LayerNorm when the spec has it; dropout is a training-only
+// transform), the output layer with the identity; result in act[n].
 static bool enqueue_forward(Handle* h, int rows, hipStream_t st) {
   const volta_mlp_spec& s = h->spec;
   const int n = h->n;
@@ -616,6 +781,7 @@ static bool enqueue_forward(Handle* h, int rows, hipStream_t st) {
     a.epi.out = h->act[i + 1];
     a.epi.bias = h->params + lp.b_off;
     VOLTA_CHECK(gemm_launch(plans[i], a, st));
+    if (!last && h->ext_ln) VOLTA_CHECK(launch_hidden_fwd(hidden_fwd_args(h, i, rows, false), st));
   }
   return true;
 }
@@ -957,6 +1123,23 @@ int64_t volta_train_debug_buffer(VoltaTrainHandle* vh, int32_t kind, int32_t lay
       src = h->grads + h->layers[layer].b_off;
       count = (size_t)h->layers[layer].c;
       break;
+    case VOLTA_BUF_LN_GAMMA:
+    case VOLTA_BUF_LN_BETA:
+      if (layer < 0 || layer >= n - 1 || !h->ext_ln) return -1;
+      src = kind == VOLTA_BUF_LN_GAMMA ? h->ln_g[layer] : h->ln_b[layer];
+      count = (size_t)h->L[layer + 1];
+      break;
+    case VOLTA_BUF_DROPOUT_MASK: {
+      if (layer < 0 || layer >= n - 1 || !h->ext_drop) return -1;
+      count = (size_t)B * h->L[layer + 1];
+      std::vector<uint8_t> m(count);
+      if (!volta::sync(h) || hipMemcpy(m.data(), h->mask[layer], count, hipMemcpyDeviceToHost) != hipSuccess) {
+        h->status |= VOLTA_STATUS_DEVICE_ERROR;
+        return -1;
+      }
+      for (size_t k = 0; k < count; ++k) out[k] = (float)m[k];
+      return (int64_t)count;
+    }
     default:
       return -1;
   }
@@ -988,15 +1171,18 @@ int64_t volta_train_state_size(VoltaTrainHandle* vh) {
   if (!h) return -1;
   int64_t per = 0;
   for (auto& lp : h->layers) per += (int64_t)lp.r * lp.c + lp.c;
+  int64_t ln = 0;
+  for (int i = 0; i < h->n - 1 && h->ext_ln; ++i) ln += 2 * (int64_t)h->L[i + 1];
   switch (h->spec.optimizer) {
     case VOLTA_OPT_ADAM:
-    case VOLTA_OPT_ADAMW: return 2 * per;
-    case VOLTA_OPT_ADAGRAD: return per;
-    default: return 0;
+    case VOLTA_OPT_ADAMW: return 2 * per + ln;
+    case VOLTA_OPT_ADAGRAD: return per + ln;
+    default: return ln;
   }
 }
 
-// State order per layer: [m_W | m_b | v_W | v_b] (Adam/AdamW) or [G_W | G_b].
+// State order per layer: [m_W | m_b | v_W | v_b] (Adam/AdamW) or [G_W | G_b],
+// then [gamma_i | beta_i] per hidden layer with LayerNorm.
 static bool state_copy(Handle* h, float* host, bool to_host) {
   const bool adam = h->spec.optimizer == VOLTA_OPT_ADAM || h->spec.optimizer == VOLTA_OPT_ADAMW;
   std::vector<float*> bufs;
@@ -1018,6 +1204,16 @@ static bool state_copy(Handle* h, float* host, bool to_host) {
       p += nw + nb;
     }
   }
+  // LayerNorm [gamma_i | beta_i] per hidden layer
+  for (int i = 0; i < h->n - 1 && h->ext_ln; ++i) {
+    const size_t c = h->L[i + 1];
+    for (float* dev : {h->ln_g[i], h->ln_b[i]}) {
+      const hipError_t e = to_host ? hipMemcpy(p, dev, c * 4, hipMemcpyDeviceToHost)
+                                   : hipMemcpy(dev, p, c * 4, hipMemcpyHostToDevice);
+      if (e != hipSuccess) return false;
+      p += c;
+    }
+  }
   return true;
 }
 
@@ -1031,6 +1227,26 @@ int32_t volta_train_get_state(VoltaTrainHandle* vh, float* state, int64_t* step)
     return -1;
   }
   if (step) *step = t;
+  return 0;
+}
+
+int32_t volta_train_get_dropout_rng(VoltaTrainHandle* vh, uint64_t* rng) {
+  Handle* h = H(vh);
+  if (!h || !rng) return -1;
+  if (!volta::sync(h) || hipMemcpy(rng, &h->scalars->rng, sizeof(uint64_t), hipMemcpyDeviceToHost) != hipSuccess) {
+    h->status |= VOLTA_STATUS_DEVICE_ERROR;
+    return -1;
+  }
+  return 0;
+}
+
+int32_t volta_train_set_dropout_rng(VoltaTrainHandle* vh, uint64_t rng) {
+  Handle* h = H(vh);
+  if (!h) return -1;
+  if (!volta::sync(h) || hipMemcpy(&h->scalars->rng, &rng, sizeof(uint64_t), hipMemcpyHostToDevice) != hipSuccess) {
+    h->status |= VOLTA_STATUS_DEVICE_ERROR;
+    return -1;
+  }
   return 0;
 }
 

@@ -365,16 +365,16 @@ bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::st
       fail_at(p->line, p->col,
               "Model '" + model->name + "' uses template '" + sym_of(single(*p, "model.use"), "model.use") +
                   "'. `compile-train` is MLP-only and does not support function-backed/custom training graphs.");
+    // codegen extras of the model (executor.rs:1930-1971 -> :1839-1841)
+    double dropout = 0.0;
     if (const Property* p = find(mb, "dropout")) {
-      const double d = num_of(single(*p, "model.dropout"), "model.dropout");
-      if (!(d >= 0.0 && d < 1.0)) fail_at(p->line, p->col, "model.dropout must be in [0, 1)");
-      if (d > 0.0) fail_at(p->line, p->col, "model.dropout is not supported by this MI355X training library yet");
+      dropout = num_of(single(*p, "model.dropout"), "model.dropout");
+      if (!(dropout >= 0.0 && dropout < 1.0)) fail_at(p->line, p->col, "model.dropout must be in [0, 1)");
     }
+    bool layernorm = false;
     if (const Property* p = find(mb, "layernorm")) {
-      const Value& v = single(*p, "model.layernorm");
-      const std::string s = sym_of(v, "model.layernorm");
-      if (s == "yes" || s == "true" || s == "on")
-        fail_at(p->line, p->col, "model.layernorm is not supported by this MI355X training library yet");
+      const std::string s = sym_of(single(*p, "model.layernorm"), "model.layernorm");
+      layernorm = s == "yes" || s == "true" || s == "on";
     }
 
     // every train statement needs a declared model and an earlier dataset
@@ -437,10 +437,6 @@ bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::st
         out.batch = int_of(single(*p, "train.batch"), "train.batch");
         if (out.batch <= 0) fail_at(p->line, p->col, "train.batch must be > 0");
       }
-      if (const Property* p = find(tb, "clip_grad")) {
-        const double c = num_of(single(*p, "train.clip_grad"), "train.clip_grad");
-        if (c > 0.0) fail_at(p->line, p->col, "train.clip_grad is not supported by this MI355X training library yet");
-      }
       if (find(tb, "weight_decay"))
         notes.push_back("train.weight_decay shapes the interpreter's training only; the generated step "
                         "uses the compile-train constant (AdamW 0.01 on weights)");
@@ -452,6 +448,18 @@ bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::st
       out.trained = true;
     } else {
       optimizer = model_opt.empty() ? "sgd" : model_opt;
+    }
+    // gradient clipping: the last training run of the model that sets
+    // clip_grad (must be positive) leaves it in the model state
+    // (executor.rs:1299, :2370-2387)
+    double clip = 0.0;
+    for (const auto& s : stmts) {
+      if (s.kind != "train" || s.name != model->name) continue;
+      if (const Property* p = find(s.block, "clip_grad")) {
+        const double c = num_of(single(*p, "train.clip_grad"), "train.clip_grad");
+        if (!(c > 0.0)) fail_at(p->line, p->col, "train.clip_grad must be positive");
+        clip = c;
+      }
     }
     // compile-train --rust guard (executor.rs:3172-3189)
     if (!(optimizer == "sgd" || optimizer == "adam" || optimizer == "adamw" || optimizer == "adagrad"))
@@ -472,6 +480,9 @@ bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::st
                     : optimizer == "adamw" ? VOLTA_OPT_ADAMW
                                            : VOLTA_OPT_ADAGRAD;
     volta_mlp_spec_default(&out.spec, (int32_t)sizes.size(), sizes.data(), act, opt, VOLTA_LOSS_MSE);
+    out.spec.clip_grad = (float)clip;
+    out.spec.dropout_p = (float)dropout;
+    out.spec.layernorm = layernorm ? 1 : 0;
     std::string why;
     if (!validate_spec(out.spec, &why)) throw Fail{"model '" + model->name + "': " + why};
     out.model = model->name;
@@ -493,6 +504,15 @@ std::string vt_plan_summary(const VtTrainPlan& p) {
   std::snprintf(buf, sizeof buf, "model=%s layers=%s activation=%s optimizer=%s loss=mse", p.model.c_str(),
                 layers.c_str(), acts[p.spec.activation], opts[p.spec.optimizer]);
   std::string s = buf;
+  if (p.spec.clip_grad > 0.0f) {
+    std::snprintf(buf, sizeof buf, " clip_grad=%g", p.spec.clip_grad);
+    s += buf;
+  }
+  if (p.spec.dropout_p > 0.0f) {
+    std::snprintf(buf, sizeof buf, " dropout=%g", p.spec.dropout_p);
+    s += buf;
+  }
+  if (p.spec.layernorm) s += " layernorm=yes";
   if (p.trained) {
     std::snprintf(buf, sizeof buf, " lr=%g epochs=%lld batch=%lld", p.lr, (long long)p.epochs, (long long)p.batch);
     s += buf;
