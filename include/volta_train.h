@@ -91,7 +91,8 @@ enum volta_activation {
   VOLTA_ACT_TANH = 2,
   VOLTA_ACT_LEAKY_RELU = 3,
   VOLTA_ACT_SILU = 4,
-  VOLTA_ACT_GELU = 5 /* tanh approximation, :580-596 */
+  VOLTA_ACT_GELU = 5, /* tanh approximation, :580-596 */
+  VOLTA_ACT_SOFTMAX = 6 /* row softmax over each hidden layer's units, :727-740, :898-906 */
 };
 
 /* Optimizer; mlp_train_rust_codegen.rs:264-268. */

@@ -245,10 +245,33 @@ struct Net {
       if (!last) {
         T* a = act[i + 1].data();
         const size_t cnt = (size_t)B * c;
-        for (size_t k = 0; k < cnt; ++k) a[k] = act_fwd<T>(spec.activation, dst[k]);
+        if (spec.activation == VOLTA_ACT_SOFTMAX) softmax_fwd(dst, a, c);
+        else
+          for (size_t k = 0; k < cnt; ++k) a[k] = act_fwd<T>(spec.activation, dst[k]);
         if (spec.layernorm) layernorm_fwd(i);
         if (train && spec.dropout_p > 0.0f) dropout_fwd(i);
       }
+    }
+  }
+
+  // Softmax as the hidden activation (:727-740): per row, the first maximum
+  // (strict >, j ascending), e = exp(pre - max) summed in column order, then
+  // act = e * (1 / sum).
+  void softmax_fwd(const T* pre_i, T* a, int c) {
+    for (int bi = 0; bi < B; ++bi) {
+      const T* p = pre_i + (size_t)bi * c;
+      T* r = a + (size_t)bi * c;
+      T mx = p[0];
+      for (int j = 1; j < c; ++j)
+        if (p[j] > mx) mx = p[j];
+      T sum = T(0);
+      for (int j = 0; j < c; ++j) {
+        const T e = std::exp(p[j] - mx);
+        r[j] = e;
+        sum = sum + e;
+      }
+      const T inv = T(1) / sum;
+      for (int j = 0; j < c; ++j) r[j] = r[j] * inv;
     }
   }
 
@@ -448,7 +471,18 @@ struct Net {
         }
         const T* p = pre[i].data();
         const T* y = act[i + 1].data();
-        for (size_t k = 0; k < cnt; ++k) d[k] = d[k] * act_bwd<T>(act_kind, p[k], y[k]);
+        if (act_kind == VOLTA_ACT_SOFTMAX) {
+          // dx = y * (upstream - dot(upstream, y)) per row, y = act_{i+1}
+          // (the LayerNorm/dropout output when those are on) (:898-906)
+          for (int bi = 0; bi < B; ++bi) {
+            const size_t base = (size_t)bi * c;
+            T dot = T(0);
+            for (int j = 0; j < c; ++j) dot = dot + d[base + j] * y[base + j];
+            for (int j = 0; j < c; ++j) d[base + j] = y[base + j] * (d[base + j] - dot);
+          }
+        } else {
+          for (size_t k = 0; k < cnt; ++k) d[k] = d[k] * act_bwd<T>(act_kind, p[k], y[k]);
+        }
       }
       if (i > 0) {
         // delta_{i-1} = delta_i · W_i^T, computed as (W_i · delta_i^T)^T in the

@@ -151,7 +151,19 @@ CASES = [
                                     clip_grad=-1.0), 64, 0.02),
     ("all_tanh_adamw_ce", MlpSpec([64, 200, 120, 30], "tanh", "adamw", "ce", layernorm=True, dropout_p=0.15,
                                   clip_grad=-1.0), 96, 1e-3),
+    # softmax as the hidden activation (a row operation, :727-740, :898-906)
+    ("softmax_sgd", MlpSpec([16, 64, 48, 4], "softmax", "sgd"), 32, 0.5),
+    ("softmax_adam_ce", MlpSpec([32, 96, 80, 24], "softmax", "adam", "ce"), 64, 1e-3),
+    ("softmax_drop_clip_adagrad", MlpSpec([24, 130, 70, 100], "softmax", "adagrad", dropout_p=0.2,
+                                          clip_grad=-1.0), 48, 1e-2),
+    ("softmax_ln_sgd", MlpSpec([20, 64, 10], "softmax", "sgd", layernorm=True), 32, 0.05),
+    ("softmax_all_adam", MlpSpec([32, 96, 12], "softmax", "adam", layernorm=True, dropout_p=0.1, clip_grad=-1.0),
+     64, 1e-3),
 ]
+# (LayerNorm over the outputs of a softmax divides by their small spread, so
+# its backward multiplies deltas by 1/sigma, ~50 per layer here; with two such
+# layers the fp32 oracle itself leaves the tolerance of its fp64 twin, so the
+# combined softmax cases use one hidden layer.)
 
 
 def resolve(spec, B, seed):
@@ -221,11 +233,11 @@ def test_extras_state_resume_matches_uninterrupted_run():
         t.close()
 
 
-@pytest.mark.parametrize("rows", [1, 37, 200])
-def test_infer_with_layernorm_matches_oracle(rows):
-    """Inference applies LayerNorm with the trained gamma/beta and no
-    dropout (and leaves the dropout stream untouched)."""
-    spec = MlpSpec([24, 64, 48, 6], "relu", "adam", layernorm=True, dropout_p=0.2)
+@pytest.mark.parametrize("act,rows", [("relu", 1), ("relu", 37), ("relu", 200), ("softmax", 45)])
+def test_infer_with_layernorm_matches_oracle(act, rows):
+    """Inference applies the activation and LayerNorm with the trained
+    gamma/beta and no dropout (and leaves the dropout stream untouched)."""
+    spec = MlpSpec([24, 64, 48, 6], act, "adam", layernorm=True, dropout_p=0.2)
     B = 32
     say(f"extras infer rows={rows}: {spec.text()}")
     outs = []

@@ -196,7 +196,7 @@ def test_ce_uniform_logits_closed_form(oracle):
     t.close()
 
 
-@pytest.mark.parametrize("act", ["relu", "sigmoid", "tanh", "leaky_relu", "silu", "gelu"])
+@pytest.mark.parametrize("act", ["relu", "sigmoid", "tanh", "leaky_relu", "silu", "gelu", "softmax"])
 @pytest.mark.parametrize("loss", ["mse", "ce"])
 def test_f64_gradient_matches_finite_differences(oracle, act, loss):
     """Gradient recovered from one SGD step (lr=1) of the fp64 twin equals the
@@ -518,6 +518,32 @@ def test_oracle_dropout_mask_follows_the_lcg_stream(oracle):
         a2 = t.debug_buffer(BUF_ACT, 2).reshape(B, 9)
         assert (a2[~k2.reshape(B, 9)] == 0).all()
     t.close()
+
+
+def test_oracle_softmax_forward_closed_form(oracle):
+    """Softmax as the hidden activation (:727-740): each row of act_1 is
+    exp(pre - max) / sum, rows sum to 1, and the fp32 oracle agrees with the
+    float64 closed form to fp32 rounding."""
+    spec = MlpSpec([6, 9, 3], "softmax", "sgd")
+    B = 5
+    rng = np.random.default_rng(8)
+    X = (rng.standard_normal((B, 6)) * 3).astype(np.float32)
+    from volta_amd.abi import BUF_ACT
+    ws = [rng.uniform(-0.8, 0.8, (r, c)).astype(np.float32) for r, c in spec.shapes()]
+    bs = [rng.uniform(-0.3, 0.3, c).astype(np.float32) for _, c in spec.shapes()]
+    # (the debug buffer hands out float32 copies, so the twin is compared to
+    # float32 rounding too)
+    for f64, rtol in ((True, 1.2e-7), (False, 1e-6)):
+        t = oracle_trainer(oracle, spec, B, f64=f64)
+        t.set_all_params(ws, bs)
+        t.step(X, np.zeros((B, 3), np.float32), 0.0)
+        pre = X.astype(np.float64) @ ws[0].astype(np.float64) + bs[0]
+        e = np.exp(pre - pre.max(axis=1, keepdims=True))
+        want = e / e.sum(axis=1, keepdims=True)
+        got = t.debug_buffer(BUF_ACT, 1).reshape(B, 9)
+        np.testing.assert_allclose(got, want, rtol=rtol, atol=1e-12)
+        np.testing.assert_allclose(got.sum(axis=1), 1.0, atol=1e-6)
+        t.close()
 
 
 def test_oracle_layernorm_forward_closed_form(oracle):

@@ -71,6 +71,7 @@ def test_headline_source():
     ("width 16  # a variable\nmodel m  # comment\n    layers 4 width 2\n    activation leakyrelu\n"
      "    seed -3\ndataset d\n    source \"x.csv\"\ntrain m on d\n    optimizer sgd\n",
      ([4, 16, 2], "leaky_relu", "sgd")),
+    ("model m\n    layers 4 8 2\n    activation softmax\n", ([4, 8, 2], "softmax", "sgd")),
     # the first model is the one compiled
     ("model a\n    layers 3 5 1\n    activation gelu\nmodel b\n    layers 9 9 9\n", ([3, 5, 1], "gelu", "sgd")),
 ])
@@ -85,7 +86,6 @@ def test_resolution(src, want):
     ("model m\n    layers 4 8 2\n    use block\n", "is MLP-only"),
     ("model m\n    layers 4 8 2\n    dropout 1.0\n", "model.dropout must be in [0, 1)"),
     ("model m\n    layers 4 8 2\ndataset d\ntrain m on d\n    clip_grad 0\n", "clip_grad must be positive"),
-    ("model m\n    layers 4 8 2\n    activation softmax\n", "softmax"),
     ("model m\n    layers 4 8 2\n    activation swish\n", "invalid value 'swish'"),
     ("model m\n    layers 4\n", "at least 2 values"),
     ("model m\n    layers 4 0 2\n", "must be > 0"),

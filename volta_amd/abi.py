@@ -25,7 +25,7 @@ import numpy as np
 
 MAX_LAYER_SIZES = 17
 
-ACTIVATIONS = {"relu": 0, "sigmoid": 1, "tanh": 2, "leaky_relu": 3, "silu": 4, "gelu": 5}
+ACTIVATIONS = {"relu": 0, "sigmoid": 1, "tanh": 2, "leaky_relu": 3, "silu": 4, "gelu": 5, "softmax": 6}
 OPTIMIZERS = {"sgd": 0, "adam": 1, "adamw": 2, "adagrad": 3}
 LOSSES = {"mse": 0, "ce": 1}
 

@@ -9,10 +9,13 @@
 
 namespace volta {
 
-// One hidden layer's forward extras on act [B x c] (after the activation).
+// One hidden layer's forward extras on act [B x c] (after the activation;
+// with `softmax` act holds the pre-activation and the row softmax comes
+// first).
 struct HiddenFwdArgs {
   float* act;            // [B x c], updated in place
   int B, c;
+  int softmax;           // 1: act = softmax(act) per row first
   const float* gamma;    // LayerNorm (null: off)
   const float* beta;
   float* mu;             // [B] per-row statistics kept for the backward
@@ -25,7 +28,7 @@ struct HiddenFwdArgs {
 
 // One hidden layer's backward extras on delta [B x c] (gradient w.r.t. the
 // layer's final output): LayerNorm backward, dropout mask, activation
-// derivative, in that order.
+// derivative (softmax: the row form y * (d - dot(d, y))), in that order.
 struct HiddenBwdArgs {
   float* delta;          // [B x c], updated in place
   const float* act;      // layer output (after LayerNorm / dropout)

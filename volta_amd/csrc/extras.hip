@@ -1,4 +1,5 @@
 // Codegen extras of the generated step, in the reference's arithmetic order:
+//   softmax as the hidden activation (:727-740, :898-906);
 //   LayerNorm after each hidden activation (:745-772) and its backward with
 //   the SGD update of gamma/beta (:829-887);
 //   inverted dropout with masks from the reference's LCG (:774-788,
@@ -38,9 +39,32 @@ __device__ __forceinline__ uint64_t lcg_jump(uint64_t s, uint64_t m) {
 }
 
 __global__ void __launch_bounds__(256) hidden_fwd_kernel(HiddenFwdArgs a) {
-  __shared__ float stat[2];
+  __shared__ float stat[4];
   const int b = blockIdx.x, c = a.c;
   float* row = a.act + (size_t)b * c;
+  if (a.softmax) {
+    // :727-740: first maximum (strict >), exp(pre - max), sum in column
+    // order, times 1/sum
+    if (threadIdx.x == 0) {
+      float mx = row[0];
+      for (int j = 1; j < c; ++j)
+        if (row[j] > mx) mx = row[j];
+      stat[2] = mx;
+    }
+    __syncthreads();
+    const float mx = stat[2];
+    for (int j = threadIdx.x; j < c; j += blockDim.x) row[j] = expf(row[j] - mx);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float sum = 0.0f;
+      for (int j = 0; j < c; ++j) sum = sum + row[j];
+      stat[3] = 1.0f / sum;
+    }
+    __syncthreads();
+    const float inv = stat[3];
+    for (int j = threadIdx.x; j < c; j += blockDim.x) row[j] = row[j] * inv;
+    __syncthreads();
+  }
   float mu = 0.0f, is = 0.0f;
   if (a.gamma) {
     if (threadIdx.x == 0) {
@@ -107,7 +131,7 @@ __global__ void __launch_bounds__(256) ln_bwd_cols_kernel(HiddenBwdArgs a) {
 // derivative takes the pre-activation (the output is no longer relu(pre));
 // sigmoid/tanh take the layer output as the reference does.
 __global__ void __launch_bounds__(256) hidden_bwd_rows_kernel(HiddenBwdArgs a) {
-  __shared__ float stat[2];
+  __shared__ float stat[3];
   const int b = blockIdx.x, c = a.c;
   float* d = a.delta + (size_t)b * c;
   const float* y = a.act + (size_t)b * c;
@@ -140,9 +164,23 @@ __global__ void __launch_bounds__(256) hidden_bwd_rows_kernel(HiddenBwdArgs a) {
       x = is * (d_xhat - sum_d - xh * sum_dxh);
     }
     if (a.mask) x = x * ((float)a.mask[(size_t)b * c + j] * a.keep_scale);
-    const float p = pre[j];
-    x = x * act_derivative(a.act_kind, p, a.act_kind == VOLTA_ACT_RELU ? p : y[j]);
+    if (a.act_kind != VOLTA_ACT_SOFTMAX) {
+      const float p = pre[j];
+      x = x * act_derivative(a.act_kind, p, a.act_kind == VOLTA_ACT_RELU ? p : y[j]);
+    }
     d[j] = x;
+  }
+  if (a.act_kind == VOLTA_ACT_SOFTMAX) {
+    // :898-906: dot(d, y) in column order, then d = y * (d - dot)
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float dot = 0.0f;
+      for (int j = 0; j < c; ++j) dot = dot + d[j] * y[j];
+      stat[2] = dot;
+    }
+    __syncthreads();
+    const float dot = stat[2];
+    for (int j = threadIdx.x; j < c; j += blockDim.x) d[j] = y[j] * (d[j] - dot);
   }
 }
 
@@ -207,7 +245,7 @@ __global__ void __launch_bounds__(256) clip_apply_kernel(ClipArgs a) {
 }  // namespace
 
 hipError_t launch_hidden_fwd(const HiddenFwdArgs& a, hipStream_t st) {
-  if (!a.gamma && !a.mask) return hipSuccess;
+  if (!a.gamma && !a.mask && !a.softmax) return hipSuccess;
   hipLaunchKernelGGL(hidden_fwd_kernel, dim3(a.B), dim3(256), 0, st, a);
   return hipGetLastError();
 }

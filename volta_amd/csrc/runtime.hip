@@ -113,13 +113,16 @@ struct Handle {
 
   // --- codegen extras (spec.layernorm / dropout_p / clip_grad) --------------
   bool ext_ln = false, ext_drop = false, ext_clip = false;
+  bool ext_softmax = false;          // softmax hidden activation (a row operation)
   std::vector<float*> ln_g, ln_b;    // gamma, beta [L[i+1]] per hidden layer i < n-1
   std::vector<float*> ln_mu, ln_is;  // row statistics [B]
   std::vector<float*> ln_dg, ln_db;  // gradients [L[i+1]]
   std::vector<uint8_t*> mask;        // dropout keep mask [B x L[i+1]]
   float* clip_partials = nullptr;    // [kClipBlocks]
-  bool hidden_ext() const { return ext_ln || ext_drop; }
-  bool extras() const { return ext_ln || ext_drop || ext_clip; }
+  bool hidden_ext() const { return ext_ln || ext_drop || ext_softmax; }
+  bool extras() const { return hidden_ext() || ext_clip; }
+  // activation of the hidden layers' GEMM epilogue (softmax runs after it)
+  int gemm_act() const { return ext_softmax ? kIdentity : spec.activation; }
 
   // --- launch sequence -------------------------------------------------------
   bool use_graph = true;
@@ -178,6 +181,7 @@ static HiddenFwdArgs hidden_fwd_args(const Handle* h, int i, int rows, bool trai
   f.act = h->act[i + 1];
   f.B = rows;
   f.c = h->L[i + 1];
+  f.softmax = h->ext_softmax ? 1 : 0;
   if (h->ext_ln) {
     f.gamma = h->ln_g[i];
     f.beta = h->ln_b[i];
@@ -246,7 +250,7 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
     a.N = lp.c;
     a.K = lp.r;
     a.epi.kind = last && h->out_mode == OUT_GEMM_LOSS ? EPI_LOSS : EPI_BIAS_ACT;
-    a.epi.act = last ? kIdentity : s.activation;
+    a.epi.act = last ? kIdentity : h->gemm_act();
     a.epi.ldc = lp.c;
     a.epi.out = h->act[i + 1];
     a.epi.pre = last ? nullptr : h->pre[i];
@@ -599,6 +603,7 @@ static bool build(Handle* h) {
   h->ext_ln = s.layernorm != 0 && n > 1;
   h->ext_drop = s.dropout_p > 0.0f && n > 1;
   h->ext_clip = s.clip_grad > 0.0f;
+  h->ext_softmax = s.activation == VOLTA_ACT_SOFTMAX && n > 1;
 
   // Flat parameter layout [W0 | b0 | W1 | b1 | ...], segments padded.
   h->layers.resize(n);
@@ -776,12 +781,13 @@ static bool enqueue_forward(Handle* h, int rows, hipStream_t st) {
     a.N = lp.c;
     a.K = lp.r;
     a.epi.kind = EPI_BIAS_ACT;
-    a.epi.act = last ? kIdentity : s.activation;
+    a.epi.act = last ? kIdentity : h->gemm_act();
     a.epi.ldc = lp.c;
     a.epi.out = h->act[i + 1];
     a.epi.bias = h->params + lp.b_off;
     VOLTA_CHECK(gemm_launch(plans[i], a, st));
-    if (!last && h->ext_ln) VOLTA_CHECK(launch_hidden_fwd(hidden_fwd_args(h, i, rows, false), st));
+    if (!last && (h->ext_ln || h->ext_softmax))
+      VOLTA_CHECK(launch_hidden_fwd(hidden_fwd_args(h, i, rows, false), st));
   }
   return true;
 }

@@ -30,6 +30,7 @@ const char* activation_name(int a) {
     case VOLTA_ACT_LEAKY_RELU: return "leaky_relu";
     case VOLTA_ACT_SILU: return "silu";
     case VOLTA_ACT_GELU: return "gelu";
+    case VOLTA_ACT_SOFTMAX: return "softmax";
     default: return "?";
   }
 }
@@ -57,7 +58,7 @@ bool validate_spec(const volta_mlp_spec& s, std::string* why) {
   for (int i = 0; i + 1 < s.n_sizes; ++i)
     if ((int64_t)s.sizes[i] * s.sizes[i + 1] >= ((int64_t)1 << 30))
       return fail("layer " + std::to_string(i) + " has 2^30 or more weights");
-  if (s.activation < VOLTA_ACT_RELU || s.activation > VOLTA_ACT_GELU)
+  if (s.activation < VOLTA_ACT_RELU || s.activation > VOLTA_ACT_SOFTMAX)
     return fail("unknown activation");
   if (s.optimizer < VOLTA_OPT_SGD || s.optimizer > VOLTA_OPT_ADAGRAD)
     return fail("unknown optimizer");
@@ -150,6 +151,7 @@ extern "C" int32_t volta_mlp_spec_parse(const char* text, volta_mlp_spec* spec) 
     else if (a == "leaky_relu" || a == "leakyrelu") act = VOLTA_ACT_LEAKY_RELU;
     else if (a == "silu") act = VOLTA_ACT_SILU;
     else if (a == "gelu") act = VOLTA_ACT_GELU;
+    else if (a == "softmax") act = VOLTA_ACT_SOFTMAX;
     else {
       set_last_error("unknown activation '" + a + "'");
       return -1;

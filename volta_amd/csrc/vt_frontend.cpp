@@ -466,14 +466,13 @@ bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::st
       throw Fail{"Model '" + model->name + "' requests optimizer '" + optimizer +
                  "', but `compile-train --rust` supports only SGD, Adam, AdamW, and Adagrad today. "
                  "Use runtime `train` for RMSProp or other optimizers."};
-    if (activation == "softmax")
-      throw Fail{"activation softmax (as a hidden activation) is not supported by this MI355X training library yet"};
 
     const int act = activation == "relu" ? VOLTA_ACT_RELU
                     : activation == "sigmoid" ? VOLTA_ACT_SIGMOID
                     : activation == "tanh" ? VOLTA_ACT_TANH
                     : (activation == "leaky_relu" || activation == "leakyrelu") ? VOLTA_ACT_LEAKY_RELU
                     : activation == "silu" ? VOLTA_ACT_SILU
+                    : activation == "softmax" ? VOLTA_ACT_SOFTMAX
                                            : VOLTA_ACT_GELU;
     const int opt = optimizer == "sgd" ? VOLTA_OPT_SGD
                     : optimizer == "adam" ? VOLTA_OPT_ADAM
@@ -496,7 +495,7 @@ bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::st
 }
 
 std::string vt_plan_summary(const VtTrainPlan& p) {
-  static const char* acts[] = {"relu", "sigmoid", "tanh", "leaky_relu", "silu", "gelu"};
+  static const char* acts[] = {"relu", "sigmoid", "tanh", "leaky_relu", "silu", "gelu", "softmax"};
   static const char* opts[] = {"sgd", "adam", "adamw", "adagrad"};
   std::string layers;
   for (int i = 0; i < p.spec.n_sizes; ++i) layers += (i ? "-" : "") + std::to_string(p.spec.sizes[i]);
