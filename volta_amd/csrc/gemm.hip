@@ -413,6 +413,50 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& args, int bx, int by, 
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
+  // MFMAs of one BK-deep stage held in LDS.  Fragments are double-buffered
+  // in registers: those of group g + 1 are read from LDS before the MFMAs of
+  // group g are issued, so the LDS latency hides behind the matrix work.
+  auto compute_stage = [&](const float* a_s, const float* b_s) {
+    floatx4 fa_n[T::TM], fb_n[T::TN];
+#pragma unroll
+    for (int i = 0; i < T::TM; ++i) fa_n[i] = load_frag<BM, BK, A_KC>(a_s, wm * WM + i * 32 + l32, h, 0);
+#pragma unroll
+    for (int j = 0; j < T::TN; ++j) fb_n[j] = load_frag<BN, BK, B_KC>(b_s, wn * WN + j * 32 + l32, h, 0);
+#pragma unroll
+    for (int g = 0; g < BK / 8; ++g) {
+      floatx4 fa[T::TM], fb[T::TN];
+#pragma unroll
+      for (int i = 0; i < T::TM; ++i) fa[i] = fa_n[i];
+#pragma unroll
+      for (int j = 0; j < T::TN; ++j) fb[j] = fb_n[j];
+      if (g + 1 < BK / 8) {
+#pragma unroll
+        for (int i = 0; i < T::TM; ++i)
+          fa_n[i] = load_frag<BM, BK, A_KC>(a_s, wm * WM + i * 32 + l32, h, g + 1);
+#pragma unroll
+        for (int j = 0; j < T::TN; ++j)
+          fb_n[j] = load_frag<BN, BK, B_KC>(b_s, wn * WN + j * 32 + l32, h, g + 1);
+      }
+      // keep the scheduler from sinking those reads below the MFMAs
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+          for (int j = 0; j < T::TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (kColsum && colsum) {
+        // rows beyond kend were loaded as zeros; adding them changes nothing
+#pragma unroll
+        for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+          for (int s = 0; s < 4; ++s) cs[j] = cs[j] + fb[j][s];
+      }
+    }
+  };
+
   if (kbeg < kend) {
     la.load(args.A, args.lda, M, kend, m0, kbeg, tid);
     lb.load(args.B, args.ldb, N, kend, n0, kbeg, tid);
@@ -427,49 +471,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& args, int bx, int by, 
         la.load(args.A, args.lda, M, kend, m0, k0 + BK, tid);
         lb.load(args.B, args.ldb, N, kend, n0, k0 + BK, tid);
       }
-      const float* a_s = lds_a(buf);
-      const float* b_s = lds_b(buf);
-      // Fragments are double-buffered in registers: those of group g + 1
-      // are read from LDS before the MFMAs of group g are issued, so the LDS
-      // latency hides behind the matrix work.
-      floatx4 fa_n[T::TM], fb_n[T::TN];
-#pragma unroll
-      for (int i = 0; i < T::TM; ++i) fa_n[i] = load_frag<BM, BK, A_KC>(a_s, wm * WM + i * 32 + l32, h, 0);
-#pragma unroll
-      for (int j = 0; j < T::TN; ++j) fb_n[j] = load_frag<BN, BK, B_KC>(b_s, wn * WN + j * 32 + l32, h, 0);
-#pragma unroll
-      for (int g = 0; g < BK / 8; ++g) {
-        floatx4 fa[T::TM], fb[T::TN];
-#pragma unroll
-        for (int i = 0; i < T::TM; ++i) fa[i] = fa_n[i];
-#pragma unroll
-        for (int j = 0; j < T::TN; ++j) fb[j] = fb_n[j];
-        if (g + 1 < BK / 8) {
-#pragma unroll
-          for (int i = 0; i < T::TM; ++i)
-            fa_n[i] = load_frag<BM, BK, A_KC>(a_s, wm * WM + i * 32 + l32, h, g + 1);
-#pragma unroll
-          for (int j = 0; j < T::TN; ++j)
-            fb_n[j] = load_frag<BN, BK, B_KC>(b_s, wn * WN + j * 32 + l32, h, g + 1);
-        }
-        // keep the scheduler from sinking those reads below the MFMAs
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-#pragma unroll
-          for (int i = 0; i < T::TM; ++i)
-#pragma unroll
-            for (int j = 0; j < T::TN; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
-        if (kColsum && colsum) {
-          // rows beyond kend were loaded as zeros; adding them changes nothing
-#pragma unroll
-          for (int j = 0; j < T::TN; ++j)
-#pragma unroll
-            for (int s = 0; s < 4; ++s) cs[j] = cs[j] + fb[j][s];
-        }
-      }
+      compute_stage(lds_a(buf), lds_b(buf));
       if (more) {
         la.store(lds_a(buf ^ 1), tid);
         lb.store(lds_b(buf ^ 1), tid);
@@ -895,6 +897,7 @@ hipError_t pair_launch(const PairOp& a, const PairOp& b, hipStream_t st, Recorde
   GemmArgs aa = a.args, bb = b.args;
   aa.k_per_split = a.plan.k_per_split;
   bb.k_per_split = b.plan.k_per_split;
+
   hipError_t err;
   if (a.kind == PAIR_GEMM && a.plan.layout == GEMM_NT) {
     err = b.kind == PAIR_GEMM ? launch_pair_t<DxOp, DwOp>(aa, na, bb, nb, st) : launch_with_narrow<DxOp>(aa, na, b, st);

@@ -17,6 +17,8 @@
 //   dX_{n-1}                    outer product (L_n <= 16) or GEMM NT
 //   dX_i | dW_{i+1}             one paired launch, i = n-2 .. 1
 //   dW_1 | dW_0                 one paired launch
+// With LayerNorm, dropout, softmax hidden activations or gradient clipping
+// the backward runs unpaired (enqueue_step's extras branch).
 // dX_i: GEMM NT with epilogue * f'(layer i-1) -> delta_{i-1}.  dW_i: GEMM TN
 // whose epilogue applies SGD/Adam/AdamW/Adagrad to W_i, and to b_i from the
 // column sums of delta_i (db_i) the same kernel forms.  dX_i reads W_i before
