@@ -614,7 +614,7 @@ gemm_f32_mfma(GemmArgs args) {
 }
 
 // Planes whose loads splitk_reduce issues together (more planes: a loop).
-constexpr int kReduceUnroll = 8;
+constexpr int kReduceUnroll = 16;
 
 // Second kernel of a split-K launch: add the planes in slice order, then the
 // epilogue (and, for dW, the bias update from the summed column sums kept in
@@ -935,8 +935,11 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus) {
   if (p.tile == TILE_64x64 && sb && std::atoi(sb) == 64) p.tile = TILE_64x64_K64;
   const int tiles = p.tiles(M, N);
   const int bk = p.tile == TILE_64x64_K64 ? 64 : 32;
+  // Smallest K slice: 64 for the forward products (their reduction is the
+  // bias/activation epilogue, read back by one latency-bound launch), 128
+  // for dX/dW, whose launches are paired and already hold enough workgroups.
   const char* mk = std::getenv("VOLTA_SPLITK_MIN_K");
-  const int min_k = mk && *mk ? std::max(32, std::atoi(mk)) : 128;
+  const int min_k = mk && *mk ? std::max(32, std::atoi(mk)) : (layout == GEMM_NN ? 64 : 128);
   const char* ik = std::getenv("VOLTA_SPLITK_INKERNEL");
   p.inkernel_reduce = ik && *ik && *ik != '0';
   const char* sw = std::getenv("VOLTA_SPLITK_WGS_PER_CU");
