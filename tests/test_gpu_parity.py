@@ -149,6 +149,44 @@ def test_optimizer_kernel_bit_exact(kind, wd, count):
     np.testing.assert_array_equal(dw.numpy(), w)
 
 
+@pytest.mark.parametrize("b1,b2,t", [(0.9, 0.999, 1), (0.9, 0.999, 3), (0.9, 0.999, 164), (0.9, 0.999, 165),
+                                     (0.9, 0.999, 4000), (0.9, 0.999, 17000), (0.5, 0.99, 2), (0.95, 0.9999, 40)])
+def test_adam_bias_correction_division_bit_exact(b1, b2, t):
+    """Adam's m/bc1 and v/bc2 on the GPU go through a double reciprocal
+    (div_by_const); with moments and gradients over the whole fp32 exponent
+    range (subnormal to near overflow, signed zeros) the update is still the
+    oracle's IEEE fp32 arithmetic bit for bit."""
+    import ctypes as C
+
+    say(f"adam division b1={b1} b2={b2} t={t}")
+    hip, orc = load_hip(), load_oracle()
+    count = 1 << 16
+    rng = np.random.default_rng(t)
+    def wide(scale_lo, scale_hi):
+        mag = np.float32(2.0) ** rng.uniform(scale_lo, scale_hi, count).astype(np.float32)
+        return (np.where(rng.random(count) < 0.5, -1, 1) * mag).astype(np.float32)
+    w = rng.standard_normal(count).astype(np.float32)
+    m = wide(-149, 100)
+    v = np.abs(wide(-149, 100))
+    g = wide(-149, 60)
+    m[:16] = 0.0
+    m[16:32] = -0.0
+    g[:8] = 0.0
+    lr, eps = 1e-3, 1e-8
+    bc1 = float(np.float32(1) - np.float32(b1) ** np.float32(t))
+    bc2 = float(np.float32(1) - np.float32(b2) ** np.float32(t))
+    dw, dm, dv, dg = (DeviceArray(x.copy()) for x in (w, m, v, g))
+    assert hip.lib.volta_hip_optimizer(1, dw.ptr, dm.ptr, dv.ptr, dg.ptr, count, lr, bc1, bc2, b1, b2, eps,
+                                       0.01) == 0, hip.lib.last_error()
+    F = C.POINTER(C.c_float)
+    p = lambda a: a.ctypes.data_as(F)  # noqa: E731
+    orc.lib.volta_oracle_adam(p(w), p(m), p(v), p(g), count, b1, b2, bc1, bc2, lr, eps, 0.01)
+    for got, want in ((dw.numpy(), w), (dm.numpy(), m), (dv.numpy(), v)):
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got), nan)
+        np.testing.assert_array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
 # ---------------------------------------------------------------------------
 # Whole step: torch-float64 goldens (tiny reference fixture + small MLPs)
 # ---------------------------------------------------------------------------

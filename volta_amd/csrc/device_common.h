@@ -79,19 +79,35 @@ __host__ __device__ inline bool act_needs_pre(int act) {
   return act == VOLTA_ACT_LEAKY_RELU || act == VOLTA_ACT_SILU || act == VOLTA_ACT_GELU;
 }
 
+// x / c for a per-step constant c, as (float)((double)x * rc) with
+// rc = 1.0 / (double)c: the correctly rounded fp32 quotient for every x.  For
+// fp32 x and c the exact quotient is never a midpoint between two fp32
+// numbers and lies at least 2^-49 (relative) from every midpoint, while the
+// double product is within about 2^-52 of it, so both round to the same
+// float (likewise for subnormal, zero, infinite and NaN x).  A third of the
+// cost of the fp32 division sequence.
+__device__ __forceinline__ float div_by_const(float x, double rc) { return (float)((double)x * rc); }
+
+// Reciprocals of Adam's two bias corrections for div_by_const (once per thread).
+struct AdamRcp {
+  double r1, r2;
+};
+__device__ __forceinline__ AdamRcp adam_rcp(float bc1, float bc2) { return {1.0 / (double)bc1, 1.0 / (double)bc2}; }
+
 // One Adam/AdamW element update (adam_update_slice,
 // mlp_train_rust_codegen.rs:341-388).  `tail` marks the last (n mod 8)
 // elements of a buffer, which the reference updates in its scalar loop with
-// v = b2*v + ((1-b2)*g)*g instead of (1-b2)*(g*g).
+// v = b2*v + ((1-b2)*g)*g instead of (1-b2)*(g*g).  mhat = m/bc1 and
+// vhat = v/bc2 are the reference's fp32 quotients (div_by_const).
 __device__ __forceinline__ void adam_elem(float* w, float* m, float* v, float g, bool tail, float lr,
-                                          float bc1, float bc2, float b1, float b2, float eps, float wd) {
+                                          AdamRcp rc, float b1, float b2, float eps, float wd) {
   const float m1 = b1 * *m + (1.0f - b1) * g;
   const float v1 = tail ? b2 * *v + (1.0f - b2) * g * g : b2 * *v + (1.0f - b2) * (g * g);
   *m = m1;
   *v = v1;
   const float w0 = *w;
-  const float mhat = m1 / bc1;
-  const float vhat = v1 / bc2;
+  const float mhat = div_by_const(m1, rc.r1);
+  const float vhat = div_by_const(v1, rc.r2);
   const float denom = sqrtf(vhat) + eps;
   *w = w0 - lr * (mhat / denom + wd * w0);
 }

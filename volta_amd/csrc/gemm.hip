@@ -145,7 +145,7 @@ __device__ __forceinline__ floatx4 load_frag(const float* lds, int row, int h, i
 // Element epilogues (called once per output element m < M, n < N).
 // ---------------------------------------------------------------------------
 template <int EPI>
-__device__ __forceinline__ void apply_epilogue(const EpiArgs& e, int m, int n, float acc) {
+__device__ __forceinline__ void apply_epilogue(const EpiArgs& e, int m, int n, float acc, AdamRcp rc = {}) {
   const size_t idx = (size_t)m * e.ldc + n;
   switch (EPI) {
     case EPI_STORE:
@@ -176,7 +176,7 @@ __device__ __forceinline__ void apply_epilogue(const EpiArgs& e, int m, int n, f
         adagrad_elem(e.out + idx, e.m + idx, acc, lr, e.eps);
       } else {
         const bool tail = (int64_t)idx >= e.count - e.count % 8;
-        adam_elem(e.out + idx, e.m + idx, e.v + idx, acc, tail, lr, e.scalars->bc1, e.scalars->bc2, e.b1,
+        adam_elem(e.out + idx, e.m + idx, e.v + idx, acc, tail, lr, rc, e.b1,
                   e.b2, e.eps, e.wd);
       }
       break;
@@ -247,11 +247,11 @@ __device__ __forceinline__ void block_epilogue(const EpiArgs& e, const floatx16&
 #pragma unroll
       for (int v = 0; v < 16; ++v) adagrad_elem(&w[v], &s1[v], acc[v], lr, e.eps);
     } else {
-      const float bc1 = e.scalars->bc1, bc2 = e.scalars->bc2;
+      const AdamRcp rc = adam_rcp(e.scalars->bc1, e.scalars->bc2);
       const uint32_t vec_end = (uint32_t)(e.count - e.count % 8);
 #pragma unroll
       for (int v = 0; v < 16; ++v)
-        adam_elem(&w[v], &s1[v], &s2[v], acc[v], off(v) >= vec_end, lr, bc1, bc2, e.b1, e.b2, e.eps, e.wd);
+        adam_elem(&w[v], &s1[v], &s2[v], acc[v], off(v) >= vec_end, lr, rc, e.b1, e.b2, e.eps, e.wd);
     }
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
@@ -271,9 +271,14 @@ __device__ __forceinline__ void block_epilogue(const EpiArgs& e, const floatx16&
   }
 }
 
+// Adam's bias-correction reciprocals when the epilogue runs Adam/AdamW.
+__device__ __forceinline__ AdamRcp adam_rcp_of(const EpiArgs& e) {
+  return e.opt == VOLTA_OPT_ADAM || e.opt == VOLTA_OPT_ADAMW ? adam_rcp(e.scalars->bc1, e.scalars->bc2) : AdamRcp{};
+}
+
 // Bias update from the fused column sum db_i[n] (:931-933, :957-993).  The
 // generated step never decays biases (:966).
-__device__ __forceinline__ void apply_bias_update(const EpiArgs& e, int n, int N, float db) {
+__device__ __forceinline__ void apply_bias_update(const EpiArgs& e, int n, int N, float db, AdamRcp rc) {
   if (e.bgrad) e.bgrad[n] = db;
   const float lr = e.scalars->lr;
   if (e.opt == VOLTA_OPT_SGD) {
@@ -282,7 +287,7 @@ __device__ __forceinline__ void apply_bias_update(const EpiArgs& e, int n, int N
     adagrad_elem(e.b + n, e.bm + n, db, lr, e.eps);
   } else {
     const bool tail = n >= N - N % 8;
-    adam_elem(e.b + n, e.bm + n, e.bv + n, db, tail, lr, e.scalars->bc1, e.scalars->bc2, e.b1, e.b2, e.eps,
+    adam_elem(e.b + n, e.bm + n, e.bv + n, db, tail, lr, rc, e.b1, e.b2, e.eps,
               0.0f);
   }
 }
@@ -593,10 +598,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& args, int bx, int by, 
       }
     if constexpr (kColsum) {
       if (cs_owner && e.b) {
+        const AdamRcp rc = adam_rcp_of(e);
 #pragma unroll
         for (int j = 0; j < T::TN; ++j) {
           const int n = n0 + wn * WN + j * 32 + l32;
-          if (n < N) apply_bias_update(e, n, N, cs[j]);
+          if (n < N) apply_bias_update(e, n, N, cs[j], rc);
         }
       }
     }
@@ -629,6 +635,8 @@ __global__ void __launch_bounds__(256) splitk_reduce(GemmArgs a, int splits) {
   const size_t extra = EPI == EPI_DW_OPT && a.colsum_b ? (size_t)N : 0;
   const size_t items = (total + extra) / W;  // W divides N
   const EpiArgs& e = a.epi;
+  AdamRcp rc{};
+  if constexpr (EPI == EPI_DW_OPT) rc = adam_rcp_of(e);
   for (size_t it = (size_t)blockIdx.x * blockDim.x + threadIdx.x; it < items;
        it += (size_t)gridDim.x * blockDim.x) {
     const size_t idx = it * W;
@@ -687,11 +695,11 @@ __global__ void __launch_bounds__(256) splitk_reduce(GemmArgs a, int splits) {
         for (int q = 0; q < W; ++q) e.out[o + q] = s[q] * act_derivative(e.act, pr[q], y[q]);
       } else {
 #pragma unroll
-        for (int q = 0; q < W; ++q) apply_epilogue<EPI>(e, m, n + q, s[q]);
+        for (int q = 0; q < W; ++q) apply_epilogue<EPI>(e, m, n + q, s[q], rc);
       }
     } else if constexpr (EPI == EPI_DW_OPT) {
 #pragma unroll
-      for (int q = 0; q < W; ++q) apply_bias_update(e, (int)(idx + q - total), N, s[q]);
+      for (int q = 0; q < W; ++q) apply_bias_update(e, (int)(idx + q - total), N, s[q], rc);
     }
   }
 }
@@ -965,7 +973,7 @@ __global__ void __launch_bounds__(256) bias_update_kernel(EpiArgs e, const float
   if (n >= N) return;
   float db = 0.0f;
   for (int b = 0; b < B; ++b) db = db + delta[(size_t)b * N + n];
-  apply_bias_update(e, n, N, db);
+  apply_bias_update(e, n, N, db, adam_rcp_of(e));
 }
 
 hipError_t launch_bias_update(const EpiArgs& e, const float* delta, int B, int N, hipStream_t st) {

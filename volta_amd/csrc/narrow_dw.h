@@ -25,7 +25,7 @@ __device__ __forceinline__ void narrow_dw_block(const NarrowDwArgs& p, int block
   const bool own = j < R;
   const bool sgd = p.opt == VOLTA_OPT_SGD, adam = p.opt == VOLTA_OPT_ADAM;
   const float lr = p.scalars->lr;
-  const float bc1 = p.scalars->bc1, bc2 = p.scalars->bc2;
+  const AdamRcp rc = adam_rcp(p.scalars->bc1, p.scalars->bc2);
   float w[NMAX], s1[NMAX], s2[NMAX];
 #pragma unroll
   for (int k = 0; k < NMAX; ++k) {
@@ -76,7 +76,7 @@ __device__ __forceinline__ void narrow_dw_block(const NarrowDwArgs& p, int block
       } else if (p.opt == VOLTA_OPT_ADAGRAD) {
         adagrad_elem(&w[k], &s1[k], acc[k], lr, p.eps);
       } else {
-        adam_elem(&w[k], &s1[k], &s2[k], acc[k], idx >= vec_end, lr, bc1, bc2, p.b1, p.b2, p.eps, p.wd);
+        adam_elem(&w[k], &s1[k], &s2[k], acc[k], idx >= vec_end, lr, rc, p.b1, p.b2, p.eps, p.wd);
       }
     }
 #pragma unroll
@@ -100,7 +100,7 @@ __device__ __forceinline__ void narrow_dw_block(const NarrowDwArgs& p, int block
     } else if (p.opt == VOLTA_OPT_ADAGRAD) {
       adagrad_elem(&x, &y1, db, lr, p.eps);
     } else {
-      adam_elem(&x, &y1, &y2, db, k >= N - N % 8, lr, bc1, bc2, p.b1, p.b2, p.eps, 0.0f);
+      adam_elem(&x, &y1, &y2, db, k >= N - N % 8, lr, rc, p.b1, p.b2, p.eps, 0.0f);
     }
     p.b[k] = x;
     if (!sgd) p.bm[k] = y1;

@@ -98,7 +98,8 @@ adam_kernel(float* __restrict__ w, float* __restrict__ m, float* __restrict__ v,
             float b1, float b2, float eps) {
   const int64_t base = (int64_t)blockIdx.x * kSegAlign;
   const int s = find_segment(segs, base);
-  const float lr = sc->lr, bc1 = sc->bc1, bc2 = sc->bc2;
+  const float lr = sc->lr;
+  const AdamRcp rc = adam_rcp(sc->bc1, sc->bc2);
   const float wd = segs.wd[s];
   const int64_t count = segs.count[s];
   const int64_t vec_end = count - count % 8;
@@ -106,7 +107,7 @@ adam_kernel(float* __restrict__ w, float* __restrict__ m, float* __restrict__ v,
     const int64_t local = base - segs.off[s] + e;
     if (local >= count) continue;
     const int64_t k = base + e;
-    adam_elem(w + k, m + k, v + k, g[k], local >= vec_end, lr, bc1, bc2, b1, b2, eps, wd);
+    adam_elem(w + k, m + k, v + k, g[k], local >= vec_end, lr, rc, b1, b2, eps, wd);
   }
 }
 
