@@ -88,11 +88,23 @@ __host__ __device__ inline bool act_needs_pre(int act) {
 // cost of the fp32 division sequence.
 __device__ __forceinline__ float div_by_const(float x, double rc) { return (float)((double)x * rc); }
 
-// Reciprocals of Adam's two bias corrections for div_by_const (once per thread).
+// A double every lane of the wave holds alike, moved to scalar registers so
+// it costs no vector registers where it is kept (readfirstlane of each half).
+__device__ __forceinline__ double wave_uniform(double x) {
+  const uint64_t b = (uint64_t)__double_as_longlong(x);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// Reciprocals of Adam's two bias corrections for div_by_const (once per
+// thread).  bc1 and bc2 are per-step scalars, the same in every lane.
 struct AdamRcp {
   double r1, r2;
 };
-__device__ __forceinline__ AdamRcp adam_rcp(float bc1, float bc2) { return {1.0 / (double)bc1, 1.0 / (double)bc2}; }
+__device__ __forceinline__ AdamRcp adam_rcp(float bc1, float bc2) {
+  return {wave_uniform(1.0 / (double)bc1), wave_uniform(1.0 / (double)bc2)};
+}
 
 // One Adam/AdamW element update (adam_update_slice,
 // mlp_train_rust_codegen.rs:341-388).  `tail` marks the last (n mod 8)

@@ -610,7 +610,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& args, int bx, int by, 
 }
 
 template <int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, bool VEC, int EPI, bool INK>
-__global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
+// Two waves per SIMD at least (at most 256 vector + accumulation registers
+// a lane): the 128x128 dW tile with an Adam epilogue otherwise settles a
+// few registers above that and runs at half occupancy.
+__global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_f32_mfma(GemmArgs args) {
   __shared__ __attribute__((aligned(16))) float lds_a[2 * LdsTile<BM, BK, A_KC>::kFloats];
   __shared__ __attribute__((aligned(16))) float lds_b[2 * LdsTile<BN, BK, B_KC>::kFloats];
@@ -823,7 +826,7 @@ struct PairLds {
 };
 
 template <class OA, class OB>
-__global__ void __launch_bounds__(256) pair_kernel(typename OA::Args a, typename OB::Args b, int na) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) pair_kernel(typename OA::Args a, typename OB::Args b, int na) {
   __shared__ __attribute__((aligned(16))) float lds[PairLds<OA, OB>::kFloats];
   if ((int)blockIdx.x < na) OA::run(a, blockIdx.x, lds);
   else OB::run(b, blockIdx.x - na, lds);
