@@ -80,13 +80,20 @@ GEMM_SHAPES = [
 ]
 
 
+TILE_SMALLM = 3
+
+
 @pytest.mark.parametrize("layout", [0, 1, 2], ids=["NN", "NT", "TN"])
 @pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
-@pytest.mark.parametrize("tile", [0, 1])
+@pytest.mark.parametrize("tile", [0, 1, TILE_SMALLM])
 def test_gemm_integer_exact(layout, M, N, K, tile):
     """Integer operands: the MFMA result must be exact (any order is exact
-    below 2^24), which pins operand indexing, the lane layout of the 32x32x2
-    MFMA and the bounds handling."""
+    below 2^24), which pins operand indexing, the lane layouts of the
+    32x32x2 and 16x16x4 MFMAs, the small-M tile's per-wave K ranges and
+    wave-order reduction, and the bounds handling (K=3 and K=257 take the
+    scalar-load path of the small-M tile)."""
+    if tile == TILE_SMALLM and layout == 2:
+        pytest.skip("the small-M tile serves the NN and NT products only")
     say(f"gemm layout={layout} M={M} N={N} K={K} tile={tile}")
     rng = np.random.default_rng(M * 7 + N * 13 + K)
     a_shape = (K, M) if layout == 2 else (M, K)
@@ -98,6 +105,32 @@ def test_gemm_integer_exact(layout, M, N, K, tile):
     Bm = B.T if layout == 1 else B
     want = (Am.astype(np.int64) @ Bm.astype(np.int64)).astype(np.float32)
     np.testing.assert_array_equal(got, want)
+
+
+def test_gemm_smallm_rejects_tn():
+    """The small-M tile has no TN form: the launch is refused on the host."""
+    lib = load_hip()
+    A = np.ones((64, 32), np.float32)
+    B = np.ones((64, 48), np.float32)
+    dA, dB = DeviceArray(A), DeviceArray(B)
+    dC = DeviceArray(np.zeros((32, 48), np.float32))
+    assert lib.lib.volta_hip_gemm(2, dA.ptr, dB.ptr, dC.ptr, 32, 48, 64, TILE_SMALLM, 0) != 0
+
+
+@pytest.mark.parametrize("layout", [0, 1], ids=["NN", "NT"])
+@pytest.mark.parametrize("M,N,K", [(64, 1024, 1024), (64, 512, 2048), (128, 256, 512), (48, 80, 1000)])
+def test_gemm_smallm_float_bound(layout, M, N, K):
+    """Random fp32 operands on the small-M tile: within the fp32 error bound
+    of a K-term sum of the fp64 product."""
+    say(f"gemm small-M float layout={layout} M={M} N={N} K={K}")
+    rng = np.random.default_rng(M + N + K + layout)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((N, K) if layout == 1 else (K, N)).astype(np.float32)
+    got = _gemm(layout, A, B, M, N, K, tile=TILE_SMALLM)
+    Bm = (B.T if layout == 1 else B).astype(np.float64)
+    want = A.astype(np.float64) @ Bm
+    bound = 2 * K * np.finfo(np.float32).eps * (np.abs(A).astype(np.float64) @ np.abs(Bm))
+    assert np.all(np.abs(got - want) <= bound)
 
 
 @pytest.mark.parametrize("splits", [2, 3, 8])
@@ -254,6 +287,32 @@ def test_sgd_config_parity_with_oracle(name):
     assert st == 0, f"status {st}"
     ok, mx, _ = close_enough(lh, lo)
     assert ok, f"{name}: losses differ, max abs {mx:.3e}\n hip={lh}\n ora={lo}"
+    assert_params_close(wh, bh, wo, bo, name)
+
+
+@pytest.mark.parametrize("name", ["c1_mlp256_relu_sgd_b64", "c4_silu_sgd_b128"])
+@pytest.mark.parametrize("small_m", ["0", "128"], ids=["splitk64", "smallm"])
+def test_sgd_config_both_small_batch_plans(name, small_m):
+    """The B <= 128 products run on the small-M tile by default; with
+    VOLTA_SMALLM_MAX_M=0 they take the 64x64 split-K tiles and reduce
+    launches instead.  Both plans stay within rel 1e-4 / abs 1e-5 of the
+    oracle over the whole trajectory."""
+    spec, B, lr, steps = CONFIGS[name]
+    say(f"config {name} VOLTA_SMALLM_MAX_M={small_m}")
+    old = os.environ.get("VOLTA_SMALLM_MAX_M")
+    os.environ["VOLTA_SMALLM_MAX_M"] = small_m
+    try:
+        ws, bs, batches = config_inputs(spec, B)
+        lh, wh, bh, st = run_steps(load_hip(), spec, B, ws, bs, batches, lr, steps)
+    finally:
+        if old is None:
+            os.environ.pop("VOLTA_SMALLM_MAX_M", None)
+        else:
+            os.environ["VOLTA_SMALLM_MAX_M"] = old
+    lo, wo, bo, _ = run_steps(load_oracle(), spec, B, ws, bs, batches, lr, steps)
+    assert st == 0, f"status {st}"
+    ok, mx, _ = close_enough(lh, lo)
+    assert ok, f"{name}: losses differ, max abs {mx:.3e}"
     assert_params_close(wh, bh, wo, bo, name)
 
 

@@ -622,6 +622,151 @@ gemm_f32_mfma(GemmArgs args) {
                                                           lds_small);
 }
 
+// ---------------------------------------------------------------------------
+// Small-M tile (M up to a few 16-row tiles: the B=64 forward and dX
+// products).  One workgroup of 4 waves owns a 16x16 output tile over the
+// whole K range.  Wave w takes the w-th quarter of K (rounded up to 16),
+// loads its operands straight into registers (nothing is shared between the
+// waves, so no LDS staging and no barrier in the K loop) and accumulates them
+// on v_mfma_f32_16x16x4f32; the four partial tiles are then added in wave
+// order through LDS and the epilogue runs one element per thread.  K never
+// leaves the workgroup -- no split-K workspace and no second launch -- while
+// the grid (M/16 x N/16 tiles) still spreads over the CUs.
+//
+// v_mfma_f32_16x16x4f32 (one block): lane l supplies A(l%16, k) and
+// B(k, l%16) for its k, and register v of lane l receives D(4*(l/16) + v, l%16).
+// Within a group of 16 k values starting at kb, MFMA s (0..3) takes
+// k = kb + 4q + s in lane quarter q = l/16, so a lane's four A operands of a
+// group are four consecutive k of one row (one 16-byte load); likewise the
+// B operands of the NT product (dX: rows of W_i).  Group g accumulates into
+// accumulator g % 4 (chains of a quarter of the wave's terms), and the four
+// accumulators, then the four waves' tiles, are added as pairwise trees:
+// a fixed order, with shorter rounding chains than one running sum.
+// ---------------------------------------------------------------------------
+constexpr int kSmallWaves = 4;
+constexpr int kSmallChunk = 8;     // 16-k groups per register chunk (128 k)
+constexpr int kSmallRedStride = 80;  // LDS floats per (wave, register) row of partials
+constexpr int kSmallLds = kSmallWaves * 4 * kSmallRedStride;
+
+// Tile order: workgroups are handed to the 8 XCDs round-robin by index, and
+// every XCD has its own L2.  The tiles that read the same columns of B (one
+// strip of W_i; for the NN product two strips share each 128-byte line) are
+// given indices of one residue mod 8, so that strip is fetched into one L2.
+template <int SW>
+__device__ __forceinline__ void smallm_coords(int blk, int tiles_m, int tiles_n, int& tm, int& tn) {
+  if (tiles_n % (8 * SW) == 0) {
+    const int xcd = blk & 7, j = blk >> 3;
+    const int per = tiles_m * SW;
+    const int grp = j / per, loc = j % per;
+    tm = loc / SW;
+    tn = (grp * 8 + xcd) * SW + loc % SW;
+  } else {
+    tm = blk % tiles_m;
+    tn = blk / tiles_m;
+  }
+}
+
+template <bool B_KC, bool VEC, int EPI>
+__device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float* lds) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int M = args.M, N = args.N, K = args.K;
+  const int tiles_m = (M + 15) / 16, tiles_n = (N + 15) / 16;
+  int tm, tn;
+  smallm_coords<B_KC ? 1 : 2>(blk, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * 16, n0 = tn * 16;
+  // this wave's K range: quarters rounded up to whole 16-k groups
+  const int kq = (K + 4 * 16 - 1) / (4 * 16) * 16;
+  const int kbeg = wave * kq, kend = min(K, kbeg + kq);
+  const bool row_ok = m0 + r < M, col_ok = n0 + r < N;
+  const int lda = args.lda, ldb = args.ldb;
+  // lane's base pointers: A row m0+r at k offset 4q; B row n0+r (NT) or
+  // column n0+r (NN)
+  const float* pa = args.A + (size_t)(row_ok ? m0 + r : 0) * lda + 4 * q;
+  const float* pb = B_KC ? args.B + (size_t)(col_ok ? n0 + r : 0) * ldb + 4 * q : args.B + (col_ok ? n0 + r : 0);
+
+  auto load = [&](floatx4(&fa)[kSmallChunk], floatx4(&fb)[kSmallChunk], int kc) {
+#pragma unroll
+    for (int g = 0; g < kSmallChunk; ++g) {
+      const int kb = kc + 16 * g;
+      const int k = kb + 4 * q;  // this lane's first k of the group
+      floatx4 x = {0.f, 0.f, 0.f, 0.f}, y = {0.f, 0.f, 0.f, 0.f};
+      if (VEC) {  // K % 4 == 0 and every range bound is a multiple of 4
+        if (k < kend) {
+          if (row_ok) x = *reinterpret_cast<const floatx4*>(pa + kb);
+          if (col_ok) {
+            if (B_KC) {
+              y = *reinterpret_cast<const floatx4*>(pb + kb);
+            } else {
+#pragma unroll
+              for (int s = 0; s < 4; ++s) y[s] = pb[(size_t)(k + s) * ldb];
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          if (k + s < kend) {
+            if (row_ok) x[s] = pa[kb + s];
+            if (col_ok) y[s] = B_KC ? pb[kb + s] : pb[(size_t)(k + s) * ldb];
+          }
+      }
+      fa[g] = x;
+      fb[g] = y;
+    }
+  };
+  floatx4 acc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+  static_assert(kSmallChunk % 4 == 0, "a chunk must hold whole rounds of the four accumulators");
+  auto compute = [&](const floatx4(&fa)[kSmallChunk], const floatx4(&fb)[kSmallChunk], int kc) {
+#pragma unroll
+    for (int g = 0; g < kSmallChunk; ++g) {
+      if (kc + 16 * g < kend) {  // wave-uniform
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          acc[g & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[g][s], fb[g][s], acc[g & 3], 0, 0, 0);
+      }
+    }
+  };
+  // Two register chunks: the next chunk's loads are in flight while the
+  // current one's MFMAs run.
+  floatx4 fa0[kSmallChunk], fb0[kSmallChunk], fa1[kSmallChunk], fb1[kSmallChunk];
+  constexpr int kStep = 16 * kSmallChunk;
+  int kc = kbeg;
+  if (kc < kend) load(fa0, fb0, kc);
+  while (kc < kend) {
+    if (kc + kStep < kend) load(fa1, fb1, kc + kStep);
+    compute(fa0, fb0, kc);
+    kc += kStep;
+    if (kc >= kend) break;
+    if (kc + kStep < kend) load(fa0, fb0, kc + kStep);
+    compute(fa1, fb1, kc);
+    kc += kStep;
+  }
+
+  // Partial tiles to LDS: row (wave, v) holds register v of every lane.
+#pragma unroll
+  for (int v = 0; v < 4; ++v)
+    lds[(wave * 4 + v) * kSmallRedStride + lane] = (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]);
+  __syncthreads();
+  // Element (i, j) of the tile: lane 16*(i/4) + j, register i%4 of each
+  // wave; the waves' values added as (w0 + w1) + (w2 + w3).
+  static_assert(kSmallWaves == 4, "the wave tree below adds four tiles");
+  const int i = tid >> 4, j = tid & 15;
+  const int src = (i & 3) * kSmallRedStride + 16 * (i >> 2) + j;
+  constexpr int kW = 4 * kSmallRedStride;
+  const float sum = (lds[src] + lds[kW + src]) + (lds[2 * kW + src] + lds[3 * kW + src]);
+  const int m = m0 + i, n = n0 + j;
+  if (m < M && n < N) apply_epilogue<EPI>(args.epi, m, n, sum);
+}
+
+template <bool B_KC, bool VEC, int EPI>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) gemm_smallm(GemmArgs args) {
+  __shared__ float lds[kSmallLds];
+  smallm_tile<B_KC, VEC, EPI>(args, blockIdx.x, lds);
+}
+
 // Planes whose loads splitk_reduce issues together (more planes: a loop).
 constexpr int kReduceUnroll = 16;
 
@@ -761,6 +906,35 @@ static hipError_t launch_reduce(const GemmArgs& a, int splits, hipStream_t st) {
   return hipGetLastError();
 }
 
+// Small-M products: NN with BIAS_ACT / STORE, NT with DX_ACT / STORE.
+template <bool B_KC, int EPI>
+static hipError_t launch_smallm_epi(const GemmArgs& a, bool vec, hipStream_t st) {
+  const int blocks = ((a.M + 15) / 16) * ((a.N + 15) / 16);
+  if (vec) hipLaunchKernelGGL((gemm_smallm<B_KC, true, EPI>), dim3(blocks), dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((gemm_smallm<B_KC, false, EPI>), dim3(blocks), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+// 16-byte operand loads need K, the leading dimensions of the K-contiguous
+// operands and their base addresses to be multiples of 4 floats.
+static bool smallm_vec_ok(const GemmArgs& a, int layout) {
+  const auto al = [](const float* p) { return ((uintptr_t)p & 15u) == 0; };
+  return a.K % 4 == 0 && a.lda % 4 == 0 && al(a.A) && (layout != GEMM_NT || (a.ldb % 4 == 0 && al(a.B)));
+}
+
+static hipError_t launch_smallm(const GemmArgs& a, int layout, bool vec, hipStream_t st) {
+  if (vec && !smallm_vec_ok(a, layout)) return hipErrorInvalidValue;
+  const int k = a.epi.kind;
+  if (layout == GEMM_NN) {
+    if (k == EPI_BIAS_ACT) return launch_smallm_epi<false, EPI_BIAS_ACT>(a, vec, st);
+    if (k == EPI_STORE) return launch_smallm_epi<false, EPI_STORE>(a, vec, st);
+  } else if (layout == GEMM_NT) {
+    if (k == EPI_DX_ACT) return launch_smallm_epi<true, EPI_DX_ACT>(a, vec, st);
+    if (k == EPI_STORE) return launch_smallm_epi<true, EPI_STORE>(a, vec, st);
+  }
+  return hipErrorInvalidValue;
+}
+
 hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& args_in, hipStream_t st, Recorder* rec,
                        const char* label, double bytes) {
   GemmArgs a = args_in;
@@ -773,6 +947,11 @@ hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& args_in, hipStream_t s
   // The loss head always reduces in-kernel (it needs whole rows).
   const bool ink = p.inkernel_reduce || a.epi.kind == EPI_LOSS;
   hipError_t err;
+  if (p.tile == TILE_SMALLM) {
+    if (p.splits != 1) return hipErrorInvalidValue;
+    if ((err = launch_smallm(a, p.layout, p.vec, st)) != hipSuccess) return err;
+    return mark(rec, label, 2.0 * a.M * a.N * a.K, bytes);
+  }
   switch (p.tile) {
     case TILE_64x64: err = launch_cfg<64, 64, 32, 32, 32>(a, p.layout, p.vec, p.splits, ink, st); break;
     case TILE_128x128: err = launch_cfg<128, 128, 32, 64, 64>(a, p.layout, p.vec, p.splits, ink, st); break;
@@ -811,6 +990,14 @@ struct GemmOp64 {  // 64x64 tiles, BK 32, 16-byte rows, split-K by a separate re
   }
 };
 
+struct SmallDxOp {  // dX on small-M tiles (16-byte rows), no split
+  using Args = GemmArgs;
+  static constexpr int kLds = kSmallLds;
+  static __device__ __forceinline__ void run(const GemmArgs& a, int blk, float* lds) {
+    smallm_tile<true, true, EPI_DX_ACT>(a, blk, lds);
+  }
+};
+
 template <int NMAX>
 struct NarrowDwOp {  // staged delta in the launch's LDS
   using Args = NarrowDwArgs;
@@ -842,11 +1029,15 @@ static int op_blocks(const PairOp& o) {
 
 static int op_lds_floats(const PairOp& o) {
   if (o.kind != PAIR_GEMM) return 0;
+  if (o.plan.tile == TILE_SMALLM) return SmallDxOp::kLds;
   return o.plan.layout == GEMM_NT ? DxOp::kLds : DwOp::kLds;
 }
 
 bool pair_supported(const PairOp& a, const PairOp& b) {
   auto gemm_ok = [](const PairOp& o) {
+    if (o.plan.tile == TILE_SMALLM)
+      return o.plan.vec && o.plan.splits == 1 && o.plan.layout == GEMM_NT && o.args.epi.kind == EPI_DX_ACT &&
+             smallm_vec_ok(o.args, GEMM_NT);
     return o.plan.tile == TILE_64x64 && o.plan.vec && !o.plan.inkernel_reduce &&
            ((o.plan.layout == GEMM_NT && o.args.epi.kind == EPI_DX_ACT) ||
             (o.plan.layout == GEMM_TN && o.args.epi.kind == EPI_DW_OPT)) &&
@@ -910,7 +1101,10 @@ hipError_t pair_launch(const PairOp& a, const PairOp& b, hipStream_t st, Recorde
   bb.k_per_split = b.plan.k_per_split;
 
   hipError_t err;
-  if (a.kind == PAIR_GEMM && a.plan.layout == GEMM_NT) {
+  if (a.kind == PAIR_GEMM && a.plan.layout == GEMM_NT && a.plan.tile == TILE_SMALLM) {
+    err = b.kind == PAIR_GEMM ? launch_pair_t<SmallDxOp, DwOp>(aa, na, bb, nb, st)
+                              : launch_with_narrow<SmallDxOp>(aa, na, b, st);
+  } else if (a.kind == PAIR_GEMM && a.plan.layout == GEMM_NT) {
     err = b.kind == PAIR_GEMM ? launch_pair_t<DxOp, DwOp>(aa, na, bb, nb, st) : launch_with_narrow<DxOp>(aa, na, b, st);
   } else if (a.kind == PAIR_GEMM) {
     err = launch_pair_t<DwOp, DwOp>(aa, na, bb, nb, st);
@@ -934,7 +1128,7 @@ hipError_t pair_launch(const PairOp& a, const PairOp& b, hipStream_t st, Recorde
   return hipSuccess;
 }
 
-GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus) {
+GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus, bool small_m) {
   GemmPlan p;
   p.layout = layout;
   p.vec = vec;
@@ -965,6 +1159,17 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus) {
   splits = (K + kps - 1) / kps;
   p.splits = splits < 1 ? 1 : splits;
   p.k_per_split = kps;
+  // A product the 64x64 plan would split over K runs on the small-M tile
+  // instead when it has few rows: the reduction over K stays inside each
+  // workgroup, which saves the reduce launch (B <= 128 by default;
+  // VOLTA_SMALLM_MAX_M changes the limit, 0 turns the tile off).
+  const char* sm = std::getenv("VOLTA_SMALLM_MAX_M");
+  const int small_max = sm && *sm ? std::atoi(sm) : 128;
+  if (small_m && (layout == GEMM_NN || layout == GEMM_NT) && p.splits > 1 && M <= small_max) {
+    p.tile = TILE_SMALLM;
+    p.splits = 1;
+    p.k_per_split = K;
+  }
   return p;
 }
 

@@ -640,8 +640,9 @@ static bool build(Handle* h) {
   for (int i = 0; i < n; ++i) {
     LayerPlan& lp = h->layers[i];
     const bool vr = lp.r % 4 == 0, vc = lp.c % 4 == 0;
-    lp.fwd = gemm_plan(GEMM_NN, B, lp.c, lp.r, vr && vc, h->num_cus);
-    if (i == n - 1 && h->out_mode == OUT_GEMM_LOSS) lp.fwd.tile = TILE_64x64;
+    const bool loss_gemm = i == n - 1 && h->out_mode == OUT_GEMM_LOSS;
+    lp.fwd = gemm_plan(GEMM_NN, B, lp.c, lp.r, vr && vc, h->num_cus, !loss_gemm);
+    if (loss_gemm) lp.fwd.tile = TILE_64x64;
     lp.dx = gemm_plan(GEMM_NT, B, lp.r, lp.c, vc, h->num_cus);
     lp.dw = gemm_plan(GEMM_TN, lp.r, lp.c, B, vr && vc, h->num_cus);
     ws_floats = std::max(ws_floats, lp.fwd.workspace_floats(B, lp.c));
