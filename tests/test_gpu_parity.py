@@ -81,11 +81,12 @@ GEMM_SHAPES = [
 
 
 TILE_SMALLM = 3
+TILE_DW_SMALLK = 4
 
 
 @pytest.mark.parametrize("layout", [0, 1, 2], ids=["NN", "NT", "TN"])
 @pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
-@pytest.mark.parametrize("tile", [0, 1, TILE_SMALLM])
+@pytest.mark.parametrize("tile", [0, 1, TILE_SMALLM, TILE_DW_SMALLK])
 def test_gemm_integer_exact(layout, M, N, K, tile):
     """Integer operands: the MFMA result must be exact (any order is exact
     below 2^24), which pins operand indexing, the lane layouts of the
@@ -94,6 +95,8 @@ def test_gemm_integer_exact(layout, M, N, K, tile):
     scalar-load path of the small-M tile)."""
     if tile == TILE_SMALLM and layout == 2:
         pytest.skip("the small-M tile serves the NN and NT products only")
+    if tile == TILE_DW_SMALLK and (layout != 2 or M % 4 or N % 4):
+        pytest.skip("the small-K dW tile serves TN products with 16-byte rows only")
     say(f"gemm layout={layout} M={M} N={N} K={K} tile={tile}")
     rng = np.random.default_rng(M * 7 + N * 13 + K)
     a_shape = (K, M) if layout == 2 else (M, K)
@@ -131,6 +134,32 @@ def test_gemm_smallm_float_bound(layout, M, N, K):
     want = A.astype(np.float64) @ Bm
     bound = 2 * K * np.finfo(np.float32).eps * (np.abs(A).astype(np.float64) @ np.abs(Bm))
     assert np.all(np.abs(got - want) <= bound)
+
+
+@pytest.mark.parametrize("M,N,K", [(1024, 1024, 64), (512, 256, 128), (96, 40, 64), (64, 32, 200)])
+def test_gemm_dw_smallk_float_bound(M, N, K):
+    """Random fp32 operands on the small-K dW tile (act^T delta): within the
+    fp32 error bound of a K-term sum; K=200 spans four 64-deep slices, the
+    last one partial."""
+    say(f"gemm small-K dW float M={M} N={N} K={K}")
+    rng = np.random.default_rng(M + N + K)
+    A = rng.standard_normal((K, M)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    got = _gemm(2, A, B, M, N, K, tile=TILE_DW_SMALLK)
+    want = A.T.astype(np.float64) @ B.astype(np.float64)
+    bound = 2 * K * np.finfo(np.float32).eps * (np.abs(A.T).astype(np.float64) @ np.abs(B).astype(np.float64))
+    assert np.all(np.abs(got - want) <= bound)
+
+
+def test_gemm_dw_smallk_rejects_ragged():
+    """The small-K dW tile needs 16-byte rows: M or N not a multiple of 4 is
+    refused on the host."""
+    lib = load_hip()
+    A = np.ones((64, 33), np.float32)
+    B = np.ones((64, 48), np.float32)
+    dA, dB = DeviceArray(A), DeviceArray(B)
+    dC = DeviceArray(np.zeros((33, 48), np.float32))
+    assert lib.lib.volta_hip_gemm(2, dA.ptr, dB.ptr, dC.ptr, 33, 48, 64, TILE_DW_SMALLK, 0) != 0
 
 
 @pytest.mark.parametrize("splits", [2, 3, 8])
@@ -290,25 +319,35 @@ def test_sgd_config_parity_with_oracle(name):
     assert_params_close(wh, bh, wo, bo, name)
 
 
+SMALL_BATCH_PLANS = {
+    "tiles64": {"VOLTA_SMALLM_MAX_M": "0", "VOLTA_DW_SMALLK_MAX_K": "0"},
+    "smallm_dw64": {"VOLTA_SMALLM_MAX_M": "128", "VOLTA_DW_SMALLK_MAX_K": "0"},
+    "default": {"VOLTA_SMALLM_MAX_M": "128", "VOLTA_DW_SMALLK_MAX_K": "128"},
+}
+
+
 @pytest.mark.parametrize("name", ["c1_mlp256_relu_sgd_b64", "c4_silu_sgd_b128"])
-@pytest.mark.parametrize("small_m", ["0", "128"], ids=["splitk64", "smallm"])
-def test_sgd_config_both_small_batch_plans(name, small_m):
-    """The B <= 128 products run on the small-M tile by default; with
-    VOLTA_SMALLM_MAX_M=0 they take the 64x64 split-K tiles and reduce
-    launches instead.  Both plans stay within rel 1e-4 / abs 1e-5 of the
+@pytest.mark.parametrize("plan", sorted(SMALL_BATCH_PLANS))
+def test_sgd_config_both_small_batch_plans(name, plan):
+    """At B <= 128 the forward and dX products run on the small-M tile and
+    the dW products on the small-K tile by default; VOLTA_SMALLM_MAX_M=0 and
+    VOLTA_DW_SMALLK_MAX_K=0 switch them back to the 64x64 tiles (split-K with
+    reduce launches).  Every plan stays within rel 1e-4 / abs 1e-5 of the
     oracle over the whole trajectory."""
     spec, B, lr, steps = CONFIGS[name]
-    say(f"config {name} VOLTA_SMALLM_MAX_M={small_m}")
-    old = os.environ.get("VOLTA_SMALLM_MAX_M")
-    os.environ["VOLTA_SMALLM_MAX_M"] = small_m
+    env = SMALL_BATCH_PLANS[plan]
+    say(f"config {name} plan {plan} {env}")
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
     try:
         ws, bs, batches = config_inputs(spec, B)
         lh, wh, bh, st = run_steps(load_hip(), spec, B, ws, bs, batches, lr, steps)
     finally:
-        if old is None:
-            os.environ.pop("VOLTA_SMALLM_MAX_M", None)
-        else:
-            os.environ["VOLTA_SMALLM_MAX_M"] = old
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
     lo, wo, bo, _ = run_steps(load_oracle(), spec, B, ws, bs, batches, lr, steps)
     assert st == 0, f"status {st}"
     ok, mx, _ = close_enough(lh, lo)

@@ -75,7 +75,9 @@ struct GemmArgs {
 
 // TILE_SMALLM: 16x16 output tiles, the whole K range in one workgroup
 // (split over its 4 waves), for NN/NT products with few rows (B <= 128).
-enum GemmTile { TILE_64x64 = 0, TILE_128x128 = 1, TILE_64x64_K64 = 2, TILE_SMALLM = 3 };
+// TILE_DW_SMALLK: 32x32 tiles of the TN (dW) product with a short K
+// (K = B <= 128), the optimizer applied on 16-byte rows.
+enum GemmTile { TILE_64x64 = 0, TILE_128x128 = 1, TILE_64x64_K64 = 2, TILE_SMALLM = 3, TILE_DW_SMALLK = 4 };
 
 struct GemmPlan {
   int layout = GEMM_NN;
@@ -85,7 +87,7 @@ struct GemmPlan {
   bool vec = false;
   bool inkernel_reduce = false;  // split-K reduced by the last slice (else a second kernel)
   int tiles(int M, int N) const {
-    const int t = tile == TILE_128x128 ? 128 : tile == TILE_SMALLM ? 16 : 64;
+    const int t = tile == TILE_128x128 ? 128 : tile == TILE_SMALLM ? 16 : tile == TILE_DW_SMALLK ? 32 : 64;
     return ((M + t - 1) / t) * ((N + t - 1) / t);
   }
   size_t workspace_floats(int M, int N) const { return splits > 1 ? (size_t)splits * (M + 1) * N : 0; }
@@ -117,9 +119,9 @@ struct PairOp {
 };
 
 // Whether a and b can share one launch: dX (NT, activation-derivative
-// epilogue; 64x64 or small-M tiles) or dW (TN, optimizer epilogue; 64x64
-// tiles) products with 16-byte rows, or the narrow output-layer dW whose
-// staged delta fits the launch's LDS.
+// epilogue; 64x64 or small-M tiles) or dW (TN, optimizer epilogue; 64x64 or
+// small-K tiles) products with 16-byte rows, or the narrow output-layer dW
+// whose staged delta fits the launch's LDS.
 bool pair_supported(const PairOp& a, const PairOp& b);
 
 // Both operations in one launch, then the split-K reductions either needs.

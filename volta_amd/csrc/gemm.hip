@@ -186,6 +186,61 @@ __device__ __forceinline__ void apply_epilogue(const EpiArgs& e, int m, int n, f
   }
 }
 
+// Optimizer state of the 16 elements of W_i a lane updates in the dW
+// epilogue (column n, rows m_base + 8*(v/4) + (v%4)), split into its loads
+// and the update + stores, so a kernel can issue the loads early and let
+// their latency run under the product.  32-bit element offsets (W_i has
+// fewer than 2^30 elements, checked at launch): one offset register per
+// element serves W, m and v alike.
+struct DwState {
+  float w[16], s1[16], s2[16];
+
+  __device__ __forceinline__ void load(const EpiArgs& e, int m_base, int n, int M, int N) {
+    const uint32_t n32 = (uint32_t)n, ldc = (uint32_t)e.ldc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int m = m_base + 8 * (v >> 2) + (v & 3);
+      const uint32_t o = (uint32_t)m * ldc + n32;
+      const bool ok = m < M && n < N;
+      w[v] = ok ? e.out[o] : 0.0f;
+      s1[v] = ok && e.opt != VOLTA_OPT_SGD ? e.m[o] : 0.0f;
+      s2[v] = ok && (e.opt == VOLTA_OPT_ADAM || e.opt == VOLTA_OPT_ADAMW) ? e.v[o] : 0.0f;
+    }
+  }
+
+  // Caller guarantees n < N.
+  __device__ __forceinline__ void update_store(const EpiArgs& e, const floatx16& acc, int m_base, int n, int M) {
+    const float lr = e.scalars->lr;
+    const uint32_t n32 = (uint32_t)n, ldc = (uint32_t)e.ldc;
+    auto row = [&](int v) { return m_base + 8 * (v >> 2) + (v & 3); };
+    auto off = [&](int v) { return (uint32_t)row(v) * ldc + n32; };
+    if (e.opt == VOLTA_OPT_SGD) {
+      // sgd_fused_tn: W = 1*W + (-lr) * (act_i^T delta_i)  (:321-324)
+      const float nlr = -lr;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) w[v] = w[v] + nlr * acc[v];
+    } else if (e.opt == VOLTA_OPT_ADAGRAD) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) adagrad_elem(&w[v], &s1[v], acc[v], lr, e.eps);
+    } else {
+      const AdamRcp rc = adam_rcp(e.scalars->bc1, e.scalars->bc2);
+      const uint32_t vec_end = (uint32_t)(e.count - e.count % 8);
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        adam_elem(&w[v], &s1[v], &s2[v], acc[v], off(v) >= vec_end, lr, rc, e.b1, e.b2, e.eps, e.wd);
+    }
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      if (row(v) < M) {
+        e.out[off(v)] = w[v];
+        if (e.opt != VOLTA_OPT_SGD) e.m[off(v)] = s1[v];
+        if (e.opt == VOLTA_OPT_ADAM || e.opt == VOLTA_OPT_ADAMW) e.v[off(v)] = s2[v];
+        if (e.grad) e.grad[off(v)] = acc[v];
+      }
+    }
+  }
+};
+
 // Epilogue for the 16 accumulators a lane holds of one 32x32 block: column n,
 // rows m_base + 8*(v/4) + (v%4).  All loads are issued before any store so
 // the memory accesses of the 16 elements overlap (the element-by-element
@@ -225,43 +280,9 @@ __device__ __forceinline__ void block_epilogue(const EpiArgs& e, const floatx16&
       if (m < M) e.out[(size_t)m * e.ldc + n] = acc[v] * act_derivative(e.act, p[v], y[v]);
     }
   } else if constexpr (EPI == EPI_DW_OPT) {
-    // 32-bit element offsets (W_i has fewer than 2^30 elements, checked at
-    // launch): one offset register per element serves W, m and v alike.
-    const float lr = e.scalars->lr;
-    const uint32_t n32 = (uint32_t)n, ldc = (uint32_t)e.ldc;
-    auto off = [&](int v) { return (uint32_t)row(v) * ldc + n32; };
-    float w[16], s1[16], s2[16];
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const bool ok = row(v) < M;
-      w[v] = ok ? e.out[off(v)] : 0.0f;
-      s1[v] = ok && e.opt != VOLTA_OPT_SGD ? e.m[off(v)] : 0.0f;
-      s2[v] = ok && (e.opt == VOLTA_OPT_ADAM || e.opt == VOLTA_OPT_ADAMW) ? e.v[off(v)] : 0.0f;
-    }
-    if (e.opt == VOLTA_OPT_SGD) {
-      // sgd_fused_tn: W = 1*W + (-lr) * (act_i^T delta_i)  (:321-324)
-      const float nlr = -lr;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) w[v] = w[v] + nlr * acc[v];
-    } else if (e.opt == VOLTA_OPT_ADAGRAD) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) adagrad_elem(&w[v], &s1[v], acc[v], lr, e.eps);
-    } else {
-      const AdamRcp rc = adam_rcp(e.scalars->bc1, e.scalars->bc2);
-      const uint32_t vec_end = (uint32_t)(e.count - e.count % 8);
-#pragma unroll
-      for (int v = 0; v < 16; ++v)
-        adam_elem(&w[v], &s1[v], &s2[v], acc[v], off(v) >= vec_end, lr, rc, e.b1, e.b2, e.eps, e.wd);
-    }
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      if (row(v) < M) {
-        e.out[off(v)] = w[v];
-        if (e.opt != VOLTA_OPT_SGD) e.m[off(v)] = s1[v];
-        if (e.opt == VOLTA_OPT_ADAM || e.opt == VOLTA_OPT_ADAMW) e.v[off(v)] = s2[v];
-        if (e.grad) e.grad[off(v)] = acc[v];
-      }
-    }
+    DwState st;
+    st.load(e, m_base, n, M, N);
+    st.update_store(e, acc, m_base, n, M);
   } else {
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
@@ -275,6 +296,35 @@ __device__ __forceinline__ void block_epilogue(const EpiArgs& e, const floatx16&
 __device__ __forceinline__ AdamRcp adam_rcp_of(const EpiArgs& e) {
   return e.opt == VOLTA_OPT_ADAM || e.opt == VOLTA_OPT_ADAMW ? adam_rcp(e.scalars->bc1, e.scalars->bc2) : AdamRcp{};
 }
+
+// b_i[n] and its optimizer state, loaded ahead of the update (same
+// arithmetic as apply_bias_update below).
+struct BiasState {
+  float b = 0.0f, m = 0.0f, v = 0.0f;
+
+  __device__ __forceinline__ void load(const EpiArgs& e, int n) {
+    b = e.b[n];
+    if (e.opt != VOLTA_OPT_SGD) m = e.bm[n];
+    if (e.opt == VOLTA_OPT_ADAM || e.opt == VOLTA_OPT_ADAMW) v = e.bv[n];
+  }
+
+  __device__ __forceinline__ void update_store(const EpiArgs& e, int n, int N, float db, AdamRcp rc) {
+    if (e.bgrad) e.bgrad[n] = db;
+    const float lr = e.scalars->lr;
+    if (e.opt == VOLTA_OPT_SGD) {
+      e.b[n] = b - lr * db;  // b -= lr*db (:986-991)
+    } else if (e.opt == VOLTA_OPT_ADAGRAD) {
+      adagrad_elem(&b, &m, db, lr, e.eps);
+      e.b[n] = b;
+      e.bm[n] = m;
+    } else {
+      adam_elem(&b, &m, &v, db, n >= N - N % 8, lr, rc, e.b1, e.b2, e.eps, 0.0f);
+      e.b[n] = b;
+      e.bm[n] = m;
+      e.bv[n] = v;
+    }
+  }
+};
 
 // Bias update from the fused column sum db_i[n] (:931-933, :957-993).  The
 // generated step never decays biases (:966).
@@ -767,6 +817,191 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) g
   smallm_tile<B_KC, VEC, EPI>(args, blockIdx.x, lds);
 }
 
+// ---------------------------------------------------------------------------
+// dW tile for a short reduction (K = B <= 128: the small-batch step).  A
+// workgroup owns a 32x32 tile of W_i -- 4 elements per thread -- so a launch
+// keeps several workgroups on each CU and the optimizer arithmetic of one
+// overlaps the memory traffic of another.  (A 64x64 tile leaves about 1.5
+// waves per SIMD at B=64, and its phases -- operands, product, optimizer
+// state loads, arithmetic, stores -- then run in lockstep over the chip.)
+//   1. 64-k slices of act_i^T (A(m,k) = act[k*lda + m]) and delta_i
+//      (B(k,n) = delta[k*ldb + n]) go to LDS with 16-byte loads.  The
+//      thread's float4 of W_i, m and v, and the state of one b_i element,
+//      are loaded right after the first slice: vector loads complete in
+//      issue order, so the wait for the operands does not wait for them, and
+//      their latency runs under the product.  Every load is unconditional
+//      (clamped address, value selected afterwards), which keeps the
+//      compiler's wait counts exact.
+//   2. wave w computes the 16x16 block (w/2, w%2) on v_mfma_f32_16x16x4f32
+//      in the small-M tile's k order, four accumulators added pairwise.
+//   3. the dW tile goes through LDS; thread t updates row t/8, columns
+//      4(t%8)..+3 of the tile: one float4 of W, m and v.
+//   4. in the first row of tiles, thread j < 32 forms db_i[n0 + j] as
+//      delta[0][n] + delta[1][n] + ... (batch ascending, the reference's
+//      order, :931-933) and updates b_i[n0 + j].
+// Needs M, N and the leading dimensions to be multiples of 4 and the
+// operands 16-byte aligned (checked at launch).
+// ---------------------------------------------------------------------------
+constexpr int kDwT = 32;
+constexpr int kDwK = 64;
+constexpr int kDwS = kDwT + 4;   // LDS row stride of the [k][32] operand slices
+constexpr int kDwDS = kDwT + 1;  // LDS row stride of the dW tile
+constexpr int kDwLds = 2 * kDwK * kDwS + kDwT * kDwDS;
+
+template <int EPI>
+__device__ __forceinline__ void dw_smallk_tile(const GemmArgs& args, int blk, float* lds) {
+  static_assert(EPI == EPI_DW_OPT || EPI == EPI_STORE, "epilogues of the dW tile");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, q = lane >> 4;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int M = args.M, N = args.N, K = args.K;
+  const int tiles_n = (N + kDwT - 1) / kDwT;
+  const int tm = blk / tiles_n, tn = blk % tiles_n;
+  const int m0 = tm * kDwT, n0 = tn * kDwT;
+  float* la = lds;                    // la[kk*kDwS + mm] = A(m0 + mm, k0 + kk)
+  float* lb = lds + kDwK * kDwS;      // lb[kk*kDwS + nn] = B(k0 + kk, n0 + nn)
+  float* ld = lds + 2 * kDwK * kDwS;  // ld[mm*kDwDS + nn] = dW(m0 + mm, n0 + nn)
+  const EpiArgs& e = args.epi;
+  const floatx4 zero4 = {0.f, 0.f, 0.f, 0.f};
+
+  // One 64-k slice of both operands: 64 rows of 8 float4 each, two of each
+  // per thread.
+  floatx4 xa[2], xb[2];
+  auto load_slice = [&](int k0) {
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int slot = tid + 256 * it;
+      const int kk = slot >> 3, c4 = (slot & 7) * 4;
+      const int k = k0 + kk;
+      const bool kok = k < K;
+      const bool aok = kok && m0 + c4 < M, bok = kok && n0 + c4 < N;
+      const size_t ka = kok ? (size_t)k : 0;
+      const floatx4 va = *reinterpret_cast<const floatx4*>(args.A + ka * args.lda + (aok ? m0 + c4 : 0));
+      const floatx4 vb = *reinterpret_cast<const floatx4*>(args.B + ka * args.ldb + (bok ? n0 + c4 : 0));
+      xa[it] = aok ? va : zero4;
+      xb[it] = bok ? vb : zero4;
+    }
+  };
+  auto store_slice = [&]() {
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int slot = tid + 256 * it;
+      const int kk = slot >> 3, c4 = (slot & 7) * 4;
+      *reinterpret_cast<floatx4*>(la + kk * kDwS + c4) = xa[it];
+      *reinterpret_cast<floatx4*>(lb + kk * kDwS + c4) = xb[it];
+    }
+  };
+
+  // This thread's elements of the tile and, for the first row of tiles,
+  // its column of b_i.
+  const int row = tid >> 3, c4 = (tid & 7) * 4;
+  const int gm = m0 + row, gn = n0 + c4;
+  const bool own = gm < M && gn < N;  // N % 4 == 0: the whole float4 is in range
+  const uint32_t o = own ? (uint32_t)gm * (uint32_t)e.ldc + (uint32_t)gn : 0u;
+  const int bn = n0 + (tid & 31);
+  const bool do_db = EPI == EPI_DW_OPT && args.colsum_b && e.b && tm == 0;
+
+  load_slice(0);
+  __builtin_amdgcn_sched_barrier(0);
+  floatx4 w4 = zero4, m4 = zero4, v4 = zero4;
+  BiasState bst;
+  if constexpr (EPI == EPI_DW_OPT) {
+    // SGD/Adagrad read their absent state buffers from W's own address (same lines)
+    const float* pm = e.m ? e.m : e.out;
+    const float* pv = e.v ? e.v : e.out;
+    w4 = *reinterpret_cast<const floatx4*>(e.out + o);
+    m4 = *reinterpret_cast<const floatx4*>(pm + o);
+    v4 = *reinterpret_cast<const floatx4*>(pv + o);
+    const float* pb = e.b ? e.b : e.out;
+    const uint32_t ob = e.b && bn < N ? (uint32_t)bn : 0u;
+    bst.b = pb[ob];
+    bst.m = (e.bm ? e.bm : pb)[ob];
+    bst.v = (e.bv ? e.bv : pb)[ob];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  floatx4 acc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) acc[c] = zero4;
+  float db = 0.0f;
+  for (int k0 = 0; k0 < K; k0 += kDwK) {
+    if (k0 > 0) {
+      __syncthreads();  // the previous slice is consumed
+      load_slice(k0);
+    }
+    store_slice();
+    __syncthreads();
+    if (do_db && tid < kDwT) {
+      const int kn = min(kDwK, K - k0);
+      for (int kk = 0; kk < kn; ++kk) db = db + lb[kk * kDwS + tid];
+    }
+#pragma unroll
+    for (int g = 0; g < kDwK / 16; ++g)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int kk = 16 * g + 4 * q + s;
+        const float a = la[kk * kDwS + wm * 16 + r16];
+        const float b = lb[kk * kDwS + wn * 16 + r16];
+        acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[g], 0, 0, 0);
+      }
+  }
+  // register v of lane (r16, q): dW(wm*16 + 4q + v, wn*16 + r16)
+#pragma unroll
+  for (int v = 0; v < 4; ++v)
+    ld[(wm * 16 + 4 * q + v) * kDwDS + wn * 16 + r16] = (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]);
+  __syncthreads();
+  floatx4 g4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) g4[j] = ld[row * kDwDS + c4 + j];
+
+  if constexpr (EPI == EPI_STORE) {
+    if (own) *reinterpret_cast<floatx4*>(e.out + o) = g4;
+  } else {
+    if (own && e.grad) *reinterpret_cast<floatx4*>(e.grad + o) = g4;
+    const float lr = e.scalars->lr;
+    const AdamRcp rc = adam_rcp_of(e);
+    float w[4], sm[4], sv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      w[j] = w4[j];
+      sm[j] = m4[j];
+      sv[j] = v4[j];
+    }
+    if (e.opt == VOLTA_OPT_SGD) {
+      // sgd_fused_tn: W = 1*W + (-lr) * (act_i^T delta_i)  (:321-324)
+      const float nlr = -lr;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w[j] = w[j] + nlr * g4[j];
+    } else if (e.opt == VOLTA_OPT_ADAGRAD) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) adagrad_elem(&w[j], &sm[j], g4[j], lr, e.eps);
+    } else {
+      const uint32_t vec_end = (uint32_t)(e.count - e.count % 8);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        adam_elem(&w[j], &sm[j], &sv[j], g4[j], o + j >= vec_end, lr, rc, e.b1, e.b2, e.eps, e.wd);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      w4[j] = w[j];
+      m4[j] = sm[j];
+      v4[j] = sv[j];
+    }
+    if (own) {
+      *reinterpret_cast<floatx4*>(e.out + o) = w4;
+      if (e.opt != VOLTA_OPT_SGD) *reinterpret_cast<floatx4*>(e.m + o) = m4;
+      if (e.opt == VOLTA_OPT_ADAM || e.opt == VOLTA_OPT_ADAMW) *reinterpret_cast<floatx4*>(e.v + o) = v4;
+    }
+    if (do_db && tid < kDwT && bn < N) bst.update_store(e, bn, N, db, rc);
+  }
+}
+
+template <int EPI>
+__global__ void __launch_bounds__(256) gemm_dw_smallk(GemmArgs args) {
+  __shared__ __attribute__((aligned(16))) float lds[kDwLds];
+  dw_smallk_tile<EPI>(args, blockIdx.x, lds);
+}
+
 // Planes whose loads splitk_reduce issues together (more planes: a loop).
 constexpr int kReduceUnroll = 16;
 
@@ -922,6 +1157,17 @@ static bool smallm_vec_ok(const GemmArgs& a, int layout) {
   return a.K % 4 == 0 && a.lda % 4 == 0 && al(a.A) && (layout != GEMM_NT || (a.ldb % 4 == 0 && al(a.B)));
 }
 
+// The small-K dW tile: 16-byte rows of both operands and of W_i and its state.
+static bool dw_smallk_ok(const GemmArgs& a, int layout) {
+  const auto al = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  const EpiArgs& e = a.epi;
+  if (layout != GEMM_TN || (e.kind != EPI_DW_OPT && e.kind != EPI_STORE)) return false;
+  if (a.M % 4 || a.N % 4 || a.lda % 4 || a.ldb % 4 || e.ldc % 4 || !al(a.A) || !al(a.B) || !al(e.out)) return false;
+  if (e.kind == EPI_DW_OPT && (!al(e.m) || !al(e.v) || !al(e.grad))) return false;
+  if (a.colsum_b && e.kind != EPI_DW_OPT) return false;
+  return (size_t)a.M * e.ldc < ((size_t)1 << 30);
+}
+
 static hipError_t launch_smallm(const GemmArgs& a, int layout, bool vec, hipStream_t st) {
   if (vec && !smallm_vec_ok(a, layout)) return hipErrorInvalidValue;
   const int k = a.epi.kind;
@@ -950,6 +1196,14 @@ hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& args_in, hipStream_t s
   if (p.tile == TILE_SMALLM) {
     if (p.splits != 1) return hipErrorInvalidValue;
     if ((err = launch_smallm(a, p.layout, p.vec, st)) != hipSuccess) return err;
+    return mark(rec, label, 2.0 * a.M * a.N * a.K, bytes);
+  }
+  if (p.tile == TILE_DW_SMALLK) {
+    if (p.splits != 1 || !dw_smallk_ok(a, p.layout)) return hipErrorInvalidValue;
+    const dim3 grid(p.tiles(a.M, a.N));
+    if (a.epi.kind == EPI_DW_OPT) hipLaunchKernelGGL(gemm_dw_smallk<EPI_DW_OPT>, grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(gemm_dw_smallk<EPI_STORE>, grid, dim3(256), 0, st, a);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
     return mark(rec, label, 2.0 * a.M * a.N * a.K, bytes);
   }
   switch (p.tile) {
@@ -998,6 +1252,14 @@ struct SmallDxOp {  // dX on small-M tiles (16-byte rows), no split
   }
 };
 
+struct DwSmallOp {  // dW on small-K tiles, optimizer epilogue
+  using Args = GemmArgs;
+  static constexpr int kLds = kDwLds;
+  static __device__ __forceinline__ void run(const GemmArgs& a, int blk, float* lds) {
+    dw_smallk_tile<EPI_DW_OPT>(a, blk, lds);
+  }
+};
+
 template <int NMAX>
 struct NarrowDwOp {  // staged delta in the launch's LDS
   using Args = NarrowDwArgs;
@@ -1030,6 +1292,7 @@ static int op_blocks(const PairOp& o) {
 static int op_lds_floats(const PairOp& o) {
   if (o.kind != PAIR_GEMM) return 0;
   if (o.plan.tile == TILE_SMALLM) return SmallDxOp::kLds;
+  if (o.plan.tile == TILE_DW_SMALLK) return DwSmallOp::kLds;
   return o.plan.layout == GEMM_NT ? DxOp::kLds : DwOp::kLds;
 }
 
@@ -1038,6 +1301,8 @@ bool pair_supported(const PairOp& a, const PairOp& b) {
     if (o.plan.tile == TILE_SMALLM)
       return o.plan.vec && o.plan.splits == 1 && o.plan.layout == GEMM_NT && o.args.epi.kind == EPI_DX_ACT &&
              smallm_vec_ok(o.args, GEMM_NT);
+    if (o.plan.tile == TILE_DW_SMALLK)
+      return o.plan.splits == 1 && o.args.epi.kind == EPI_DW_OPT && dw_smallk_ok(o.args, GEMM_TN);
     return o.plan.tile == TILE_64x64 && o.plan.vec && !o.plan.inkernel_reduce &&
            ((o.plan.layout == GEMM_NT && o.args.epi.kind == EPI_DX_ACT) ||
             (o.plan.layout == GEMM_TN && o.args.epi.kind == EPI_DW_OPT)) &&
@@ -1060,6 +1325,11 @@ bool pair_supported(const PairOp& a, const PairOp& b) {
   const bool a_dx = a.kind == PAIR_GEMM && a.plan.layout == GEMM_NT;
   const bool b_dw = b.kind == PAIR_GEMM && b.plan.layout == GEMM_TN;
   if (!((a_dx && (b_dw || b.kind == PAIR_NARROW_DW)) || (!a_dx && b_dw))) return false;
+  // tile combinations with a paired kernel (the 64x64 dX beside 64x64 dW
+  // or narrow dW; a dW beside a dW of the same tile)
+  const bool b_small = b.kind == PAIR_GEMM && b.plan.tile == TILE_DW_SMALLK;
+  if (a_dx && a.plan.tile != TILE_SMALLM && b_small) return false;
+  if (a.kind == PAIR_GEMM && !a_dx && (a.plan.tile == TILE_DW_SMALLK) != b_small) return false;
   for (const PairOp* o : ops)  // the narrow dW stages B x N floats of delta in the GEMM's LDS
     if (o->kind == PAIR_NARROW_DW && (size_t)o->nd.B * o->nd.N > (size_t)lds) return false;
   // no split product in the pair may share the other's workspace
@@ -1101,13 +1371,20 @@ hipError_t pair_launch(const PairOp& a, const PairOp& b, hipStream_t st, Recorde
   bb.k_per_split = b.plan.k_per_split;
 
   hipError_t err;
+  const bool b_small = b.kind == PAIR_GEMM && b.plan.tile == TILE_DW_SMALLK;
   if (a.kind == PAIR_GEMM && a.plan.layout == GEMM_NT && a.plan.tile == TILE_SMALLM) {
-    err = b.kind == PAIR_GEMM ? launch_pair_t<SmallDxOp, DwOp>(aa, na, bb, nb, st)
-                              : launch_with_narrow<SmallDxOp>(aa, na, b, st);
+    if (b.kind != PAIR_GEMM) err = launch_with_narrow<SmallDxOp>(aa, na, b, st);
+    else if (b_small) err = launch_pair_t<SmallDxOp, DwSmallOp>(aa, na, bb, nb, st);
+    else err = launch_pair_t<SmallDxOp, DwOp>(aa, na, bb, nb, st);
   } else if (a.kind == PAIR_GEMM && a.plan.layout == GEMM_NT) {
     err = b.kind == PAIR_GEMM ? launch_pair_t<DxOp, DwOp>(aa, na, bb, nb, st) : launch_with_narrow<DxOp>(aa, na, b, st);
   } else if (a.kind == PAIR_GEMM) {
-    err = launch_pair_t<DwOp, DwOp>(aa, na, bb, nb, st);
+    err = b_small ? launch_pair_t<DwSmallOp, DwSmallOp>(aa, na, bb, nb, st)
+                  : launch_pair_t<DwOp, DwOp>(aa, na, bb, nb, st);
+  } else if (b_small) {
+    if (a.nd.N <= 1) err = launch_pair_t<NarrowDwOp<1>, DwSmallOp>(a.nd, na, bb, nb, st);
+    else if (a.nd.N <= 4) err = launch_pair_t<NarrowDwOp<4>, DwSmallOp>(a.nd, na, bb, nb, st);
+    else err = launch_pair_t<NarrowDwOp<16>, DwSmallOp>(a.nd, na, bb, nb, st);
   } else if (a.nd.N <= 1) {
     err = launch_pair_t<NarrowDwOp<1>, DwOp>(a.nd, na, bb, nb, st);
   } else if (a.nd.N <= 4) {
@@ -1167,6 +1444,16 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus, bool 
   const int small_max = sm && *sm ? std::atoi(sm) : 128;
   if (small_m && (layout == GEMM_NN || layout == GEMM_NT) && p.splits > 1 && M <= small_max) {
     p.tile = TILE_SMALLM;
+    p.splits = 1;
+    p.k_per_split = K;
+  }
+  // dW with a short reduction (K = B) on 32x32 tiles: more workgroups per
+  // CU to overlap the optimizer's streaming and arithmetic (K <= 128 by
+  // default; VOLTA_DW_SMALLK_MAX_K changes the limit, 0 turns the tile off).
+  const char* dk = std::getenv("VOLTA_DW_SMALLK_MAX_K");
+  const int dw_kmax = dk && *dk ? std::atoi(dk) : 128;
+  if (layout == GEMM_TN && vec && M % 4 == 0 && N % 4 == 0 && K <= dw_kmax) {
+    p.tile = TILE_DW_SMALLK;
     p.splits = 1;
     p.k_per_split = K;
   }
