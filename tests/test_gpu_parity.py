@@ -110,6 +110,28 @@ def test_gemm_integer_exact(layout, M, N, K, tile):
     np.testing.assert_array_equal(got, want)
 
 
+@pytest.mark.parametrize("layout", [0, 1], ids=["NN", "NT"])
+@pytest.mark.parametrize("M,N,K", [(64, 512, 256), (33, 130, 257), (7, 5, 3), (64, 64, 1024)])
+def test_gemm_smallm_8_waves_integer_exact(layout, M, N, K):
+    """The 8-wave small-M workgroup (eighths of K, two four-tile trees) is
+    exact on integer operands, ragged shapes included."""
+    say(f"gemm small-M 8 waves layout={layout} M={M} N={N} K={K}")
+    rng = np.random.default_rng(M * 5 + N * 3 + K)
+    A = rng.integers(-4, 5, (M, K)).astype(np.float32)
+    B = rng.integers(-4, 5, (N, K) if layout == 1 else (K, N)).astype(np.float32)
+    old = os.environ.get("VOLTA_SMALLM_WAVES")
+    os.environ["VOLTA_SMALLM_WAVES"] = "8"
+    try:
+        got = _gemm(layout, A, B, M, N, K, tile=TILE_SMALLM)
+    finally:
+        if old is None:
+            os.environ.pop("VOLTA_SMALLM_WAVES", None)
+        else:
+            os.environ["VOLTA_SMALLM_WAVES"] = old
+    Bm = B.T if layout == 1 else B
+    np.testing.assert_array_equal(got, (A.astype(np.int64) @ Bm.astype(np.int64)).astype(np.float32))
+
+
 def test_gemm_smallm_rejects_tn():
     """The small-M tile has no TN form: the launch is refused on the host."""
     lib = load_hip()
@@ -122,14 +144,24 @@ def test_gemm_smallm_rejects_tn():
 
 @pytest.mark.parametrize("layout", [0, 1], ids=["NN", "NT"])
 @pytest.mark.parametrize("M,N,K", [(64, 1024, 1024), (64, 512, 2048), (128, 256, 512), (48, 80, 1000)])
-def test_gemm_smallm_float_bound(layout, M, N, K):
-    """Random fp32 operands on the small-M tile: within the fp32 error bound
-    of a K-term sum of the fp64 product."""
-    say(f"gemm small-M float layout={layout} M={M} N={N} K={K}")
+@pytest.mark.parametrize("waves", ["4", "8"])
+def test_gemm_smallm_float_bound(layout, M, N, K, waves):
+    """Random fp32 operands on the small-M tile with 4 or 8 waves per
+    workgroup (VOLTA_SMALLM_WAVES): within the fp32 error bound of a K-term
+    sum of the fp64 product."""
+    say(f"gemm small-M float layout={layout} M={M} N={N} K={K} waves={waves}")
     rng = np.random.default_rng(M + N + K + layout)
     A = rng.standard_normal((M, K)).astype(np.float32)
     B = rng.standard_normal((N, K) if layout == 1 else (K, N)).astype(np.float32)
-    got = _gemm(layout, A, B, M, N, K, tile=TILE_SMALLM)
+    old = os.environ.get("VOLTA_SMALLM_WAVES")
+    os.environ["VOLTA_SMALLM_WAVES"] = waves
+    try:
+        got = _gemm(layout, A, B, M, N, K, tile=TILE_SMALLM)
+    finally:
+        if old is None:
+            os.environ.pop("VOLTA_SMALLM_WAVES", None)
+        else:
+            os.environ["VOLTA_SMALLM_WAVES"] = old
     Bm = (B.T if layout == 1 else B).astype(np.float64)
     want = A.astype(np.float64) @ Bm
     bound = 2 * K * np.finfo(np.float32).eps * (np.abs(A).astype(np.float64) @ np.abs(Bm))
@@ -349,6 +381,33 @@ def test_sgd_config_both_small_batch_plans(name, plan):
             else:
                 os.environ[k] = v
     lo, wo, bo, _ = run_steps(load_oracle(), spec, B, ws, bs, batches, lr, steps)
+    assert st == 0, f"status {st}"
+    ok, mx, _ = close_enough(lh, lo)
+    assert ok, f"{name}: losses differ, max abs {mx:.3e}"
+    assert_params_close(wh, bh, wo, bo, name)
+
+
+NARROW_HEAD_CASES = {
+    # W_{n-1} of 2048 x 12 floats: too large for the LDS copy, read from global memory
+    "w_global": (MlpSpec([64, 2048, 12], "relu", "sgd", "ce"), 48, 0.05),
+    # staged W, width 1, a batch that is not a multiple of the 16-row blocks
+    "w_lds_b37": (MlpSpec([96, 256, 1], "tanh", "sgd"), 37, 0.01),
+    # staged W, width 10, more than one output-layer block (B > 256)
+    "w_lds_b300": (MlpSpec([64, 128, 10], "silu", "sgd", "ce"), 300, 0.05),
+}
+
+
+@pytest.mark.parametrize("name", sorted(NARROW_HEAD_CASES))
+def test_narrow_output_layer_paths(name):
+    """The narrow output layer's kernels (dot-product forward + loss head with
+    W from LDS or from global memory, the outer-product dX over 16-row
+    blocks, the narrow dW): 6 SGD steps within rel 1e-4 / abs 1e-5 of the
+    oracle."""
+    spec, B, lr = NARROW_HEAD_CASES[name]
+    say(f"narrow head {name}: {spec.text()} B={B}")
+    ws, bs, batches = config_inputs(spec, B, seed=5)
+    lh, wh, bh, st = run_steps(load_hip(), spec, B, ws, bs, batches, lr, 6)
+    lo, wo, bo, _ = run_steps(load_oracle(), spec, B, ws, bs, batches, lr, 6)
     assert st == 0, f"status {st}"
     ok, mx, _ = close_enough(lh, lo)
     assert ok, f"{name}: losses differ, max abs {mx:.3e}"

@@ -674,12 +674,13 @@ gemm_f32_mfma(GemmArgs args) {
 
 // ---------------------------------------------------------------------------
 // Small-M tile (M up to a few 16-row tiles: the B=64 forward and dX
-// products).  One workgroup of 4 waves owns a 16x16 output tile over the
-// whole K range.  Wave w takes the w-th quarter of K (rounded up to 16),
-// loads its operands straight into registers (nothing is shared between the
-// waves, so no LDS staging and no barrier in the K loop) and accumulates them
-// on v_mfma_f32_16x16x4f32; the four partial tiles are then added in wave
-// order through LDS and the epilogue runs one element per thread.  K never
+// products).  One workgroup of 4 (or 8) waves owns a 16x16 output tile over
+// the whole K range.  Wave w takes the w-th quarter (eighth) of K, rounded
+// up to whole 16-k groups, loads its operands straight into registers
+// (nothing is shared between the waves, so no LDS staging and no barrier in
+// the K loop) and accumulates them on v_mfma_f32_16x16x4f32; the partial
+// tiles are then added in wave order through LDS and the epilogue runs one
+// element per thread.  K never
 // leaves the workgroup -- no split-K workspace and no second launch -- while
 // the grid (M/16 x N/16 tiles) still spreads over the CUs.
 //
@@ -690,13 +691,15 @@ gemm_f32_mfma(GemmArgs args) {
 // group are four consecutive k of one row (one 16-byte load); likewise the
 // B operands of the NT product (dX: rows of W_i).  Group g accumulates into
 // accumulator g % 4 (chains of a quarter of the wave's terms), and the four
-// accumulators, then the four waves' tiles, are added as pairwise trees:
-// a fixed order, with shorter rounding chains than one running sum.
+// accumulators, then the waves' tiles, are added as pairwise trees: a fixed
+// order, with shorter rounding chains than one running sum.
 // ---------------------------------------------------------------------------
-constexpr int kSmallWaves = 4;
 constexpr int kSmallChunk = 8;     // 16-k groups per register chunk (128 k)
 constexpr int kSmallRedStride = 80;  // LDS floats per (wave, register) row of partials
-constexpr int kSmallLds = kSmallWaves * 4 * kSmallRedStride;
+template <int NW>
+struct SmallLds {
+  static constexpr int kFloats = NW * 4 * kSmallRedStride;
+};
 
 // Tile order: workgroups are handed to the 8 XCDs round-robin by index, and
 // every XCD has its own L2.  The tiles that read the same columns of B (one
@@ -716,8 +719,11 @@ __device__ __forceinline__ void smallm_coords(int blk, int tiles_m, int tiles_n,
   }
 }
 
-template <bool B_KC, bool VEC, int EPI>
+// NW waves per workgroup (4, or 8 for a stand-alone launch), each taking
+// one NW-th of the K range.
+template <bool B_KC, bool VEC, int EPI, int NW>
 __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float* lds) {
+  static_assert(NW == 4 || NW == 8, "wave trees for 4 or 8 partial tiles");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int M = args.M, N = args.N, K = args.K;
@@ -725,8 +731,8 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
   int tm, tn;
   smallm_coords<B_KC ? 1 : 2>(blk, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * 16, n0 = tn * 16;
-  // this wave's K range: quarters rounded up to whole 16-k groups
-  const int kq = (K + 4 * 16 - 1) / (4 * 16) * 16;
+  // this wave's K range: NW-ths rounded up to whole 16-k groups
+  const int kq = (K + NW * 16 - 1) / (NW * 16) * 16;
   const int kbeg = wave * kq, kend = min(K, kbeg + kq);
   const bool row_ok = m0 + r < M, col_ok = n0 + r < N;
   const int lda = args.lda, ldb = args.ldb;
@@ -801,20 +807,23 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
     lds[(wave * 4 + v) * kSmallRedStride + lane] = (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]);
   __syncthreads();
   // Element (i, j) of the tile: lane 16*(i/4) + j, register i%4 of each
-  // wave; the waves' values added as (w0 + w1) + (w2 + w3).
-  static_assert(kSmallWaves == 4, "the wave tree below adds four tiles");
+  // wave; the waves' values added as (w0 + w1) + (w2 + w3) (then the same
+  // for w4..w7, and the two halves).  Threads 0..255 hold one element each.
+  if (tid >= 256) return;
   const int i = tid >> 4, j = tid & 15;
   const int src = (i & 3) * kSmallRedStride + 16 * (i >> 2) + j;
   constexpr int kW = 4 * kSmallRedStride;
-  const float sum = (lds[src] + lds[kW + src]) + (lds[2 * kW + src] + lds[3 * kW + src]);
+  float sum = (lds[src] + lds[kW + src]) + (lds[2 * kW + src] + lds[3 * kW + src]);
+  if constexpr (NW == 8)
+    sum = sum + ((lds[4 * kW + src] + lds[5 * kW + src]) + (lds[6 * kW + src] + lds[7 * kW + src]));
   const int m = m0 + i, n = n0 + j;
   if (m < M && n < N) apply_epilogue<EPI>(args.epi, m, n, sum);
 }
 
-template <bool B_KC, bool VEC, int EPI>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) gemm_smallm(GemmArgs args) {
-  __shared__ float lds[kSmallLds];
-  smallm_tile<B_KC, VEC, EPI>(args, blockIdx.x, lds);
+template <bool B_KC, bool VEC, int EPI, int NW>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) gemm_smallm(GemmArgs args) {
+  __shared__ float lds[SmallLds<NW>::kFloats];
+  smallm_tile<B_KC, VEC, EPI, NW>(args, blockIdx.x, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -932,8 +941,16 @@ __device__ __forceinline__ void dw_smallk_tile(const GemmArgs& args, int blk, fl
     store_slice();
     __syncthreads();
     if (do_db && tid < kDwT) {
+      // batch order; the slice's 64 reads are issued before the first add
       const int kn = min(kDwK, K - k0);
-      for (int kk = 0; kk < kn; ++kk) db = db + lb[kk * kDwS + tid];
+      float col[kDwK];
+#pragma unroll
+      for (int kk = 0; kk < kDwK; ++kk) col[kk] = lb[kk * kDwS + tid];
+#pragma unroll
+      for (int kk = 0; kk < kDwK; ++kk) {
+        const float t = db + col[kk];
+        db = kk < kn ? t : db;
+      }
     }
 #pragma unroll
     for (int g = 0; g < kDwK / 16; ++g)
@@ -1142,11 +1159,23 @@ static hipError_t launch_reduce(const GemmArgs& a, int splits, hipStream_t st) {
 }
 
 // Small-M products: NN with BIAS_ACT / STORE, NT with DX_ACT / STORE.
+// Waves per workgroup of a stand-alone small-M launch (VOLTA_SMALLM_WAVES,
+// 4 or 8); a paired launch always has 4.
+static int smallm_waves() {
+  const char* w = std::getenv("VOLTA_SMALLM_WAVES");
+  return w && std::atoi(w) == 8 ? 8 : 4;
+}
+
 template <bool B_KC, int EPI>
 static hipError_t launch_smallm_epi(const GemmArgs& a, bool vec, hipStream_t st) {
   const int blocks = ((a.M + 15) / 16) * ((a.N + 15) / 16);
-  if (vec) hipLaunchKernelGGL((gemm_smallm<B_KC, true, EPI>), dim3(blocks), dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((gemm_smallm<B_KC, false, EPI>), dim3(blocks), dim3(256), 0, st, a);
+  if (smallm_waves() == 8) {
+    if (vec) hipLaunchKernelGGL((gemm_smallm<B_KC, true, EPI, 8>), dim3(blocks), dim3(512), 0, st, a);
+    else hipLaunchKernelGGL((gemm_smallm<B_KC, false, EPI, 8>), dim3(blocks), dim3(512), 0, st, a);
+  } else {
+    if (vec) hipLaunchKernelGGL((gemm_smallm<B_KC, true, EPI, 4>), dim3(blocks), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((gemm_smallm<B_KC, false, EPI, 4>), dim3(blocks), dim3(256), 0, st, a);
+  }
   return hipGetLastError();
 }
 
@@ -1246,9 +1275,9 @@ struct GemmOp64 {  // 64x64 tiles, BK 32, 16-byte rows, split-K by a separate re
 
 struct SmallDxOp {  // dX on small-M tiles (16-byte rows), no split
   using Args = GemmArgs;
-  static constexpr int kLds = kSmallLds;
+  static constexpr int kLds = SmallLds<4>::kFloats;
   static __device__ __forceinline__ void run(const GemmArgs& a, int blk, float* lds) {
-    smallm_tile<true, true, EPI_DX_ACT>(a, blk, lds);
+    smallm_tile<true, true, EPI_DX_ACT, 4>(a, blk, lds);
   }
 };
 
@@ -1286,7 +1315,7 @@ using DwOp = GemmOp64<EPI_DW_OPT, false, false>;
 
 static int op_blocks(const PairOp& o) {
   if (o.kind == PAIR_GEMM) return o.plan.tiles(o.args.M, o.args.N) * o.plan.splits;
-  return (o.nd.R + 255) / 256;
+  return (o.nd.R + kNarrowRows - 1) / kNarrowRows;
 }
 
 static int op_lds_floats(const PairOp& o) {
@@ -1330,8 +1359,8 @@ bool pair_supported(const PairOp& a, const PairOp& b) {
   const bool b_small = b.kind == PAIR_GEMM && b.plan.tile == TILE_DW_SMALLK;
   if (a_dx && a.plan.tile != TILE_SMALLM && b_small) return false;
   if (a.kind == PAIR_GEMM && !a_dx && (a.plan.tile == TILE_DW_SMALLK) != b_small) return false;
-  for (const PairOp* o : ops)  // the narrow dW stages B x N floats of delta in the GEMM's LDS
-    if (o->kind == PAIR_NARROW_DW && (size_t)o->nd.B * o->nd.N > (size_t)lds) return false;
+  for (const PairOp* o : ops)  // the narrow dW stages its deltas and partial sums in the GEMM's LDS
+    if (o->kind == PAIR_NARROW_DW && narrow_lds_floats_n(o->nd.B, o->nd.N) > lds) return false;
   // no split product in the pair may share the other's workspace
   if (a.kind == PAIR_GEMM && b.kind == PAIR_GEMM && a.plan.splits > 1 && b.plan.splits > 1 &&
       a.args.partial == b.args.partial)

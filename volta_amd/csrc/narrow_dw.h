@@ -9,59 +9,117 @@
 
 namespace volta {
 
-// dW[j][k] = sum_b act[b][j] * delta[b][k] (b ascending, as sgemm_tn sums),
-// one thread per row j of W (rows block*blockDim.x + threadIdx.x); delta is
-// staged in LDS.  Block 0 also forms db[k] = sum_b
-// delta[b][k] (:931-933).  Then the optimizer update of W and b (same
-// element functions as the MFMA path).  Latency: the optimizer state, the
-// scalars and the first chunk of act are loaded before the LDS staging
-// barrier, and act is read in chunks of kChunk rows whose loads are all
-// issued before the chunk's first multiply.
+// Rows of W a block of kNarrowThreads threads updates, and the LDS floats
+// it needs beyond the staged deltas (the waves' partial sums).
+constexpr int kNarrowThreads = 256;
+constexpr int kNarrowRows = 64;
 template <int NMAX>
-__device__ __forceinline__ void narrow_dw_block(const NarrowDwArgs& p, int block, float* sdelta /* [B x N] */) {
-  constexpr int kChunk = 64;
+struct NarrowLds {
+  static constexpr int kPartials = (kNarrowThreads / 64) * NMAX * 64;
+};
+
+// Floats of LDS a narrow dW block uses: the B x N deltas (padded to 4), then
+// the partial sums.
+template <int NMAX>
+__host__ __device__ inline int narrow_lds_floats(int B, int N) {
+  return (B * N + 3) / 4 * 4 + NarrowLds<NMAX>::kPartials;
+}
+
+// The same for the instantiation that serves N columns (NMAX = 1, 4 or 16).
+__host__ __device__ inline int narrow_lds_floats_n(int B, int N) {
+  return N <= 1 ? narrow_lds_floats<1>(B, N) : N <= 4 ? narrow_lds_floats<4>(B, N) : narrow_lds_floats<16>(B, N);
+}
+
+// dW[j][k] = sum_b act[b][j] * delta[b][k] for the kNarrowRows rows j of W
+// of this block: lane l of wave q takes row j = block*64 + l and, of every
+// 64 batch rows, the 16 rows 16q..16q+15 (ascending; all chunks into one
+// partial), and the four waves' partials are added as (P0 + P1) + (P2 + P3)
+// by wave 0, which runs the optimizer on W.  Block 0 also forms db[k] =
+// sum_b delta[b][k] (:931-933) over four interleaved accumulators (b mod 4)
+// added pairwise.  Latency: every global load is unconditional (clamped
+// addresses; values outside the batch are never used); the delta staging
+// loads go first, so staging waits for them alone, then the activations
+// (16 a thread) and wave 0's optimizer state; the staged deltas are read
+// from LDS in batches before the multiplies, and guards are selects.
+template <int NMAX>
+__device__ __forceinline__ void narrow_dw_block(const NarrowDwArgs& p, int block, float* lds) {
+  constexpr int kQ = 16;  // batch rows per wave per 64-row chunk
+  constexpr int kDBatch = NMAX == 1 ? 16 : NMAX <= 4 ? 8 : 2;  // batch rows per LDS read batch
   const int B = p.B, N = p.N, R = p.R;
-  const int j = block * blockDim.x + threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
+  const int j = block * kNarrowRows + lane;
   const bool own = j < R;
+  const int jc = own ? j : 0;
   const bool sgd = p.opt == VOLTA_OPT_SGD, adam = p.opt == VOLTA_OPT_ADAM;
-  const float lr = p.scalars->lr;
-  const AdamRcp rc = adam_rcp(p.scalars->bc1, p.scalars->bc2);
+  const int BN = B * N;
+  float* sdelta = lds;
+  float* part = lds + (BN + 3) / 4 * 4;  // part[(q*NMAX + k)*64 + lane]
+  const bool one = BN <= kNarrowThreads;  // one staged delta per thread at most
+  float dst = 0.0f;
+  if (one) dst = p.delta[min(tid, BN - 1)];
+  float a[kQ];
+#pragma unroll
+  for (int c = 0; c < kQ; ++c) a[c] = p.act[(size_t)min(kQ * q + c, B - 1) * R + jc];
   float w[NMAX], s1[NMAX], s2[NMAX];
+  const float* pm = sgd ? p.w : p.m;
+  const float* pv = adam ? p.v : p.w;
 #pragma unroll
   for (int k = 0; k < NMAX; ++k) {
-    const size_t idx = (size_t)j * N + k;
-    const bool ok = own && k < N;
-    w[k] = ok ? p.w[idx] : 0.0f;
-    s1[k] = ok && !sgd ? p.m[idx] : 0.0f;
-    s2[k] = ok && adam ? p.v[idx] : 0.0f;
+    const size_t idx = (size_t)jc * N + min(k, N - 1);
+    w[k] = p.w[idx];
+    s1[k] = pm[idx];
+    s2[k] = pv[idx];
   }
   // bias state (block 0, threads k < N; no bias work when p.b is null)
-  const bool bown = block == 0 && (int)threadIdx.x < N && p.b;
-  const float bw = bown ? p.b[threadIdx.x] : 0.0f;
-  const float bs1 = bown && !sgd ? p.bm[threadIdx.x] : 0.0f;
-  const float bs2 = bown && adam ? p.bv[threadIdx.x] : 0.0f;
-  float a[kChunk];
-#pragma unroll
-  for (int c = 0; c < kChunk; ++c) a[c] = own && c < B ? p.act[(size_t)c * R + j] : 0.0f;
-  for (int i = threadIdx.x; i < B * N; i += blockDim.x) sdelta[i] = p.delta[i];
+  const bool bown = block == 0 && tid < N && p.b;
+  const int kb = min(tid, N - 1);
+  const float* pb = p.b ? p.b : p.w;
+  const float bw = pb[kb];
+  const float bs1 = (sgd || !p.b ? pb : p.bm)[kb];
+  const float bs2 = (adam && p.b ? p.bv : pb)[kb];
+  const float lr = p.scalars->lr;
+  const AdamRcp rc = adam_rcp(p.scalars->bc1, p.scalars->bc2);
+  if (one) {
+    if (tid < BN) sdelta[tid] = dst;
+  } else {
+    for (int i = tid; i < BN; i += kNarrowThreads) sdelta[i] = p.delta[i];
+  }
   __syncthreads();
 
   float acc[NMAX];
 #pragma unroll
   for (int k = 0; k < NMAX; ++k) acc[k] = 0.0f;
-  for (int b0 = 0; b0 < B; b0 += kChunk) {
+  for (int b0 = 0; b0 < B; b0 += 4 * kQ) {
     if (b0 > 0) {
 #pragma unroll
-      for (int c = 0; c < kChunk; ++c) a[c] = own && b0 + c < B ? p.act[(size_t)(b0 + c) * R + j] : 0.0f;
+      for (int c = 0; c < kQ; ++c) a[c] = p.act[(size_t)min(b0 + kQ * q + c, B - 1) * R + jc];
     }
 #pragma unroll
-    for (int c = 0; c < kChunk; ++c) {
-      if (b0 + c < B) {
+    for (int c0 = 0; c0 < kQ; c0 += kDBatch) {
+      float d[kDBatch][NMAX];
 #pragma unroll
-        for (int k = 0; k < NMAX; ++k)
-          if (k < N) acc[k] = acc[k] + a[c] * sdelta[(b0 + c) * N + k];
+      for (int c = 0; c < kDBatch; ++c)
+#pragma unroll
+        for (int k = 0; k < NMAX; ++k) d[c][k] = sdelta[min(b0 + kQ * q + c0 + c, B - 1) * N + min(k, N - 1)];
+#pragma unroll
+      for (int c = 0; c < kDBatch; ++c) {
+        const bool in = b0 + kQ * q + c0 + c < B;
+#pragma unroll
+        for (int k = 0; k < NMAX; ++k) {
+          const float t = acc[k] + a[c0 + c] * d[c][k];
+          acc[k] = in && k < N ? t : acc[k];
+        }
       }
     }
+  }
+#pragma unroll
+  for (int k = 0; k < NMAX; ++k) part[(q * NMAX + k) * 64 + lane] = acc[k];
+  __syncthreads();
+  if (q != 0) return;
+#pragma unroll
+  for (int k = 0; k < NMAX; ++k) {
+    const float* pk = part + k * 64 + lane;
+    acc[k] = (pk[0] + pk[NMAX * 64]) + (pk[2 * NMAX * 64] + pk[3 * NMAX * 64]);
   }
   if (own) {
     const int64_t count = (int64_t)R * N;
@@ -91,8 +149,21 @@ __device__ __forceinline__ void narrow_dw_block(const NarrowDwArgs& p, int block
   }
   if (bown) {
     const int k = threadIdx.x;
-    float db = 0.0f;
-    for (int b = 0; b < B; ++b) db = db + sdelta[b * N + k];
+    // four interleaved accumulators; each chunk's reads are issued before
+    // its first add
+    constexpr int kDbChunk = 64;
+    float dba[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int b0 = 0; b0 < B; b0 += kDbChunk) {
+      float d[kDbChunk];
+#pragma unroll
+      for (int c = 0; c < kDbChunk; ++c) d[c] = sdelta[min(b0 + c, B - 1) * N + k];
+#pragma unroll
+      for (int c = 0; c < kDbChunk; ++c) {
+        const float t = dba[c & 3] + d[c];
+        dba[c & 3] = b0 + c < B ? t : dba[c & 3];
+      }
+    }
+    const float db = (dba[0] + dba[1]) + (dba[2] + dba[3]);
     if (p.bgrad) p.bgrad[k] = db;
     float x = bw, y1 = bs1, y2 = bs2;
     if (sgd) {

@@ -42,7 +42,9 @@ struct NarrowDwArgs {
   DevScalars* scalars;
 };
 
-constexpr size_t kNarrowDwLdsBytes = 64 * 1024;
+// Largest staged delta (B x N floats) of the narrow dW; its partial sums
+// (16 KiB at most) come on top.
+constexpr size_t kNarrowDwLdsBytes = 48 * 1024;
 
 int out_layer_blocks(int B);
 hipError_t launch_out_layer(const OutLayerArgs& p, hipStream_t st);

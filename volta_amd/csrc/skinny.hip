@@ -8,8 +8,9 @@
 //   narrow_dw_kernel   dW = act^T delta, db, optimizer update (N = L[n])
 //
 // Every sum has a fixed order: per-lane k-strided partials then a fixed
-// butterfly (out_layer), or a sequential loop in the reference's order
-// (outer_dx over k, narrow_dw over the batch).
+// butterfly (out_layer), a sequential loop in the reference's order
+// (outer_dx over k), or interleaved accumulators over the batch added
+// pairwise (narrow_dw).
 #include "skinny.h"
 
 #include "narrow_dw.h"
@@ -19,11 +20,17 @@ namespace volta {
 // Output rows z[g][0..N) of RG rows (rows[g], valid where rows[g] >= 0),
 // computed by a whole wave: lane l sums k = l, l+64, ... in ascending order,
 // then a fixed butterfly adds the lanes.  The k loop runs in chunks of C
-// values per lane whose loads (activations of all RG rows and the matching
-// rows of W) are all issued before the chunk's first multiply, so a chunk
-// costs one memory latency.
-template <int NMAX, int RG, int C>
-__device__ __forceinline__ void wave_rows(const OutLayerArgs& p, const int* rows, float (*z)[NMAX]) {
+// values per lane whose activation loads (all RG rows) are issued before
+// the chunk's first multiply, so a chunk costs one memory latency.  W comes
+// from the block's LDS copy `wl` (WL) -- lane l reads row k of W, so for
+// N > 1 global loads of W would touch a cache line per lane for each of its
+// N columns -- or, for one column or a W too large to stage, from global
+// memory with the chunk's other loads.  Every global load is unconditional (clamped row and k;
+// terms outside the matrix are not added), so no branch or wait separates
+// them.
+template <int NMAX, int RG, int C, bool WL>
+__device__ __forceinline__ void wave_rows(const OutLayerArgs& p, const float* wl, const int* rows,
+                                          float (*z)[NMAX]) {
   const int lane = threadIdx.x & 63;
   const int K = p.K, N = p.N;
   float acc[RG][NMAX];
@@ -31,26 +38,34 @@ __device__ __forceinline__ void wave_rows(const OutLayerArgs& p, const int* rows
   for (int g = 0; g < RG; ++g)
 #pragma unroll
     for (int j = 0; j < NMAX; ++j) acc[g][j] = 0.0f;
-  for (int k0 = lane; k0 < K; k0 += 64 * C) {
-    float x[RG][C], wv[C][NMAX];
+  for (int kb = 0; kb < K; kb += 64 * C) {
+    float x[RG][C], wg[WL ? 1 : C][NMAX];
 #pragma unroll
     for (int c = 0; c < C; ++c) {
-      const int k = k0 + 64 * c;
+      const int kc = min(kb + 64 * c + lane, K - 1);
+      if constexpr (!WL) {
 #pragma unroll
-      for (int j = 0; j < NMAX; ++j) wv[c][j] = k < K && j < N ? p.W[(size_t)k * N + j] : 0.0f;
+        for (int j = 0; j < NMAX; ++j) wg[c][j] = p.W[(size_t)kc * N + min(j, N - 1)];
+      }
 #pragma unroll
-      for (int g = 0; g < RG; ++g) x[g][c] = k < K && rows[g] >= 0 ? p.act[(size_t)rows[g] * K + k] : 0.0f;
+      for (int g = 0; g < RG; ++g) x[g][c] = p.act[(size_t)(rows[g] >= 0 ? rows[g] : 0) * K + kc];
     }
 #pragma unroll
-    for (int g = 0; g < RG; ++g)
+    for (int c = 0; c < C; ++c) {
+      const int kc = min(kb + 64 * c + lane, K - 1);
+      float wv[NMAX];
 #pragma unroll
-      for (int c = 0; c < C; ++c) {
-        if (k0 + 64 * c < K) {
+      for (int j = 0; j < NMAX; ++j) wv[j] = WL ? wl[kc * N + min(j, N - 1)] : wg[WL ? 0 : c][j];
 #pragma unroll
-          for (int j = 0; j < NMAX; ++j)
-            if (j < N) acc[g][j] = acc[g][j] + x[g][c] * wv[c][j];
+      for (int g = 0; g < RG; ++g) {
+        const bool in = kb + 64 * c + lane < K && rows[g] >= 0;
+#pragma unroll
+        for (int j = 0; j < NMAX; ++j) {
+          const float t = acc[g][j] + x[g][c] * wv[j];
+          acc[g][j] = in && j < N ? t : acc[g][j];
         }
       }
+    }
   }
 #pragma unroll
   for (int g = 0; g < RG; ++g)
@@ -114,13 +129,19 @@ __device__ __forceinline__ float head_row(const OutLayerArgs& p, const float* z,
 // finishes the step's loss directly, otherwise it lands in partials[b] for
 // loss_finish_kernel.  Lane 0 loads the bias, the targets/labels of its
 // rows and the next step counter before the dot products.
-template <int NMAX>
+// W of at most kOutWlFloats floats (60 KiB) is staged in LDS, at most
+// kOutStage per thread of the 1024-thread block.
+constexpr int kOutStage = 15;
+constexpr int kOutWlFloats = kOutStage * 1024;
+
+template <int NMAX, bool WL>
 __global__ void __launch_bounds__(1024) out_layer_kernel(OutLayerArgs p, int rows_per_block) {
   // rows per group and k per lane per chunk, sized to stay within the 128
   // registers a 1024-thread block allows
   constexpr int RG = NMAX >= 16 ? 1 : 4;
-  constexpr int C = NMAX >= 16 ? 2 : 4;
+  constexpr int C = NMAX >= 16 ? (WL ? 4 : 2) : 4;
   __shared__ float wave_loss[16];
+  extern __shared__ float w_lds[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int waves = blockDim.x >> 6;
   const int r0 = blockIdx.x * rows_per_block;
@@ -129,9 +150,21 @@ __global__ void __launch_bounds__(1024) out_layer_kernel(OutLayerArgs p, int row
   const bool single = gridDim.x == 1;
   StepNext next{};
   if (single && threadIdx.x == 0) next = step_prefetch(p.scalars, p.bc_table, p.bc_len);
+  if constexpr (WL) {
+    // W to LDS: coalesced, every load issued before the first store
+    const int KN = p.K * N;
+    float t[kOutStage];
+#pragma unroll
+    for (int it = 0; it < kOutStage; ++it) t[it] = p.W[min((int)threadIdx.x + 1024 * it, KN - 1)];
+#pragma unroll
+    for (int it = 0; it < kOutStage; ++it)
+      if ((int)threadIdx.x + 1024 * it < KN) w_lds[threadIdx.x + 1024 * it] = t[it];
+    __syncthreads();
+  }
   float bias[NMAX];
 #pragma unroll
-  for (int j = 0; j < NMAX; ++j) bias[j] = lane == 0 && j < N ? p.bias[j] : 0.0f;
+  for (int j = 0; j < NMAX; ++j) bias[j] = p.bias[min(j, N - 1)];
+  const bool mse = p.loss == VOLTA_LOSS_MSE;
   float wl = 0.0f;
   for (int m0 = r0 + wave; m0 < r1; m0 += waves * RG) {
     int rows[RG];
@@ -141,18 +174,14 @@ __global__ void __launch_bounds__(1024) out_layer_kernel(OutLayerArgs p, int row
     for (int g = 0; g < RG; ++g) {
       const int m = m0 + g * waves;
       rows[g] = m < r1 ? m : -1;
-      lab[g] = 0;
-      if (lane == 0 && rows[g] >= 0) {
-        if (p.loss == VOLTA_LOSS_MSE) {
+      const int mc = m < r1 ? m : r0;  // clamped: a row this block owns
+      // targets (MSE) or label (CE) of the row, loaded by every lane
 #pragma unroll
-          for (int j = 0; j < NMAX; ++j) y[g][j] = j < N ? p.y[(size_t)m * N + j] : 0.0f;
-        } else {
-          lab[g] = p.labels[m];
-        }
-      }
+      for (int j = 0; j < NMAX; ++j) y[g][j] = mse ? p.y[(size_t)mc * N + min(j, N - 1)] : 0.0f;
+      lab[g] = mse ? 0 : p.labels[mc];
     }
     float z[RG][NMAX];
-    wave_rows<NMAX, RG, C>(p, rows, z);
+    wave_rows<NMAX, RG, C, WL>(p, w_lds, rows, z);
     if (lane == 0) {
 #pragma unroll
       for (int g = 0; g < RG; ++g) {
@@ -188,29 +217,52 @@ __global__ void __launch_bounds__(64) loss_finish_kernel(OutLayerArgs p, int blo
 }
 
 // delta_out[b][j] = (sum_{k<K} delta[b][k] * W[j][k]) * f'(layer below)[b][j]
-// for K <= 16 (reference order: k ascending, :919-929).
+// for K <= KMAX <= 16 (reference order: k ascending, :919-929).  Thread j of
+// a block keeps row j of W in registers for the block's RB batch rows, whose
+// deltas are staged in LDS; its loads (W row, then the activation operands
+// of all RB rows) are unconditional (clamped indices) and issued together.
+// RB = 16 on large layers (the W row is loaded once per 16 outputs), 1 on
+// small ones (more blocks).
+template <int KMAX, int RB>
 __global__ void __launch_bounds__(256)
 outer_dx_kernel(const float* __restrict__ delta, const float* __restrict__ W, int B, int R, int K, int act,
                 const float* __restrict__ aux_act, const float* __restrict__ aux_pre, float* __restrict__ out) {
-  const size_t total = (size_t)B * R;
-  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
-       idx += (size_t)gridDim.x * blockDim.x) {
-    const int b = (int)(idx / R), j = (int)(idx % R);
-    const float* d = delta + (size_t)b * K;
-    const float* w = W + (size_t)j * K;
-    const float y = aux_act[idx];
-    const float pre = (aux_pre ? aux_pre : aux_act)[idx];
+  static_assert(RB * KMAX <= 256, "one staged delta per thread");
+  __shared__ float sd[RB * KMAX];
+  const int t = threadIdx.x;
+  const int j = blockIdx.x * 256 + t, jc = min(j, R - 1);
+  const int b0 = blockIdx.y * RB;
+  const float dv = delta[(size_t)min(b0 + t / KMAX, B - 1) * K + min(t % KMAX, K - 1)];
+  float wv[KMAX];
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) wv[k] = W[(size_t)jc * K + min(k, K - 1)];
+  const float* pp = aux_pre ? aux_pre : aux_act;
+  float y[RB], pr[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const size_t o = (size_t)min(b0 + r, B - 1) * R + jc;
+    y[r] = aux_act[o];
+    pr[r] = pp[o];
+  }
+  if (t < RB * KMAX) sd[t] = dv;
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
     float s = 0.0f;
-    for (int k = 0; k < K; ++k) s = s + d[k] * w[k];
-    out[idx] = s * act_derivative(act, pre, y);
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      const float u = s + sd[r * KMAX + k] * wv[k];
+      s = k < K ? u : s;
+    }
+    if (j < R && b0 + r < B) out[(size_t)(b0 + r) * R + j] = s * act_derivative(act, pr[r], y[r]);
   }
 }
 
-// Stand-alone launch: one wave per block, so R/64 CUs share the loads.
+// Stand-alone launch: 64 rows of W per block.
 template <int NMAX>
-__global__ void __launch_bounds__(64) narrow_dw_kernel(NarrowDwArgs p) {
-  extern __shared__ float sdelta[];
-  narrow_dw_block<NMAX>(p, blockIdx.x, sdelta);
+__global__ void __launch_bounds__(kNarrowThreads) narrow_dw_kernel(NarrowDwArgs p) {
+  extern __shared__ float lds[];
+  narrow_dw_block<NMAX>(p, blockIdx.x, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -221,39 +273,59 @@ hipError_t launch_out_layer(const OutLayerArgs& p, hipStream_t st) {
   const int blocks = out_layer_blocks(p.B);
   const int rows = blocks == 1 ? p.B : 16;
   if (blocks > 1 && !p.partials) return hipErrorInvalidValue;
-  if (p.N <= 1)
-    hipLaunchKernelGGL(out_layer_kernel<1>, dim3(blocks), dim3(1024), 0, st, p, rows);
-  else if (p.N <= 4)
-    hipLaunchKernelGGL(out_layer_kernel<4>, dim3(blocks), dim3(1024), 0, st, p, rows);
-  else
-    hipLaunchKernelGGL(out_layer_kernel<16>, dim3(blocks), dim3(1024), 0, st, p, rows);
+  // with one column, lanes read consecutive floats of W: no staging needed
+  const bool wl = p.N > 1 && (size_t)p.K * p.N <= (size_t)kOutWlFloats;
+  const size_t lds = wl ? (size_t)p.K * p.N * sizeof(float) : 0;
+  if (p.N <= 1) {
+    if (wl) hipLaunchKernelGGL((out_layer_kernel<1, true>), dim3(blocks), dim3(1024), lds, st, p, rows);
+    else hipLaunchKernelGGL((out_layer_kernel<1, false>), dim3(blocks), dim3(1024), 0, st, p, rows);
+  } else if (p.N <= 4) {
+    if (wl) hipLaunchKernelGGL((out_layer_kernel<4, true>), dim3(blocks), dim3(1024), lds, st, p, rows);
+    else hipLaunchKernelGGL((out_layer_kernel<4, false>), dim3(blocks), dim3(1024), 0, st, p, rows);
+  } else {
+    if (wl) hipLaunchKernelGGL((out_layer_kernel<16, true>), dim3(blocks), dim3(1024), lds, st, p, rows);
+    else hipLaunchKernelGGL((out_layer_kernel<16, false>), dim3(blocks), dim3(1024), 0, st, p, rows);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || blocks == 1) return e;
   hipLaunchKernelGGL(loss_finish_kernel, dim3(1), dim3(64), 0, st, p, blocks);
   return hipGetLastError();
 }
 
+template <int KMAX>
+static void launch_outer_k(bool big, dim3 blocks, hipStream_t st, const float* delta, const float* W, int B, int R,
+                           int K, int act, const float* aux_act, const float* aux_pre, float* out) {
+  if (big)
+    hipLaunchKernelGGL((outer_dx_kernel<KMAX, 16>), blocks, dim3(256), 0, st, delta, W, B, R, K, act, aux_act,
+                       aux_pre, out);
+  else
+    hipLaunchKernelGGL((outer_dx_kernel<KMAX, 1>), blocks, dim3(256), 0, st, delta, W, B, R, K, act, aux_act,
+                       aux_pre, out);
+}
+
 hipError_t launch_outer_dx(const float* delta, const float* W, int B, int R, int K, int act, const float* aux_act,
                            const float* aux_pre, float* out, hipStream_t st) {
   if (K > 16 || K < 1) return hipErrorInvalidValue;
-  const size_t total = (size_t)B * R;
-  const int blocks = (int)std::min<size_t>((total + 255) / 256, 8192);
-  hipLaunchKernelGGL(outer_dx_kernel, dim3(blocks), dim3(256), 0, st, delta, W, B, R, K, act, aux_act, aux_pre,
-                     out);
+  // 16 batch rows per block once the layer has a million outputs
+  const bool big = (size_t)B * R >= ((size_t)1 << 20);
+  const dim3 blocks((R + 255) / 256, (B + (big ? 16 : 1) - 1) / (big ? 16 : 1));
+  if (K <= 1) launch_outer_k<1>(big, blocks, st, delta, W, B, R, K, act, aux_act, aux_pre, out);
+  else if (K <= 4) launch_outer_k<4>(big, blocks, st, delta, W, B, R, K, act, aux_act, aux_pre, out);
+  else launch_outer_k<16>(big, blocks, st, delta, W, B, R, K, act, aux_act, aux_pre, out);
   return hipGetLastError();
 }
 
 hipError_t launch_narrow_dw(const NarrowDwArgs& p, hipStream_t st) {
   if (p.N > 16 || p.N < 1 || (size_t)p.B * p.N * sizeof(float) > kNarrowDwLdsBytes) return hipErrorInvalidValue;
   if (p.opt != VOLTA_OPT_SGD && p.opt != VOLTA_OPT_ADAM && p.opt != VOLTA_OPT_ADAGRAD) return hipErrorInvalidValue;
-  const int blocks = (p.R + 63) / 64;
-  const size_t lds = (size_t)p.B * p.N * sizeof(float);
+  const int blocks = (p.R + kNarrowRows - 1) / kNarrowRows;
+  const dim3 block(kNarrowThreads);
   if (p.N <= 1)
-    hipLaunchKernelGGL(narrow_dw_kernel<1>, dim3(blocks), dim3(64), lds, st, p);
+    hipLaunchKernelGGL(narrow_dw_kernel<1>, dim3(blocks), block, narrow_lds_floats<1>(p.B, p.N) * 4, st, p);
   else if (p.N <= 4)
-    hipLaunchKernelGGL(narrow_dw_kernel<4>, dim3(blocks), dim3(64), lds, st, p);
+    hipLaunchKernelGGL(narrow_dw_kernel<4>, dim3(blocks), block, narrow_lds_floats<4>(p.B, p.N) * 4, st, p);
   else
-    hipLaunchKernelGGL(narrow_dw_kernel<16>, dim3(blocks), dim3(64), lds, st, p);
+    hipLaunchKernelGGL(narrow_dw_kernel<16>, dim3(blocks), block, narrow_lds_floats<16>(p.B, p.N) * 4, st, p);
   return hipGetLastError();
 }
 
