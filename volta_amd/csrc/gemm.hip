@@ -694,7 +694,7 @@ gemm_f32_mfma(GemmArgs args) {
 // accumulators, then the waves' tiles, are added as pairwise trees: a fixed
 // order, with shorter rounding chains than one running sum.
 // ---------------------------------------------------------------------------
-constexpr int kSmallChunk = 8;     // 16-k groups per register chunk (128 k)
+constexpr int kSmallChunk = 16;    // 16-k groups per register chunk (256 k)
 constexpr int kSmallRedStride = 80;  // LDS floats per (wave, register) row of partials
 template <int NW>
 struct SmallLds {
@@ -736,40 +736,41 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
   const int kbeg = wave * kq, kend = min(K, kbeg + kq);
   const bool row_ok = m0 + r < M, col_ok = n0 + r < N;
   const int lda = args.lda, ldb = args.ldb;
-  // lane's base pointers: A row m0+r at k offset 4q; B row n0+r (NT) or
-  // column n0+r (NN)
-  const float* pa = args.A + (size_t)(row_ok ? m0 + r : 0) * lda + 4 * q;
-  const float* pb = B_KC ? args.B + (size_t)(col_ok ? n0 + r : 0) * ldb + 4 * q : args.B + (col_ok ? n0 + r : 0);
+  // lane's base pointers: A row m0+r; B row n0+r (NT) or column n0+r (NN)
+  // (row 0 / column 0 stand in for rows and columns outside the matrix)
+  const float* pa = args.A + (size_t)(row_ok ? m0 + r : 0) * lda;
+  const float* pb = B_KC ? args.B + (size_t)(col_ok ? n0 + r : 0) * ldb : args.B + (col_ok ? n0 + r : 0);
 
+  // A chunk's loads: per group unconditional within the lane (k clamped
+  // into the wave's range), keeping the raw values; compute() replaces those
+  // outside the matrix by zero.  (Guarded loads, or selects placed between
+  // the loads, make the compiler wait for earlier loads in the middle of
+  // the chunk.)  Groups past the wave's range are skipped as a whole
+  // (wave-uniform).  Only called with kc < kend.
   auto load = [&](floatx4(&fa)[kSmallChunk], floatx4(&fb)[kSmallChunk], int kc) {
 #pragma unroll
     for (int g = 0; g < kSmallChunk; ++g) {
-      const int kb = kc + 16 * g;
-      const int k = kb + 4 * q;  // this lane's first k of the group
-      floatx4 x = {0.f, 0.f, 0.f, 0.f}, y = {0.f, 0.f, 0.f, 0.f};
+      if (kc + 16 * g >= kend) break;
+      const int k = kc + 16 * g + 4 * q;  // this lane's first k of the group
       if (VEC) {  // K % 4 == 0 and every range bound is a multiple of 4
-        if (k < kend) {
-          if (row_ok) x = *reinterpret_cast<const floatx4*>(pa + kb);
-          if (col_ok) {
-            if (B_KC) {
-              y = *reinterpret_cast<const floatx4*>(pb + kb);
-            } else {
+        const int kl = min(k, kend - 4);
+        fa[g] = *reinterpret_cast<const floatx4*>(pa + kl);
+        if (B_KC) {
+          fb[g] = *reinterpret_cast<const floatx4*>(pb + kl);
+        } else {
 #pragma unroll
-              for (int s = 0; s < 4; ++s) y[s] = pb[(size_t)(k + s) * ldb];
-            }
-          }
+          for (int s = 0; s < 4; ++s) fb[g][s] = pb[(size_t)(kl + s) * ldb];
         }
       } else {
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-          if (k + s < kend) {
-            if (row_ok) x[s] = pa[kb + s];
-            if (col_ok) y[s] = B_KC ? pb[kb + s] : pb[(size_t)(k + s) * ldb];
-          }
+        for (int s = 0; s < 4; ++s) {
+          const int kl = min(k + s, kend - 1);
+          fa[g][s] = pa[kl];
+          fb[g][s] = B_KC ? pb[kl] : pb[(size_t)kl * ldb];
+        }
       }
-      fa[g] = x;
-      fb[g] = y;
     }
+    __builtin_amdgcn_sched_barrier(0);
   };
   floatx4 acc[4];
 #pragma unroll
@@ -779,26 +780,24 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
 #pragma unroll
     for (int g = 0; g < kSmallChunk; ++g) {
       if (kc + 16 * g < kend) {  // wave-uniform
+        const int k = kc + 16 * g + 4 * q;
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-          acc[g & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[g][s], fb[g][s], acc[g & 3], 0, 0, 0);
+        for (int s = 0; s < 4; ++s) {
+          const bool in = VEC ? k < kend : k + s < kend;
+          const float x = in && row_ok ? fa[g][s] : 0.0f;
+          const float y = in && col_ok ? fb[g][s] : 0.0f;
+          acc[g & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, y, acc[g & 3], 0, 0, 0);
+        }
       }
     }
   };
-  // Two register chunks: the next chunk's loads are in flight while the
-  // current one's MFMAs run.
-  floatx4 fa0[kSmallChunk], fb0[kSmallChunk], fa1[kSmallChunk], fb1[kSmallChunk];
-  constexpr int kStep = 16 * kSmallChunk;
-  int kc = kbeg;
-  if (kc < kend) load(fa0, fb0, kc);
-  while (kc < kend) {
-    if (kc + kStep < kend) load(fa1, fb1, kc + kStep);
-    compute(fa0, fb0, kc);
-    kc += kStep;
-    if (kc >= kend) break;
-    if (kc + kStep < kend) load(fa0, fb0, kc + kStep);
-    compute(fa1, fb1, kc);
-    kc += kStep;
+  // One register chunk covers the wave's range for K <= 256 * waves (every
+  // small-batch product of the step): all its loads are in flight together,
+  // then its MFMAs run.  Longer ranges take one memory latency per chunk.
+  floatx4 fa[kSmallChunk], fb[kSmallChunk];
+  for (int kc = kbeg; kc < kend; kc += 16 * kSmallChunk) {
+    load(fa, fb, kc);
+    compute(fa, fb, kc);
   }
 
   // Partial tiles to LDS: row (wave, v) holds register v of every lane.
@@ -1160,10 +1159,11 @@ static hipError_t launch_reduce(const GemmArgs& a, int splits, hipStream_t st) {
 
 // Small-M products: NN with BIAS_ACT / STORE, NT with DX_ACT / STORE.
 // Waves per workgroup of a stand-alone small-M launch (VOLTA_SMALLM_WAVES,
-// 4 or 8); a paired launch always has 4.
+// 8 by default or 4; measured at B=64: C2 0.0663 vs 0.0686 ms/step, C1
+// 0.0391 vs 0.0400); a paired launch always has 4.
 static int smallm_waves() {
   const char* w = std::getenv("VOLTA_SMALLM_WAVES");
-  return w && std::atoi(w) == 8 ? 8 : 4;
+  return w && std::atoi(w) == 4 ? 4 : 8;
 }
 
 template <bool B_KC, int EPI>
