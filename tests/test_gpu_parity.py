@@ -110,11 +110,12 @@ def test_gemm_integer_exact(layout, M, N, K, tile):
     np.testing.assert_array_equal(got, want)
 
 
-@pytest.mark.parametrize("layout", [0, 1], ids=["NN", "NT"])
+@pytest.mark.parametrize("layout", [0], ids=["NN"])
 @pytest.mark.parametrize("M,N,K", [(64, 512, 256), (33, 130, 257), (7, 5, 3), (64, 64, 1024)])
 def test_gemm_smallm_8_waves_integer_exact(layout, M, N, K):
-    """The 8-wave small-M workgroup (eighths of K, two four-tile trees) is
-    exact on integer operands, ragged shapes included."""
+    """The 8-wave small-M workgroup (eighths of K, two four-tile trees; the
+    forward products' default) is exact on integer operands, ragged shapes
+    included."""
     say(f"gemm small-M 8 waves layout={layout} M={M} N={N} K={K}")
     rng = np.random.default_rng(M * 5 + N * 3 + K)
     A = rng.integers(-4, 5, (M, K)).astype(np.float32)
@@ -147,8 +148,8 @@ def test_gemm_smallm_rejects_tn():
 @pytest.mark.parametrize("waves", ["4", "8"])
 def test_gemm_smallm_float_bound(layout, M, N, K, waves):
     """Random fp32 operands on the small-M tile with 4 or 8 waves per
-    workgroup (VOLTA_SMALLM_WAVES): within the fp32 error bound of a K-term
-    sum of the fp64 product."""
+    workgroup (VOLTA_SMALLM_WAVES; the NT product always takes 4): within the
+    fp32 error bound of a K-term sum of the fp64 product."""
     say(f"gemm small-M float layout={layout} M={M} N={N} K={K} waves={waves}")
     rng = np.random.default_rng(M + N + K + layout)
     A = rng.standard_normal((M, K)).astype(np.float32)
@@ -353,15 +354,15 @@ def test_sgd_config_parity_with_oracle(name):
 
 SMALL_BATCH_PLANS = {
     "tiles64": {"VOLTA_SMALLM_MAX_M": "0", "VOLTA_DW_SMALLK_MAX_K": "0"},
-    "smallm_dw64": {"VOLTA_SMALLM_MAX_M": "128", "VOLTA_DW_SMALLK_MAX_K": "0"},
-    "default": {"VOLTA_SMALLM_MAX_M": "128", "VOLTA_DW_SMALLK_MAX_K": "128"},
+    "smallm_dw64": {"VOLTA_SMALLM_MAX_M": "256", "VOLTA_DW_SMALLK_MAX_K": "0"},
+    "default": {"VOLTA_SMALLM_MAX_M": "256", "VOLTA_DW_SMALLK_MAX_K": "256"},
 }
 
 
-@pytest.mark.parametrize("name", ["c1_mlp256_relu_sgd_b64", "c4_silu_sgd_b128"])
+@pytest.mark.parametrize("name", ["c1_mlp256_relu_sgd_b64", "c4_silu_sgd_b128", "c4_silu_sgd_b256"])
 @pytest.mark.parametrize("plan", sorted(SMALL_BATCH_PLANS))
 def test_sgd_config_both_small_batch_plans(name, plan):
-    """At B <= 128 the forward and dX products run on the small-M tile and
+    """At B <= 256 the forward and dX products run on the small-M tile and
     the dW products on the small-K tile by default; VOLTA_SMALLM_MAX_M=0 and
     VOLTA_DW_SMALLK_MAX_K=0 switch them back to the 64x64 tiles (split-K with
     reduce launches).  Every plan stays within rel 1e-4 / abs 1e-5 of the

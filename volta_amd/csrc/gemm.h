@@ -74,9 +74,9 @@ struct GemmArgs {
 };
 
 // TILE_SMALLM: 16x16 output tiles, the whole K range in one workgroup
-// (split over its 4 waves), for NN/NT products with few rows (B <= 128).
+// (split over its 4 or 8 waves), for NN/NT products with few rows (B <= 256).
 // TILE_DW_SMALLK: 32x32 tiles of the TN (dW) product with a short K
-// (K = B <= 128), the optimizer applied on 16-byte rows.
+// (K = B <= 256), the optimizer applied on 16-byte rows.
 enum GemmTile { TILE_64x64 = 0, TILE_128x128 = 1, TILE_64x64_K64 = 2, TILE_SMALLM = 3, TILE_DW_SMALLK = 4 };
 
 struct GemmPlan {

@@ -826,7 +826,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
 }
 
 // ---------------------------------------------------------------------------
-// dW tile for a short reduction (K = B <= 128: the small-batch step).  A
+// dW tile for a short reduction (K = B <= 256: the small-batch step).  A
 // workgroup owns a 32x32 tile of W_i -- 4 elements per thread -- so a launch
 // keeps several workgroups on each CU and the optimizer arithmetic of one
 // overlaps the memory traffic of another.  (A 64x64 tile leaves about 1.5
@@ -1158,10 +1158,12 @@ static hipError_t launch_reduce(const GemmArgs& a, int splits, hipStream_t st) {
 }
 
 // Small-M products: NN with BIAS_ACT / STORE, NT with DX_ACT / STORE.
-// Waves per workgroup of a stand-alone small-M launch (VOLTA_SMALLM_WAVES,
-// 8 by default or 4; measured at B=64: C2 0.0663 vs 0.0686 ms/step, C1
-// 0.0391 vs 0.0400); a paired launch always has 4.
-static int smallm_waves() {
+// Waves per workgroup of a stand-alone forward (NN) small-M launch
+// (VOLTA_SMALLM_WAVES, 8 by default or 4; measured at B=64: C2 0.0663 vs
+// 0.0686 ms/step, C1 0.0391 vs 0.0400).  dX (NT) products always take 4, as
+// in a paired launch, so paired and separate launches give the same bits.
+static int smallm_waves(bool b_kc) {
+  if (b_kc) return 4;
   const char* w = std::getenv("VOLTA_SMALLM_WAVES");
   return w && std::atoi(w) == 4 ? 4 : 8;
 }
@@ -1169,7 +1171,7 @@ static int smallm_waves() {
 template <bool B_KC, int EPI>
 static hipError_t launch_smallm_epi(const GemmArgs& a, bool vec, hipStream_t st) {
   const int blocks = ((a.M + 15) / 16) * ((a.N + 15) / 16);
-  if (smallm_waves() == 8) {
+  if (smallm_waves(B_KC) == 8) {
     if (vec) hipLaunchKernelGGL((gemm_smallm<B_KC, true, EPI, 8>), dim3(blocks), dim3(512), 0, st, a);
     else hipLaunchKernelGGL((gemm_smallm<B_KC, false, EPI, 8>), dim3(blocks), dim3(512), 0, st, a);
   } else {
@@ -1339,7 +1341,7 @@ bool pair_supported(const PairOp& a, const PairOp& b) {
            (o.args.epi.kind != EPI_DW_OPT || (size_t)o.args.M * o.args.epi.ldc < ((size_t)1 << 30));
   };
   auto narrow_ok = [](const PairOp& o) {
-    return o.nd.N >= 1 && o.nd.N <= 16 &&
+    return o.nd.N >= 1 && o.nd.N <= 16 && o.nd.B >= 1 && o.nd.B <= kNarrowMaxB &&
            (o.nd.opt == VOLTA_OPT_SGD || o.nd.opt == VOLTA_OPT_ADAM || o.nd.opt == VOLTA_OPT_ADAGRAD);
   };
   const PairOp* ops[2] = {&a, &b};
@@ -1467,20 +1469,22 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus, bool 
   p.k_per_split = kps;
   // A product the 64x64 plan would split over K runs on the small-M tile
   // instead when it has few rows: the reduction over K stays inside each
-  // workgroup, which saves the reduce launch (B <= 128 by default;
-  // VOLTA_SMALLM_MAX_M changes the limit, 0 turns the tile off).
+  // workgroup, which saves the reduce launch (B <= 256 by default;
+  // VOLTA_SMALLM_MAX_M changes the limit, 0 turns the tile off).  Measured
+  // with the small-K dW tile below: C4 B=256 0.1624 -> 0.1415 ms/step; at
+  // B=1024 both tiles are slower than the 64x64 family (0.45 vs 0.30 ms).
   const char* sm = std::getenv("VOLTA_SMALLM_MAX_M");
-  const int small_max = sm && *sm ? std::atoi(sm) : 128;
+  const int small_max = sm && *sm ? std::atoi(sm) : 256;
   if (small_m && (layout == GEMM_NN || layout == GEMM_NT) && p.splits > 1 && M <= small_max) {
     p.tile = TILE_SMALLM;
     p.splits = 1;
     p.k_per_split = K;
   }
   // dW with a short reduction (K = B) on 32x32 tiles: more workgroups per
-  // CU to overlap the optimizer's streaming and arithmetic (K <= 128 by
+  // CU to overlap the optimizer's streaming and arithmetic (K <= 256 by
   // default; VOLTA_DW_SMALLK_MAX_K changes the limit, 0 turns the tile off).
   const char* dk = std::getenv("VOLTA_DW_SMALLK_MAX_K");
-  const int dw_kmax = dk && *dk ? std::atoi(dk) : 128;
+  const int dw_kmax = dk && *dk ? std::atoi(dk) : 256;
   if (layout == GEMM_TN && vec && M % 4 == 0 && N % 4 == 0 && K <= dw_kmax) {
     p.tile = TILE_DW_SMALLK;
     p.splits = 1;

@@ -13,6 +13,8 @@ namespace volta {
 // it needs beyond the staged deltas (the waves' partial sums).
 constexpr int kNarrowThreads = 256;
 constexpr int kNarrowRows = 64;
+// Deltas a thread stages at most (B <= kNarrowMaxB, N <= 16).
+constexpr int kNarrowStage = kNarrowMaxB * 16 / kNarrowThreads;
 template <int NMAX>
 struct NarrowLds {
   static constexpr int kPartials = (kNarrowThreads / 64) * NMAX * 64;
@@ -39,11 +41,13 @@ __host__ __device__ inline int narrow_lds_floats_n(int B, int N) {
 // added pairwise.  Latency: every global load is unconditional (clamped
 // addresses; values outside the batch are never used); the delta staging
 // loads go first, so staging waits for them alone, then the activations
-// (16 a thread) and wave 0's optimizer state; the staged deltas are read
-// from LDS in batches before the multiplies, and guards are selects.
+// (16 a thread for each of up to four 64-row chunks a round) and wave 0's
+// optimizer state; the staged deltas are read from LDS in batches before
+// the multiplies, and guards are selects.
 template <int NMAX>
 __device__ __forceinline__ void narrow_dw_block(const NarrowDwArgs& p, int block, float* lds) {
   constexpr int kQ = 16;  // batch rows per wave per 64-row chunk
+  constexpr int kU = 4;   // 64-row chunks whose loads one round issues together
   constexpr int kDBatch = NMAX == 1 ? 16 : NMAX <= 4 ? 8 : 2;  // batch rows per LDS read batch
   const int B = p.B, N = p.N, R = p.R;
   const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
@@ -54,12 +58,24 @@ __device__ __forceinline__ void narrow_dw_block(const NarrowDwArgs& p, int block
   const int BN = B * N;
   float* sdelta = lds;
   float* part = lds + (BN + 3) / 4 * 4;  // part[(q*NMAX + k)*64 + lane]
-  const bool one = BN <= kNarrowThreads;  // one staged delta per thread at most
-  float dst = 0.0f;
-  if (one) dst = p.delta[min(tid, BN - 1)];
-  float a[kQ];
+  // staged deltas: at most kNarrowStage per thread (B <= kNarrowMaxB, N <= 16)
+  float dst[kNarrowStage];
 #pragma unroll
-  for (int c = 0; c < kQ; ++c) a[c] = p.act[(size_t)min(kQ * q + c, B - 1) * R + jc];
+  for (int i = 0; i < kNarrowStage; ++i) {
+    if (i * kNarrowThreads >= BN) break;  // block-uniform
+    dst[i] = p.delta[min(tid + i * kNarrowThreads, BN - 1)];
+  }
+  // activations of a round: chunk u holds batch rows b0 + 64u + 16q + c
+  float a[kU][kQ];
+  auto load_round = [&](int b0) {
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      if (b0 + 64 * u >= B) break;  // wave-uniform
+#pragma unroll
+      for (int c = 0; c < kQ; ++c) a[u][c] = p.act[(size_t)min(b0 + 64 * u + kQ * q + c, B - 1) * R + jc];
+    }
+  };
+  load_round(0);
   float w[NMAX], s1[NMAX], s2[NMAX];
   const float* pm = sgd ? p.w : p.m;
   const float* pv = adam ? p.v : p.w;
@@ -79,35 +95,37 @@ __device__ __forceinline__ void narrow_dw_block(const NarrowDwArgs& p, int block
   const float bs2 = (adam && p.b ? p.bv : pb)[kb];
   const float lr = p.scalars->lr;
   const AdamRcp rc = adam_rcp(p.scalars->bc1, p.scalars->bc2);
-  if (one) {
-    if (tid < BN) sdelta[tid] = dst;
-  } else {
-    for (int i = tid; i < BN; i += kNarrowThreads) sdelta[i] = p.delta[i];
+#pragma unroll
+  for (int i = 0; i < kNarrowStage; ++i) {
+    if (i * kNarrowThreads >= BN) break;
+    if (tid + i * kNarrowThreads < BN) sdelta[tid + i * kNarrowThreads] = dst[i];
   }
   __syncthreads();
 
   float acc[NMAX];
 #pragma unroll
   for (int k = 0; k < NMAX; ++k) acc[k] = 0.0f;
-  for (int b0 = 0; b0 < B; b0 += 4 * kQ) {
-    if (b0 > 0) {
+  for (int r0 = 0; r0 < B; r0 += 64 * kU) {
+    if (r0 > 0) load_round(r0);
 #pragma unroll
-      for (int c = 0; c < kQ; ++c) a[c] = p.act[(size_t)min(b0 + kQ * q + c, B - 1) * R + jc];
-    }
+    for (int u = 0; u < kU; ++u) {
+      const int b0 = r0 + 64 * u;
+      if (b0 >= B) break;  // wave-uniform
 #pragma unroll
-    for (int c0 = 0; c0 < kQ; c0 += kDBatch) {
-      float d[kDBatch][NMAX];
+      for (int c0 = 0; c0 < kQ; c0 += kDBatch) {
+        float d[kDBatch][NMAX];
 #pragma unroll
-      for (int c = 0; c < kDBatch; ++c)
+        for (int c = 0; c < kDBatch; ++c)
 #pragma unroll
-        for (int k = 0; k < NMAX; ++k) d[c][k] = sdelta[min(b0 + kQ * q + c0 + c, B - 1) * N + min(k, N - 1)];
+          for (int k = 0; k < NMAX; ++k) d[c][k] = sdelta[min(b0 + kQ * q + c0 + c, B - 1) * N + min(k, N - 1)];
 #pragma unroll
-      for (int c = 0; c < kDBatch; ++c) {
-        const bool in = b0 + kQ * q + c0 + c < B;
+        for (int c = 0; c < kDBatch; ++c) {
+          const bool in = b0 + kQ * q + c0 + c < B;
 #pragma unroll
-        for (int k = 0; k < NMAX; ++k) {
-          const float t = acc[k] + a[c0 + c] * d[c][k];
-          acc[k] = in && k < N ? t : acc[k];
+          for (int k = 0; k < NMAX; ++k) {
+            const float t = acc[k] + a[u][c0 + c] * d[c][k];
+            acc[k] = in && k < N ? t : acc[k];
+          }
         }
       }
     }

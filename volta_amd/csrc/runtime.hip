@@ -634,7 +634,7 @@ static bool build(Handle* h) {
   const int Ln = h->L[n];
   h->out_mode = Ln <= 16 ? OUT_NARROW : Ln <= 64 ? OUT_GEMM_LOSS : OUT_GEMM;
   h->narrow_dx = Ln <= 16 && n > 1;
-  h->narrow_dw = Ln <= 16 && (size_t)B * Ln * sizeof(float) <= kNarrowDwLdsBytes;
+  h->narrow_dw = Ln <= 16 && B <= kNarrowMaxB;
   size_t ws_floats = 0;
   int max_tiles = 1;
   for (int i = 0; i < n; ++i) {

@@ -42,9 +42,9 @@ struct NarrowDwArgs {
   DevScalars* scalars;
 };
 
-// Largest staged delta (B x N floats) of the narrow dW; its partial sums
-// (16 KiB at most) come on top.
-constexpr size_t kNarrowDwLdsBytes = 48 * 1024;
+// Largest batch the narrow dW serves (one round of four 64-row chunks of
+// the batch); larger batches take the TN GEMM.
+constexpr int kNarrowMaxB = 256;
 
 int out_layer_blocks(int B);
 hipError_t launch_out_layer(const OutLayerArgs& p, hipStream_t st);

@@ -316,7 +316,7 @@ hipError_t launch_outer_dx(const float* delta, const float* W, int B, int R, int
 }
 
 hipError_t launch_narrow_dw(const NarrowDwArgs& p, hipStream_t st) {
-  if (p.N > 16 || p.N < 1 || (size_t)p.B * p.N * sizeof(float) > kNarrowDwLdsBytes) return hipErrorInvalidValue;
+  if (p.N > 16 || p.N < 1 || p.B < 1 || p.B > kNarrowMaxB) return hipErrorInvalidValue;
   if (p.opt != VOLTA_OPT_SGD && p.opt != VOLTA_OPT_ADAM && p.opt != VOLTA_OPT_ADAGRAD) return hipErrorInvalidValue;
   const int blocks = (p.R + kNarrowRows - 1) / kNarrowRows;
   const dim3 block(kNarrowThreads);
