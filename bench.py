@@ -18,7 +18,9 @@ The JSON line also carries:
                 flops per launch / its average duration, timed with HIP events
                 on the handle's stream (kernel-by-kernel replay of the step);
   cpu_baseline  the CPU oracle (C++ restatement of Volta's compile-train step,
-                OpenMP GEMMs) on this host's cores, on a bounded sample.
+                OpenMP GEMMs) on this host's cores, on a bounded sample;
+  runtime_optimizer  the runtime optimizer (Backend::apply_gradients path,
+                include/volta_backend.h) over C5's parameter tensors, Adam.
 """
 from __future__ import annotations
 
@@ -180,6 +182,42 @@ def run_gpu(name, steps, warmup, want_profile=True):
         out["kernel_sum_ms"] = sum(r["ms"] for r in rows)
     t.close()
     return spec, B, lr, out
+
+
+def run_rt_optimizer(name="c5", kind="adam", reps=20):
+    """The runtime optimizer (volta_rt_apply_gradients, Backend::apply_gradients
+    of the reference's runtime) over the parameter tensors of a workload:
+    one multi-tensor launch per call; HBM-bound, 28 bytes per element for
+    Adam (p, m, v read and written, g read)."""
+    from volta_amd import DeviceArray
+    from volta_amd.backend import RtOptimizer, config
+
+    spec, _, _ = WORKLOADS[name]
+    lib = load_hip()
+    rng = np.random.default_rng(1)
+    counts = []
+    for r, c in spec.shapes():
+        counts += [r * c, c]
+    params = [DeviceArray(rng.standard_normal(n).astype(np.float32), lib) for n in counts]
+    grads = [DeviceArray((rng.standard_normal(n) * 0.01).astype(np.float32), lib) for n in counts]
+    opt = RtOptimizer(lib.lib, counts)
+    cfg = config(kind, 1e-3)
+    pp, gp = [d.ptr for d in params], [d.ptr for d in grads]
+    opt.apply(cfg, pp, gp)  # state allocation, warm-up
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        opt.apply(cfg, pp, gp)
+    dt = (time.perf_counter() - t0) / reps
+    n = sum(counts)
+    nbytes = {"sgd": 12, "adagrad": 20, "adam": 28, "adamw": 28}[kind] * n
+    out = {"workload": name, "optimizer": kind, "tensors": len(counts), "elements": n,
+           "ms_per_call": round(dt * 1e3, 4), "algorithmic_bytes": nbytes,
+           "achieved_GBs": round(nbytes / dt / 1e9, 1), "frac_hbm": round(nbytes / dt / 1e9 / PEAK_HBM_GBS, 4),
+           "note": "synchronous call: one multi-tensor launch plus a descriptor upload and a stream synchronize"}
+    opt.close()
+    for d in params + grads:
+        d.free()
+    return out
 
 
 def run_cpu(name, budget_s=10.0, max_steps=200):
@@ -418,6 +456,9 @@ def main():
     if not a.no_cpu:
         line["cpu_baseline"] = run_cpu(a.config)
         log(f"cpu baseline: {line['cpu_baseline']}")
+    if not a.no_profile:
+        line["runtime_optimizer"] = run_rt_optimizer()
+        log(f"runtime optimizer: {line['runtime_optimizer']}")
     if a.secondary and a.secondary != "none":
         s_steps = max(5, a.steps // 20)
         s_spec, s_B, s_lr, s_res = run_gpu(a.secondary, s_steps, max(2, a.warmup // 10),

@@ -59,3 +59,32 @@ def test_hip_code_object_is_gfx950():
     blob = open(HIP_LIB, "rb").read()
     targets = set(re.findall(rb"amdgcn-amd-amdhsa--(gfx\w+)", blob))
     assert targets == {b"gfx950"}, targets
+
+
+def test_backend_header_symbols_exported_by_hip_and_oracle():
+    """Every function include/volta_backend.h declares (the runtime optimizer
+    boundary) is exported by libvolta_hip.so and by the CPU oracle."""
+    import ctypes
+
+    from tests.oracle_lib import load_oracle
+    from volta_amd.backend import _SIGS
+
+    names = header_functions("volta_backend.h")
+    assert sorted(_SIGS) == names
+    oracle = load_oracle().lib
+    for name in names:
+        assert hasattr(oracle, name), name
+    if os.path.exists(HIP_LIB):
+        hip = ctypes.CDLL(HIP_LIB)
+        for name in names:
+            assert hasattr(hip, name), name
+
+
+@pytest.mark.skipif(not os.path.exists(HIP_LIB), reason="libvolta_hip.so not built")
+def test_hip_backend_capabilities_without_gpu():
+    """The capabilities a HIP backend reports need no device."""
+    from volta_amd.backend import capabilities
+
+    caps = capabilities(load_hip().lib)
+    assert caps["device_class"] == 1 and caps["vendor"] == 2 and caps["supports_adam"] == 1
+    assert caps["default_determinism"] == 0

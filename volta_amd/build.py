@@ -24,7 +24,7 @@ CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libvolta_hip.so")
 
-SOURCES = ["gemm.hip", "skinny.hip", "step_kernels.hip", "extras.hip", "runtime.hip", "test_hooks.hip",
+SOURCES = ["gemm.hip", "skinny.hip", "step_kernels.hip", "extras.hip", "runtime.hip", "test_hooks.hip", "rt_optimizer.hip",
            "spec.cpp", "vt_frontend.cpp"]
 HEADERS = ["gemm.h", "skinny.h", "step_kernels.h", "extras.h", "device_common.h", "recorder.h", "spec.h",
            "narrow_dw.h", "vt_frontend.h"]
