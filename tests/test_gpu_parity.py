@@ -646,6 +646,32 @@ def test_paired_backward_launches_bit_identical(name):
         np.testing.assert_array_equal(a, b)
 
 
+OUT_DX_CASES = {
+    "c2": (MlpSpec([512, 1024, 1024, 512, 256, 1], "relu", "adam"), 64, 1e-3),
+    "gelu_b37": (MlpSpec([96, 256, 128, 1], "gelu", "sgd"), 37, 0.01),
+    "ce10_b200": (MlpSpec([64, 192, 10], "silu", "adagrad", "ce"), 200, 1e-2),
+    "mse3_b256": (MlpSpec([32, 512, 3], "tanh", "adamw"), 256, 1e-3),
+}
+
+
+@pytest.mark.parametrize("name", sorted(OUT_DX_CASES))
+def test_merged_output_layer_dx_bit_identical(name):
+    """The output layer, its loss head and its dX in one launch
+    (out_layer_dx_kernel) against the separate output and outer-product
+    launches (VOLTA_NO_OUT_DX=1): parameters, activations and deltas after 4
+    steps bit-identical (same arithmetic per row); the loss equal up to the
+    order its block partials are added in."""
+    spec, B, lr = OUT_DX_CASES[name]
+    say(f"merged output layer + dX {name}")
+    l1, p1, b1 = _run_with_env({"VOLTA_NO_OUT_DX": "1"}, spec, B, lr, 4)
+    l2, p2, b2 = _run_with_env({"VOLTA_NO_OUT_DX": "0"}, spec, B, lr, 4)
+    np.testing.assert_allclose(l1, l2, rtol=1e-6, atol=0)
+    for a, b in zip(p1, p2):
+        np.testing.assert_array_equal(a, b)
+    for a, b in zip(b1, b2):
+        np.testing.assert_array_equal(a, b)
+
+
 # ---------------------------------------------------------------------------
 # ABI behaviour
 # ---------------------------------------------------------------------------

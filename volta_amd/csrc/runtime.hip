@@ -102,6 +102,7 @@ struct Handle {
   float* loss_partials = nullptr;  // one float per output-layer M-tile
   int out_mode = 0;           // OUT_NARROW / OUT_GEMM_LOSS / OUT_GEMM (output layer + loss head)
   bool narrow_dx = false;     // dX of the output layer as an outer product (L[n] <= 16)
+  bool out_dx_merged = false; // ... formed by the output layer's own launch (out_layer_dx_kernel)
   bool narrow_dw = false;     // dW of the output layer by narrow_dw_kernel
   bool keep_grads = false;    // also store dW/db in `grads` (VOLTA_KEEP_GRADS=1)
   DevScalars* scalars = nullptr;
@@ -235,11 +236,23 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
       o.scalars = h->scalars;
       o.bc_table = h->bc_table;
       o.bc_len = h->bc_len;
-      VOLTA_CHECK(launch_out_layer(o, st));
       // algorithmic bytes: 4(B*r + r*c + B*c) + loss head 8*B*c
+      const double fb = 4.0 * ((double)B * lp.r + (double)lp.r * lp.c + (double)B * lp.c) + 8.0 * B * lp.c;
+      if (h->out_dx_merged) {
+        // the output layer's dX_{n-1} in the same launch (row-local)
+        o.dx_act = s.activation;
+        o.dx_pre = h->pre[i - 1];
+        o.dx_out = h->delta[i - 1];
+        o.loss_counter = h->counters + h->n_counters - 1;
+        VOLTA_CHECK(launch_out_layer_dx(o, st));
+        // dX bytes: 4(B*c + r*c + 2*B*r), act re-read from cache not counted again
+        std::snprintf(label, sizeof label, "fwd%d+loss+dx%d", i, i);
+        VOLTA_CHECK(mark(rec, label, 4.0 * B * lp.r * lp.c, fb + 4.0 * (double)B * lp.r));
+        continue;
+      }
+      VOLTA_CHECK(launch_out_layer(o, st));
       std::snprintf(label, sizeof label, "fwd%d+loss", i);
-      VOLTA_CHECK(mark(rec, label, 2.0 * B * lp.r * lp.c,
-                       4.0 * ((double)B * lp.r + (double)lp.r * lp.c + (double)B * lp.c) + 8.0 * B * lp.c));
+      VOLTA_CHECK(mark(rec, label, 2.0 * B * lp.r * lp.c, fb));
       continue;
     }
     GemmArgs a{};
@@ -513,8 +526,8 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
     }
     return true;
   }
-  // dX_{n-1}
-  if (n > 1) {
+  // dX_{n-1} (already formed by the output launch when merged)
+  if (n > 1 && !h->out_dx_merged) {
     const int i = n - 1;
     const LayerPlan& lp = h->layers[i];
     std::snprintf(lx, sizeof lx, "dx%d", i);
@@ -634,6 +647,9 @@ static bool build(Handle* h) {
   const int Ln = h->L[n];
   h->out_mode = Ln <= 16 ? OUT_NARROW : Ln <= 64 ? OUT_GEMM_LOSS : OUT_GEMM;
   h->narrow_dx = Ln <= 16 && n > 1;
+  const char* nod = std::getenv("VOLTA_NO_OUT_DX");
+  h->out_dx_merged = h->narrow_dx && !h->extras() && !(nod && *nod && *nod != '0') &&
+                     out_layer_dx_supported(B, h->L[n - 1], Ln);
   h->narrow_dw = Ln <= 16 && B <= kNarrowMaxB;
   size_t ws_floats = 0;
   int max_tiles = 1;
@@ -703,7 +719,8 @@ static bool build(Handle* h) {
   req(&h->target, s.loss == VOLTA_LOSS_MSE ? (size_t)B * h->L[n] * 4 : (size_t)B * 4);
   if (ws_floats) req((void**)&h->gemm_ws, ws_floats * 4);
   req((void**)&h->counters, (size_t)h->n_counters * sizeof(unsigned));
-  req((void**)&h->loss_partials, (size_t)std::max((B + 63) / 64, out_layer_blocks(B)) * 4);
+  req((void**)&h->loss_partials,
+      (size_t)std::max({(B + 63) / 64, out_layer_blocks(B), out_layer_dx_blocks(B)}) * 4);
   size_t total = 0;
   for (auto& r : reqs) total += r.bytes;
   h->arena_bytes = total;

@@ -23,6 +23,11 @@ struct OutLayerArgs {
   DevScalars* scalars;
   const float2* bc_table;
   int bc_len;
+  // launch_out_layer_dx only: delta_{n-2} = (delta_{n-1} W^T) * f'(layer n-2)
+  int dx_act;               // activation of layer n-2 (enum volta_activation)
+  const float* dx_pre;      // its pre-activation [B x K] (null when not kept)
+  float* dx_out;            // delta_{n-2} [B x K]
+  unsigned* loss_counter;   // arrival ticket of the blocks (zero between launches)
 };
 
 struct NarrowDwArgs {
@@ -48,6 +53,13 @@ constexpr int kNarrowMaxB = 256;
 
 int out_layer_blocks(int B);
 hipError_t launch_out_layer(const OutLayerArgs& p, hipStream_t st);
+// The output layer, its loss head and the output layer's dX in one launch
+// (one batch row per wave, 4 rows per block; the last block to finish adds
+// the blocks' losses in block order).  For B <= kNarrowMaxB with a
+// K x N W of at most kOutWlFloats floats when N > 1.
+int out_layer_dx_blocks(int B);
+bool out_layer_dx_supported(int B, int K, int N);
+hipError_t launch_out_layer_dx(const OutLayerArgs& p, hipStream_t st);
 hipError_t launch_outer_dx(const float* delta, const float* W, int B, int R, int K, int act, const float* aux_act,
                            const float* aux_pre, float* out, hipStream_t st);
 hipError_t launch_narrow_dw(const NarrowDwArgs& p, hipStream_t st);

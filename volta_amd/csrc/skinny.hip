@@ -75,18 +75,16 @@ __device__ __forceinline__ void wave_rows(const OutLayerArgs& p, const float* wl
 
 // Loss head of one row (same definitions as the MFMA path's loss epilogue):
 // MSE (:792-798) d = z - y, loss += d^2, delta = 2d/nt; softmax-CE
-// (interpreter.rs:762-812, autograd.rs:467-534).  Returns the row's loss.
+// (interpreter.rs:762-812, autograd.rs:467-534).  head_delta forms the
+// row's deltas and returns its loss without storing anything, so every lane
+// of a wave can hold the deltas; head_row also stores z and the deltas.
 // `y` holds the row's targets (MSE), `lab` its label (CE), both loaded
 // before z was computed.  (Loops run to NMAX with a j < N guard so z stays
 // in registers.)
 template <int NMAX>
-__device__ __forceinline__ float head_row(const OutLayerArgs& p, const float* z, const float* y, int lab, int m) {
+__device__ __forceinline__ float head_delta(const OutLayerArgs& p, const float* z, const float* y, int lab,
+                                            float* d) {
   const int N = p.N;
-  float* out = p.out + (size_t)m * N;
-  float* d = p.delta + (size_t)m * N;
-#pragma unroll
-  for (int j = 0; j < NMAX; ++j)
-    if (j < N) out[j] = z[j];
   if (p.loss == VOLTA_LOSS_MSE) {
     const float nt = (float)(p.B * N);
     float acc = 0.0f;
@@ -96,6 +94,8 @@ __device__ __forceinline__ float head_row(const OutLayerArgs& p, const float* z,
         const float dj = z[j] - y[j];
         acc = acc + dj * dj;
         d[j] = 2.0f * dj / nt;
+      } else {
+        d[j] = 0.0f;
       }
     }
     return acc;
@@ -117,10 +117,29 @@ __device__ __forceinline__ float head_row(const OutLayerArgs& p, const float* z,
       const bool on = j == lab;
       if (on) sample = -(z[j] - lse);
       d[j] = (expf(z[j] - mx) / sum - (on ? 1.0f : 0.0f)) / bf;
+    } else {
+      d[j] = 0.0f;
     }
   }
-  if (lab < 0 || lab >= N) atomicOr(&p.scalars->flags, (uint32_t)VOLTA_STATUS_BAD_ARGUMENT);
   return sample;
+}
+
+template <int NMAX>
+__device__ __forceinline__ float head_row(const OutLayerArgs& p, const float* z, const float* y, int lab, int m) {
+  const int N = p.N;
+  float d[NMAX];
+  const float l = head_delta<NMAX>(p, z, y, lab, d);
+  float* out = p.out + (size_t)m * N;
+  float* dd = p.delta + (size_t)m * N;
+#pragma unroll
+  for (int j = 0; j < NMAX; ++j) {
+    if (j < N) {
+      out[j] = z[j];
+      dd[j] = d[j];
+    }
+  }
+  if (p.loss != VOLTA_LOSS_MSE && (lab < 0 || lab >= N)) atomicOr(&p.scalars->flags, (uint32_t)VOLTA_STATUS_BAD_ARGUMENT);
+  return l;
 }
 
 // Block b handles rows [b*rows_per_block, ...): wave w takes every
@@ -214,6 +233,147 @@ __global__ void __launch_bounds__(64) loss_finish_kernel(OutLayerArgs p, int blo
   for (int b = 1; b < blocks; ++b) s = s + p.partials[b];
   const float denom = p.loss == VOLTA_LOSS_MSE ? (float)(p.B * p.N) : (float)p.B;
   step_epilogue(p.scalars, p.bc_table, p.bc_len, s / denom);
+}
+
+// The narrow output layer, its loss head and its dX in one launch (B <=
+// kNarrowMaxB).  Wave w of block b owns batch row m = 4b + w:
+//   z = act_{n-1}[m] W + bias     (wave_rows: lane k-strided, fixed butterfly)
+//   delta_{n-1}[m] and the row loss (head_delta, identical in every lane;
+//                                     lane 0 stores z and the deltas)
+//   delta_{n-2}[m][k] = (sum_j delta_{n-1}[m][j] W[k][j]) * f'(pre, act)
+//                                    for the lane's k = lane + 64c (j ascending,
+//                                    outer_dx_kernel's order)
+// Everything but the loss is row-local.  The block's row losses are added in
+// row order into partials[b]; the last block to finish (integer ticket)
+// adds the partials in block order and records the step's loss, the
+// non-finite flag and the Adam step counter (step_epilogue).  A separate
+// one-block output launch plus the outer-product dX launch cost more: one
+// CU for 64 rows, and a dependent launch between them.
+constexpr int kOutDxRows = 4;  // rows (waves) per block
+constexpr int kOutDxMaxBlocks = (kNarrowMaxB + kOutDxRows - 1) / kOutDxRows;
+
+template <int NMAX, bool WL>
+__global__ void __launch_bounds__(kOutDxRows * 64) out_layer_dx_kernel(OutLayerArgs p) {
+  constexpr int C = 4;
+  __shared__ float wave_loss[kOutDxRows];
+  __shared__ unsigned last_block;
+  extern __shared__ float w_lds[];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int N = p.N, K = p.K;
+  if constexpr (WL) {
+    const int KN = K * N;
+    for (int i0 = 0; i0 < KN; i0 += kOutDxRows * 64 * kOutStage) {
+      float t[kOutStage];
+#pragma unroll
+      for (int it = 0; it < kOutStage; ++it) t[it] = p.W[min(i0 + (int)threadIdx.x + kOutDxRows * 64 * it, KN - 1)];
+#pragma unroll
+      for (int it = 0; it < kOutStage; ++it) {
+        const int i = i0 + (int)threadIdx.x + kOutDxRows * 64 * it;
+        if (i < KN) w_lds[i] = t[it];
+      }
+    }
+    __syncthreads();
+  }
+  // the next step counter and its bias corrections, in case this block
+  // finishes last (nothing else in the launch writes them)
+  StepNext next{};
+  if (threadIdx.x == 0) next = step_prefetch(p.scalars, p.bc_table, p.bc_len);
+  const int m = blockIdx.x * kOutDxRows + wave;
+  const bool has = m < p.B;
+  const int mc = has ? m : p.B - 1;
+  const bool mse = p.loss == VOLTA_LOSS_MSE;
+  float bias[NMAX], y[NMAX];
+#pragma unroll
+  for (int j = 0; j < NMAX; ++j) {
+    bias[j] = p.bias[min(j, N - 1)];
+    y[j] = mse ? p.y[(size_t)mc * N + min(j, N - 1)] : 0.0f;
+  }
+  const int lab = mse ? 0 : p.labels[mc];
+  const int rows[1] = {has ? m : -1};
+  float z[1][NMAX];
+  wave_rows<NMAX, 1, C, WL>(p, w_lds, rows, z);
+#pragma unroll
+  for (int j = 0; j < NMAX; ++j) z[0][j] = z[0][j] + bias[j];
+  float d[NMAX];
+  const float row_loss = head_delta<NMAX>(p, z[0], y, lab, d);
+  if (has && lane == 0) (void)head_row<NMAX>(p, z[0], y, lab, m);
+
+  // delta_{n-2} of this row
+  if (has) {
+    const float* act = p.act + (size_t)m * K;
+    const float* pre = p.dx_pre ? p.dx_pre + (size_t)m * K : act;
+    float* out = p.dx_out + (size_t)m * K;
+    for (int kb = 0; kb < K; kb += 64 * C) {
+      float av[C], pv[C], wv[C][NMAX];
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const int kc = min(kb + 64 * c + lane, K - 1);
+        av[c] = act[kc];
+        pv[c] = pre[kc];
+#pragma unroll
+        for (int j = 0; j < NMAX; ++j) wv[c][j] = WL ? w_lds[kc * N + min(j, N - 1)] : p.W[(size_t)kc * N + min(j, N - 1)];
+      }
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        float sacc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NMAX; ++j) {
+          const float u = sacc + d[j] * wv[c][j];
+          sacc = j < N ? u : sacc;
+        }
+        const int k = kb + 64 * c + lane;
+        if (k < K) out[k] = sacc * act_derivative(p.dx_act, pv[c], av[c]);
+      }
+    }
+  }
+
+  if (lane == 0) wave_loss[wave] = has ? row_loss : 0.0f;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float sb = wave_loss[0];
+    for (int w = 1; w < kOutDxRows; ++w) sb = sb + wave_loss[w];
+    p.partials[blockIdx.x] = sb;
+    __threadfence();
+    last_block = atomicAdd(p.loss_counter, 1u) == gridDim.x - 1 ? 1u : 0u;
+    if (last_block) {
+      __threadfence();
+      // all partials' loads issued together (at most kOutDxMaxBlocks), added in block order
+      float part[kOutDxMaxBlocks];
+#pragma unroll
+      for (int b = 0; b < kOutDxMaxBlocks; ++b) part[b] = p.partials[min(b, (int)gridDim.x - 1)];
+      float total = part[0];
+#pragma unroll
+      for (int b = 1; b < kOutDxMaxBlocks; ++b) {
+        const float t = total + part[b];
+        total = b < (int)gridDim.x ? t : total;
+      }
+      const float denom = mse ? (float)(p.B * N) : (float)p.B;
+      step_finish(p.scalars, next, p.bc_table != nullptr, total / denom);
+      *p.loss_counter = 0u;
+    }
+  }
+}
+
+int out_layer_dx_blocks(int B) { return (B + kOutDxRows - 1) / kOutDxRows; }
+
+bool out_layer_dx_supported(int B, int K, int N) {
+  return B >= 1 && B <= kNarrowMaxB && K >= 1 && N >= 1 && N <= 16 &&
+         (N == 1 || (size_t)K * N <= (size_t)kOutWlFloats);
+}
+
+hipError_t launch_out_layer_dx(const OutLayerArgs& p, hipStream_t st) {
+  if (!out_layer_dx_supported(p.B, p.K, p.N) || !p.partials || !p.loss_counter || !p.dx_out)
+    return hipErrorInvalidValue;
+  const dim3 grid(out_layer_dx_blocks(p.B)), block(kOutDxRows * 64);
+  const bool wl = p.N > 1;
+  const size_t lds = wl ? (size_t)p.K * p.N * sizeof(float) : 0;
+  if (p.N <= 1)
+    hipLaunchKernelGGL((out_layer_dx_kernel<1, false>), grid, block, 0, st, p);
+  else if (p.N <= 4)
+    hipLaunchKernelGGL((out_layer_dx_kernel<4, true>), grid, block, lds, st, p);
+  else
+    hipLaunchKernelGGL((out_layer_dx_kernel<16, true>), grid, block, lds, st, p);
+  return hipGetLastError();
 }
 
 // delta_out[b][j] = (sum_{k<K} delta[b][k] * W[j][k]) * f'(layer below)[b][j]
