@@ -940,15 +940,19 @@ __device__ __forceinline__ void dw_smallk_tile(const GemmArgs& args, int blk, fl
     store_slice();
     __syncthreads();
     if (do_db && tid < kDwT) {
-      // batch order; the slice's 64 reads are issued before the first add
+      // batch order; each batch of 16 reads is issued before its first add
+      // (16 registers, not the slice's 64: the kernel's occupancy)
       const int kn = min(kDwK, K - k0);
-      float col[kDwK];
 #pragma unroll
-      for (int kk = 0; kk < kDwK; ++kk) col[kk] = lb[kk * kDwS + tid];
+      for (int k1 = 0; k1 < kDwK; k1 += 16) {
+        float col[16];
 #pragma unroll
-      for (int kk = 0; kk < kDwK; ++kk) {
-        const float t = db + col[kk];
-        db = kk < kn ? t : db;
+        for (int kk = 0; kk < 16; ++kk) col[kk] = lb[(k1 + kk) * kDwS + tid];
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) {
+          const float t = db + col[kk];
+          db = k1 + kk < kn ? t : db;
+        }
       }
     }
 #pragma unroll
@@ -1305,12 +1309,26 @@ struct PairLds {
   static constexpr int kFloats = OA::kLds > OB::kLds ? OA::kLds : (OB::kLds > 0 ? OB::kLds : 1);
 };
 
+// Waves per SIMD a paired launch is compiled for: two in general; five for
+// two small-K dW operations (C2's last launch has 1536 workgroups; six
+// would need 80 registers and spills).
 template <class OA, class OB>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) pair_kernel(typename OA::Args a, typename OB::Args b, int na) {
+struct PairOccupancy {
+  static constexpr int kWaves = 2;
+};
+
+template <class OA, class OB>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PairOccupancy<OA, OB>::kWaves)))
+pair_kernel(typename OA::Args a, typename OB::Args b, int na) {
   __shared__ __attribute__((aligned(16))) float lds[PairLds<OA, OB>::kFloats];
   if ((int)blockIdx.x < na) OA::run(a, blockIdx.x, lds);
   else OB::run(b, blockIdx.x - na, lds);
 }
+
+template <>
+struct PairOccupancy<DwSmallOp, DwSmallOp> {
+  static constexpr int kWaves = 5;
+};
 
 using DxOp = GemmOp64<EPI_DX_ACT, true, true>;
 using DwOp = GemmOp64<EPI_DW_OPT, false, false>;
