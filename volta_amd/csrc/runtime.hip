@@ -581,6 +581,17 @@ static bool make_bc_table(Handle* h) {
   return true;
 }
 
+// HIP's runtime replays an instantiated graph either from kernel packets it
+// recorded at instantiation ("packet capture", the default) or by
+// dispatching the nodes in order as stream launches.  For this step's chain
+// of nine to seventeen dependent kernels the second is faster on MI355X (C2:
+// 65.2 -> 61.6 us per replay, no other change).  The runtime reads the
+// setting once, at its initialisation, so it is put in the environment when
+// the library is loaded; a value the caller has set is kept.
+__attribute__((constructor)) static void graph_dispatch_setting() {
+  setenv("DEBUG_CLR_GRAPH_PACKET_CAPTURE", "0", 0);
+}
+
 // Capture the step into a fresh graph (hyperparameters are kernel
 // arguments, so a change of them is a new capture).
 static bool capture(Handle* h) {
