@@ -672,6 +672,65 @@ def test_merged_output_layer_dx_bit_identical(name):
         np.testing.assert_array_equal(a, b)
 
 
+FWD_HEAD_CASES = {
+    "c1": (MlpSpec([256, 512, 512, 256, 1], "relu", "sgd"), 64, 0.01),
+    "c2": (MlpSpec([512, 1024, 1024, 512, 256, 1], "relu", "adam"), 64, 1e-3),
+    "c3": (MlpSpec([512, 2048, 2048, 512, 1], "gelu", "adamw"), 64, 1e-3),
+    "c4_b256": (MlpSpec([512, 1024, 1024, 512, 256, 1], "silu", "sgd"), 256, 0.01),
+    "gelu_b37": (MlpSpec([96, 256, 128, 1], "gelu", "sgd"), 37, 0.01),  # strips of 16, 16 and 5 rows
+    "tanh_b200": (MlpSpec([64, 192, 96, 1], "tanh", "adam"), 200, 1e-3),
+    "leaky_k130_b19": (MlpSpec([130, 66, 1], "leaky_relu", "adagrad"), 19, 1e-2),  # K % 4 != 0: scalar loads
+}
+
+
+def _launch_labels(env, spec, B):
+    import ctypes as C
+
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        hip = load_hip()
+        t = Trainer(hip, spec, B)
+        fn = hip.lib.volta_hip_profile_step
+        fn.restype = C.c_int32
+        fn.argtypes = [C.c_void_p, C.c_int32, C.c_char_p, C.c_int32]
+        buf = C.create_string_buffer(1 << 16)
+        assert fn(t.h, 1, buf, len(buf)) > 0
+        t.close()
+        return [line.split("\t")[0] for line in buf.value.decode().strip().splitlines()]
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+@pytest.mark.parametrize("name", sorted(FWD_HEAD_CASES))
+def test_forward_head_launch_bit_identical(name):
+    """The last hidden layer's forward product and the output layer (loss
+    head and dX_{n-1}) in one launch (gemm_smallm_head: each 16-row strip
+    finished by its last workgroup; opt-in, VOLTA_FWD_HEAD=1) against the
+    output layer's own launch (the default): one launch fewer, and parameters, activations,
+    deltas and losses after 4 steps bit-identical (same per-row code, same
+    block partials, same order)."""
+    spec, B, lr = FWD_HEAD_CASES[name]
+    say(f"forward + output head launch {name}")
+    n = len(spec.sizes) - 1
+    fused = f"fwd{n - 2}+fwd{n - 1}+loss+dx{n - 1}"
+    lab_sep = _launch_labels({"VOLTA_FWD_HEAD": "0"}, spec, B)
+    lab_fused = _launch_labels({"VOLTA_FWD_HEAD": "1"}, spec, B)
+    assert fused in lab_fused and fused not in lab_sep
+    assert len(lab_fused) == len(lab_sep) - 1
+    l1, p1, b1 = _run_with_env({"VOLTA_FWD_HEAD": "0"}, spec, B, lr, 4)
+    l2, p2, b2 = _run_with_env({"VOLTA_FWD_HEAD": "1"}, spec, B, lr, 4)
+    np.testing.assert_array_equal(l1, l2)
+    for a, b in zip(p1, p2):
+        np.testing.assert_array_equal(a, b)
+    for a, b in zip(b1, b2):
+        np.testing.assert_array_equal(a, b)
+
+
 # ---------------------------------------------------------------------------
 # ABI behaviour
 # ---------------------------------------------------------------------------

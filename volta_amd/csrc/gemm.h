@@ -102,6 +102,15 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus, bool 
 hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& a, hipStream_t st, Recorder* rec = nullptr,
                        const char* label = "gemm", double bytes = 0.0);
 
+// The last hidden layer's forward product (plan p: small-M tile, bias +
+// activation, 8 waves) and the output layer of width 1 (o, with its dX
+// fields and loss ticket) in one launch; strip_counters: one zeroed
+// counter per 16 rows of the batch (at least (M + 15) / 16 of the
+// n_counters), left zero.
+bool fwd_head_supported(const GemmPlan& p, const GemmArgs& a, const OutLayerArgs& o, int n_counters);
+hipError_t launch_fwd_head(const GemmPlan& p, const GemmArgs& a, const OutLayerArgs& o, unsigned* strip_counters,
+                           int n_counters, hipStream_t st);
+
 // b_i update (optimizer of EpiArgs: opt, b, bm, bv, bgrad, b1, b2, eps,
 // scalars) from db_i = the column sums of delta_i [B x N], b ascending.
 hipError_t launch_bias_update(const EpiArgs& e, const float* delta, int B, int N, hipStream_t st);

@@ -28,6 +28,7 @@
 // resets the counter to zero for the next launch.
 #include "gemm.h"
 #include "narrow_dw.h"
+#include "out_head.h"
 
 #include <cstdlib>
 
@@ -825,6 +826,72 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
   smallm_tile<B_KC, VEC, EPI, NW>(args, blockIdx.x, lds);
 }
 
+// The last hidden layer's forward product (small-M tile, bias + activation)
+// and, in the same launch, the output layer of width 1 with its loss head
+// and dX_{n-1} -- one dependent launch fewer than running the output layer
+// on its own (out_layer_dx_kernel).  The output layer needs whole rows of
+// the hidden layer's output, so each 16-row strip is finished by the
+// workgroup that stores the strip's last tile: every thread releases its
+// stores (agent-scope fence), one thread takes the strip's ticket, and the
+// workgroup that arrives last acquires the strip and runs the stand-alone
+// output launch's per-row code (out_dx_row) for its 16 rows, two per wave.
+// It adds its rows' losses into the stand-alone launch's per-4-row
+// partials, in row order, and the last strip to finish forms the step's
+// loss from them in the same block order; so parameters, activations,
+// deltas and loss equal the two-launch path's bit for bit.
+template <bool VEC>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
+gemm_smallm_head(GemmArgs args, OutLayerArgs p, unsigned* strip_counters) {
+  __shared__ float lds[SmallLds<8>::kFloats];
+  __shared__ float row_loss[16];
+  __shared__ unsigned last_tile;
+  smallm_tile<false, VEC, EPI_BIAS_ACT, 8>(args, blockIdx.x, lds);
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tiles_m = (args.M + 15) / 16, tiles_n = (args.N + 15) / 16;
+  int tm, tn;
+  smallm_coords<2>(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  // The barrier completes every wave's tile stores into this XCD's L2; one
+  // agent-scope release by thread 0 then writes them back for the other
+  // XCDs (a fence per wave costs a write-back per wave), and one acquire by
+  // the last workgroup's thread 0 invalidates this CU's caches before the
+  // strip is read.
+  __syncthreads();
+  if (tid == 0) {
+    __threadfence();
+    last_tile = atomicAdd(strip_counters + tm, 1u) == (unsigned)(tiles_n - 1) ? 1u : 0u;
+    if (last_tile) __threadfence();
+  }
+  __syncthreads();
+  if (!last_tile) return;  // workgroup-uniform
+  StepNext next{};
+  if (tid == 0) {
+    strip_counters[tm] = 0u;
+    next = step_prefetch(p.scalars, p.bc_table, p.bc_len);
+  }
+  const float l0 = out_dx_row<1, false>(p, nullptr, 16 * tm + wave);
+  const float l1 = out_dx_row<1, false>(p, nullptr, 16 * tm + 8 + wave);
+  if (lane == 0) {
+    row_loss[wave] = l0;
+    row_loss[8 + wave] = l1;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    const int nblocks = (p.B + kOutDxRows - 1) / kOutDxRows;
+#pragma unroll
+    for (int g = 0; g < 16 / kOutDxRows; ++g) {
+      const int b = (16 / kOutDxRows) * tm + g;
+      float sb = row_loss[kOutDxRows * g];
+      for (int w = 1; w < kOutDxRows; ++w) sb = sb + row_loss[kOutDxRows * g + w];
+      if (b < nblocks) p.partials[b] = sb;
+    }
+    __threadfence();
+    if (atomicAdd(p.loss_counter, 1u) == (unsigned)(tiles_m - 1)) {
+      __threadfence();
+      out_dx_finish(p, nblocks, next);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // dW tile for a short reduction (K = B <= 256: the small-batch step).  A
 // workgroup owns a 32x32 tile of W_i -- 4 elements per thread -- so a launch
@@ -1214,6 +1281,25 @@ static hipError_t launch_smallm(const GemmArgs& a, int layout, bool vec, hipStre
     if (k == EPI_STORE) return launch_smallm_epi<true, EPI_STORE>(a, vec, st);
   }
   return hipErrorInvalidValue;
+}
+
+bool fwd_head_supported(const GemmPlan& p, const GemmArgs& a, const OutLayerArgs& o, int n_counters) {
+  const int tiles_m = (a.M + 15) / 16;
+  return p.tile == TILE_SMALLM && p.layout == GEMM_NN && p.splits == 1 && a.epi.kind == EPI_BIAS_ACT &&
+         smallm_waves(false) == 8 && (!p.vec || smallm_vec_ok(a, GEMM_NN)) && o.N == 1 && o.B == a.M &&
+         o.K == a.N && o.act == a.epi.out && o.B <= kNarrowMaxB && tiles_m <= n_counters && o.partials &&
+         o.loss_counter && o.dx_out;
+}
+
+hipError_t launch_fwd_head(const GemmPlan& p, const GemmArgs& args_in, const OutLayerArgs& o,
+                           unsigned* strip_counters, int n_counters, hipStream_t st) {
+  GemmArgs a = args_in;
+  a.k_per_split = p.k_per_split;
+  if (!strip_counters || !fwd_head_supported(p, a, o, n_counters)) return hipErrorInvalidValue;
+  const dim3 grid(((a.M + 15) / 16) * ((a.N + 15) / 16));
+  if (p.vec) hipLaunchKernelGGL(gemm_smallm_head<true>, grid, dim3(512), 0, st, a, o, strip_counters);
+  else hipLaunchKernelGGL(gemm_smallm_head<false>, grid, dim3(512), 0, st, a, o, strip_counters);
+  return hipGetLastError();
 }
 
 hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& args_in, hipStream_t st, Recorder* rec,

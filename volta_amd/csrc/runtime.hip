@@ -103,6 +103,7 @@ struct Handle {
   int out_mode = 0;           // OUT_NARROW / OUT_GEMM_LOSS / OUT_GEMM (output layer + loss head)
   bool narrow_dx = false;     // dX of the output layer as an outer product (L[n] <= 16)
   bool out_dx_merged = false; // ... formed by the output layer's own launch (out_layer_dx_kernel)
+  bool fwd_head = false;      // ... and that launch folded into the last hidden forward launch (opt-in)
   bool narrow_dw = false;     // dW of the output layer by narrow_dw_kernel
   bool keep_grads = false;    // also store dW/db in `grads` (VOLTA_KEEP_GRADS=1)
   DevScalars* scalars = nullptr;
@@ -215,39 +216,55 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
     a.counters = h->counters;
     a.epi.scalars = h->scalars;
   };
+  // The narrow output layer's arguments (layer n-1), with its dX_{n-1}
+  // fields when that is formed in the same launch.
+  auto out_args = [&]() {
+    const LayerPlan& lp = h->layers[n - 1];
+    OutLayerArgs o{};
+    o.act = h->act[n - 1];
+    o.W = h->params + lp.w_off;
+    o.bias = h->params + lp.b_off;
+    o.B = B;
+    o.K = lp.r;
+    o.N = lp.c;
+    o.loss = s.loss;
+    o.y = static_cast<const float*>(h->target);
+    o.labels = static_cast<const int32_t*>(h->target);
+    o.out = h->act[n];
+    o.delta = h->delta[n - 1];
+    o.partials = h->loss_partials;
+    o.scalars = h->scalars;
+    o.bc_table = h->bc_table;
+    o.bc_len = h->bc_len;
+    if (h->out_dx_merged) {
+      o.dx_act = s.activation;
+      o.dx_pre = h->pre[n - 2];
+      o.dx_out = h->delta[n - 2];
+      o.loss_counter = h->counters + h->n_counters - 1;
+    }
+    return o;
+  };
+  // algorithmic bytes of the narrow output layer: 4(B*r + r*c + B*c) + loss
+  // head 8*B*c; with its dX: + 4*B*r (act re-read from cache not counted)
+  auto out_bytes = [&]() {
+    const LayerPlan& lp = h->layers[n - 1];
+    return 4.0 * ((double)B * lp.r + (double)lp.r * lp.c + (double)B * lp.c) + 8.0 * B * lp.c +
+           (h->out_dx_merged ? 4.0 * (double)B * lp.r : 0.0);
+  };
+  bool head_done = false;  // the output layer ran in the last hidden forward launch
   // Forward (:702-789); the output layer also runs the loss head (:792-798).
   for (int i = 0; i < n; ++i) {
     const LayerPlan& lp = h->layers[i];
     const bool last = i == n - 1;
+    if (last && head_done) continue;
     if (last && h->out_mode == OUT_NARROW) {
-      OutLayerArgs o{};
-      o.act = h->act[i];
-      o.W = h->params + lp.w_off;
-      o.bias = h->params + lp.b_off;
-      o.B = B;
-      o.K = lp.r;
-      o.N = lp.c;
-      o.loss = s.loss;
-      o.y = static_cast<const float*>(h->target);
-      o.labels = static_cast<const int32_t*>(h->target);
-      o.out = h->act[n];
-      o.delta = h->delta[n - 1];
-      o.partials = h->loss_partials;
-      o.scalars = h->scalars;
-      o.bc_table = h->bc_table;
-      o.bc_len = h->bc_len;
-      // algorithmic bytes: 4(B*r + r*c + B*c) + loss head 8*B*c
-      const double fb = 4.0 * ((double)B * lp.r + (double)lp.r * lp.c + (double)B * lp.c) + 8.0 * B * lp.c;
+      const OutLayerArgs o = out_args();
+      const double fb = out_bytes();
       if (h->out_dx_merged) {
         // the output layer's dX_{n-1} in the same launch (row-local)
-        o.dx_act = s.activation;
-        o.dx_pre = h->pre[i - 1];
-        o.dx_out = h->delta[i - 1];
-        o.loss_counter = h->counters + h->n_counters - 1;
         VOLTA_CHECK(launch_out_layer_dx(o, st));
-        // dX bytes: 4(B*c + r*c + 2*B*r), act re-read from cache not counted again
         std::snprintf(label, sizeof label, "fwd%d+loss+dx%d", i, i);
-        VOLTA_CHECK(mark(rec, label, 4.0 * B * lp.r * lp.c, fb + 4.0 * (double)B * lp.r));
+        VOLTA_CHECK(mark(rec, label, 4.0 * B * lp.r * lp.c, fb));
         continue;
       }
       VOLTA_CHECK(launch_out_layer(o, st));
@@ -285,6 +302,19 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
     // algorithmic bytes: 4(B*r + r*c + B*c*(2 if hidden else 1)) (+ loss head)
     const double bytes = 4.0 * ((double)B * lp.r + (double)lp.r * lp.c + (double)B * lp.c * (last ? 1 : 2)) +
                          (last && h->out_mode == OUT_GEMM_LOSS ? 8.0 * B * Ln : 0.0);
+    if (i == n - 2 && h->fwd_head) {
+      const OutLayerArgs o = out_args();
+      GemmArgs af = a;
+      af.k_per_split = lp.fwd.k_per_split;
+      if (fwd_head_supported(lp.fwd, af, o, h->n_counters - 1)) {
+        VOLTA_CHECK(launch_fwd_head(lp.fwd, a, o, h->counters, h->n_counters - 1, st));
+        const LayerPlan& lo = h->layers[n - 1];
+        std::snprintf(label, sizeof label, "fwd%d+fwd%d+loss+dx%d", i, i + 1, i + 1);
+        VOLTA_CHECK(mark(rec, label, 2.0 * a.M * a.N * a.K + 4.0 * B * lo.r * lo.c, bytes + out_bytes()));
+        head_done = true;
+        continue;
+      }
+    }
     VOLTA_CHECK(gemm_launch(lp.fwd, a, st, rec, label, bytes));
     if (!last && h->hidden_ext()) {
       VOLTA_CHECK(launch_hidden_fwd(hidden_fwd_args(h, i, B, true), st));
@@ -661,6 +691,11 @@ static bool build(Handle* h) {
   const char* nod = std::getenv("VOLTA_NO_OUT_DX");
   h->out_dx_merged = h->narrow_dx && !h->extras() && !(nod && *nod && *nod != '0') &&
                      out_layer_dx_supported(B, h->L[n - 1], Ln);
+  // Opt-in: its per-workgroup release fence costs more than the launch it
+  // saves on C2/C3 (0.0613 -> 0.0643, 0.1035 -> 0.1096 ms), less on C1
+  // (0.0402 -> 0.0384 ms).
+  const char* fh = std::getenv("VOLTA_FWD_HEAD");
+  h->fwd_head = h->out_dx_merged && Ln == 1 && fh && *fh && *fh != '0';
   h->narrow_dw = Ln <= 16 && B <= kNarrowMaxB;
   size_t ws_floats = 0;
   int max_tiles = 1;

@@ -14,133 +14,9 @@
 #include "skinny.h"
 
 #include "narrow_dw.h"
+#include "out_head.h"
 
 namespace volta {
-
-// Output rows z[g][0..N) of RG rows (rows[g], valid where rows[g] >= 0),
-// computed by a whole wave: lane l sums k = l, l+64, ... in ascending order,
-// then a fixed butterfly adds the lanes.  The k loop runs in chunks of C
-// values per lane whose activation loads (all RG rows) are issued before
-// the chunk's first multiply, so a chunk costs one memory latency.  W comes
-// from the block's LDS copy `wl` (WL) -- lane l reads row k of W, so for
-// N > 1 global loads of W would touch a cache line per lane for each of its
-// N columns -- or, for one column or a W too large to stage, from global
-// memory with the chunk's other loads.  Every global load is unconditional (clamped row and k;
-// terms outside the matrix are not added), so no branch or wait separates
-// them.
-template <int NMAX, int RG, int C, bool WL>
-__device__ __forceinline__ void wave_rows(const OutLayerArgs& p, const float* wl, const int* rows,
-                                          float (*z)[NMAX]) {
-  const int lane = threadIdx.x & 63;
-  const int K = p.K, N = p.N;
-  float acc[RG][NMAX];
-#pragma unroll
-  for (int g = 0; g < RG; ++g)
-#pragma unroll
-    for (int j = 0; j < NMAX; ++j) acc[g][j] = 0.0f;
-  for (int kb = 0; kb < K; kb += 64 * C) {
-    float x[RG][C], wg[WL ? 1 : C][NMAX];
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-      const int kc = min(kb + 64 * c + lane, K - 1);
-      if constexpr (!WL) {
-#pragma unroll
-        for (int j = 0; j < NMAX; ++j) wg[c][j] = p.W[(size_t)kc * N + min(j, N - 1)];
-      }
-#pragma unroll
-      for (int g = 0; g < RG; ++g) x[g][c] = p.act[(size_t)(rows[g] >= 0 ? rows[g] : 0) * K + kc];
-    }
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-      const int kc = min(kb + 64 * c + lane, K - 1);
-      float wv[NMAX];
-#pragma unroll
-      for (int j = 0; j < NMAX; ++j) wv[j] = WL ? wl[kc * N + min(j, N - 1)] : wg[WL ? 0 : c][j];
-#pragma unroll
-      for (int g = 0; g < RG; ++g) {
-        const bool in = kb + 64 * c + lane < K && rows[g] >= 0;
-#pragma unroll
-        for (int j = 0; j < NMAX; ++j) {
-          const float t = acc[g][j] + x[g][c] * wv[j];
-          acc[g][j] = in && j < N ? t : acc[g][j];
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int g = 0; g < RG; ++g)
-#pragma unroll
-    for (int j = 0; j < NMAX; ++j) z[g][j] = wave_sum(acc[g][j]);
-}
-
-// Loss head of one row (same definitions as the MFMA path's loss epilogue):
-// MSE (:792-798) d = z - y, loss += d^2, delta = 2d/nt; softmax-CE
-// (interpreter.rs:762-812, autograd.rs:467-534).  head_delta forms the
-// row's deltas and returns its loss without storing anything, so every lane
-// of a wave can hold the deltas; head_row also stores z and the deltas.
-// `y` holds the row's targets (MSE), `lab` its label (CE), both loaded
-// before z was computed.  (Loops run to NMAX with a j < N guard so z stays
-// in registers.)
-template <int NMAX>
-__device__ __forceinline__ float head_delta(const OutLayerArgs& p, const float* z, const float* y, int lab,
-                                            float* d) {
-  const int N = p.N;
-  if (p.loss == VOLTA_LOSS_MSE) {
-    const float nt = (float)(p.B * N);
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NMAX; ++j) {
-      if (j < N) {
-        const float dj = z[j] - y[j];
-        acc = acc + dj * dj;
-        d[j] = 2.0f * dj / nt;
-      } else {
-        d[j] = 0.0f;
-      }
-    }
-    return acc;
-  }
-  const float bf = (float)p.B;
-  float mx = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < NMAX; ++j)
-    if (j < N) mx = fmaxf(mx, z[j]);
-  float sum = 0.0f;
-#pragma unroll
-  for (int j = 0; j < NMAX; ++j)
-    if (j < N) sum = sum + expf(z[j] - mx);
-  const float lse = mx + logf(sum);
-  float sample = __builtin_nanf("");
-#pragma unroll
-  for (int j = 0; j < NMAX; ++j) {
-    if (j < N) {
-      const bool on = j == lab;
-      if (on) sample = -(z[j] - lse);
-      d[j] = (expf(z[j] - mx) / sum - (on ? 1.0f : 0.0f)) / bf;
-    } else {
-      d[j] = 0.0f;
-    }
-  }
-  return sample;
-}
-
-template <int NMAX>
-__device__ __forceinline__ float head_row(const OutLayerArgs& p, const float* z, const float* y, int lab, int m) {
-  const int N = p.N;
-  float d[NMAX];
-  const float l = head_delta<NMAX>(p, z, y, lab, d);
-  float* out = p.out + (size_t)m * N;
-  float* dd = p.delta + (size_t)m * N;
-#pragma unroll
-  for (int j = 0; j < NMAX; ++j) {
-    if (j < N) {
-      out[j] = z[j];
-      dd[j] = d[j];
-    }
-  }
-  if (p.loss != VOLTA_LOSS_MSE && (lab < 0 || lab >= N)) atomicOr(&p.scalars->flags, (uint32_t)VOLTA_STATUS_BAD_ARGUMENT);
-  return l;
-}
 
 // Block b handles rows [b*rows_per_block, ...): wave w takes every
 // (waves)-th row, RG rows at a time (in increasing row order).  The block's
@@ -249,12 +125,9 @@ __global__ void __launch_bounds__(64) loss_finish_kernel(OutLayerArgs p, int blo
 // non-finite flag and the Adam step counter (step_epilogue).  A separate
 // one-block output launch plus the outer-product dX launch cost more: one
 // CU for 64 rows, and a dependent launch between them.
-constexpr int kOutDxRows = 4;  // rows (waves) per block
-constexpr int kOutDxMaxBlocks = (kNarrowMaxB + kOutDxRows - 1) / kOutDxRows;
 
 template <int NMAX, bool WL>
 __global__ void __launch_bounds__(kOutDxRows * 64) out_layer_dx_kernel(OutLayerArgs p) {
-  constexpr int C = 4;
   __shared__ float wave_loss[kOutDxRows];
   __shared__ unsigned last_block;
   extern __shared__ float w_lds[];
@@ -278,56 +151,8 @@ __global__ void __launch_bounds__(kOutDxRows * 64) out_layer_dx_kernel(OutLayerA
   // finishes last (nothing else in the launch writes them)
   StepNext next{};
   if (threadIdx.x == 0) next = step_prefetch(p.scalars, p.bc_table, p.bc_len);
-  const int m = blockIdx.x * kOutDxRows + wave;
-  const bool has = m < p.B;
-  const int mc = has ? m : p.B - 1;
-  const bool mse = p.loss == VOLTA_LOSS_MSE;
-  float bias[NMAX], y[NMAX];
-#pragma unroll
-  for (int j = 0; j < NMAX; ++j) {
-    bias[j] = p.bias[min(j, N - 1)];
-    y[j] = mse ? p.y[(size_t)mc * N + min(j, N - 1)] : 0.0f;
-  }
-  const int lab = mse ? 0 : p.labels[mc];
-  const int rows[1] = {has ? m : -1};
-  float z[1][NMAX];
-  wave_rows<NMAX, 1, C, WL>(p, w_lds, rows, z);
-#pragma unroll
-  for (int j = 0; j < NMAX; ++j) z[0][j] = z[0][j] + bias[j];
-  float d[NMAX];
-  const float row_loss = head_delta<NMAX>(p, z[0], y, lab, d);
-  if (has && lane == 0) (void)head_row<NMAX>(p, z[0], y, lab, m);
-
-  // delta_{n-2} of this row
-  if (has) {
-    const float* act = p.act + (size_t)m * K;
-    const float* pre = p.dx_pre ? p.dx_pre + (size_t)m * K : act;
-    float* out = p.dx_out + (size_t)m * K;
-    for (int kb = 0; kb < K; kb += 64 * C) {
-      float av[C], pv[C], wv[C][NMAX];
-#pragma unroll
-      for (int c = 0; c < C; ++c) {
-        const int kc = min(kb + 64 * c + lane, K - 1);
-        av[c] = act[kc];
-        pv[c] = pre[kc];
-#pragma unroll
-        for (int j = 0; j < NMAX; ++j) wv[c][j] = WL ? w_lds[kc * N + min(j, N - 1)] : p.W[(size_t)kc * N + min(j, N - 1)];
-      }
-#pragma unroll
-      for (int c = 0; c < C; ++c) {
-        float sacc = 0.0f;
-#pragma unroll
-        for (int j = 0; j < NMAX; ++j) {
-          const float u = sacc + d[j] * wv[c][j];
-          sacc = j < N ? u : sacc;
-        }
-        const int k = kb + 64 * c + lane;
-        if (k < K) out[k] = sacc * act_derivative(p.dx_act, pv[c], av[c]);
-      }
-    }
-  }
-
-  if (lane == 0) wave_loss[wave] = has ? row_loss : 0.0f;
+  const float row_loss = out_dx_row<NMAX, WL>(p, w_lds, blockIdx.x * kOutDxRows + wave);
+  if (lane == 0) wave_loss[wave] = row_loss;
   __syncthreads();
   if (threadIdx.x == 0) {
     float sb = wave_loss[0];
@@ -337,19 +162,7 @@ __global__ void __launch_bounds__(kOutDxRows * 64) out_layer_dx_kernel(OutLayerA
     last_block = atomicAdd(p.loss_counter, 1u) == gridDim.x - 1 ? 1u : 0u;
     if (last_block) {
       __threadfence();
-      // all partials' loads issued together (at most kOutDxMaxBlocks), added in block order
-      float part[kOutDxMaxBlocks];
-#pragma unroll
-      for (int b = 0; b < kOutDxMaxBlocks; ++b) part[b] = p.partials[min(b, (int)gridDim.x - 1)];
-      float total = part[0];
-#pragma unroll
-      for (int b = 1; b < kOutDxMaxBlocks; ++b) {
-        const float t = total + part[b];
-        total = b < (int)gridDim.x ? t : total;
-      }
-      const float denom = mse ? (float)(p.B * N) : (float)p.B;
-      step_finish(p.scalars, next, p.bc_table != nullptr, total / denom);
-      *p.loss_counter = 0u;
+      out_dx_finish(p, (int)gridDim.x, next);
     }
   }
 }
