@@ -95,6 +95,7 @@ struct GemmPlan {
   int k_per_split = 0;
   bool vec = false;
   bool inkernel_reduce = false;  // split-K reduced by the last slice (else a second kernel)
+  int waves = 0;                 // TILE_SMALLM: waves per workgroup (4 or 8)
   int tiles(int M, int N) const {
     const int t = tile == TILE_256x256   ? 256
                   : tile == TILE_128x128  ? 128

@@ -1249,20 +1249,27 @@ static hipError_t launch_reduce(const GemmArgs& a, int splits, hipStream_t st) {
 }
 
 // Small-M products: NN with BIAS_ACT / STORE, NT with DX_ACT / STORE.
-// Waves per workgroup of a stand-alone forward (NN) small-M launch
-// (VOLTA_SMALLM_WAVES, 8 by default or 4; measured at B=64: C2 0.0663 vs
-// 0.0686 ms/step, C1 0.0391 vs 0.0400).  dX (NT) products always take 4, as
-// in a paired launch, so paired and separate launches give the same bits.
-static int smallm_waves(bool b_kc) {
+// Waves per workgroup of a stand-alone forward (NN) small-M launch: 8 while
+// the grid has at most one workgroup per CU, else 4.  An 8-wave workgroup
+// (168 registers a lane) leaves room for no second one on its CU, so a
+// larger grid would take two rounds; 4-wave workgroups fit three to a CU.
+// Measured: C2 (every forward grid <= 256 workgroups) 0.0641 ms/step with 4
+// waves against 0.0618 with 8; C3's 512-workgroup fwd0/fwd1 4.16/14.36 us
+// with 4 against 5.28/16.1 us with 8, its 128-workgroup fwd2 9.92 against
+// 7.96 us.  VOLTA_SMALLM_WAVES=4 or 8 fixes the count.  dX (NT) products
+// always take 4, as in a paired launch, so paired and separate launches
+// give the same bits.
+static int smallm_waves(bool b_kc, int blocks, int num_cus) {
   if (b_kc) return 4;
   const char* w = std::getenv("VOLTA_SMALLM_WAVES");
-  return w && std::atoi(w) == 4 ? 4 : 8;
+  if (w && *w) return std::atoi(w) == 4 ? 4 : 8;
+  return blocks <= num_cus ? 8 : 4;
 }
 
 template <bool B_KC, int EPI>
-static hipError_t launch_smallm_epi(const GemmArgs& a, bool vec, hipStream_t st) {
+static hipError_t launch_smallm_epi(const GemmArgs& a, bool vec, int waves, hipStream_t st) {
   const int blocks = ((a.M + 15) / 16) * ((a.N + 15) / 16);
-  if (smallm_waves(B_KC) == 8) {
+  if (waves == 8) {
     if (vec) hipLaunchKernelGGL((gemm_smallm<B_KC, true, EPI, 8>), dim3(blocks), dim3(512), 0, st, a);
     else hipLaunchKernelGGL((gemm_smallm<B_KC, false, EPI, 8>), dim3(blocks), dim3(512), 0, st, a);
   } else {
@@ -1290,15 +1297,17 @@ static bool dw_smallk_ok(const GemmArgs& a, int layout) {
   return (size_t)a.M * e.ldc < ((size_t)1 << 30);
 }
 
-static hipError_t launch_smallm(const GemmArgs& a, int layout, bool vec, hipStream_t st) {
+static hipError_t launch_smallm(const GemmArgs& a, int layout, bool vec, int waves, hipStream_t st) {
   if (vec && !smallm_vec_ok(a, layout)) return hipErrorInvalidValue;
+  if (waves != 4 && waves != 8) return hipErrorInvalidValue;
+  if (layout == GEMM_NT && waves != 4) return hipErrorInvalidValue;
   const int k = a.epi.kind;
   if (layout == GEMM_NN) {
-    if (k == EPI_BIAS_ACT) return launch_smallm_epi<false, EPI_BIAS_ACT>(a, vec, st);
-    if (k == EPI_STORE) return launch_smallm_epi<false, EPI_STORE>(a, vec, st);
+    if (k == EPI_BIAS_ACT) return launch_smallm_epi<false, EPI_BIAS_ACT>(a, vec, waves, st);
+    if (k == EPI_STORE) return launch_smallm_epi<false, EPI_STORE>(a, vec, waves, st);
   } else if (layout == GEMM_NT) {
-    if (k == EPI_DX_ACT) return launch_smallm_epi<true, EPI_DX_ACT>(a, vec, st);
-    if (k == EPI_STORE) return launch_smallm_epi<true, EPI_STORE>(a, vec, st);
+    if (k == EPI_DX_ACT) return launch_smallm_epi<true, EPI_DX_ACT>(a, vec, waves, st);
+    if (k == EPI_STORE) return launch_smallm_epi<true, EPI_STORE>(a, vec, waves, st);
   }
   return hipErrorInvalidValue;
 }
@@ -1306,7 +1315,7 @@ static hipError_t launch_smallm(const GemmArgs& a, int layout, bool vec, hipStre
 bool fwd_head_supported(const GemmPlan& p, const GemmArgs& a, const OutLayerArgs& o, int n_counters) {
   const int tiles_m = (a.M + 15) / 16;
   return p.tile == TILE_SMALLM && p.layout == GEMM_NN && p.splits == 1 && a.epi.kind == EPI_BIAS_ACT &&
-         smallm_waves(false) == 8 && (!p.vec || smallm_vec_ok(a, GEMM_NN)) && o.N == 1 && o.B == a.M &&
+         p.waves == 8 && (!p.vec || smallm_vec_ok(a, GEMM_NN)) && o.N == 1 && o.B == a.M &&
          o.K == a.N && o.act == a.epi.out && o.B <= kNarrowMaxB && tiles_m <= n_counters && o.partials &&
          o.loss_counter && o.dx_out;
 }
@@ -1336,7 +1345,7 @@ hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& args_in, hipStream_t s
   hipError_t err;
   if (p.tile == TILE_SMALLM) {
     if (p.splits != 1) return hipErrorInvalidValue;
-    if ((err = launch_smallm(a, p.layout, p.vec, st)) != hipSuccess) return err;
+    if ((err = launch_smallm(a, p.layout, p.vec, p.waves, st)) != hipSuccess) return err;
     return mark(rec, label, 2.0 * a.M * a.N * a.K, bytes);
   }
   if (p.tile == TILE_DW_SMALLK) {
@@ -1617,6 +1626,7 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus, bool 
     p.tile = TILE_SMALLM;
     p.splits = 1;
     p.k_per_split = K;
+    p.waves = smallm_waves(layout == GEMM_NT, ((M + 15) / 16) * ((N + 15) / 16), num_cus);
   }
   // dW with a short reduction (K = B) on 32x32 tiles: more workgroups per
   // CU to overlap the optimizer's streaming and arithmetic (K <= 256 by
