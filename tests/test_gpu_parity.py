@@ -82,21 +82,17 @@ GEMM_SHAPES = [
 
 TILE_SMALLM = 3
 TILE_DW_SMALLK = 4
-TILE_256 = 5
 
 
 @pytest.mark.parametrize("layout", [0, 1, 2], ids=["NN", "NT", "TN"])
-@pytest.mark.parametrize("M,N,K", GEMM_SHAPES + [(300, 520, 77), (520, 300, 1030), (768, 512, 2048)])
-@pytest.mark.parametrize("tile", [0, 1, TILE_SMALLM, TILE_DW_SMALLK, TILE_256])
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+@pytest.mark.parametrize("tile", [0, 1, TILE_SMALLM, TILE_DW_SMALLK])
 def test_gemm_integer_exact(layout, M, N, K, tile):
     """Integer operands: the MFMA result must be exact (any order is exact
     below 2^24), which pins operand indexing, the lane layouts of the
     32x32x2 and 16x16x4 MFMAs, the small-M tile's per-wave K ranges and
     wave-order reduction, and the bounds handling (K=3 and K=257 take the
-    scalar-load path of the small-M tile; the 256x256 tile's 16-deep
-    stages and partial tiles at K=77/1030 and M, N off multiples of 256)."""
-    if tile != TILE_256 and K > 1024 and M * N > 64 * 1024:
-        pytest.skip("large shapes are for the 256x256 tile")
+    scalar-load path of the small-M tile)."""
     if tile == TILE_SMALLM and layout == 2:
         pytest.skip("the small-M tile serves the NN and NT products only")
     if tile == TILE_DW_SMALLK and (layout != 2 or M % 4 or N % 4):

@@ -77,16 +77,7 @@ struct GemmArgs {
 // (split over its 4 or 8 waves), for NN/NT products with few rows (B <= 256).
 // TILE_DW_SMALLK: 32x32 tiles of the TN (dW) product with a short K
 // (K = B <= 256), the optimizer applied on 16-byte rows.
-// TILE_256x256: 256x256 tiles (four waves of 128x128), one workgroup per CU,
-// for products with at least one tile per CU and a long K (opt-in).
-enum GemmTile {
-  TILE_64x64 = 0,
-  TILE_128x128 = 1,
-  TILE_64x64_K64 = 2,
-  TILE_SMALLM = 3,
-  TILE_DW_SMALLK = 4,
-  TILE_256x256 = 5
-};
+enum GemmTile { TILE_64x64 = 0, TILE_128x128 = 1, TILE_64x64_K64 = 2, TILE_SMALLM = 3, TILE_DW_SMALLK = 4 };
 
 struct GemmPlan {
   int layout = GEMM_NN;
@@ -97,11 +88,7 @@ struct GemmPlan {
   bool inkernel_reduce = false;  // split-K reduced by the last slice (else a second kernel)
   int waves = 0;                 // TILE_SMALLM: waves per workgroup (4 or 8)
   int tiles(int M, int N) const {
-    const int t = tile == TILE_256x256   ? 256
-                  : tile == TILE_128x128  ? 128
-                  : tile == TILE_SMALLM   ? 16
-                  : tile == TILE_DW_SMALLK ? 32
-                                          : 64;
+    const int t = tile == TILE_128x128 ? 128 : tile == TILE_SMALLM ? 16 : tile == TILE_DW_SMALLK ? 32 : 64;
     return ((M + t - 1) / t) * ((N + t - 1) / t);
   }
   size_t workspace_floats(int M, int N) const { return splits > 1 ? (size_t)splits * (M + 1) * N : 0; }

@@ -648,9 +648,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& args, int bx, int by, 
     __syncthreads();
     loss_tile<BM>(e, z, ZS, m0, tm, M, N, lds_small);
   } else {
-    // Blocks in (i, j) order, unrolled at compile time (the 4x4 blocks of a
-    // 128x128 wave tile exceed the loop unroller's limits, and a runtime
-    // index would put the accumulators in scratch memory).
+    // Blocks in (i, j) order, unrolled at compile time: a loop the unroller
+    // gives up on (it did for 4x4 blocks of 32x32) would index the
+    // accumulators at run time and put them in scratch memory.
     static_for_blocks<0, T::TM, T::TN>([&](auto I, auto J) {
       constexpr int i = decltype(I)::value, j = decltype(J)::value;
       block_epilogue<EPI>(e, acc[i][j], m0 + wm * WM + i * 32 + 4 * h, n0 + wn * WN + j * 32 + l32, M, N);
@@ -672,20 +672,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& args, int bx, int by, 
   }
 }
 
-// Waves per SIMD a tile kernel is compiled for.  Two at least (at most 256
-// vector + accumulation registers a lane): the 128x128 dW tile with an Adam
-// epilogue otherwise settles a few registers above that and runs at half
-// occupancy.  One for the 128x128 wave tiles of the 256x256 tile, whose
-// accumulators alone take 256 registers (its LDS holds one workgroup per CU
-// anyway).
-template <int WM, int WN>
-struct TileOccupancy {
-  static constexpr int kWaves = WM * WN >= 128 * 128 ? 1 : 2;
-};
-
+// Two waves per SIMD at least (at most 256 vector + accumulation registers
+// a lane): the 128x128 dW tile with an Adam epilogue otherwise settles a
+// few registers above that and runs at half occupancy.
 template <int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, bool VEC, int EPI, bool INK>
-__global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
-__attribute__((amdgpu_waves_per_eu(TileOccupancy<WM, WN>::kWaves))) gemm_f32_mfma(GemmArgs args) {
+__global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64) __attribute__((amdgpu_waves_per_eu(2)))
+gemm_f32_mfma(GemmArgs args) {
   __shared__ __attribute__((aligned(16))) float lds_a[2 * LdsTile<BM, BK, A_KC>::kFloats];
   __shared__ __attribute__((aligned(16))) float lds_b[2 * LdsTile<BN, BK, B_KC>::kFloats];
   __shared__ float lds_small[BM + 2];
@@ -1359,7 +1351,6 @@ hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& args_in, hipStream_t s
   switch (p.tile) {
     case TILE_64x64: err = launch_cfg<64, 64, 32, 32, 32>(a, p.layout, p.vec, p.splits, ink, st); break;
     case TILE_128x128: err = launch_cfg<128, 128, 32, 64, 64>(a, p.layout, p.vec, p.splits, ink, st); break;
-    case TILE_256x256: err = launch_cfg<256, 256, 32, 128, 128>(a, p.layout, p.vec, p.splits, ink, st); break;
     case TILE_64x64_K64: err = launch_cfg<64, 64, 64, 32, 32>(a, p.layout, p.vec, p.splits, ink, st); break;
     default: return hipErrorInvalidValue;
   }
@@ -1578,19 +1569,6 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus, bool 
   // (dW at small batch) is epilogue bound and wants the 4x larger grid.
   p.tile = ((size_t)M * N >= (size_t)1024 * 1024 && M >= 128 && N >= 128 && K > 256) ? TILE_128x128
                                                                                       : TILE_64x64;
-  // 256x256 tiles (opt-in, VOLTA_TILE256=1) where they alone fill the chip
-  // (one workgroup per CU) and K is long: the B=4096 products with
-  // 4096x4096 outputs.  Measured slower than the 128x128 tile's two
-  // workgroups per CU (C5 5.08 -> 5.30 ms): with one wave per SIMD nothing
-  // covers a stage's LDS stores, barrier and first fragment reads.
-  const char* t256 = std::getenv("VOLTA_TILE256");
-  const bool allow256 = t256 && *t256 == '1';
-  if (allow256 && (size_t)((M + 255) / 256) * ((N + 255) / 256) >= (size_t)num_cus && K >= 1024) {
-    p.tile = TILE_256x256;
-    p.splits = 1;
-    p.k_per_split = K;
-    return p;
-  }
   const char* sb = std::getenv("VOLTA_SMALL_BK");
   if (p.tile == TILE_64x64 && sb && std::atoi(sb) == 64) p.tile = TILE_64x64_K64;
   const int tiles = p.tiles(M, N);
