@@ -24,6 +24,13 @@
  *   volta_amd/libvolta_hip.so      -- the product: HIP kernels for gfx950
  *   oracle/liboracle_volta.so      -- the CPU restatement used as the checker
  *
+ * Loading libvolta_hip.so sets DEBUG_CLR_GRAPH_PACKET_CAPTURE=0 in the
+ * process environment unless the caller has set it, so that HIP replays the
+ * step graph by dispatching its nodes in order (faster for this chain of
+ * short dependent kernels).  HIP reads the variable once, when its runtime
+ * initialises: a host that made HIP calls before loading the library keeps
+ * its own setting.
+ *
  * Layout conventions (all row-major fp32, as in the reference):
  *   W_i  [L[i] x L[i+1]],  b_i [L[i+1]],  X [B x L[0]],  Y [B x L[n]]
  *
