@@ -89,10 +89,14 @@ def launches(lib, t):
     return rows
 
 
-def profile(lib, t, step_ms):
+def profile(lib, t, step_ms, spec, B):
     """Per-launch duration inside whole steps (time_in_step for every launch);
-    about 0.4 s of steps per launch, 3..50 repetitions."""
+    about 0.4 s of steps per launch, 3..50 repetitions.  Each row carries the
+    launch's fused-kernel flops/bytes from the library and the survey-model
+    flops/bytes (survey_cost)."""
     rows = launches(lib, t)
+    for r in rows:
+        r["survey_flops"], r["survey_bytes"] = survey_cost(spec, B, r["kernel"])
     reps = int(max(3, min(50, 200.0 / max(step_ms, 1e-3))))
     for i, r in enumerate(rows):
         ms, bracket, marker, label = time_in_step(lib, t, i, reps)
@@ -116,29 +120,77 @@ def time_in_step(lib, t, index, reps=50):
     return max(avg[0] - avg[1], 0.0), float(avg[0]), float(avg[1]), lab.value.decode()
 
 
+OPT_STATE_STREAMS = {"sgd": 3, "adagrad": 5, "adam": 7, "adamw": 7}
+
+
+def survey_cost(spec: MlpSpec, B: int, label: str):
+    """Algorithmic (flops, bytes) of one launch by the unfused-kernel model of
+    the hot-path survey, from the launch's label (parts joined by '|' and
+    '+'): per layer i (r = L[i], c = L[i+1]) fwd 4(B r + r c + B c (2 if
+    hidden else 1)), dW 4(B r + B c + r c), dX (i > 0) 4(B c + r c + 2 B r),
+    db 4(B c + c), optimizer 4 s (r c + c) with s = 3 (SGD), 5 (Adagrad), 7
+    (Adam/AdamW); flops 2 B r c per product; loss terms and the split-K
+    reduce launches carry none (the product's launch carries its bytes)."""
+    import re
+
+    if label.endswith(".splitk_reduce"):
+        return 0.0, 0.0
+    n = spec.n_layers
+    s_opt = OPT_STATE_STREAMS[spec.optimizer]
+    flops = nbytes = 0.0
+    for half in label.split("|"):
+        parts = half.split("+")
+        for part in parts:
+            m = re.fullmatch(r"(fwd|dx|dw)(\d+)", part)
+            if not m:
+                continue
+            kind, i = m.group(1), int(m.group(2))
+            r, c = spec.sizes[i], spec.sizes[i + 1]
+            flops += 2.0 * B * r * c
+            if kind == "fwd":
+                nbytes += 4.0 * (B * r + r * c + B * c * (2 if i < n - 1 else 1))
+            elif kind == "dx":
+                nbytes += 4.0 * (B * c + r * c + 2 * B * r)
+            else:
+                nbytes += 4.0 * (B * r + B * c + r * c)
+                if "db" in parts:
+                    nbytes += 4.0 * (B * c + c)
+                if "opt" in parts:
+                    nbytes += 4.0 * s_opt * (r * c + c)
+    return flops, nbytes
+
+
+def survey_step_cost(spec: MlpSpec, B: int):
+    """(flops, bytes) of the whole step by the same model."""
+    n = spec.n_layers
+    labels = [f"fwd{i}" for i in range(n)] + [f"dx{i}" for i in range(1, n)]
+    labels += [f"dw{i}+db+opt" for i in range(n)]
+    tot = [survey_cost(spec, B, lab) for lab in labels]
+    return sum(f for f, _ in tot), sum(b for _, b in tot)
+
+
 def roofline_of(row):
-    ai = row["flops"] / row["bytes"] if row["bytes"] > 0 else math.inf
+    """Roofline fraction of one launch from its survey-model flops and bytes
+    and its measured in-step duration; the launch's own fused-kernel byte
+    count (what it must move once fused) is kept beside it."""
+    fl, by = row["survey_flops"], row["survey_bytes"]
+    ai = fl / by if by > 0 else math.inf
     sec = row["ms"] * 1e-3
+    base = {"kernel": row["kernel"], "traffic": None, "avg_ms": round(row["ms"], 5),
+            "algorithmic_flops": fl, "algorithmic_bytes": by, "fused_model_bytes": row["bytes"],
+            "model": "hot-path survey unfused-kernel bytes (fwd, dW, dX, db, optimizer 4 s P)"}
     if ai > RIDGE:
-        ach = row["flops"] / sec / 1e12
-        return {"kernel": row["kernel"], "bound": "mfma", "achieved": round(ach, 3),
-                "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s", "frac": round(ach / PEAK_FP32_MFMA_TFLOPS, 4),
-                "traffic": None, "avg_ms": round(row["ms"], 5), "algorithmic_flops": row["flops"],
-                "algorithmic_bytes": row["bytes"]}
-    ach = row["bytes"] / sec / 1e9
-    return {"kernel": row["kernel"], "bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBS,
-            "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None,
-            "avg_ms": round(row["ms"], 5), "algorithmic_flops": row["flops"], "algorithmic_bytes": row["bytes"]}
+        ach = fl / sec / 1e12
+        return {**base, "bound": "mfma", "achieved": round(ach, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(ach / PEAK_FP32_MFMA_TFLOPS, 4)}
+    ach = by / sec / 1e9
+    return {**base, "bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(ach / PEAK_HBM_GBS, 4)}
 
 
 def dominance(row):
-    """The dominant launch of a step: the one with the longest time at its
-    roofline (algorithmic bytes at peak HBM bandwidth or flops at peak fp32
-    MFMA rate, whichever is longer), ties (equal GEMM shapes) broken by the
-    measured time.  Fixed by the workload, unlike the measured time alone,
-    which at B=64 puts two launches within a few percent of each other."""
-    sol = max(row["bytes"] / (PEAK_HBM_GBS * 1e9), row["flops"] / (PEAK_FP32_MFMA_TFLOPS * 1e12))
-    return (round(sol, 12), row["ms"])
+    """The dominant launch of a step: the longest measured in-step duration."""
+    return row["ms"]
 
 
 def run_gpu(name, steps, warmup, want_profile=True):
@@ -182,7 +234,7 @@ def run_gpu(name, steps, warmup, want_profile=True):
     extra.argtypes = [C.c_void_p]
     out["arena_bytes"] = int(extra(t.h))
     if want_profile:
-        rows = profile(lib, t, ms)
+        rows = profile(lib, t, ms, spec, B)
         out["kernels"] = rows
         out["roofline"] = roofline_of(max(rows, key=dominance))
         tr = measured_traffic(name, out["roofline"]["kernel"])
@@ -230,30 +282,99 @@ def run_rt_optimizer(name="c5", kind="adam", reps=20):
     return out
 
 
-def run_cpu(name, budget_s=10.0, max_steps=200):
-    """Oracle on this host's cores; bounded sample of ~budget_s seconds."""
-    from tests.oracle_lib import load_oracle
+CPU_REF_SO = os.path.join(ROOT, "oracle", "_ref", "libvolta_cpu_ref.so")
 
+
+def host_cpu():
+    """This host's CPU: model name, logical CPUs, physical cores (lscpu-style
+    count of distinct (package, core) pairs in /proc/cpuinfo)."""
+    model, cores, phys, cur = "unknown", set(), None, {}
+    try:
+        for line in open("/proc/cpuinfo"):
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "model name":
+                model = v
+            elif k in ("physical id", "core id"):
+                cur[k] = v
+            elif not k and cur:
+                cores.add((cur.get("physical id"), cur.get("core id")))
+                cur = {}
+        if cur:
+            cores.add((cur.get("physical id"), cur.get("core id")))
+        phys = len(cores) or None
+    except OSError:
+        pass
+    return {"model": model, "logical_cpus": os.cpu_count(), "physical_cores": phys,
+            "affinity_cpus": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None}
+
+
+def _cpu_leg(lib, name, threads, warmup, runs, steps_per_run):
+    """Time one CPU library on workload `name` at `threads` OpenMP threads:
+    `warmup` untimed steps, then `runs` runs of `steps_per_run` steps; the
+    per-step time of each run, and their median (the reference's protocol,
+    docs/BENCHMARKS.md:11-24: 10 warm-up steps, 7 runs of 50 steps, median)."""
     spec, B, lr = WORKLOADS[name]
-    lib = load_oracle()
+    lib.lib.volta_oracle_set_threads(threads)
     ws, bs = data.he_uniform(42, spec.sizes)
     X, Y = data.batch(42, spec.sizes, B, spec.loss)
     t = Trainer(lib, spec, B)
     t.set_all_params(ws, bs)
-    t.step(X, Y, lr)  # warm-up (page in, thread pool)
-    n = 0
-    t0 = time.perf_counter()
-    while n < max_steps:
+    for _ in range(warmup):
         t.step(X, Y, lr)
-        n += 1
-        if time.perf_counter() - t0 >= budget_s:
-            break
-    dt = (time.perf_counter() - t0) / n
+    per = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        for _ in range(steps_per_run):
+            t.step(X, Y, lr)
+        per.append((time.perf_counter() - t0) / steps_per_run)
     t.close()
-    return {"value": round(B / dt, 2), "unit": "samples/s", "ms_per_step": round(dt * 1e3, 3),
-            "cores": int(lib.lib.volta_oracle_threads()), "kind": "port",
-            "sample": f"{n} steps of workload {name} (B={B}) after 1 warm-up step, oracle/liboracle_volta.so "
-                      f"(C++ restatement of Volta compile-train, OpenMP GEMMs)"}
+    med = float(np.median(per))
+    return {"value": round(B / med, 2), "unit": "samples/s", "ms_per_step": round(med * 1e3, 3),
+            "cores": threads, "runs_ms": [round(x * 1e3, 3) for x in per]}
+
+
+def run_cpu(name, threads_all, full_protocol=True):
+    """CPU baseline legs on this host, rank 0 only.  Leg "port": the oracle
+    (oracle/liboracle_volta.so, the C++ restatement of Volta's compile-train
+    step: ascending-k OpenMP GEMMs, Adam over 8192-element chunks in parallel
+    as the reference's Rayon loop) at all threads and at 6 threads (the
+    reference's published machine).  Leg "port+ref_gemm": the same step with
+    every fp32 GEMM done by the reference's own C GEMM (gemm_shim.c, compiled
+    from its source into oracle/_ref/; single-threaded, the reference's build
+    without an OpenMP runtime) -- only where that build is present.  Protocol:
+    10 warm-up steps, 7 x 50 steps, median; a bounded sample for workloads
+    whose steps take seconds (stated in `sample`).  Returns (primary, legs)."""
+    from tests.oracle_lib import load_oracle
+    from volta_amd.abi import TrainLibrary
+
+    spec, B, lr = WORKLOADS[name]
+    proto = (10, 7, 50) if full_protocol else (1, 3, 1)
+    what = ("10 warm-up steps, 7 runs x 50 steps, median run" if full_protocol else
+            "bounded sample: 1 warm-up step, 3 runs x 1 step, median run")
+    legs = []
+    orc = load_oracle()
+    for th in sorted({threads_all, 6}, reverse=True) if full_protocol else [threads_all]:
+        r = _cpu_leg(orc, name, th, *proto)
+        r.update(kind="port", sample=f"workload {name} (B={B}), {what}; oracle/liboracle_volta.so "
+                                     f"(C++ restatement of Volta compile-train), {th} threads")
+        legs.append(r)
+        log(f"cpu baseline leg: {r}")
+    if full_protocol and os.path.exists(CPU_REF_SO):
+        from tests.oracle_lib import ORACLE_EXTRA
+
+        ref = TrainLibrary(CPU_REF_SO, extra=ORACLE_EXTRA)
+        r = _cpu_leg(ref, name, threads_all, 2, 7, 5)
+        r.update(kind="port+ref_gemm",
+                 sample=f"workload {name} (B={B}), bounded sample: 2 warm-up steps, 7 runs x 5 steps, median run; "
+                        f"oracle/_ref/libvolta_cpu_ref.so: the restatement's step "
+                        f"with the reference's own gemm_shim.c GEMMs (single-threaded), "
+                        f"{threads_all} threads elsewhere")
+        legs.append(r)
+        log(f"cpu baseline leg: {r}")
+    primary = dict(legs[0])
+    primary.pop("runs_ms", None)
+    return primary, legs
 
 
 def calibration_copy(mib, reps=10):
@@ -414,6 +535,12 @@ def main():
     ap.add_argument("--secondary", default="c5", help="second workload in the same line, or 'none'")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-profile", action="store_true", help="skip the per-kernel profile")
+    ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+                    or len(os.sched_getaffinity(0)), help="threads of the CPU baseline's all-cores leg")
+    ap.add_argument("--graph-dispatch", choices=("nodes", "packets"), default="nodes",
+                    help="how HIP replays the step graph in this process: 'nodes' sets "
+                         "DEBUG_CLR_GRAPH_PACKET_CAPTURE=0 before the first HIP call (nodes dispatched in order "
+                         "as stream launches); 'packets' leaves HIP's default (recorded kernel packets)")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB 10 times (scales rocprofv3 HBM counters)")
     ap.add_argument("--traffic-table", nargs=2, metavar=("PMC_DIR", "BENCH_JSON"),
@@ -433,6 +560,12 @@ def main():
               "(the step would shard by data parallelism over B; see DESIGN.md).", file=sys.stderr)
         return 2
 
+    # The host's choice of HIP's graph replay mode; HIP reads it once, at its
+    # first call, so it is set before the library is loaded.
+    if a.graph_dispatch == "nodes":
+        os.environ["DEBUG_CLR_GRAPH_PACKET_CAPTURE"] = "0"
+    else:
+        os.environ.pop("DEBUG_CLR_GRAPH_PACKET_CAPTURE", None)
     spec, B, lr, res = run_gpu(a.config, a.steps, a.warmup, want_profile=not a.no_profile)
     log(f"{a.config}: {res['ms_per_step']:.4f} ms/step, {res['samples_per_s']:.0f} samples/s")
     line = {
@@ -451,7 +584,7 @@ def main():
                 "one resident batch reused every step",
         "config": {"workload": a.config, "layers": list(spec.sizes), "activation": spec.activation,
                    "loss": spec.loss, "optimizer": spec.optimizer, "lr": lr, "batch": B,
-                   "parallelism": "single GPU"},
+                   "parallelism": "single GPU", "graph_dispatch": a.graph_dispatch},
         "mfma_frac_step": round(res["mfma_frac_step"], 5),
         "gemm_gflop_per_step": round(res["gemm_gflop_per_step"], 4),
         "loss_after": res["loss_after"],
@@ -466,8 +599,8 @@ def main():
     if a.config in PUBLISHED_CPU:
         line["reference_published_cpu"] = PUBLISHED_CPU[a.config]
     if not a.no_cpu:
-        line["cpu_baseline"] = run_cpu(a.config)
-        log(f"cpu baseline: {line['cpu_baseline']}")
+        line["cpu_baseline"], line["cpu_baseline_legs"] = run_cpu(a.config, a.cpu_threads)
+        line["cpu_host"] = host_cpu()
     if not a.no_profile:
         line["runtime_optimizer"] = run_rt_optimizer()
         log(f"runtime optimizer: {line['runtime_optimizer']}")
@@ -488,7 +621,7 @@ def main():
             sec["kernels"] = [{k: (round(v, 5) if isinstance(v, float) else v) for k, v in r.items()}
                               for r in s_res["kernels"]]
         if not a.no_cpu:
-            sec["cpu_baseline"] = run_cpu(a.secondary, budget_s=10.0, max_steps=3)
+            sec["cpu_baseline"], _ = run_cpu(a.secondary, a.cpu_threads, full_protocol=False)
         line["secondary"] = sec
     print(json.dumps(line), flush=True)
     return 0

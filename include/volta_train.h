@@ -24,12 +24,12 @@
  *   volta_amd/libvolta_hip.so      -- the product: HIP kernels for gfx950
  *   oracle/liboracle_volta.so      -- the CPU restatement used as the checker
  *
- * Loading libvolta_hip.so sets DEBUG_CLR_GRAPH_PACKET_CAPTURE=0 in the
- * process environment unless the caller has set it, so that HIP replays the
- * step graph by dispatching its nodes in order (faster for this chain of
- * short dependent kernels).  HIP reads the variable once, when its runtime
- * initialises: a host that made HIP calls before loading the library keeps
- * its own setting.
+ * The library leaves the process environment alone.  HIP replays the step
+ * graph from the kernel packets it recorded at instantiation unless the
+ * host sets DEBUG_CLR_GRAPH_PACKET_CAPTURE=0 before its first HIP call
+ * (then the nodes are dispatched in order as stream launches, which is
+ * faster for this chain of short dependent kernels); that choice is the
+ * host's.
  *
  * Layout conventions (all row-major fp32, as in the reference):
  *   W_i  [L[i] x L[i+1]],  b_i [L[i+1]],  X [B x L[0]],  Y [B x L[n]]
@@ -226,6 +226,11 @@ int64_t volta_train_state_size(VoltaTrainHandle* h);
 #define VOLTA_BUF_LN_GAMMA 4
 #define VOLTA_BUF_LN_BETA 5
 #define VOLTA_BUF_DROPOUT_MASK 6
+/*   VOLTA_BUF_PRE        pre_i [B x L[i+1]], i = 0..n-2: the hidden layer's
+ *                        pre-activation act_i W_i + b_i (GPU library: kept
+ *                        only where the backward needs it -- leaky ReLU,
+ *                        SiLU, GELU, softmax, LayerNorm or dropout) */
+#define VOLTA_BUF_PRE 7
 int64_t volta_train_debug_buffer(VoltaTrainHandle* h, int32_t kind, int32_t layer, float* out);
 int32_t volta_train_get_state(VoltaTrainHandle* h, float* state, int64_t* step);
 int32_t volta_train_set_state(VoltaTrainHandle* h, const float* state, int64_t step);

@@ -170,6 +170,26 @@ void gemm_tn(T* C, const T* A, const T* B, int m, int k, int n) {
   }
 }
 
+#ifdef VOLTA_CPU_REF_GEMM
+// CPU-baseline build only (oracle/_ref/libvolta_cpu_ref.so, never a
+// checker): the fp32 step's GEMMs are the reference's own C GEMM
+// (gemm_shim.c:152-210, compiled from its source by oracle/Makefile), as
+// the reference's C compile-train path calls them (mlp_train_codegen.rs:
+// 291-384).  The fp64 twin keeps the loops above.
+extern "C" {
+void volta_gemm_f32(float* C, const float* A, const float* B, int64_t m, int64_t k, int64_t n);
+void volta_gemm_tn_f32(float* C, const float* A, const float* B, int64_t m, int64_t k, int64_t n);
+}
+template <>
+void gemm_nn<float>(float* C, const float* A, const float* B, int m, int k, int n) {
+  volta_gemm_f32(C, A, B, m, k, n);
+}
+template <>
+void gemm_tn<float>(float* C, const float* A, const float* B, int m, int k, int n) {
+  volta_gemm_tn_f32(C, A, B, m, k, n);
+}
+#endif
+
 // dst[cols x rows] = src[rows x cols]^T (fast_transpose, :389-440).
 template <typename T>
 void transpose(T* dst, const T* src, int rows, int cols) {
@@ -424,11 +444,22 @@ struct Net {
     *w = w0 - lr * (mhat / denom + wd * w0);
   }
 
+  // adam_update (:326-340): buffers of at least 2^17 elements are cut into
+  // 8192-element chunks updated in parallel (Rayon there, OpenMP here).
+  // Every chunk but the last is a multiple of 8 long, so the scalar-tail
+  // elements are the last (cnt mod 8) of the buffer either way and the
+  // result does not depend on the thread count.
   static void adam_update(T* w, T* m, T* v, const T* g, size_t cnt, T b1, T b2, T bc1, T bc2,
                           T lr, T eps, T wd) {
     const size_t vec_end = cnt - cnt % 8;
-    for (size_t k = 0; k < cnt; ++k)
-      adam_elem(w + k, m + k, v + k, g[k], b1, b2, bc1, bc2, lr, eps, wd, k >= vec_end);
+    const size_t kChunk = 8192;
+    const long long chunks = (long long)((cnt + kChunk - 1) / kChunk);
+#pragma omp parallel for schedule(static) if (cnt >= (size_t(1) << 17))
+    for (long long q = 0; q < chunks; ++q) {
+      const size_t k0 = (size_t)q * kChunk, k1 = std::min(cnt, k0 + kChunk);
+      for (size_t k = k0; k < k1; ++k)
+        adam_elem(w + k, m + k, v + k, g[k], b1, b2, bc1, bc2, lr, eps, wd, k >= vec_end);
+    }
   }
 
   // Adagrad, :967-985.
@@ -528,12 +559,22 @@ struct Net {
         T* wi = w[i].data();
         const T* g = dw[i].data();
         const T nlr = -tlr;
-        for (size_t k = 0; k < rc; ++k) wi[k] = wi[k] + nlr * g[k];
+#pragma omp parallel for schedule(static) if (rc >= (size_t(1) << 17))
+        for (long long k = 0; k < (long long)rc; ++k) wi[k] = wi[k] + nlr * g[k];
         for (int k = 0; k < c; ++k) b[i][k] = b[i][k] - tlr * db[i][k];
       }
     }
   }
 };
+
+// The handle bound for volta_infer (volta_infer_bind); cleared when freed.
+static std::mutex g_infer_mu;
+static VoltaTrainHandle* g_infer_model = nullptr;
+
+static void unbind_infer(VoltaTrainHandle* vh) {
+  std::lock_guard<std::mutex> lock(g_infer_mu);
+  if (g_infer_model == vh) g_infer_model = nullptr;
+}
 
 struct Handle {
   int precision = 32;  // 32: reference-faithful fp32; 64: fp64 twin
@@ -743,7 +784,11 @@ void volta_train_set_params(VoltaTrainHandle* vh, int32_t li, const float* w, co
   }
 }
 
-void volta_train_free(VoltaTrainHandle* vh) { delete H(vh); }
+void volta_train_free(VoltaTrainHandle* vh) {
+  if (!vh) return;
+  unbind_infer(vh);
+  delete H(vh);
+}
 
 int32_t volta_train_sync(VoltaTrainHandle*) { return 0; }
 
@@ -858,19 +903,27 @@ static int64_t copy_out(const std::vector<T>& v, float* out) {
 }
 
 template <typename T>
-static int64_t debug_buffer(Net<T>& f, int kind, int layer, float* out) {
+static int64_t copy_out(const std::vector<T>& v, double* out) {
+  for (size_t k = 0; k < v.size(); ++k) out[k] = (double)v[k];
+  return (int64_t)v.size();
+}
+
+template <typename T, typename O>
+static int64_t debug_buffer(Net<T>& f, int kind, int layer, O* out) {
   switch (kind) {
     case VOLTA_BUF_ACT: return layer >= 0 && layer <= f.n ? copy_out(f.act[layer], out) : -1;
     case VOLTA_BUF_DELTA: return layer >= 0 && layer < f.n ? copy_out(f.delta[layer], out) : -1;
     case VOLTA_BUF_GRAD_W: return layer >= 0 && layer < f.n ? copy_out(f.dw[layer], out) : -1;
     case VOLTA_BUF_GRAD_B: return layer >= 0 && layer < f.n ? copy_out(f.db[layer], out) : -1;
+    case VOLTA_BUF_PRE:
+      return layer >= 0 && layer < f.n - 1 && f.pre[layer].size() ? copy_out(f.pre[layer], out) : -1;
     case VOLTA_BUF_LN_GAMMA:
       return f.spec.layernorm && layer >= 0 && layer < f.n - 1 ? copy_out(f.ln_g[layer], out) : -1;
     case VOLTA_BUF_LN_BETA:
       return f.spec.layernorm && layer >= 0 && layer < f.n - 1 ? copy_out(f.ln_b[layer], out) : -1;
     case VOLTA_BUF_DROPOUT_MASK:
       if (!(f.spec.dropout_p > 0.0f) || layer < 0 || layer >= f.n - 1) return -1;
-      for (size_t k = 0; k < f.mask[layer].size(); ++k) out[k] = (float)f.mask[layer][k];
+      for (size_t k = 0; k < f.mask[layer].size(); ++k) out[k] = (O)f.mask[layer][k];
       return (int64_t)f.mask[layer].size();
   }
   return -1;
@@ -879,6 +932,14 @@ static int64_t debug_buffer(Net<T>& f, int kind, int layer, float* out) {
 extern "C" {
 
 int64_t volta_train_debug_buffer(VoltaTrainHandle* vh, int32_t kind, int32_t layer, float* out) {
+  Handle* h = H(vh);
+  if (!h || !out) return -1;
+  return h->precision == 64 ? debug_buffer(h->d, kind, layer, out) : debug_buffer(h->f, kind, layer, out);
+}
+
+// The same buffers in double: the fp64 twin's values without rounding to
+// fp32 (the fp32 oracle's values widened).
+int64_t volta_oracle_debug_buffer_f64(VoltaTrainHandle* vh, int32_t kind, int32_t layer, double* out) {
   Handle* h = H(vh);
   if (!h || !out) return -1;
   return h->precision == 64 ? debug_buffer(h->d, kind, layer, out) : debug_buffer(h->f, kind, layer, out);
@@ -916,6 +977,15 @@ void volta_oracle_lcg_xavier(float* w, int64_t cnt, int32_t r, int32_t c, uint64
   lcg_xavier_init(w, (size_t)cnt, r, c, rng);
 }
 
+// Adam's bias correction 1 - beta^t as the step computes it: f32 powf of
+// the step counter (:803-811).
+float volta_oracle_bias_correction(float beta, int64_t t) { return 1.0f - powf(beta, (float)t); }
+
+// Activation derivative over n elements in double (checks of whole buffers).
+void volta_oracle_act_bwd_f64_n(int32_t act, const double* pre, const double* y, double* out, int64_t n) {
+  for (int64_t k = 0; k < n; ++k) out[k] = act_bwd<double>(act, pre[k], y[k]);
+}
+
 float volta_oracle_act_fwd(int32_t act, float x) { return act_fwd<float>(act, x); }
 float volta_oracle_act_bwd(int32_t act, float pre, float y) { return act_bwd<float>(act, pre, y); }
 double volta_oracle_act_fwd_f64(int32_t act, double x) { return act_fwd<double>(act, x); }
@@ -928,6 +998,15 @@ int32_t volta_oracle_threads(void) {
   return omp_get_max_threads();
 #else
   return 1;
+#endif
+}
+
+// Thread count of the OpenMP loops (CPU-baseline timing at a stated count).
+void volta_oracle_set_threads(int32_t n) {
+#ifdef _OPENMP
+  if (n > 0) omp_set_num_threads(n);
+#else
+  (void)n;
 #endif
 }
 
@@ -949,9 +1028,6 @@ static void infer_rows(Net<T>& net, const float* X, int64_t rows, float* out) {
     for (int64_t k = 0; k < m * Ln; ++k) out[r0 * Ln + k] = (float)net.act[net.n][(size_t)k];
   }
 }
-
-static std::mutex g_infer_mu;
-static VoltaTrainHandle* g_infer_model = nullptr;
 
 extern "C" {
 

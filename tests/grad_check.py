@@ -1,0 +1,275 @@
+"""Gradient-level checks of one training step (test infrastructure).
+
+A candidate step (the HIP library, or the fp32 oracle when the checker itself
+is tested) is compared with the fp64 twin of the oracle run from the same
+state on the same batch.  Every product of the step is checked elementwise
+against a bound built by the triangle inequality from quantities the test
+measures:
+
+  C = op(A) . op(B) computed in fp32 from the candidate's own operands
+  A_c, B_c, against the twin's C_t = A_t . B_t:
+
+    |C_c - C_t| <= |A_c - A_t| . |B_c| + |A_t| . |B_c - B_t|      (input deviation)
+                 + 2 K eps |A_c| . |B_c|                          (fp32 summation of K terms)
+
+with eps = 2^-24 and the products of absolute values taken in float64.  The
+same bound with zero input deviation is the local check of each product on
+the candidate's own operands (the bound the GEMM kernel tests use).  The
+activation derivative, the loss gradient and the bias-gradient sum get the
+analogous bounds.  A gradient that is wrong in magnitude (a dropped term, a
+wrong scale, a transposed operand) exceeds them; rounding in another
+summation order, and ReLU masks that flip at a pre-activation within
+rounding of zero, stay inside because the measured input deviation carries
+them.
+
+The step's formulas are those of mlp_train_rust_codegen.rs:698-994: forward
+act_{i+1} = f(act_i W_i + b_i) (:719-743), MSE delta 2(y^ - y)/(B L_n)
+(:792-798) or softmax-CE (softmax - onehot)/B (interpreter.rs:762-812),
+delta_{i-1} = (delta_i W_i^T) * f'(pre_{i-1}) (:893-929), dW_i = act_i^T
+delta_i (:315-317), db_i = sum_b delta_i (:931-933).
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from volta_amd.abi import ACTIVATIONS, BUF_ACT, BUF_DELTA, BUF_GRAD_B, BUF_GRAD_W, BUF_PRE
+
+EPS = 2.0 ** -24
+# max |f'| of each hidden activation (bounds |f(a) - f(b)| by L |a - b|)
+LIPSCHITZ = {"relu": 1.0, "leaky_relu": 1.0, "sigmoid": 0.25, "tanh": 1.0, "silu": 1.1, "gelu": 1.13}
+RELU_LIKE = ("relu",)
+
+_D = C.POINTER(C.c_double)
+
+
+class StepBuffers:
+    """The buffers of one step: act_0..act_n, delta_0..delta_{n-1},
+    pre_0..pre_{n-2} (None where the library keeps none), dW_i, db_i, all
+    float64 arrays shaped as matrices."""
+
+    def __init__(self, act, delta, pre, dw, db):
+        self.act, self.delta, self.pre, self.dw, self.db = act, delta, pre, dw, db
+
+
+def read_candidate(t, spec, B) -> StepBuffers:
+    """Buffers of a Trainer's last step through volta_train_debug_buffer
+    (fp32 values widened)."""
+    n, L = spec.n_layers, spec.sizes
+    act = [t.debug_buffer(BUF_ACT, i).astype(np.float64).reshape(B, L[i]) for i in range(n + 1)]
+    delta = [t.debug_buffer(BUF_DELTA, i).astype(np.float64).reshape(B, L[i + 1]) for i in range(n)]
+    pre = []
+    for i in range(n - 1):
+        try:
+            pre.append(t.debug_buffer(BUF_PRE, i).astype(np.float64).reshape(B, L[i + 1]))
+        except RuntimeError:
+            pre.append(None)
+    dw = [t.debug_buffer(BUF_GRAD_W, i).astype(np.float64).reshape(L[i], L[i + 1]) for i in range(n)]
+    db = [t.debug_buffer(BUF_GRAD_B, i).astype(np.float64) for i in range(n)]
+    return StepBuffers(act, delta, pre, dw, db)
+
+
+def read_twin(orc, t, spec, B) -> StepBuffers:
+    """Buffers of the fp64 twin's last step, unrounded."""
+    n, L = spec.n_layers, spec.sizes
+    fn = orc.lib.volta_oracle_debug_buffer_f64
+
+    def get(kind, i, shape):
+        out = np.zeros(int(np.prod(shape)), np.float64)
+        got = fn(t.h, kind, i, out.ctypes.data_as(_D))
+        if got != out.size:
+            return None
+        return out.reshape(shape)
+
+    act = [get(BUF_ACT, i, (B, L[i])) for i in range(n + 1)]
+    delta = [get(BUF_DELTA, i, (B, L[i + 1])) for i in range(n)]
+    pre = [get(BUF_PRE, i, (B, L[i + 1])) for i in range(n - 1)]
+    dw = [get(BUF_GRAD_W, i, (L[i], L[i + 1])) for i in range(n)]
+    db = [get(BUF_GRAD_B, i, (L[i + 1],)) for i in range(n)]
+    return StepBuffers(act, delta, pre, dw, db)
+
+
+def act_derivative(orc, spec, pre, y):
+    """f'(pre) in float64 by the oracle's activation derivative (y is the
+    layer output, which sigmoid/tanh derive from)."""
+    pre = np.ascontiguousarray(pre, np.float64)
+    y = np.ascontiguousarray(y, np.float64)
+    out = np.empty_like(pre)
+    orc.lib.volta_oracle_act_bwd_f64_n(ACTIVATIONS[spec.activation], pre.ctypes.data_as(_D),
+                                       y.ctypes.data_as(_D), out.ctypes.data_as(_D), pre.size)
+    return out
+
+
+class Report:
+    def __init__(self, label):
+        self.label = label
+        self.rows = []
+        self.failures = []
+
+    def check(self, name, got, want, bound):
+        got, want, bound = (np.asarray(x, np.float64) for x in (got, want, bound))
+        err = np.abs(got - want)
+        bad = ~(err <= bound)
+        ratio = float(np.max(err / np.maximum(bound, 1e-300))) if err.size else 0.0
+        self.rows.append((name, ratio, int(bad.sum()), err.size))
+        if bad.any():
+            k = int(np.flatnonzero(bad.ravel())[0])
+            self.failures.append(f"{self.label} {name}: {int(bad.sum())} of {err.size} elements beyond the bound "
+                                 f"(first at flat index {k}: got {got.ravel()[k]:.9g} want {want.ravel()[k]:.9g} "
+                                 f"bound {bound.ravel()[k]:.3g})")
+
+    def summary(self):
+        return "\n".join(f"  {self.label} {n}: max err/bound {r:.3f} ({b} of {s} beyond)" for n, r, b, s in self.rows)
+
+
+def check_step(orc, spec, B, X, Y, W0, b0, cand: StepBuffers, twin: StepBuffers, label, local=True) -> Report:
+    """All product checks of one step.  W0/b0: the parameters the step
+    started from (float32 arrays), X/Y the batch."""
+    n, L = spec.n_layers, spec.sizes
+    rep = Report(label)
+    W = [np.asarray(w, np.float64).reshape(L[i], L[i + 1]) for i, w in enumerate(W0)]
+    bvec = [np.asarray(b, np.float64) for b in b0]
+    aW = [np.abs(w) for w in W]
+    lip = LIPSCHITZ.get(spec.activation, 1.0)
+
+    rep.check("act0 (input)", cand.act[0], np.asarray(X, np.float64).reshape(B, L[0]), np.zeros((B, L[0])))
+    # forward: z_i = act_i W_i + b_i (K = r terms plus the bias)
+    for i in range(n):
+        r = L[i]
+        A_c, A_t = cand.act[i], twin.act[i]
+        rnd = 2 * (r + 1) * EPS * (np.abs(A_c) @ aW[i] + np.abs(bvec[i]))
+        zdev = np.abs(A_c - A_t) @ aW[i] + rnd
+        if local:
+            z_own = A_c @ W[i] + bvec[i]
+            if i == n - 1:
+                rep.check(f"fwd{i} local (output)", cand.act[n], z_own, rnd)
+            elif cand.pre[i] is not None:
+                rep.check(f"fwd{i} local (pre)", cand.pre[i], z_own, rnd)
+        if i == n - 1:
+            rep.check(f"fwd{i} vs fp64 (output)", cand.act[n], twin.act[n], zdev)
+        else:
+            if cand.pre[i] is not None and twin.pre[i] is not None:
+                rep.check(f"fwd{i} vs fp64 (pre)", cand.pre[i], twin.pre[i], zdev)
+            # fp32 evaluation of f: relative to the larger of |f| and |z|
+            # (GELU's 1 + tanh cancels in the negative tail)
+            f_rnd = 16 * EPS * (np.abs(twin.act[i + 1]) + np.abs(twin.pre[i]))
+            rep.check(f"fwd{i} vs fp64 (act)", cand.act[i + 1], twin.act[i + 1], lip * zdev + f_rnd + 1e-37)
+
+    # loss gradient
+    Ln = L[n]
+    yh_c, yh_t = cand.act[n], twin.act[n]
+    if spec.loss == "mse":
+        Yv = np.asarray(Y, np.float64).reshape(B, Ln)
+        scale = 2.0 / (B * Ln)
+        own = scale * (yh_c - Yv)
+        rnd = 8 * EPS * scale * (np.abs(yh_c) + np.abs(Yv))
+        if local:
+            rep.check("loss grad local", cand.delta[n - 1], own, rnd)
+        rep.check("loss grad vs fp64", cand.delta[n - 1], twin.delta[n - 1], scale * np.abs(yh_c - yh_t) + rnd)
+    else:
+        lab = np.asarray(Y).reshape(B)
+        z = yh_c - yh_c.max(axis=1, keepdims=True)
+        p = np.exp(z)
+        p /= p.sum(axis=1, keepdims=True)
+        onehot = np.zeros((B, Ln))
+        onehot[np.arange(B), lab] = 1.0
+        own = (p - onehot) / B
+        rnd = (4 * Ln + 16) * EPS / B * np.ones((B, Ln))
+        if local:
+            rep.check("loss grad local", cand.delta[n - 1], own, rnd)
+        dz = np.abs(yh_c - yh_t).max(axis=1, keepdims=True)
+        rep.check("loss grad vs fp64", cand.delta[n - 1], twin.delta[n - 1], dz / B + rnd)
+
+    # backward: delta_{i-1} = (delta_i W_i^T) * f'(pre_{i-1}) (K = c terms)
+    for i in range(n - 1, 0, -1):
+        c = L[i + 1]
+        D_c, D_t = cand.delta[i], twin.delta[i]
+        P_c = D_c @ W[i].T
+        P_t = D_t @ W[i].T
+        rnd = 2 * c * EPS * (np.abs(D_c) @ aW[i].T)
+        pdev = np.abs(D_c - D_t) @ aW[i].T + rnd
+        if spec.activation in RELU_LIKE:
+            f_c = (cand.act[i] > 0).astype(np.float64)
+            f_t = (twin.act[i] > 0).astype(np.float64)
+            f_rnd = 0.0
+        else:
+            pre_c = cand.pre[i - 1]
+            if pre_c is None:  # derivative from the output (sigmoid/tanh) or recomputed pre
+                pre_c = cand.act[i - 1] @ W[i - 1] + bvec[i - 1]
+            f_c = act_derivative(orc, spec, pre_c, cand.act[i])
+            f_t = act_derivative(orc, spec, twin.pre[i - 1], twin.act[i])
+            f_rnd = 32 * EPS  # the candidate's fp32 evaluation of f' (absolute; terms of f' are O(1))
+        if local:
+            rep.check(f"dx{i} local", cand.delta[i - 1], P_c * f_c,
+                      rnd * (np.abs(f_c) + f_rnd) + np.abs(P_c) * f_rnd + 8 * EPS * np.abs(P_c * f_c) + 1e-37)
+        bound = pdev * (np.abs(f_c) + f_rnd) + np.abs(P_t) * (np.abs(f_c - f_t) + f_rnd) \
+            + 8 * EPS * np.abs(P_t * f_c) + 1e-37
+        rep.check(f"dx{i} vs fp64", cand.delta[i - 1], twin.delta[i - 1], bound)
+
+    # dW_i = act_i^T delta_i and db_i = sum_b delta_i (K = B terms)
+    for i in range(n):
+        A_c, A_t = cand.act[i], twin.act[i]
+        D_c, D_t = cand.delta[i], twin.delta[i]
+        rnd = 2 * B * EPS * (np.abs(A_c).T @ np.abs(D_c))
+        if local:
+            rep.check(f"dw{i} local", cand.dw[i], A_c.T @ D_c, rnd + 1e-37)
+        bound = np.abs(A_c - A_t).T @ np.abs(D_c) + np.abs(A_t).T @ np.abs(D_c - D_t) + rnd + 1e-37
+        rep.check(f"dw{i} vs fp64", cand.dw[i], twin.dw[i], bound)
+        rnd_b = 2 * B * EPS * np.abs(D_c).sum(axis=0)
+        if local:
+            rep.check(f"db{i} local", cand.db[i], D_c.sum(axis=0), rnd_b + 1e-37)
+        rep.check(f"db{i} vs fp64", cand.db[i], twin.db[i], np.abs(D_c - D_t).sum(axis=0) + rnd_b + 1e-37)
+    return rep
+
+
+def expected_update(orc, spec, lr, t_next, W0, b0, state0, dw, db):
+    """The oracle's fp32 optimizer applied to the given gradients from the
+    starting parameters and state: (W list, b list, state) -- what the
+    candidate's fused update must equal bit for bit.  `t_next` is the step
+    counter after the step (Adam's bias correction uses it)."""
+    F = C.POINTER(C.c_float)
+
+    def p(a):
+        return a.ctypes.data_as(F)
+
+    n = spec.n_layers
+    W = [np.array(w, np.float32, copy=True).ravel() for w in W0]
+    bb = [np.array(b, np.float32, copy=True).ravel() for b in b0]
+    st = np.array(state0, np.float32, copy=True)
+    g_w = [np.ascontiguousarray(np.asarray(g, np.float32).ravel()) for g in dw]
+    g_b = [np.ascontiguousarray(np.asarray(g, np.float32).ravel()) for g in db]
+    off = 0
+    adam = spec.optimizer in ("adam", "adamw")
+    if adam:
+        bc1 = orc.lib.volta_oracle_bias_correction(spec.beta1, t_next)
+        bc2 = orc.lib.volta_oracle_bias_correction(spec.beta2, t_next)
+    for i in range(n):
+        nw, nb = W[i].size, bb[i].size
+        if adam:
+            mw, mb = st[off:off + nw], st[off + nw:off + nw + nb]
+            vw, vb = st[off + nw + nb:off + 2 * nw + nb], st[off + 2 * nw + nb:off + 2 * (nw + nb)]
+            mw, mb, vw, vb = (np.ascontiguousarray(x) for x in (mw, mb, vw, vb))
+            wd = spec.to_c().weight_decay if spec.optimizer == "adamw" else 0.0
+            orc.lib.volta_oracle_adam(p(W[i]), p(mw), p(vw), p(g_w[i]), nw, spec.beta1, spec.beta2, bc1, bc2, lr,
+                                      spec.eps, wd)
+            orc.lib.volta_oracle_adam(p(bb[i]), p(mb), p(vb), p(g_b[i]), nb, spec.beta1, spec.beta2, bc1, bc2, lr,
+                                      spec.eps, 0.0)
+            st[off:off + nw], st[off + nw:off + nw + nb] = mw, mb
+            st[off + nw + nb:off + 2 * nw + nb], st[off + 2 * nw + nb:off + 2 * (nw + nb)] = vw, vb
+            off += 2 * (nw + nb)
+        elif spec.optimizer == "adagrad":
+            gw, gb = (np.ascontiguousarray(x) for x in (st[off:off + nw], st[off + nw:off + nw + nb]))
+            orc.lib.volta_oracle_adagrad(p(W[i]), p(gw), p(g_w[i]), nw, lr, spec.eps)
+            orc.lib.volta_oracle_adagrad(p(bb[i]), p(gb), p(g_b[i]), nb, lr, spec.eps)
+            st[off:off + nw], st[off + nw:off + nw + nb] = gw, gb
+            off += nw + nb
+        else:
+            raise ValueError("expected_update covers the adaptive optimizers")
+    return W, bb, st
+
+
+def bits_equal(a, b):
+    a = np.ascontiguousarray(a, np.float32).ravel()
+    b = np.ascontiguousarray(b, np.float32).ravel()
+    return a.shape == b.shape and bool(np.array_equal(a.view(np.uint32), b.view(np.uint32)))

@@ -28,6 +28,10 @@ ORACLE_EXTRA = {
     "volta_oracle_act_fwd_f64": (C.c_double, [C.c_int32, C.c_double]),
     "volta_oracle_act_bwd_f64": (C.c_double, [C.c_int32, C.c_double, C.c_double]),
     "volta_oracle_threads": (C.c_int32, []),
+    "volta_oracle_set_threads": (None, [C.c_int32]),
+    "volta_oracle_bias_correction": (C.c_float, [C.c_float, C.c_int64]),
+    "volta_oracle_act_bwd_f64_n": (None, [C.c_int32, _D, _D, _D, C.c_int64]),
+    "volta_oracle_debug_buffer_f64": (C.c_int64, [C.c_void_p, C.c_int32, C.c_int32, _D]),
 }
 
 _cache = {}

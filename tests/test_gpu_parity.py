@@ -323,7 +323,7 @@ CONFIGS = {
     "c3_mlp512w_gelu_adamw_b64": (MlpSpec([512, 2048, 2048, 512, 1], "gelu", "adamw"), 64, 1e-3, 50),
     "c4_silu_sgd_b128": (MlpSpec([512, 1024, 1024, 512, 256, 1], "silu", "sgd"), 128, 0.01, 50),
     "c4_silu_sgd_b256": (MlpSpec([512, 1024, 1024, 512, 256, 1], "silu", "sgd"), 256, 0.01, 50),
-    "c4_silu_sgd_b1024": (MlpSpec([512, 1024, 1024, 512, 256, 1], "silu", "sgd"), 1024, 0.01, 20),
+    "c4_silu_sgd_b1024": (MlpSpec([512, 1024, 1024, 512, 256, 1], "silu", "sgd"), 1024, 0.01, 50),
     "c5_wide_ce_adagrad_b4096": (MlpSpec([1024, 4096, 4096, 1024, 10], "relu", "adagrad", "ce", eps=1e-10),
                                  4096, 1e-2, 3),
 }

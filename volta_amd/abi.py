@@ -154,7 +154,7 @@ VT_SIGNATURES = {
 }
 
 BUF_ACT, BUF_DELTA, BUF_GRAD_W, BUF_GRAD_B = 0, 1, 2, 3
-BUF_LN_GAMMA, BUF_LN_BETA, BUF_DROPOUT_MASK = 4, 5, 6
+BUF_LN_GAMMA, BUF_LN_BETA, BUF_DROPOUT_MASK, BUF_PRE = 4, 5, 6, 7
 
 # Every symbol include/volta_train.h declares (checked by the CPU tests).
 HEADER_SYMBOLS = tuple(_SIGNATURES)
@@ -329,7 +329,7 @@ class Trainer:
         count = {BUF_ACT: lambda i: B * sizes[i], BUF_DELTA: lambda i: B * sizes[i + 1],
                  BUF_GRAD_W: lambda i: sizes[i] * sizes[i + 1], BUF_GRAD_B: lambda i: sizes[i + 1],
                  BUF_LN_GAMMA: lambda i: sizes[i + 1], BUF_LN_BETA: lambda i: sizes[i + 1],
-                 BUF_DROPOUT_MASK: lambda i: B * sizes[i + 1]}[kind](layer)
+                 BUF_DROPOUT_MASK: lambda i: B * sizes[i + 1], BUF_PRE: lambda i: B * sizes[i + 1]}[kind](layer)
         out = np.zeros(count, np.float32)
         n = self.lib.lib.volta_train_debug_buffer(self.h, kind, layer, fptr(out))
         if n != count:

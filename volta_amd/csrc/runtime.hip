@@ -611,17 +611,6 @@ static bool make_bc_table(Handle* h) {
   return true;
 }
 
-// HIP's runtime replays an instantiated graph either from kernel packets it
-// recorded at instantiation ("packet capture", the default) or by
-// dispatching the nodes in order as stream launches.  For this step's chain
-// of nine to seventeen dependent kernels the second is faster on MI355X (C2:
-// 65.2 -> 61.6 us per replay, no other change).  The runtime reads the
-// setting once, at its initialisation, so it is put in the environment when
-// the library is loaded; a value the caller has set is kept.
-__attribute__((constructor)) static void graph_dispatch_setting() {
-  setenv("DEBUG_CLR_GRAPH_PACKET_CAPTURE", "0", 0);
-}
-
 // Capture the step into a fresh graph (hyperparameters are kernel
 // arguments, so a change of them is a new capture).
 static bool capture(Handle* h) {
@@ -1045,7 +1034,18 @@ void volta_train_set_params(VoltaTrainHandle* vh, int32_t li, const float* w, co
     h->status |= VOLTA_STATUS_DEVICE_ERROR;
 }
 
-void volta_train_free(VoltaTrainHandle* vh) { delete H(vh); }
+// The handle bound for volta_infer (volta_infer_bind); cleared when freed.
+static std::mutex g_infer_mu;
+static VoltaTrainHandle* g_infer_model = nullptr;
+
+void volta_train_free(VoltaTrainHandle* vh) {
+  if (!vh) return;
+  {
+    std::lock_guard<std::mutex> lock(g_infer_mu);
+    if (g_infer_model == vh) g_infer_model = nullptr;
+  }
+  delete H(vh);
+}
 
 int32_t volta_train_sync(VoltaTrainHandle* vh) {
   Handle* h = H(vh);
@@ -1194,6 +1194,11 @@ int64_t volta_train_debug_buffer(VoltaTrainHandle* vh, int32_t kind, int32_t lay
       if (layer < 0 || layer >= n || !h->keep_grads) return -1;
       src = h->grads + h->layers[layer].b_off;
       count = (size_t)h->layers[layer].c;
+      break;
+    case VOLTA_BUF_PRE:
+      if (layer < 0 || layer >= n - 1 || !h->pre[layer]) return -1;
+      src = h->pre[layer];
+      count = (size_t)B * h->L[layer + 1];
       break;
     case VOLTA_BUF_LN_GAMMA:
     case VOLTA_BUF_LN_BETA:
@@ -1374,9 +1379,6 @@ int32_t volta_train_infer(VoltaTrainHandle* vh, const float* X, int64_t rows, fl
   }
   return 0;
 }
-
-static std::mutex g_infer_mu;
-static VoltaTrainHandle* g_infer_model = nullptr;
 
 int32_t volta_infer_bind(VoltaTrainHandle* vh) {
   std::lock_guard<std::mutex> lock(g_infer_mu);
