@@ -256,6 +256,19 @@ int32_t volta_train_set_hparams(VoltaTrainHandle* h, float beta1, float beta2, f
  * Returns 0 on success. */
 int32_t volta_train_infer(VoltaTrainHandle* h, const float* X, int64_t rows, float* out);
 
+/* Allocation-free variant of volta_train_infer.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under stream capture, serving loops, harnesses that forbid hipMalloc).
+ * X [rows x L0] and out [rows x Ln] are 16-byte aligned device buffers; the
+ * forward runs on the handle's weights and activation buffers with its
+ * split-K partial planes in a static 64 MiB device array per GPU (held from
+ * library load to process end); rows whose plan needs more are rejected
+ * with an error.  Nothing is allocated, freed or synchronized: the launches
+ * are enqueued on the handle's stream (volta_train_sync before reading
+ * out).  Calls that overlap on one GPU share that GPU's scratch and race.
+ * Returns 0, or -1 with volta_train_last_error() set. */
+int32_t volta_train_infer_device_noalloc(VoltaTrainHandle* h, const float* X, int64_t rows, float* out);
+
 /* The inference library's entry point (codegen/inner.rs:198; contract
  * docs/ARCHITECTURE.md:125-141): output = forward(input) for in_n = rows*L0
  * input floats, writing rows*Ln floats (out_n must be at least that).  The

@@ -1063,6 +1063,12 @@ int32_t volta_train_infer(VoltaTrainHandle* vh, const float* X, int64_t rows, fl
   return 0;
 }
 
+// The CPU library's memory is host memory: the allocation-free variant is
+// volta_train_infer on the same buffers.
+int32_t volta_train_infer_device_noalloc(VoltaTrainHandle* vh, const float* X, int64_t rows, float* out) {
+  return volta_train_infer(vh, X, rows, out);
+}
+
 int32_t volta_infer_bind(VoltaTrainHandle* vh) {
   std::lock_guard<std::mutex> lock(g_infer_mu);
   g_infer_model = vh;

@@ -144,6 +144,7 @@ _SIGNATURES = {
     "volta_train_debug_buffer": (C.c_int64, [_P, C.c_int32, C.c_int32, _F]),
     "volta_train_set_hparams": (C.c_int32, [_P, C.c_float, C.c_float, C.c_float, C.c_float]),
     "volta_train_infer": (C.c_int32, [_P, _F, C.c_int64, _F]),
+    "volta_train_infer_device_noalloc": (C.c_int32, [_P, C.c_void_p, C.c_int64, C.c_void_p]),
     "volta_infer_bind": (C.c_int32, [_P]),
     "volta_infer": (None, [_F, C.c_int64, _F, C.c_int64]),
 }

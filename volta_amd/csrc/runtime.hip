@@ -111,6 +111,7 @@ struct Handle {
   int bc_len = 0;
   float* infer_x = nullptr;    // inference input rows (allocated on first use)
   float* infer_ws = nullptr;   // split-K workspace of inference plans (grown on demand)
+  float* scratch = nullptr;    // this device's static scratch (allocation-free inference)
   size_t infer_ws_floats = 0;
   SegTable segs{};
   std::vector<LayerPlan> layers;
@@ -637,11 +638,45 @@ static bool capture(Handle* h) {
   return true;
 }
 
+// ---------------------------------------------------------------------------
+// Static scratch for the allocation-free inference entry point
+// (volta_train_infer_device_noalloc): the split-K partial planes of its
+// forward products.  Every GPU the library runs on holds its own copy of
+// the array from module load until the process ends.  In host code
+// `scratch` names a host-side stand-in, not a device address: the device
+// address of each GPU's copy comes from hipGetSymbolAddress, taken once per
+// device (at volta_train_init on that device, with it current) and kept in
+// g_scratch_dev.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchFloats = size_t(16) << 20;  // 64 MiB
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+static std::mutex g_scratch_mu;
+static std::vector<float*> g_scratch_dev;  // device address per device ordinal (null until taken)
+
+// Device address of `dev`'s scratch copy; `dev` must be the current device.
+static float* scratch_address(int dev) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (dev < 0) return nullptr;
+  if ((int)g_scratch_dev.size() <= dev) g_scratch_dev.resize(dev + 1, nullptr);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_last_error(hip_msg("hipGetSymbolAddress(scratch)", e));
+      return nullptr;
+    }
+    g_scratch_dev[dev] = static_cast<float*>(p);
+  }
+  return g_scratch_dev[dev];
+}
+
 static bool build(Handle* h) {
   const volta_mlp_spec& s = h->spec;
   const int n = h->n, B = h->B;
   VOLTA_CHECK(hipGetDevice(&h->device));
   VOLTA_CHECK(hipDeviceGetAttribute(&h->num_cus, hipDeviceAttributeMultiprocessorCount, h->device));
+  h->scratch = scratch_address(h->device);  // null: the allocation-free entry point reports it
   VOLTA_CHECK(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
   const char* kg = std::getenv("VOLTA_KEEP_GRADS");
   h->keep_grads = kg && *kg && *kg != '0';
@@ -797,38 +832,37 @@ static bool build(Handle* h) {
   return capture(h);
 }
 
-// Forward pass only for `rows` <= B rows already in h->infer_x: hidden
-// layers as in the step (bias + activation epilogue, or the split-K
-// reduction, then LayerNorm when the spec has it; dropout is a training-only
-// transform), the output layer with the identity; result in act[n].
-static bool enqueue_forward(Handle* h, int rows, hipStream_t st) {
-  const volta_mlp_spec& s = h->spec;
-  const int n = h->n;
-  // plans for `rows` (a smaller M may split K where the step's plan did not)
-  std::vector<GemmPlan> plans(n);
+// Plans of the forward products for `rows` <= B rows (a smaller M may split
+// K where the step's plan did not); returns the split-K workspace they need
+// in floats.
+static size_t forward_plans(const Handle* h, int rows, std::vector<GemmPlan>* plans) {
+  plans->assign(h->n, GemmPlan{});
   size_t ws = 0;
-  for (int i = 0; i < n; ++i) {
+  for (int i = 0; i < h->n; ++i) {
     const LayerPlan& lp = h->layers[i];
-    plans[i] = gemm_plan(GEMM_NN, rows, lp.c, lp.r, lp.fwd.vec, h->num_cus);
-    plans[i].inkernel_reduce = false;
-    ws = std::max(ws, plans[i].workspace_floats(rows, lp.c));
+    (*plans)[i] = gemm_plan(GEMM_NN, rows, lp.c, lp.r, lp.fwd.vec, h->num_cus);
+    (*plans)[i].inkernel_reduce = false;
+    ws = std::max(ws, (*plans)[i].workspace_floats(rows, lp.c));
   }
-  if (ws > h->infer_ws_floats) {
-    VOLTA_CHECK(hipStreamSynchronize(st));
-    if (h->infer_ws) VOLTA_CHECK(hipFree(h->infer_ws));
-    h->infer_ws = nullptr;
-    h->infer_ws_floats = 0;
-    VOLTA_CHECK(hipMalloc((void**)&h->infer_ws, ws * sizeof(float)));
-    h->infer_ws_floats = ws;
-  }
+  return ws;
+}
+
+// Forward pass only for `rows` <= B rows of `x` (device, [rows x L0]):
+// hidden layers as in the step (bias + activation epilogue, or the split-K
+// reduction through `ws`, then LayerNorm when the spec has it; dropout is a
+// training-only transform) into the handle's activations, the output layer
+// with the identity into `out` (device, [rows x Ln]).
+static bool enqueue_forward_into(Handle* h, const std::vector<GemmPlan>& plans, int rows, const float* x, float* out,
+                                 float* ws, hipStream_t st) {
+  const int n = h->n;
   for (int i = 0; i < n; ++i) {
     const LayerPlan& lp = h->layers[i];
     const bool last = i == n - 1;
     GemmArgs a{};
-    a.partial = h->infer_ws;
+    a.partial = ws;
     a.counters = h->counters;
     a.epi.scalars = h->scalars;
-    a.A = i == 0 ? h->infer_x : h->act[i];
+    a.A = i == 0 ? x : h->act[i];
     a.lda = lp.r;
     a.B = h->params + lp.w_off;
     a.ldb = lp.c;
@@ -838,13 +872,29 @@ static bool enqueue_forward(Handle* h, int rows, hipStream_t st) {
     a.epi.kind = EPI_BIAS_ACT;
     a.epi.act = last ? kIdentity : h->gemm_act();
     a.epi.ldc = lp.c;
-    a.epi.out = h->act[i + 1];
+    a.epi.out = last ? out : h->act[i + 1];
     a.epi.bias = h->params + lp.b_off;
     VOLTA_CHECK(gemm_launch(plans[i], a, st));
     if (!last && (h->ext_ln || h->ext_softmax))
       VOLTA_CHECK(launch_hidden_fwd(hidden_fwd_args(h, i, rows, false), st));
   }
   return true;
+}
+
+// The same for rows already in h->infer_x, result in act[n]; the handle's
+// inference workspace grows (hipMalloc) when a plan needs more.
+static bool enqueue_forward(Handle* h, int rows, hipStream_t st) {
+  std::vector<GemmPlan> plans;
+  const size_t ws = forward_plans(h, rows, &plans);
+  if (ws > h->infer_ws_floats) {
+    VOLTA_CHECK(hipStreamSynchronize(st));
+    if (h->infer_ws) VOLTA_CHECK(hipFree(h->infer_ws));
+    h->infer_ws = nullptr;
+    h->infer_ws_floats = 0;
+    VOLTA_CHECK(hipMalloc((void**)&h->infer_ws, ws * sizeof(float)));
+    h->infer_ws_floats = ws;
+  }
+  return enqueue_forward_into(h, plans, rows, h->infer_x, h->act[h->n], h->infer_ws, st);
 }
 
 static void fail(Handle* h, int bits, const std::string& msg) {
@@ -1374,6 +1424,52 @@ int32_t volta_train_infer(VoltaTrainHandle* vh, const float* X, int64_t rows, fl
                        h->stream) != hipSuccess ||
         hipStreamSynchronize(h->stream) != hipSuccess) {
       volta::fail(h, VOLTA_STATUS_DEVICE_ERROR, "volta_train_infer: device error");
+      return -1;
+    }
+  }
+  return 0;
+}
+
+// Allocation-free variant of volta_train_infer for callers that cannot
+// allocate device memory (code under stream capture, serving loops): X and
+// out are device buffers, the forward's split-K partial planes go to this
+// device's static scratch, and nothing is allocated, freed or synchronized.
+// The launches are enqueued on the handle's stream (volta_train_sync before
+// reading `out`).  Calls that overlap on one GPU share its scratch and race.
+int32_t volta_train_infer_device_noalloc(VoltaTrainHandle* vh, const float* X, int64_t rows, float* out) {
+  Handle* h = H(vh);
+  if (!h) return -1;
+  const char* fn = "volta_train_infer_device_noalloc";
+  if (!X || !out || rows <= 0) {
+    volta::fail(h, VOLTA_STATUS_BAD_ARGUMENT, std::string(fn) + ": bad arguments");
+    return -1;
+  }
+  if (((uintptr_t)X | (uintptr_t)out) & 15) {
+    volta::fail(h, VOLTA_STATUS_BAD_ARGUMENT, std::string(fn) + ": X and out must be 16-byte aligned device pointers");
+    return -1;
+  }
+  if (!h->scratch) {
+    volta::fail(h, VOLTA_STATUS_DEVICE_ERROR, std::string(fn) + ": the static scratch address is unavailable");
+    return -1;
+  }
+  const int B = h->B, L0 = h->L[0], Ln = h->L[h->n];
+  // every chunk is B rows but the last; check both plans before launching
+  std::vector<volta::GemmPlan> full, tail;
+  const int tail_rows = (int)(rows % B);
+  const size_t need = std::max(rows >= B ? volta::forward_plans(h, B, &full) : 0,
+                               tail_rows ? volta::forward_plans(h, tail_rows, &tail) : 0);
+  if (need > volta::kScratchFloats) {
+    volta::fail(h, VOLTA_STATUS_BAD_ARGUMENT,
+                std::string(fn) + ": the forward at this row count needs " + std::to_string(need * 4) +
+                    " bytes of split-K workspace; the static scratch holds " +
+                    std::to_string(volta::kScratchFloats * 4));
+    return -1;
+  }
+  for (int64_t r0 = 0; r0 < rows; r0 += B) {
+    const int m = (int)std::min<int64_t>(B, rows - r0);
+    if (!volta::enqueue_forward_into(h, m == B ? full : tail, m, X + r0 * L0, out + r0 * Ln, h->scratch,
+                                     h->stream)) {
+      h->status |= VOLTA_STATUS_DEVICE_ERROR;
       return -1;
     }
   }
