@@ -133,6 +133,45 @@ def test_gemm_smallm_8_waves_integer_exact(layout, M, N, K):
     np.testing.assert_array_equal(got, (A.astype(np.int64) @ Bm.astype(np.int64)).astype(np.float32))
 
 
+TILE_BIG = 5
+
+
+@pytest.mark.parametrize("layout", [0, 1, 2], ids=["NN", "NT", "TN"])
+@pytest.mark.parametrize("M,N,K", [(256, 256, 64), (512, 768, 192), (768, 256, 1024), (256, 512, 4096)])
+def test_gemm_big_tile_integer_exact(layout, M, N, K):
+    """The 256x256 direct-to-LDS tile (C5's 4096 x 4096 products): exact on
+    integer operands for all three layouts, which pins the swizzled
+    K-contiguous LDS layout, the k-row MN layout, the wave/lane -> block
+    mapping and the XCD tile order."""
+    say(f"gemm big tile layout={layout} M={M} N={N} K={K}")
+    rng = np.random.default_rng(M * 3 + N * 5 + K * 7 + layout)
+    a_shape = (K, M) if layout == 2 else (M, K)
+    b_shape = (N, K) if layout == 1 else (K, N)
+    A = rng.integers(-4, 5, a_shape).astype(np.float32)
+    B = rng.integers(-4, 5, b_shape).astype(np.float32)
+    got = _gemm(layout, A, B, M, N, K, tile=TILE_BIG)
+    Am = A.T if layout == 2 else A
+    Bm = B.T if layout == 1 else B
+    np.testing.assert_array_equal(got, (Am.astype(np.int64) @ Bm.astype(np.int64)).astype(np.float32))
+
+
+@pytest.mark.parametrize("layout", [0, 1, 2], ids=["NN", "NT", "TN"])
+def test_gemm_big_tile_float_bound(layout):
+    """Random fp32 operands at a C5-like shape: within 2 K eps |A||B| of the
+    float64 product."""
+    M, N, K = 1024, 1024, 2048
+    say(f"gemm big tile float layout={layout}")
+    rng = np.random.default_rng(17 + layout)
+    A = rng.standard_normal((K, M) if layout == 2 else (M, K)).astype(np.float32)
+    B = rng.standard_normal((N, K) if layout == 1 else (K, N)).astype(np.float32)
+    got = _gemm(layout, A, B, M, N, K, tile=TILE_BIG).astype(np.float64)
+    Am = (A.T if layout == 2 else A).astype(np.float64)
+    Bm = (B.T if layout == 1 else B).astype(np.float64)
+    want = Am @ Bm
+    bound = 2 * K * 2.0 ** -24 * (np.abs(Am) @ np.abs(Bm))
+    assert np.all(np.abs(got - want) <= bound)
+
+
 def test_gemm_smallm_rejects_tn():
     """The small-M tile has no TN form: the launch is refused on the host."""
     lib = load_hip()

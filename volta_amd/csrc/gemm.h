@@ -77,7 +77,11 @@ struct GemmArgs {
 // (split over its 4 or 8 waves), for NN/NT products with few rows (B <= 256).
 // TILE_DW_SMALLK: 32x32 tiles of the TN (dW) product with a short K
 // (K = B <= 256), the optimizer applied on 16-byte rows.
-enum GemmTile { TILE_64x64 = 0, TILE_128x128 = 1, TILE_64x64_K64 = 2, TILE_SMALLM = 3, TILE_DW_SMALLK = 4 };
+// TILE_BIG: 256x256 tiles, direct-to-LDS operand loads, one workgroup per
+// CU, for exact 256-multiples with at least one tile per CU (C5's 4096 x 4096
+// products).
+enum GemmTile { TILE_64x64 = 0, TILE_128x128 = 1, TILE_64x64_K64 = 2, TILE_SMALLM = 3, TILE_DW_SMALLK = 4,
+                TILE_BIG = 5 };
 
 struct GemmPlan {
   int layout = GEMM_NN;
@@ -88,7 +92,8 @@ struct GemmPlan {
   bool inkernel_reduce = false;  // split-K reduced by the last slice (else a second kernel)
   int waves = 0;                 // TILE_SMALLM: waves per workgroup (4 or 8)
   int tiles(int M, int N) const {
-    const int t = tile == TILE_128x128 ? 128 : tile == TILE_SMALLM ? 16 : tile == TILE_DW_SMALLK ? 32 : 64;
+    const int t = tile == TILE_BIG ? 256 : tile == TILE_128x128 ? 128 : tile == TILE_SMALLM ? 16
+                  : tile == TILE_DW_SMALLK ? 32 : 64;
     return ((M + t - 1) / t) * ((N + t - 1) / t);
   }
   size_t workspace_floats(int M, int N) const { return splits > 1 ? (size_t)splits * (M + 1) * N : 0; }

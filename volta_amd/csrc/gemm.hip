@@ -483,7 +483,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& args, int bx, int by, 
   // MFMAs of one BK-deep stage held in LDS.  Fragments are double-buffered
   // in registers: those of group g + 1 are read from LDS before the MFMAs of
   // group g are issued, so the LDS latency hides behind the matrix work.
-  auto compute_stage = [&](const float* a_s, const float* b_s) {
+  auto compute_stage = [&](const float* a_s, const float* b_s, auto&& mid) {
     floatx4 fa_n[T::TM], fb_n[T::TN];
 #pragma unroll
     for (int i = 0; i < T::TM; ++i) fa_n[i] = load_frag<BM, BK, A_KC>(a_s, wm * WM + i * 32 + l32, h, 0);
@@ -514,6 +514,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& args, int bx, int by, 
           for (int j = 0; j < T::TN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
+      if (g == BK / 16 - 1) {
+        mid();
+        __builtin_amdgcn_sched_barrier(0);
+      }
       if (kColsum && colsum) {
         // rows beyond kend were loaded as zeros; adding them changes nothing
 #pragma unroll
@@ -538,7 +542,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& args, int bx, int by, 
         la.load(args.A, args.lda, M, kend, m0, k0 + BK, tid);
         lb.load(args.B, args.ldb, N, kend, n0, k0 + BK, tid);
       }
-      compute_stage(lds_a(buf), lds_b(buf));
+      __builtin_amdgcn_s_setprio(1);
+      compute_stage(lds_a(buf), lds_b(buf), [] {});
+      __builtin_amdgcn_s_setprio(0);
       if (more) {
         la.store(lds_a(buf ^ 1), tid);
         lb.store(lds_b(buf ^ 1), tid);
@@ -672,6 +678,31 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& args, int bx, int by, 
   }
 }
 
+// Output tile of workgroup `bx`.  Workgroups are dispatched round-robin
+// over the 8 XCDs (workgroup bx runs on XCD bx % 8), and each XCD has its
+// own L2.  When the tile grid splits into 8 equal rectangles, XCD x takes
+// rectangle x in row order, so an XCD's workgroups share the A row panels
+// and B column panels of one sub-grid instead of every XCD streaming all of
+// A (the identity order puts tiles tn, tn + 8, ... of every row on one XCD).
+// The rectangle shape is the one closest to square in tiles.
+__device__ __forceinline__ int xcd_tile(int bx, int tiles_m, int tiles_n) {
+  const int tiles = tiles_m * tiles_n;
+  if (tiles < 64 || (tiles & 7)) return bx;
+  int rm = 0, best = 1 << 30;
+  for (int c = 1; c <= 8; c *= 2) {  // rm x (8 / rm) rectangles
+    const int cn = 8 / c;
+    if (tiles_m % c || tiles_n % cn) continue;
+    const int hm = tiles_m / c, hn = tiles_n / cn;
+    const int d = hm > hn ? hm - hn : hn - hm;
+    if (d < best) best = d, rm = c;
+  }
+  if (!rm) return bx;
+  const int rn = 8 / rm, hm = tiles_m / rm, hn = tiles_n / rn;
+  const int x = bx & 7, j = bx >> 3;
+  const int tm = (x / rn) * hm + j / hn, tn = (x % rn) * hn + j % hn;
+  return tm * tiles_n + tn;
+}
+
 // Two waves per SIMD at least (at most 256 vector + accumulation registers
 // a lane): the 128x128 dW tile with an Adam epilogue otherwise settles a
 // few registers above that and runs at half occupancy.
@@ -681,8 +712,186 @@ gemm_f32_mfma(GemmArgs args) {
   __shared__ __attribute__((aligned(16))) float lds_a[2 * LdsTile<BM, BK, A_KC>::kFloats];
   __shared__ __attribute__((aligned(16))) float lds_b[2 * LdsTile<BN, BK, B_KC>::kFloats];
   __shared__ float lds_small[BM + 2];
-  gemm_tile<BM, BN, BK, WM, WN, A_KC, B_KC, VEC, EPI, INK>(args, blockIdx.x, blockIdx.y, gridDim.y, lds_a, lds_b,
-                                                          lds_small);
+  const int bx = xcd_tile(blockIdx.x, (args.M + BM - 1) / BM, (args.N + BN - 1) / BN);
+  gemm_tile<BM, BN, BK, WM, WN, A_KC, B_KC, VEC, EPI, INK>(args, bx, blockIdx.y, gridDim.y, lds_a, lds_b, lds_small);
+}
+
+// ---------------------------------------------------------------------------
+// Large tile for the C5-scale products: 256x256 outputs per workgroup, eight
+// waves of 64x128 (a 2x4 grid of 32x32 accumulator blocks each: 128
+// accumulation registers), one workgroup -- two waves per SIMD -- per CU.
+// Operand tiles (BK = 32 k) go from global memory straight into LDS
+// (global_load_lds_dwordx4: no register staging and no LDS stores),
+// double-buffered in two distinct LDS arrays: the loads of stage s+1 are
+// issued before the MFMAs of stage s, and a wave issues 128 MFMAs per stage
+// between its two synchronisations (wait for its own loads, then the
+// workgroup barrier).
+//
+// LDS layouts.  K-contiguous tile [256 rows][32 k] in 16-byte chunks: (row
+// r, k-quad q) at chunk r*8 + (q ^ (r & 7)), so the fragment reads of 8
+// consecutive rows at one k-quad hit 8 distinct 4-bank groups (each load
+// instruction fills 64 consecutive chunks: 8 rows, their k-quads permuted,
+// from 8 whole 128-byte row segments).  MN-contiguous tile [32 k][256]: one
+// k row of 256 floats per load instruction; a lane's four k values of a
+// column are four 4-byte reads, conflict-free across consecutive columns.
+//
+// Exact tiles only (M, N multiples of 256, K of 64, 16-byte aligned rows and
+// bases): every load is in bounds without a guard; gemm_plan checks.
+// ---------------------------------------------------------------------------
+constexpr int kBigBM = 256, kBigBK = 32;
+constexpr int kBigTileFloats = kBigBM * kBigBK;  // one operand tile of one stage (32 KB)
+
+typedef __attribute__((address_space(3))) void* LdsVoidPtr;
+
+// Issue this wave's 4 of the 32 one-kilobyte load instructions of an operand
+// tile (rows row0.., k k0..k0+31) into `tile`; `wave` (0..7) is wave-uniform.
+// Instruction j = wave + 8t fills chunks 64j..64j+63: K-contiguous, rows
+// 8j..8j+7 (lane: row 8j + lane/8, k-quad (lane & 7) ^ (row & 7));
+// MN-contiguous, k row j.  32-bit element offsets (big_tile_fits bounds the
+// operands).
+template <bool KC>
+__device__ __forceinline__ void big_load(const float* __restrict__ p, int ld, int row0, int k0, float* tile,
+                                         int wave, int lane) {
+  uint32_t off, step;
+  if constexpr (KC) {
+    const int r = wave * 8 + (lane >> 3);
+    const int q = (lane & 7) ^ ((lane >> 3) & 7);
+    off = (uint32_t)(row0 + r) * (uint32_t)ld + (uint32_t)(k0 + 4 * q);
+    step = 64u * (uint32_t)ld;
+  } else {
+    off = (uint32_t)(k0 + wave) * (uint32_t)ld + (uint32_t)(row0 + 4 * lane);
+    step = 8u * (uint32_t)ld;
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+    __builtin_amdgcn_global_load_lds((const void*)(p + off + t * step), (LdsVoidPtr)(tile + (wave + 8 * t) * 256), 16,
+                                     0, 0);
+}
+
+// The 4 operands (k = 8g + 4h + s) of lane (row, h) for k-group g.
+template <bool KC>
+__device__ __forceinline__ floatx4 big_frag(const float* tile, int row, int h, int g) {
+  if constexpr (KC) {
+    const int q = 2 * g + h;
+    return *reinterpret_cast<const floatx4*>(tile + 4 * (row * 8 + (q ^ (row & 7))));
+  } else {
+    floatx4 f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) f[s] = tile[(8 * g + 4 * h + s) * kBigBM + row];
+    return f;
+  }
+}
+
+template <bool A_KC, bool B_KC, int EPI>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) gemm_big(GemmArgs args) {
+  __shared__ __attribute__((aligned(16))) float lds_a0[kBigTileFloats];
+  __shared__ __attribute__((aligned(16))) float lds_b0[kBigTileFloats];
+  __shared__ __attribute__((aligned(16))) float lds_a1[kBigTileFloats];
+  __shared__ __attribute__((aligned(16))) float lds_b1[kBigTileFloats];
+  constexpr int TM = 2, TN = 4, WM = 64, WN = 128;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1, h = lane >> 5, l32 = lane & 31;
+  const int M = args.M, N = args.N, K = args.K;
+  const int tiles_n = N / kBigBM;
+  const int bx = xcd_tile(blockIdx.x, M / kBigBM, tiles_n);
+  const int tm = bx / tiles_n, tn = bx % tiles_n;
+  const int m0 = tm * kBigBM, n0 = tn * kBigBM;
+
+  constexpr bool kColsum = EPI == EPI_DW_OPT && !B_KC;
+  const bool colsum = kColsum && args.colsum_b && tm == 0 && wm == 0;
+  float cs[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) cs[j] = 0.0f;
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  // One stage: per k-group, the wave's fragments from LDS, then its 32 MFMAs
+  // (the other wave of the SIMD covers the LDS latency).
+  auto compute = [&](const float* a_s, const float* b_s) {
+#pragma unroll
+    for (int g = 0; g < kBigBK / 8; ++g) {
+      floatx4 fa[TM], fb[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[i] = big_frag<A_KC>(a_s, wm * WM + i * 32 + l32, h, g);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) fb[j] = big_frag<B_KC>(b_s, wn * WN + j * 32 + l32, h, g);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
+      if (kColsum && colsum) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int s = 0; s < 4; ++s) cs[j] = cs[j] + fb[j][s];
+      }
+    }
+  };
+
+  // Stage s reads buffer s & 1; the loads of stage s + 1 go to the other
+  // buffer, which every wave finished reading before the barrier of stage s.
+  // S is even (big_tile_fits: K a multiple of 64), so every pass of the
+  // loop runs both stages.
+  const int S = K / kBigBK;
+  big_load<A_KC>(args.A, args.lda, m0, 0, lds_a0, wave, lane);
+  big_load<B_KC>(args.B, args.ldb, n0, 0, lds_b0, wave, lane);
+  for (int s = 0; s < S; s += 2) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    big_load<A_KC>(args.A, args.lda, m0, (s + 1) * kBigBK, lds_a1, wave, lane);
+    big_load<B_KC>(args.B, args.ldb, n0, (s + 1) * kBigBK, lds_b1, wave, lane);
+    __builtin_amdgcn_sched_barrier(0);  // the loads stay ahead of this stage's MFMAs
+    compute(lds_a0, lds_b0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (s + 2 < S) {
+      big_load<A_KC>(args.A, args.lda, m0, (s + 2) * kBigBK, lds_a0, wave, lane);
+      big_load<B_KC>(args.B, args.ldb, n0, (s + 2) * kBigBK, lds_b0, wave, lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    compute(lds_a1, lds_b1);
+  }
+
+  if (kColsum && colsum) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) cs[j] = cs[j] + __shfl_xor(cs[j], 32, kWave);
+  }
+  const bool cs_owner = kColsum && colsum && h == 0;
+  const EpiArgs& e = args.epi;
+  static_for_blocks<0, TM, TN>([&](auto I, auto J) {
+    constexpr int i = decltype(I)::value, j = decltype(J)::value;
+    block_epilogue<EPI>(e, acc[i][j], m0 + wm * WM + i * 32 + 4 * h, n0 + wn * WN + j * 32 + l32, M, N);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+  if constexpr (kColsum) {
+    if (cs_owner && e.b) {
+      const AdamRcp rc = adam_rcp_of(e);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) apply_bias_update(e, n0 + wn * WN + j * 32 + l32, N, cs[j], rc);
+    }
+  }
+}
+
+// Whether the large tile serves a product: exact 256-multiples, K of 32,
+// 16-byte aligned operand rows, a grid of at least one workgroup per CU.
+static bool big_tile_fits(int layout, int M, int N, int K, bool vec, int num_cus) {
+  const char* bt = std::getenv("VOLTA_BIG_TILE");
+  if (bt && *bt == '0') return false;
+  // every operand element offset must fit 32 bits (big_load)
+  const size_t a_elems = (size_t)M * K, b_elems = (size_t)N * K;
+  return vec && layout >= GEMM_NN && layout <= GEMM_TN && M % kBigBM == 0 && N % kBigBM == 0 &&
+         K % (2 * kBigBK) == 0 && K >= 4 * kBigBK && (M / kBigBM) * (N / kBigBM) >= num_cus &&
+         a_elems < ((size_t)1 << 31) && b_elems < ((size_t)1 << 31);
 }
 
 // ---------------------------------------------------------------------------
@@ -1323,6 +1532,32 @@ hipError_t launch_fwd_head(const GemmPlan& p, const GemmArgs& args_in, const Out
   return hipGetLastError();
 }
 
+template <bool A_KC, bool B_KC, int EPI>
+static hipError_t launch_big_epi(const GemmArgs& a, hipStream_t st) {
+  const dim3 grid((a.M / kBigBM) * (a.N / kBigBM));
+  hipLaunchKernelGGL((gemm_big<A_KC, B_KC, EPI>), grid, dim3(512), 0, st, a);
+  return hipGetLastError();
+}
+
+static hipError_t launch_big(const GemmArgs& a, int layout, hipStream_t st) {
+  const int k = a.epi.kind;
+  switch (layout) {
+    case GEMM_NN:
+      if (k == EPI_BIAS_ACT) return launch_big_epi<true, false, EPI_BIAS_ACT>(a, st);
+      if (k == EPI_STORE) return launch_big_epi<true, false, EPI_STORE>(a, st);
+      break;
+    case GEMM_NT:
+      if (k == EPI_DX_ACT) return launch_big_epi<true, true, EPI_DX_ACT>(a, st);
+      if (k == EPI_STORE) return launch_big_epi<true, true, EPI_STORE>(a, st);
+      break;
+    case GEMM_TN:
+      if (k == EPI_DW_OPT) return launch_big_epi<false, false, EPI_DW_OPT>(a, st);
+      if (k == EPI_STORE) return launch_big_epi<false, false, EPI_STORE>(a, st);
+      break;
+  }
+  return hipErrorInvalidValue;
+}
+
 hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& args_in, hipStream_t st, Recorder* rec,
                        const char* label, double bytes) {
   GemmArgs a = args_in;
@@ -1338,6 +1573,14 @@ hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& args_in, hipStream_t s
   if (p.tile == TILE_SMALLM) {
     if (p.splits != 1) return hipErrorInvalidValue;
     if ((err = launch_smallm(a, p.layout, p.vec, p.waves, st)) != hipSuccess) return err;
+    return mark(rec, label, 2.0 * a.M * a.N * a.K, bytes);
+  }
+  if (p.tile == TILE_BIG) {
+    // exact tiles and 16-byte aligned operands, or no launch
+    const bool fits = p.splits == 1 && a.M % kBigBM == 0 && a.N % kBigBM == 0 && a.K % (2 * kBigBK) == 0 &&
+                      a.lda % 4 == 0 && a.ldb % 4 == 0 && ((uintptr_t)a.A & 15) == 0 && ((uintptr_t)a.B & 15) == 0;
+    if (!fits) return hipErrorInvalidValue;
+    if ((err = launch_big(a, p.layout, st)) != hipSuccess) return err;
     return mark(rec, label, 2.0 * a.M * a.N * a.K, bytes);
   }
   if (p.tile == TILE_DW_SMALLK) {
@@ -1571,6 +1814,12 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus, bool 
                                                                                       : TILE_64x64;
   const char* sb = std::getenv("VOLTA_SMALL_BK");
   if (p.tile == TILE_64x64 && sb && std::atoi(sb) == 64) p.tile = TILE_64x64_K64;
+  if (big_tile_fits(layout, M, N, K, vec, num_cus)) {
+    p.tile = TILE_BIG;
+    p.splits = 1;
+    p.k_per_split = K;
+    return p;
+  }
   const int tiles = p.tiles(M, N);
   const int bk = p.tile == TILE_64x64_K64 ? 64 : 32;
   // Smallest K slice: 64 for the forward products (their reduction is the
