@@ -812,16 +812,30 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  // One stage: per k-group, the wave's fragments from LDS, then its 32 MFMAs
-  // (the other wave of the SIMD covers the LDS latency).
+  // One stage: the fragments of k-group g + 1 are read from LDS before the
+  // 32 MFMAs of group g are issued, so their latency hides behind the
+  // matrix work; the wave's priority is raised while it issues MFMAs.
   auto compute = [&](const float* a_s, const float* b_s) {
+    floatx4 fa_n[TM], fb_n[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa_n[i] = big_frag<A_KC>(a_s, wm * WM + i * 32 + l32, h, 0);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fb_n[j] = big_frag<B_KC>(b_s, wn * WN + j * 32 + l32, h, 0);
 #pragma unroll
     for (int g = 0; g < kBigBK / 8; ++g) {
       floatx4 fa[TM], fb[TN];
 #pragma unroll
-      for (int i = 0; i < TM; ++i) fa[i] = big_frag<A_KC>(a_s, wm * WM + i * 32 + l32, h, g);
+      for (int i = 0; i < TM; ++i) fa[i] = fa_n[i];
 #pragma unroll
-      for (int j = 0; j < TN; ++j) fb[j] = big_frag<B_KC>(b_s, wn * WN + j * 32 + l32, h, g);
+      for (int j = 0; j < TN; ++j) fb[j] = fb_n[j];
+      if (g + 1 < kBigBK / 8) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) fa_n[i] = big_frag<A_KC>(a_s, wm * WM + i * 32 + l32, h, g + 1);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) fb_n[j] = big_frag<B_KC>(b_s, wn * WN + j * 32 + l32, h, g + 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -829,6 +843,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
 #pragma unroll
           for (int j = 0; j < TN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_s_setprio(0);
+      __builtin_amdgcn_sched_barrier(0);
       if (kColsum && colsum) {
 #pragma unroll
         for (int j = 0; j < TN; ++j)
