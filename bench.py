@@ -450,8 +450,8 @@ def _per_launch(rows, labels, value):
         seq.append([nm, wg, v])
     order = list(labels)
     regions = [seq]
-    if len(order) > 1:  # the secondary's first launch is a 128x128 tile kernel (B=4096)
-        i2 = next(i for i, x in enumerate(seq) if "128, 128" in x[0])
+    if len(order) > 1:  # the secondary's first launch is a large-tile kernel (B=4096)
+        i2 = next(i for i, x in enumerate(seq) if "gemm_big" in x[0] or "128, 128" in x[0])
         regions = [seq[:i2], seq[i2:]]
     out = {}
     for wl, reg in zip(order, regions):
@@ -496,7 +496,8 @@ def traffic_table(pmc_dir, bench_json):
 def trace_summary(trace_csv, bench_json):
     """Per-launch kernel durations from a rocprofv3 --kernel-trace of one
     bench run, averaged over every whole step the run executed, beside the
-    bench's own in-step figure for the same launch."""
+    in-step figure of the same launch from `bench_json` (a plain run of the
+    same build: the profiler itself slows the B=64 launches)."""
     import csv
 
     b, labels = _bench_labels(bench_json)
@@ -512,10 +513,15 @@ def trace_summary(trace_csv, bench_json):
         lst = per[wl]
         tot = sum(sum(v) / len(v) for _, _, v in lst)
         rf = roofline_of(max(r["kernels"], key=dominance))
-        out += [f"## workload {wl}: step {r['ms_per_step'] * 1000:.1f} us (bench wall clock, graph replay); "
-                f"sum of kernel durations per step {tot:.1f} us over {len(lst[0][2])} steps",
-                f"## roofline launch {rf['kernel']}: bench {rf['avg_ms'] * 1000:.2f} us (events around it inside "
-                f"whole steps), {rf['achieved']} {rf['unit']} = {rf['frac'] * 100:.1f}% of {rf['peak']}",
+        trace_of = {lab: sum(v) / len(v) for (_, _, v), lab in zip(lst, labels[wl])}
+        t_us = trace_of[rf["kernel"]]
+        t_frac = (rf["algorithmic_bytes"] / (t_us * 1e-6) / 1e9 / PEAK_HBM_GBS if rf["bound"] == "hbm"
+                  else rf["algorithmic_flops"] / (t_us * 1e-6) / 1e12 / PEAK_FP32_MFMA_TFLOPS)
+        out += [f"## workload {wl}: step {r['ms_per_step'] * 1000:.1f} us (plain bench run, graph replay); "
+                f"sum of traced kernel durations per step {tot:.1f} us over {len(lst[0][2])} steps",
+                f"## roofline launch {rf['kernel']} (longest in-step launch): plain run {rf['avg_ms'] * 1000:.2f} us "
+                f"-> {rf['achieved']} {rf['unit']} = {rf['frac'] * 100:.1f}% of {rf['peak']}; traced average "
+                f"{t_us:.2f} us -> {t_frac * 100:.1f}%",
                 f"{'avg_us':>9} {'min_us':>9} {'bench_us':>9}  launch  [kernel (workgroups)]"]
         for (k, w, v), lab in zip(lst, labels[wl]):
             out.append(f"{sum(v) / len(v):9.2f} {min(v):9.2f} {bench_ms[lab] * 1000:9.2f}  {lab}  [{k} ({w})]")
