@@ -112,16 +112,17 @@ def test_gemm_integer_exact(layout, M, N, K, tile):
 
 @pytest.mark.parametrize("layout", [0], ids=["NN"])
 @pytest.mark.parametrize("M,N,K", [(64, 512, 256), (33, 130, 257), (7, 5, 3), (64, 64, 1024)])
-def test_gemm_smallm_8_waves_integer_exact(layout, M, N, K):
-    """The 8-wave small-M workgroup (eighths of K, two four-tile trees; the
-    forward products' default) is exact on integer operands, ragged shapes
-    included."""
-    say(f"gemm small-M 8 waves layout={layout} M={M} N={N} K={K}")
+@pytest.mark.parametrize("waves", [8, 16])
+def test_gemm_smallm_8_waves_integer_exact(layout, M, N, K, waves):
+    """The 8- and 16-wave small-M workgroups (eighths / sixteenths of K, trees
+    of four-tile sums; the forward products' defaults) are exact on integer
+    operands, ragged shapes included."""
+    say(f"gemm small-M {waves} waves layout={layout} M={M} N={N} K={K}")
     rng = np.random.default_rng(M * 5 + N * 3 + K)
     A = rng.integers(-4, 5, (M, K)).astype(np.float32)
     B = rng.integers(-4, 5, (N, K) if layout == 1 else (K, N)).astype(np.float32)
     old = os.environ.get("VOLTA_SMALLM_WAVES")
-    os.environ["VOLTA_SMALLM_WAVES"] = "8"
+    os.environ["VOLTA_SMALLM_WAVES"] = str(waves)
     try:
         got = _gemm(layout, A, B, M, N, K, tile=TILE_SMALLM)
     finally:
@@ -757,12 +758,15 @@ def test_forward_head_launch_bit_identical(name):
     say(f"forward + output head launch {name}")
     n = len(spec.sizes) - 1
     fused = f"fwd{n - 2}+fwd{n - 1}+loss+dx{n - 1}"
-    lab_sep = _launch_labels({"VOLTA_FWD_HEAD": "0"}, spec, B)
-    lab_fused = _launch_labels({"VOLTA_FWD_HEAD": "1"}, spec, B)
+    # the fused launch's forward tile has 8 waves: both runs use 8
+    sep_env = {"VOLTA_FWD_HEAD": "0", "VOLTA_SMALLM_WAVES": "8"}
+    fused_env = {"VOLTA_FWD_HEAD": "1", "VOLTA_SMALLM_WAVES": "8"}
+    lab_sep = _launch_labels(sep_env, spec, B)
+    lab_fused = _launch_labels(fused_env, spec, B)
     assert fused in lab_fused and fused not in lab_sep
     assert len(lab_fused) == len(lab_sep) - 1
-    l1, p1, b1 = _run_with_env({"VOLTA_FWD_HEAD": "0"}, spec, B, lr, 4)
-    l2, p2, b2 = _run_with_env({"VOLTA_FWD_HEAD": "1"}, spec, B, lr, 4)
+    l1, p1, b1 = _run_with_env(sep_env, spec, B, lr, 4)
+    l2, p2, b2 = _run_with_env(fused_env, spec, B, lr, 4)
     np.testing.assert_array_equal(l1, l2)
     for a, b in zip(p1, p2):
         np.testing.assert_array_equal(a, b)

@@ -103,6 +103,10 @@ struct GemmPlan {
 // chosen (NN/NT products whose epilogue is per element: not the loss head).
 GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus, bool small_m = true);
 
+// Waves per workgroup of a small-M product of M x N outputs: 4 when it runs
+// in a 256-thread paired launch, else by the grid's size (16, 8 or 4).
+int gemm_smallm_waves(bool paired, int M, int N, int num_cus);
+
 // `bytes` is the caller's algorithmic HBM traffic of the product (for the
 // profiler); `rec`/`label` are optional.
 hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& a, hipStream_t st, Recorder* rec = nullptr,
@@ -142,5 +146,22 @@ bool pair_supported(const PairOp& a, const PairOp& b);
 // Both operations in one launch, then the split-K reductions either needs.
 hipError_t pair_launch(const PairOp& a, const PairOp& b, hipStream_t st, Recorder* rec, const char* label,
                        double flops, double bytes);
+
+// Every dW product of a small-batch step in one launch: the small-K dW
+// tiles of up to kMaxDwGroup products and the narrow output-layer dW.  The
+// products are independent of each other (each reads its own act_i and
+// delta_i and rewrites only W_i, b_i and their state), so once the last dX
+// has run they share one launch.
+constexpr int kMaxDwGroup = 8;
+struct DwGroup {
+  int n = 0;                        // small-K dW products (plan TILE_DW_SMALLK)
+  GemmArgs g[kMaxDwGroup];
+  int start[kMaxDwGroup + 1] = {};  // first workgroup of product i after the narrow ones; start[n] = total
+  int narrow_blocks = 0;            // 0: no narrow dW
+  NarrowDwArgs nd{};
+};
+bool dw_group_supported(const DwGroup& d);
+hipError_t dw_group_launch(const DwGroup& d, hipStream_t st, Recorder* rec, const char* label, double flops,
+                           double bytes);
 
 }  // namespace volta

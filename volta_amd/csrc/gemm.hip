@@ -961,7 +961,9 @@ __device__ __forceinline__ void smallm_coords(int blk, int tiles_m, int tiles_n,
 // one NW-th of the K range.
 template <bool B_KC, bool VEC, int EPI, int NW>
 __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float* lds) {
-  static_assert(NW == 4 || NW == 8, "wave trees for 4 or 8 partial tiles");
+  static_assert(NW == 4 || NW == 8 || NW == 16, "wave trees for 4, 8 or 16 partial tiles");
+  // 16-wave workgroups (four waves per SIMD) hold a quarter chunk per wave
+  constexpr int CH = NW == 16 ? kSmallChunk / 4 : kSmallChunk;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int M = args.M, N = args.N, K = args.K;
@@ -985,9 +987,9 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
   // the loads, make the compiler wait for earlier loads in the middle of
   // the chunk.)  Groups past the wave's range are skipped as a whole
   // (wave-uniform).  Only called with kc < kend.
-  auto load = [&](floatx4(&fa)[kSmallChunk], floatx4(&fb)[kSmallChunk], int kc) {
+  auto load = [&](floatx4(&fa)[CH], floatx4(&fb)[CH], int kc) {
 #pragma unroll
-    for (int g = 0; g < kSmallChunk; ++g) {
+    for (int g = 0; g < CH; ++g) {
       if (kc + 16 * g >= kend) break;
       const int k = kc + 16 * g + 4 * q;  // this lane's first k of the group
       if (VEC) {  // K % 4 == 0 and every range bound is a multiple of 4
@@ -1010,13 +1012,29 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
     }
     __builtin_amdgcn_sched_barrier(0);
   };
+  // The epilogue's operands (bias; the layer's output and pre-activation for
+  // the activation derivative) of the element thread t < 256 finishes,
+  // (t / 16, t % 16), loaded before the operands: loads complete in issue
+  // order, so they cost no wait of their own, and the epilogue then runs
+  // without a dependent memory latency.  Unconditional (index clamped).
+  const EpiArgs& ep = args.epi;
+  const int em = m0 + (tid >> 4), en = n0 + (tid & 15);
+  const bool eok = tid < 256 && em < M && en < N;
+  const size_t eidx = eok ? (size_t)em * ep.ldc + en : 0;
+  float e_y = 0.0f, e_p = 0.0f;
+  if constexpr (EPI == EPI_BIAS_ACT) e_y = ep.bias[eok ? en : 0];
+  if constexpr (EPI == EPI_DX_ACT) {
+    e_y = ep.aux_act[eidx];
+    e_p = ep.aux_pre ? ep.aux_pre[eidx] : e_y;
+  }
+
   floatx4 acc[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
   static_assert(kSmallChunk % 4 == 0, "a chunk must hold whole rounds of the four accumulators");
-  auto compute = [&](const floatx4(&fa)[kSmallChunk], const floatx4(&fb)[kSmallChunk], int kc) {
+  auto compute = [&](const floatx4(&fa)[CH], const floatx4(&fb)[CH], int kc) {
 #pragma unroll
-    for (int g = 0; g < kSmallChunk; ++g) {
+    for (int g = 0; g < CH; ++g) {
       if (kc + 16 * g < kend) {  // wave-uniform
         const int k = kc + 16 * g + 4 * q;
 #pragma unroll
@@ -1032,8 +1050,8 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
   // One register chunk covers the wave's range for K <= 256 * waves (every
   // small-batch product of the step): all its loads are in flight together,
   // then its MFMAs run.  Longer ranges take one memory latency per chunk.
-  floatx4 fa[kSmallChunk], fb[kSmallChunk];
-  for (int kc = kbeg; kc < kend; kc += 16 * kSmallChunk) {
+  floatx4 fa[CH], fb[CH];
+  for (int kc = kbeg; kc < kend; kc += 16 * CH) {
     load(fa, fb, kc);
     compute(fa, fb, kc);
   }
@@ -1050,15 +1068,30 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
   const int i = tid >> 4, j = tid & 15;
   const int src = (i & 3) * kSmallRedStride + 16 * (i >> 2) + j;
   constexpr int kW = 4 * kSmallRedStride;
-  float sum = (lds[src] + lds[kW + src]) + (lds[2 * kW + src] + lds[3 * kW + src]);
-  if constexpr (NW == 8)
-    sum = sum + ((lds[4 * kW + src] + lds[5 * kW + src]) + (lds[6 * kW + src] + lds[7 * kW + src]));
+  auto quad = [&](int w) {
+    return (lds[w * kW + src] + lds[(w + 1) * kW + src]) + (lds[(w + 2) * kW + src] + lds[(w + 3) * kW + src]);
+  };
+  float sum = quad(0);
+  if constexpr (NW == 8) sum = sum + quad(4);
+  if constexpr (NW == 16) sum = (sum + quad(4)) + (quad(8) + quad(12));
   const int m = m0 + i, n = n0 + j;
-  if (m < M && n < N) apply_epilogue<EPI>(args.epi, m, n, sum);
+  if (m < M && n < N) {
+    // apply_epilogue's arithmetic on the prefetched operands
+    if constexpr (EPI == EPI_BIAS_ACT) {
+      const float v = sum + e_y;  // pre = act_i W_i + b_i (:716-724)
+      if (ep.pre) ep.pre[eidx] = v;
+      ep.out[eidx] = act_forward(ep.act, v);  // (:725-743)
+    } else if constexpr (EPI == EPI_DX_ACT) {
+      ep.out[eidx] = sum * act_derivative(ep.act, e_p, e_y);  // (:893-929)
+    } else {
+      apply_epilogue<EPI>(ep, m, n, sum);
+    }
+  }
 }
 
 template <bool B_KC, bool VEC, int EPI, int NW>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) gemm_smallm(GemmArgs args) {
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW == 16 ? 4 : 2)))
+gemm_smallm(GemmArgs args) {
   __shared__ float lds[SmallLds<NW>::kFloats];
   smallm_tile<B_KC, VEC, EPI, NW>(args, blockIdx.x, lds);
 }
@@ -1160,10 +1193,11 @@ constexpr int kDwS = kDwT + 4;   // LDS row stride of the [k][32] operand slices
 constexpr int kDwDS = kDwT + 1;  // LDS row stride of the dW tile
 constexpr int kDwLds = 2 * kDwK * kDwS + kDwT * kDwDS;
 
+// `tid` (0..255): the thread's index among the tile's 256.
 template <int EPI>
-__device__ __forceinline__ void dw_smallk_tile(const GemmArgs& args, int blk, float* lds) {
+__device__ __forceinline__ void dw_smallk_tile(const GemmArgs& args, int blk, float* lds, int tid) {
   static_assert(EPI == EPI_DW_OPT || EPI == EPI_STORE, "epilogues of the dW tile");
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, q = lane >> 4;
   const int wm = wave >> 1, wn = wave & 1;
   const int M = args.M, N = args.N, K = args.K;
@@ -1323,7 +1357,7 @@ __device__ __forceinline__ void dw_smallk_tile(const GemmArgs& args, int blk, fl
 template <int EPI>
 __global__ void __launch_bounds__(256) gemm_dw_smallk(GemmArgs args) {
   __shared__ __attribute__((aligned(16))) float lds[kDwLds];
-  dw_smallk_tile<EPI>(args, blockIdx.x, lds);
+  dw_smallk_tile<EPI>(args, blockIdx.x, lds, threadIdx.x);
 }
 
 // Planes whose loads splitk_reduce issues together (more planes: a loop).
@@ -1466,27 +1500,38 @@ static hipError_t launch_reduce(const GemmArgs& a, int splits, hipStream_t st) {
 }
 
 // Small-M products: NN with BIAS_ACT / STORE, NT with DX_ACT / STORE.
-// Waves per workgroup of a stand-alone forward (NN) small-M launch: 8 while
-// the grid has at most one workgroup per CU, else 4.  An 8-wave workgroup
-// (168 registers a lane) leaves room for no second one on its CU, so a
-// larger grid would take two rounds; 4-wave workgroups fit three to a CU.
-// Measured: C2 (every forward grid <= 256 workgroups) 0.0641 ms/step with 4
-// waves against 0.0618 with 8; C3's 512-workgroup fwd0/fwd1 4.16/14.36 us
-// with 4 against 5.28/16.1 us with 8, its 128-workgroup fwd2 9.92 against
-// 7.96 us.  VOLTA_SMALLM_WAVES=4 or 8 fixes the count.  dX (NT) products
-// always take 4, as in a paired launch, so paired and separate launches
-// give the same bits.
+// Waves per workgroup of a small-M launch (forward NN or dX NT): 16 while the
+// grid has at most one workgroup per two CUs, 8 while it has at most one per
+// CU, else 4.  More waves split K into shorter chains per wave; an 8-wave
+// workgroup (168 registers a lane) leaves room for no second one on its CU,
+// so a larger grid would take two rounds, and 4-wave workgroups fit three
+// to a CU.  Measured on C2: the 128- and 64-workgroup forwards 4.1-4.5 ->
+// 3.5 and 2.3 -> 2.0 us with 16 waves against 8; C3's 512-workgroup
+// fwd0/fwd1 4.16/14.36 us with 4 against 5.28/16.1 us with 8.  dX (NT)
+// products take 4, as in a paired launch (256 threads), so paired and
+// separate launches give the same bits: a 512-thread pair of an 8-wave dX
+// with two small-K dW tiles per workgroup measured slower (C2's dx1|dw2
+// 8.1 -> 10.0 us).  VOLTA_SMALLM_WAVES=4, 8 or 16 fixes the forward count.
+static int smallm_waves(bool b_kc, int blocks, int num_cus);
+
+int gemm_smallm_waves(bool paired, int M, int N, int num_cus) {
+  return paired ? 4 : smallm_waves(false, ((M + 15) / 16) * ((N + 15) / 16), num_cus);
+}
+
 static int smallm_waves(bool b_kc, int blocks, int num_cus) {
-  if (b_kc) return 4;
   const char* w = std::getenv("VOLTA_SMALLM_WAVES");
-  if (w && *w) return std::atoi(w) == 4 ? 4 : 8;
-  return blocks <= num_cus ? 8 : 4;
+  int waves = 2 * blocks <= num_cus ? 16 : blocks <= num_cus ? 8 : 4;
+  if (w && *w) waves = std::atoi(w) == 4 ? 4 : std::atoi(w) == 16 ? 16 : 8;
+  return b_kc ? 4 : waves;
 }
 
 template <bool B_KC, int EPI>
 static hipError_t launch_smallm_epi(const GemmArgs& a, bool vec, int waves, hipStream_t st) {
   const int blocks = ((a.M + 15) / 16) * ((a.N + 15) / 16);
-  if (waves == 8) {
+  if (waves == 16) {
+    if (vec) hipLaunchKernelGGL((gemm_smallm<B_KC, true, EPI, 16>), dim3(blocks), dim3(1024), 0, st, a);
+    else hipLaunchKernelGGL((gemm_smallm<B_KC, false, EPI, 16>), dim3(blocks), dim3(1024), 0, st, a);
+  } else if (waves == 8) {
     if (vec) hipLaunchKernelGGL((gemm_smallm<B_KC, true, EPI, 8>), dim3(blocks), dim3(512), 0, st, a);
     else hipLaunchKernelGGL((gemm_smallm<B_KC, false, EPI, 8>), dim3(blocks), dim3(512), 0, st, a);
   } else {
@@ -1516,8 +1561,8 @@ static bool dw_smallk_ok(const GemmArgs& a, int layout) {
 
 static hipError_t launch_smallm(const GemmArgs& a, int layout, bool vec, int waves, hipStream_t st) {
   if (vec && !smallm_vec_ok(a, layout)) return hipErrorInvalidValue;
-  if (waves != 4 && waves != 8) return hipErrorInvalidValue;
-  if (layout == GEMM_NT && waves != 4) return hipErrorInvalidValue;
+  if (waves != 4 && waves != 8 && waves != 16) return hipErrorInvalidValue;
+  if (layout == GEMM_NT && waves == 16 && !vec) return hipErrorInvalidValue;
   const int k = a.epi.kind;
   if (layout == GEMM_NN) {
     if (k == EPI_BIAS_ACT) return launch_smallm_epi<false, EPI_BIAS_ACT>(a, vec, waves, st);
@@ -1657,7 +1702,7 @@ struct DwSmallOp {  // dW on small-K tiles, optimizer epilogue
   using Args = GemmArgs;
   static constexpr int kLds = kDwLds;
   static __device__ __forceinline__ void run(const GemmArgs& a, int blk, float* lds) {
-    dw_smallk_tile<EPI_DW_OPT>(a, blk, lds);
+    dw_smallk_tile<EPI_DW_OPT>(a, blk, lds, threadIdx.x);
   }
 };
 
@@ -1715,7 +1760,7 @@ bool pair_supported(const PairOp& a, const PairOp& b) {
   auto gemm_ok = [](const PairOp& o) {
     if (o.plan.tile == TILE_SMALLM)
       return o.plan.vec && o.plan.splits == 1 && o.plan.layout == GEMM_NT && o.args.epi.kind == EPI_DX_ACT &&
-             smallm_vec_ok(o.args, GEMM_NT);
+             o.plan.waves == 4 && smallm_vec_ok(o.args, GEMM_NT);
     if (o.plan.tile == TILE_DW_SMALLK)
       return o.plan.splits == 1 && o.args.epi.kind == EPI_DW_OPT && dw_smallk_ok(o.args, GEMM_TN);
     return o.plan.tile == TILE_64x64 && o.plan.vec && !o.plan.inkernel_reduce &&
@@ -1775,6 +1820,58 @@ static hipError_t reduce_after(const PairOp& o, hipStream_t st) {
   a.k_per_split = o.plan.k_per_split;
   if (o.args.epi.kind == EPI_DX_ACT) return launch_reduce<EPI_DX_ACT>(a, o.plan.splits, st);
   return launch_reduce<EPI_DW_OPT>(a, o.plan.splits, st);
+}
+
+// The step's dW products in one launch: workgroups [0, narrow_blocks) run
+// the narrow output-layer dW (its staged deltas and partial sums in the
+// small-K tile's LDS), the rest the small-K tiles of product i for
+// workgroups [start[i], start[i+1]) after them.
+static_assert(sizeof(DwGroup) <= 4000, "DwGroup is passed by value as a kernel argument (4 KiB limit)");
+
+template <int NMAX>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) dw_group_kernel(DwGroup d) {
+  __shared__ __attribute__((aligned(16))) float lds[kDwLds];
+  int b = blockIdx.x;
+  if (b < d.narrow_blocks) {
+    narrow_dw_block<NMAX>(d.nd, b, lds);
+    return;
+  }
+  b -= d.narrow_blocks;
+  int i = 0;
+#pragma unroll
+  for (int k = 1; k < kMaxDwGroup; ++k)
+    if (k < d.n && b >= d.start[k]) i = k;
+  dw_smallk_tile<EPI_DW_OPT>(d.g[i], b - d.start[i], lds, threadIdx.x);
+}
+
+bool dw_group_supported(const DwGroup& d) {
+  if (d.n < 1 || d.n > kMaxDwGroup || d.start[0] != 0) return false;
+  for (int i = 0; i < d.n; ++i) {
+    const GemmArgs& a = d.g[i];
+    if (a.epi.kind != EPI_DW_OPT || !dw_smallk_ok(a, GEMM_TN)) return false;
+    const int tiles = ((a.M + kDwT - 1) / kDwT) * ((a.N + kDwT - 1) / kDwT);
+    if (d.start[i + 1] - d.start[i] != tiles) return false;
+  }
+  if (d.narrow_blocks) {
+    const NarrowDwArgs& p = d.nd;
+    if (p.N < 1 || p.N > 16 || p.B < 1 || p.B > kNarrowMaxB || narrow_lds_floats_n(p.B, p.N) > kDwLds) return false;
+    if (p.opt != VOLTA_OPT_SGD && p.opt != VOLTA_OPT_ADAM && p.opt != VOLTA_OPT_ADAGRAD) return false;
+    if (d.narrow_blocks != (p.R + kNarrowRows - 1) / kNarrowRows) return false;
+  }
+  return true;
+}
+
+hipError_t dw_group_launch(const DwGroup& d, hipStream_t st, Recorder* rec, const char* label, double flops,
+                           double bytes) {
+  if (!dw_group_supported(d)) return hipErrorInvalidValue;
+  const dim3 grid(d.narrow_blocks + d.start[d.n]);
+  const int nn = d.narrow_blocks ? d.nd.N : 1;
+  if (nn <= 1) hipLaunchKernelGGL(dw_group_kernel<1>, grid, dim3(256), 0, st, d);
+  else if (nn <= 4) hipLaunchKernelGGL(dw_group_kernel<4>, grid, dim3(256), 0, st, d);
+  else hipLaunchKernelGGL(dw_group_kernel<16>, grid, dim3(256), 0, st, d);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  return mark(rec, label, flops, bytes);
 }
 
 hipError_t pair_launch(const PairOp& a, const PairOp& b, hipStream_t st, Recorder* rec, const char* label,

@@ -37,6 +37,7 @@
 #include <vector>
 
 #include "extras.h"
+#include "narrow_dw.h"
 #include "gemm.h"
 #include "skinny.h"
 #include "spec.h"
@@ -112,6 +113,8 @@ struct Handle {
   float* infer_x = nullptr;    // inference input rows (allocated on first use)
   float* infer_ws = nullptr;   // split-K workspace of inference plans (grown on demand)
   float* scratch = nullptr;    // this device's static scratch (allocation-free inference)
+  bool dx_alone = false;       // small-batch backward: dX launches alone, dW products grouped
+  bool dw_group = false;       // ... in one launch (off with VOLTA_NO_PAIR)
   size_t infer_ws_floats = 0;
   SegTable segs{};
   std::vector<LayerPlan> layers;
@@ -570,6 +573,45 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
       return false;
     }
   }
+  if (h->dx_alone) {
+    // Small-batch step: the dX chain alone (each on its grid's wave count),
+    // then every dW product in one launch -- dW_i only needs act_i and
+    // delta_i, and dX_i has read W_i before that launch updates it.
+    for (int i = n - 2; i >= 1; --i) {
+      std::snprintf(lx, sizeof lx, "dx%d", i);
+      if (!run_single(make_dx(i, ws0), lx, dx_cost(i))) return false;
+    }
+    DwGroup d;
+    std::string lab;
+    double fl = 0.0, by = 0.0;
+    for (int i = n - 1; i >= 0; --i) {
+      const PairOp o = make_dw(i, ws0);
+      if (o.kind == PAIR_NARROW_DW) {
+        d.nd = o.nd;
+        d.narrow_blocks = (o.nd.R + kNarrowRows - 1) / kNarrowRows;
+      } else {
+        d.g[d.n] = o.args;
+        d.g[d.n].k_per_split = o.plan.k_per_split;
+        d.start[d.n + 1] = d.start[d.n] + o.plan.tiles(o.args.M, o.args.N);
+        ++d.n;
+      }
+      std::snprintf(lx, sizeof lx, "dw%d+db+opt", i);
+      lab += (lab.empty() ? "" : "|") + std::string(lx);
+      fl += dw_cost(i).first;
+      by += dw_cost(i).second;
+    }
+    if (h->dw_group && dw_group_supported(d)) {
+      VOLTA_CHECK(dw_group_launch(d, st, rec, lab.c_str(), fl, by));
+      return true;
+    }
+    // one launch each (VOLTA_NO_PAIR, or a narrow dW whose staged deltas
+    // exceed the small-K tile's LDS)
+    for (int i = n - 1; i >= 0; --i) {
+      std::snprintf(lx, sizeof lx, "dw%d+db+opt", i);
+      if (!run_single(make_dw(i, ws0), lx, dw_cost(i))) return false;
+    }
+    return true;
+  }
   for (int i = n - 2; i >= 1; --i) {
     std::snprintf(lx, sizeof lx, "dx%d", i);
     std::snprintf(ly, sizeof ly, "dw%d+db+opt", i + 1);
@@ -741,6 +783,24 @@ static bool build(Handle* h) {
   h->n_counters = max_tiles + 1;  // last one: the loss head's tile counter
   const char* np = std::getenv("VOLTA_NO_PAIR");
   h->pair_backward = !(np && *np && *np != '0') && !h->extras();
+  // Small-batch backward (every dW on the small-K tile, the output layer's
+  // possibly narrow): the dX products run alone with their grid's wave
+  // count, and the dW products share one launch after them (VOLTA_NO_PAIR:
+  // one launch each, same plans, same bits).
+  int n_small = 0;
+  bool all_small = !h->extras() && n >= 2;
+  for (int i = 0; i < n; ++i) {
+    if (i == n - 1 && h->narrow_dw) continue;
+    all_small = all_small && h->layers[i].dw.tile == TILE_DW_SMALLK;
+    ++n_small;
+  }
+  h->dx_alone = all_small && n_small <= kMaxDwGroup;
+  h->dw_group = h->dx_alone && h->pair_backward;
+  if (h->dx_alone)
+    for (int i = 1; i < n; ++i) {
+      LayerPlan& lp = h->layers[i];
+      if (lp.dx.tile == TILE_SMALLM) lp.dx.waves = gemm_smallm_waves(false, B, lp.r, h->num_cus);
+    }
   ws_floats = align_up(ws_floats, 64);
   h->ws_half = ws_floats;
   ws_floats *= 2;

@@ -62,7 +62,7 @@ int32_t volta_hip_gemm(int32_t layout, const float* A, const float* B, float* Cm
   if (force_tile >= 0) p.tile = force_tile;
   if (p.tile == TILE_SMALLM && p.waves == 0) {  // forced onto a shape planned otherwise
     const char* w = std::getenv("VOLTA_SMALLM_WAVES");
-    p.waves = layout == GEMM_NT || (w && std::atoi(w) == 4) ? 4 : 8;
+    p.waves = layout == GEMM_NT || (w && std::atoi(w) == 4) ? 4 : (w && std::atoi(w) == 16) ? 16 : 8;
   }
   if (force_tile == TILE_SMALLM || force_tile == TILE_DW_SMALLK || force_tile == TILE_BIG) {  // whole K in each workgroup
     p.splits = 1;
