@@ -571,47 +571,68 @@ def test_adaptive_config_teacher_forced_steps(name):
     to.close()
 
 
+BUDGET_SEEDS = {"c5_wide_ce_adagrad_b4096": [42]}  # one trajectory (each C5 step takes seconds on the CPU)
+
+
 @pytest.mark.parametrize("name", ADAPTIVE_CONFIGS)
 def test_adaptive_config_error_budget(name):
+    """Free-running trajectories of the HIP library, the fp32 oracle and the
+    fp64 twin: the loss agrees with the oracle's on the leading steps where
+    the oracle still tracks fp64, and after all steps the HIP run is no
+    further from fp64 than 3x the oracle (final loss, and per layer the RMS
+    distance of the parameters).  After a few Adam steps on one batch the
+    trajectories are chaotic (the oracle's own loss leaves fp64 by 1e-5 at
+    step 4 on C2), so one trajectory's distance ratio is noisy: the per-layer
+    ratio is taken as the median over three input seeds (C5: one).  The
+    teacher-forced gradient tests (test_gpu_grad_parity.py) check every
+    product of single steps along the same trajectories against error
+    bounds."""
     from tests.test_oracle import oracle_trainer
 
     spec, B, lr, steps = CONFIGS[name]
-    say(f"error budget {name}: {spec.text()} B={B} steps={steps}")
-    ws, bs, batches = config_inputs(spec, B)
-    X, Y = batches[0]
+    seeds = BUDGET_SEEDS.get(name, [42, 7, 11])
+    ratios = {i: [] for i in range(spec.n_layers)}
     hip, orc = load_hip(), load_oracle()
-    th = Trainer(hip, spec, B)
-    to = Trainer(orc, spec, B)
-    tt = oracle_trainer(orc, spec, B, f64=True)
-    for t in (th, to, tt):
-        t.set_all_params(ws, bs)
-    lh, lo, lt = [], [], []
-    for s in range(steps):
+    for seed in seeds:
+        say(f"error budget {name}: {spec.text()} B={B} steps={steps} seed={seed}")
+        ws, bs, batches = config_inputs(spec, B, seed=seed)
+        X, Y = batches[0]
+        th = Trainer(hip, spec, B)
+        to = Trainer(orc, spec, B)
+        tt = oracle_trainer(orc, spec, B, f64=True)
         for t in (th, to, tt):
-            t.step(X, Y, lr)
-        lh.append(th.loss())
-        lo.append(to.loss())
-        lt.append(orc.lib.volta_oracle_loss_f64(tt.h))
-    lh, lo, lt = map(np.array, (lh, lo, lt))
-    # the leading steps on which fp32 arithmetic still tracks fp64
-    calm = np.logical_and.accumulate(np.abs(lo - lt) <= 1e-5 * np.abs(lt))
-    assert calm[0], "the oracle leaves fp64 at step 1"
-    ok, mx, _ = close_enough(lh[calm], lo[calm])
-    say(f"  loss compared on {int(calm.sum())} of {steps} steps")
-    assert ok, f"losses differ on well-conditioned steps: max {mx:.3e}\n hip={lh[calm]}\n ora={lo[calm]}"
-    e_h = abs(lh[-1] - lt[-1])
-    e_o = abs(lo[-1] - lt[-1])
-    say(f"  final loss: hip {lh[-1]:.7g} oracle {lo[-1]:.7g} fp64 {lt[-1]:.7g}")
-    assert e_h <= 3 * e_o + 1e-6 + 1e-5 * abs(lt[-1]), f"final loss error {e_h:.3e} vs oracle's {e_o:.3e}"
-    truth = _flat_f64(orc, tt, spec)
-    for i, (a, b, t) in enumerate(zip(_flat(*th.get_params()), _flat(*to.get_params()), truth)):
-        rh = float(np.sqrt(np.mean((a - t) ** 2)))
-        ro = float(np.sqrt(np.mean((b - t) ** 2)))
-        say(f"  layer {i}: rms err vs fp64 hip {rh:.3e} oracle {ro:.3e}")
-        assert rh <= 3 * ro + 1e-7, f"layer {i}: hip rms error {rh:.3e} vs oracle {ro:.3e}"
-    assert th.status() == 0
-    for t in (th, to, tt):
-        t.close()
+            t.set_all_params(ws, bs)
+        lh, lo, lt = [], [], []
+        for s in range(steps):
+            for t in (th, to, tt):
+                t.step(X, Y, lr)
+            lh.append(th.loss())
+            lo.append(to.loss())
+            lt.append(orc.lib.volta_oracle_loss_f64(tt.h))
+        lh, lo, lt = map(np.array, (lh, lo, lt))
+        # the leading steps on which fp32 arithmetic still tracks fp64
+        calm = np.logical_and.accumulate(np.abs(lo - lt) <= 1e-5 * np.abs(lt))
+        assert calm[0], "the oracle leaves fp64 at step 1"
+        ok, mx, _ = close_enough(lh[calm], lo[calm])
+        say(f"  loss compared on {int(calm.sum())} of {steps} steps")
+        assert ok, f"losses differ on well-conditioned steps: max {mx:.3e}\n hip={lh[calm]}\n ora={lo[calm]}"
+        e_h = abs(lh[-1] - lt[-1])
+        e_o = abs(lo[-1] - lt[-1])
+        say(f"  final loss: hip {lh[-1]:.7g} oracle {lo[-1]:.7g} fp64 {lt[-1]:.7g}")
+        truth = _flat_f64(orc, tt, spec)
+        for i, (a, b, t) in enumerate(zip(_flat(*th.get_params()), _flat(*to.get_params()), truth)):
+            rh = float(np.sqrt(np.mean((a - t) ** 2)))
+            ro = float(np.sqrt(np.mean((b - t) ** 2)))
+            say(f"  layer {i}: rms err vs fp64 hip {rh:.3e} oracle {ro:.3e}")
+            ratios[i].append((rh - 1e-7) / ro if ro > 0 else 0.0)
+        ratios.setdefault("loss", []).append((e_h - 1e-6 - 1e-5 * abs(lt[-1])) / e_o if e_o > 0 else 0.0)
+        assert th.status() == 0
+        for t in (th, to, tt):
+            t.close()
+    for key, r in ratios.items():
+        med = float(np.median(r))
+        say(f"  {key}: hip/oracle distance from fp64, median over seeds {med:.2f} ({', '.join(f'{x:.2f}' for x in r)})")
+        assert med <= 3.0, f"{key}: hip is {med:.2f}x further from fp64 than the fp32 oracle"
 
 
 @pytest.mark.parametrize("name", ["c1_mlp256_relu_sgd_b64", "c2_mlp512_relu_adam_b64", "c5_wide_ce_adagrad_b4096"])

@@ -1501,17 +1501,15 @@ static hipError_t launch_reduce(const GemmArgs& a, int splits, hipStream_t st) {
 
 // Small-M products: NN with BIAS_ACT / STORE, NT with DX_ACT / STORE.
 // Waves per workgroup of a small-M launch (forward NN or dX NT): 16 while the
-// grid has at most one workgroup per two CUs, 8 while it has at most one per
-// CU, else 4.  More waves split K into shorter chains per wave; an 8-wave
-// workgroup (168 registers a lane) leaves room for no second one on its CU,
-// so a larger grid would take two rounds, and 4-wave workgroups fit three
-// to a CU.  Measured on C2: the 128- and 64-workgroup forwards 4.1-4.5 ->
-// 3.5 and 2.3 -> 2.0 us with 16 waves against 8; C3's 512-workgroup
-// fwd0/fwd1 4.16/14.36 us with 4 against 5.28/16.1 us with 8.  dX (NT)
-// products take 4, as in a paired launch (256 threads), so paired and
-// separate launches give the same bits: a 512-thread pair of an 8-wave dX
-// with two small-K dW tiles per workgroup measured slower (C2's dx1|dw2
-// 8.1 -> 10.0 us).  VOLTA_SMALLM_WAVES=4, 8 or 16 fixes the forward count.
+// grid has at most one workgroup per CU, else 4.  More waves split K into
+// shorter chains per wave; a 16-wave workgroup fills its CU, so a larger grid
+// would take two rounds, while 4-wave workgroups fit three to a CU.
+// Measured on C2 (every grid <= 256 workgroups): 57.8 us/step with 8 waves
+// against 56.7 with 16 (three alternating runs each); C3's 512-workgroup
+// fwd0/fwd1 4.16/14.36 us with 4 against 5.28/16.1 us with 8.  A dX in a
+// 256-thread paired launch takes 4 (the large-batch pairs); the small-batch
+// step runs its dX launches alone.  VOLTA_SMALLM_WAVES=4, 8 or 16 fixes the
+// count.
 static int smallm_waves(bool b_kc, int blocks, int num_cus);
 
 int gemm_smallm_waves(bool paired, int M, int N, int num_cus) {
@@ -1520,7 +1518,7 @@ int gemm_smallm_waves(bool paired, int M, int N, int num_cus) {
 
 static int smallm_waves(bool b_kc, int blocks, int num_cus) {
   const char* w = std::getenv("VOLTA_SMALLM_WAVES");
-  int waves = 2 * blocks <= num_cus ? 16 : blocks <= num_cus ? 8 : 4;
+  int waves = blocks <= num_cus ? 16 : 4;
   if (w && *w) waves = std::atoi(w) == 4 ? 4 : std::atoi(w) == 16 ? 16 : 8;
   return b_kc ? 4 : waves;
 }
