@@ -1,7 +1,7 @@
 """The .vt front end of compile-train (include/volta_vt.h) and the volta-hip
-command line, on the CPU: what spec each source resolves to, the guards,
-and the generated per-model library's exports.  The sources are written
-here in the language's MLP subset (model / dataset / train blocks)."""
+command line, on the CPU: what spec each source resolves to on either code
+path, the guards, the reference's own example scripts, the command line's
+argument rules and the generated per-model library's exports."""
 import ctypes as C
 import os
 import subprocess
@@ -95,7 +95,9 @@ def test_resolution(src, want):
     ("model m\n  layers 4 8 2\n", "inconsistent indentation"),
     ("model m\n    layers 4 8 2\ntrain m on nowhere\n", "Undefined dataset: 'nowhere'"),
     ("dataset d\n", "No models found"),
-    ("model m\n    layers 4 8 2\nloop 3\n    print 1\n", "not part of the compile-train subset"),
+    ("// a comment the language does not have\nmodel m\n    layers 4 8 2\n",
+     "Unexpected token at start of statement"),
+    ("model m\n    layers 4 8 2\nelse\n    print 1\n", "Unexpected keyword in this position"),
 ])
 def test_guards(src, msg):
     with pytest.raises(ValueError) as e:
@@ -121,20 +123,147 @@ def test_codegen_extras(src, want):
         assert "layernorm=yes" in summary
 
 
+def test_statements_outside_compile_train_are_noted_not_run():
+    """Every other statement of the language is parsed structurally and
+    noted (the reference's interpreter runs it before compiling the first
+    model, main.rs:224-246); the model resolves as without it."""
+    src = ("lr 0.01\nfn f(x)\n    print x\n    return x + 1\nif lr > 0.005\n    print \"high\"\n"
+           "elif lr > 0.001\n    print \"mid\"\nelse\n    print \"low\"\nfor i in 0..3\n    print i\n"
+           "loop 2\n    print 1\nprint f(5)\nmodel m\n    layers 4 8 2\n    activation tanh\n"
+           "dataset d\n    batch 4\ntrain m on d\n    optimizer sgd\n    lr lr\n"
+           "save m \"m.bin\"\ninfer m\n    input 1 2 3 4\n")
+    spec, summary = resolve(src)
+    assert names(spec) == ([4, 8, 2], "tanh", "sgd")
+    for kw in ("fn", "if", "elif", "else", "for", "loop", "save", "infer"):
+        assert f"'{kw}' statement not run" in summary, kw
+    assert "lr=0.01" in summary
+
+
+def test_c_path_resolution():
+    """Without --rust the reference's C path: SGD only (its own message),
+    ReLU hidden layers, MSE and no codegen extras whatever the model says
+    (mlp_train_codegen.rs:291-384), each dropped property noted."""
+    lib = load_hip()
+
+    def resolve_c(src):
+        spec = CSpec()
+        buf = C.create_string_buffer(4096)
+        if lib.lib.volta_vt_compile_train_spec_path(src.encode(), 0, C.byref(spec), buf, len(buf)) != 0:
+            raise ValueError(lib.last_error())
+        return spec, buf.value.decode()
+
+    spec, summary = resolve_c("model m\n    layers 4 8 2\n    activation gelu\n    dropout 0.5\n"
+                              "    layernorm yes\ndataset d\ntrain m on d\n    optimizer sgd\n    clip_grad 1\n")
+    assert names(spec) == ([4, 8, 2], "relu", "sgd") and spec.loss == 0
+    assert (spec.clip_grad, spec.dropout_p, spec.layernorm) == (0.0, 0.0, 0)
+    assert "path=c" in summary and "activation 'gelu' applies with --rust only" in summary
+    assert "no dropout, LayerNorm or gradient clipping" in summary
+    with pytest.raises(ValueError) as e:
+        resolve_c("model m\n    layers 4 8 2\ndataset d\ntrain m on d\n    optimizer adam\n")
+    assert "the default C compile-train path supports only SGD today" in str(e.value)
+
+
+REF_EXAMPLES = "/root/reference/examples"
+EXAMPLES_WANT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "vt_examples.json")
+
+
+@pytest.mark.skipif(not os.path.isdir(REF_EXAMPLES), reason="reference examples not mounted")
+@pytest.mark.parametrize("path", ["c", "rust"])
+def test_reference_examples(path):
+    """The reference's own example scripts (examples/*.vt, read where they
+    lie) against a table written by hand from reading them: layers,
+    activation, optimizer, lr, epochs and batch per path, or the error the
+    reference's parser or guards give (five examples open with `//` lines,
+    which its lexer reads as two Slash tokens: "Unexpected token at start of
+    statement", parser.rs:83-86)."""
+    import glob
+    import json
+
+    want = json.load(open(EXAMPLES_WANT))
+    files = sorted(glob.glob(os.path.join(REF_EXAMPLES, "*.vt")))
+    assert sorted(os.path.basename(f) for f in files) == sorted(want), "example set changed"
+    for f in files:
+        w = want[os.path.basename(f)]
+        r = subprocess.run([CLI, "check", f] + (["--rust"] if path == "rust" else []), capture_output=True,
+                           text=True)
+        exp = w.get(path, w.get("both"))
+        if "error" in exp:
+            assert r.returncode == 1 and exp["error"] in r.stderr, (f, r.stderr)
+            continue
+        assert r.returncode == 0, (f, r.stderr)
+        line = r.stdout.splitlines()[0]
+        fields = dict(kv.split("=", 1) for kv in line.split())
+        for k, v in exp.items():
+            assert fields.get(k) == v, (f, k, fields.get(k), v)
+
+
+def test_cli_flags_as_the_reference_checks_them(tmp_path):
+    """compile-train's arguments (main.rs:587-650): -o once, --rust once,
+    --cpu-target portable|native (separate or =), no other flag, one file."""
+    vt = tmp_path / "net.vt"
+    vt.write_text(HEADLINE)
+    cases = [
+        (["--rust", "--rust"], "accepts '--rust' at most once"),
+        (["--cpu-target", "fast"], "accepts only 'portable' or 'native', got 'fast'"),
+        (["--cpu-target"], "requires 'portable' or 'native'"),
+        (["-o"], "requires an output path"),
+        (["-o", "a.so", "-o", "b.so"], "accepts '-o' at most once"),
+        (["--frobnicate"], "does not accept flag '--frobnicate'"),
+        ([str(vt)], "expects exactly one .vt file"),
+    ]
+    for extra, msg in cases:
+        r = subprocess.run([CLI, "compile-train", str(vt)] + extra, capture_output=True, text=True)
+        assert r.returncode == 2 and msg in r.stderr, (extra, r.stderr)
+    r = subprocess.run([CLI, "compile-train"], capture_output=True, text=True)
+    assert r.returncode == 2
+    for flags, name in ((["--rust", "--cpu-target=native"], "net.train_rust.so"),
+                        (["--cpu-target", "portable", "--rust"], "net.train_rust.so")):
+        r = subprocess.run([CLI, "compile-train", str(vt)] + flags, capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr
+        assert r.stdout.startswith(f"Training DLL compiled: {tmp_path / name} (cpu-target=")
+        assert (tmp_path / name).exists()
+    # the C path refuses Adam with the reference's message
+    r = subprocess.run([CLI, "compile-train", str(vt)], capture_output=True, text=True)
+    assert r.returncode == 1 and "supports only SGD today" in r.stderr
+
+
+def test_cli_weights_export_load_pretrained(tmp_path):
+    """--weights embeds trained parameters and exports
+    volta_train_load_pretrained (the C path's loader,
+    mlp_train_codegen.rs:386-413); a file of the wrong size is refused."""
+    import numpy as np
+
+    vt = tmp_path / "m.vt"
+    vt.write_text("model m\n    layers 4 3 2\n")
+    w = tmp_path / "m.f32"
+    np.arange(4 * 3 + 3 + 3 * 2 + 2, dtype=np.float32).tofile(w)
+    r = subprocess.run([CLI, "compile-train", str(vt), "--weights", str(w)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    lib = C.CDLL(str(tmp_path / "m.train.so"))
+    assert hasattr(lib, "volta_train_load_pretrained")
+    r = subprocess.run([CLI, "compile-train", str(vt), "-o", str(tmp_path / "plain.so")], capture_output=True,
+                       text=True)
+    assert r.returncode == 0, r.stderr
+    assert not hasattr(C.CDLL(str(tmp_path / "plain.so")), "volta_train_load_pretrained")
+    np.zeros(5, np.float32).tofile(w)
+    r = subprocess.run([CLI, "compile-train", str(vt), "--weights", str(w)], capture_output=True, text=True)
+    assert r.returncode == 1 and "holds 20 bytes" in r.stderr
+
+
 def test_cli_check_and_compile_train(tmp_path):
     vt = tmp_path / "net.vt"
     vt.write_text(HEADLINE)
-    r = subprocess.run([CLI, "check", str(vt)], capture_output=True, text=True)
+    r = subprocess.run([CLI, "check", str(vt), "--rust"], capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
-    assert r.stdout.startswith("model=net layers=512-1024-1024-512-256-1 activation=relu optimizer=adam")
+    assert r.stdout.startswith("model=net path=rust layers=512-1024-1024-512-256-1 activation=relu optimizer=adam")
     bad = tmp_path / "bad.vt"
     bad.write_text("model m\n    layers 4 8 2\ndataset d\ntrain m on d\n    optimizer rmsprop\n")
-    r = subprocess.run([CLI, "compile-train", str(bad)], capture_output=True, text=True)
+    r = subprocess.run([CLI, "compile-train", str(bad), "--rust"], capture_output=True, text=True)
     assert r.returncode == 1 and "rmsprop" in r.stderr
-    r = subprocess.run([CLI, "compile-train", str(vt)], capture_output=True, text=True)
+    r = subprocess.run([CLI, "compile-train", str(vt), "--rust"], capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
-    out = tmp_path / "net.train_hip.so"
-    assert out.exists() and not (tmp_path / "net.train_hip.so.c").exists()
+    out = tmp_path / "net.train_rust.so"
+    assert out.exists() and not (tmp_path / "net.train_rust.so.c").exists()
     lib = C.CDLL(str(out))
     for sym in ("volta_train_init", "volta_train_step", "volta_train_loss", "volta_train_get_params",
                 "volta_train_set_params", "volta_train_free", "volta_train_step_labels"):
@@ -147,7 +276,7 @@ def test_cli_check_and_compile_train(tmp_path):
         lib.volta_train_free(h)
     else:
         assert b"HIP" in lib.volta_train_last_error()
-    r = subprocess.run([CLI, "compile-train", str(vt), "-o", str(tmp_path / "x.so"), "--keep-source"],
+    r = subprocess.run([CLI, "compile-train", str(vt), "--rust", "-o", str(tmp_path / "x.so"), "--keep-source"],
                        capture_output=True, text=True)
     assert r.returncode == 0 and (tmp_path / "x.so.c").exists()
     assert subprocess.run([CLI, "frobnicate", str(vt)], capture_output=True).returncode == 2

@@ -152,6 +152,8 @@ _SIGNATURES = {
 # include/volta_vt.h (the .vt front end; GPU library only)
 VT_SIGNATURES = {
     "volta_vt_compile_train_spec": (C.c_int32, [C.c_char_p, C.POINTER(CSpec), C.c_char_p, C.c_int32]),
+    "volta_vt_compile_train_spec_path": (C.c_int32, [C.c_char_p, C.c_int32, C.POINTER(CSpec), C.c_char_p,
+                                                     C.c_int32]),
 }
 
 BUF_ACT, BUF_DELTA, BUF_GRAD_W, BUF_GRAD_B = 0, 1, 2, 3

@@ -251,12 +251,13 @@ struct Statement {
 
 }  // namespace
 
-bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::string* error) {
+bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::string* error, bool rust) {
   try {
     const std::vector<Line> lines = lex(source);
     std::vector<Statement> stmts;
     std::map<std::string, double> vars;
     std::vector<std::string> notes;
+    bool after_if = false;  // the previous top-level statement was an if / elif block
     for (size_t li = 0; li < lines.size();) {
       const Line& ln = lines[li];
       if (ln.indent != 0) fail_at(ln.number, 1, "unexpected indentation");
@@ -264,6 +265,30 @@ bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::st
       Statement st;
       st.line = ln.number;
       const std::string kw = head.kind == T_IDENT ? head.text : "";
+      // Statements of the language outside compile-train's input: the
+      // reference's executor runs them before compiling the first model
+      // (main.rs:224-246); none of them changes the generated library, so
+      // they are parsed structurally (header line and indented block) and
+      // noted, not run.  elif / else only follow an if block
+      // (parser.rs:78-81).
+      if (kw == "save" || kw == "load" || kw == "infer" || kw == "fn" || kw == "struct" || kw == "loop" ||
+          kw == "for" || kw == "if" || kw == "elif" || kw == "else" || kw == "return" || kw == "precision" ||
+          kw == "memory") {
+        if ((kw == "elif" || kw == "else") && !after_if)
+          fail_at(ln.number, head.col, "Unexpected keyword in this position");
+        after_if = kw == "if" || kw == "elif";
+        notes.push_back("line " + std::to_string(ln.number) + ": '" + kw +
+                        "' statement not run (the reference's interpreter runs it before compiling the first "
+                        "model; it does not change the generated library)");
+        ++li;
+        while (li < lines.size() && lines[li].indent > 0) ++li;
+        continue;
+      }
+      after_if = false;
+      if (head.kind != T_IDENT)
+        fail_at(ln.number, head.col,
+                "Unexpected token at start of statement (start a statement with an identifier, or a keyword "
+                "such as model, dataset, train, if, loop, fn, print, save, load)");
       if (kw == "model" || kw == "dataset") {
         if (ln.toks.size() != 2 || ln.toks[1].kind != T_IDENT)
           fail_at(ln.number, head.col, "use: " + kw + " <name>");
@@ -280,10 +305,7 @@ bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::st
         notes.push_back("line " + std::to_string(ln.number) + ": print skipped");
         ++li;
         continue;
-      } else if (head.kind == T_IDENT && ln.toks.size() >= 2 &&
-                 !(kw == "save" || kw == "load" || kw == "infer" || kw == "fn" || kw == "struct" ||
-                   kw == "loop" || kw == "for" || kw == "if" || kw == "elif" || kw == "else" ||
-                   kw == "return")) {
+      } else if (ln.toks.size() >= 2) {
         // top-level variable: `name <number>` or `name = <number>`
         size_t k = 1;
         if (ln.toks[k].kind == T_SYM && ln.toks[k].text == "=") ++k;
@@ -302,7 +324,7 @@ bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::st
         continue;
       } else {
         fail_at(ln.number, head.col,
-                "statement '" + head.text + "' is not part of the compile-train subset (model, dataset, train)");
+                "Unknown keyword '" + head.text + "' (a variable needs a value: '" + head.text + " <expression>')");
       }
       ++li;
       // property block: the following lines indented by exactly 4
@@ -440,11 +462,17 @@ bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::st
       if (find(tb, "weight_decay"))
         notes.push_back("train.weight_decay shapes the interpreter's training only; the generated step "
                         "uses the compile-train constant (AdamW 0.01 on weights)");
-      if (out.epochs > 0)
+      if (out.epochs > 0 && rust)
         notes.push_back("the reference trains the model in its interpreter for " + std::to_string(out.epochs) +
-                        " epoch(s) before generating the library and starts the library from those weights; "
-                        "this library starts from the LCG Xavier init (seed 42) — load trained weights with "
-                        "volta_train_set_params");
+                        " epoch(s) first; its --rust library does not take those weights (the generator "
+                        "ignores them, mlp_train_rust_codegen.rs:249-251) and starts from the LCG Xavier init "
+                        "(seed 42), as this library does");
+      if (out.epochs > 0 && !rust)
+        notes.push_back("the reference's C-path library exports volta_train_load_pretrained with the weights "
+                        "its interpreter trained for " + std::to_string(out.epochs) +
+                        " epoch(s) (mlp_train_codegen.rs:386-413); this build has no interpreter: the library "
+                        "starts from the LCG Xavier init (seed 42), and compile-train --weights FILE embeds "
+                        "trained weights and exports volta_train_load_pretrained");
       out.trained = true;
     } else {
       optimizer = model_opt.empty() ? "sgd" : model_opt;
@@ -461,11 +489,34 @@ bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::st
         clip = c;
       }
     }
-    // compile-train --rust guard (executor.rs:3172-3189)
-    if (!(optimizer == "sgd" || optimizer == "adam" || optimizer == "adamw" || optimizer == "adagrad"))
-      throw Fail{"Model '" + model->name + "' requests optimizer '" + optimizer +
-                 "', but `compile-train --rust` supports only SGD, Adam, AdamW, and Adagrad today. "
-                 "Use runtime `train` for RMSProp or other optimizers."};
+    if (rust) {
+      // compile-train --rust guard (executor.rs:3174-3189)
+      if (!(optimizer == "sgd" || optimizer == "adam" || optimizer == "adamw" || optimizer == "adagrad"))
+        throw Fail{"Model '" + model->name + "' requests optimizer '" + optimizer +
+                   "', but `compile-train --rust` supports only SGD, Adam, AdamW, and Adagrad today. "
+                   "Use runtime `train` for RMSProp or other optimizers."};
+    } else {
+      // default (C) compile-train guard (executor.rs:3160-3172); the C
+      // step has ReLU hidden layers, MSE and SGD whatever the model says
+      // and none of the codegen extras (mlp_train_codegen.rs:291-384)
+      if (optimizer != "sgd")
+        throw Fail{"Model '" + model->name + "' requests optimizer '" + optimizer +
+                   "', but the default C compile-train path supports only SGD today. Use `compile-train --rust` "
+                   "for Adam/AdamW/Adagrad, or use runtime `train`."};
+      if (activation != "relu") {
+        notes.push_back("the C compile-train path generates ReLU hidden layers whatever model.activation says "
+                        "(mlp_train_codegen.rs:316-321); activation '" + activation +
+                        "' applies with --rust only, and this library follows the path chosen");
+        activation = "relu";
+      }
+      if (dropout > 0.0 || layernorm || clip > 0.0) {
+        notes.push_back("the C compile-train path generates no dropout, LayerNorm or gradient clipping; they "
+                        "apply with --rust only, and this library follows the path chosen");
+        dropout = 0.0;
+        layernorm = false;
+        clip = 0.0;
+      }
+    }
 
     const int act = activation == "relu" ? VOLTA_ACT_RELU
                     : activation == "sigmoid" ? VOLTA_ACT_SIGMOID
@@ -485,6 +536,7 @@ bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::st
     std::string why;
     if (!validate_spec(out.spec, &why)) throw Fail{"model '" + model->name + "': " + why};
     out.model = model->name;
+    out.rust = rust;
     out.notes = notes;
     *plan = out;
     return true;
@@ -500,8 +552,8 @@ std::string vt_plan_summary(const VtTrainPlan& p) {
   std::string layers;
   for (int i = 0; i < p.spec.n_sizes; ++i) layers += (i ? "-" : "") + std::to_string(p.spec.sizes[i]);
   char buf[512];
-  std::snprintf(buf, sizeof buf, "model=%s layers=%s activation=%s optimizer=%s loss=mse", p.model.c_str(),
-                layers.c_str(), acts[p.spec.activation], opts[p.spec.optimizer]);
+  std::snprintf(buf, sizeof buf, "model=%s path=%s layers=%s activation=%s optimizer=%s loss=mse", p.model.c_str(),
+                p.rust ? "rust" : "c", layers.c_str(), acts[p.spec.activation], opts[p.spec.optimizer]);
   std::string s = buf;
   if (p.spec.clip_grad > 0.0f) {
     std::snprintf(buf, sizeof buf, " clip_grad=%g", p.spec.clip_grad);
@@ -526,13 +578,18 @@ std::string vt_plan_summary(const VtTrainPlan& p) {
 // ---------------------------------------------------------------------------
 extern "C" int32_t volta_vt_compile_train_spec(const char* source, volta_mlp_spec* spec, char* summary,
                                                 int32_t summary_len) {
+  return volta_vt_compile_train_spec_path(source, 1, spec, summary, summary_len);
+}
+
+extern "C" int32_t volta_vt_compile_train_spec_path(const char* source, int32_t rust, volta_mlp_spec* spec,
+                                                     char* summary, int32_t summary_len) {
   if (!source || !spec) {
     volta::set_last_error("volta_vt_compile_train_spec: null argument");
     return -1;
   }
   volta::VtTrainPlan plan;
   std::string err;
-  if (!volta::vt_compile_train_plan(source, &plan, &err)) {
+  if (!volta::vt_compile_train_plan(source, &plan, &err, rust != 0)) {
     volta::set_last_error(err);
     return -1;
   }

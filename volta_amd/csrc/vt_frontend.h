@@ -13,6 +13,7 @@ namespace volta {
 struct VtTrainPlan {
   volta_mlp_spec spec{};
   std::string model;          // first model declared (the one compile-train builds)
+  bool rust = true;           // compile-train --rust (else the default C path)
   bool trained = false;       // a `train <model> on <dataset>` statement names it
   double lr = 0.0;            // resolved learning rate of the last such statement (0: none)
   int64_t epochs = 0;         // its resolved epochs
@@ -21,9 +22,10 @@ struct VtTrainPlan {
 };
 
 // Parse `source` and resolve the first model as `volta compile-train --rust`
-// does (executor.rs:1806-1863, guards :3147-3189).  Returns false with a
-// message (line:column: text) on a parse error or an unsupported model.
-bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::string* error);
+// (rust) or plain `volta compile-train` (the C path) does (executor.rs:
+// 1759-1863, guards :3147-3189).  Returns false with a message (line:column:
+// text) on a parse error or an unsupported model.
+bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::string* error, bool rust = true);
 
 // One-line description of a plan ("model=... layers=a-b-c activation=...").
 std::string vt_plan_summary(const VtTrainPlan& plan);
