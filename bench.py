@@ -563,7 +563,8 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the step would shard by data parallelism over B; see DESIGN.md).", file=sys.stderr)
+              "(the step would shard by data parallelism over B, with one all-reduce of the flat "
+              "[dW; db] buffer before the optimizer).", file=sys.stderr)
         return 2
 
     # The host's choice of HIP's graph replay mode; HIP reads it once, at its

@@ -96,6 +96,9 @@ float* state(VoltaRtOptimizer* h, int which, int i) {
 
 }  // namespace
 
+// volta_rt_last_error's text for the graph interpreter (rt_graph.cpp).
+void oracle_rt_set_error(const std::string& m) { g_rt_err = m; }
+
 extern "C" {
 
 VoltaRtOptimizer* volta_rt_optimizer_new(int32_t n, const int64_t* counts) {

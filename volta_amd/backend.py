@@ -1,12 +1,17 @@
-"""Host mirror of Volta's runtime Backend for the HIP library: capabilities()
-and apply_gradients() of the Backend trait (src/engine/ir/backend.rs:24-69),
-whose update is optimizer::apply_gradients (src/engine/ir/optimizer.rs:
-36-178), over the volta_rt_* C ABI (include/volta_backend.h).
+"""Host mirror of Volta's runtime Backend for the HIP library, over the
+volta_rt_* C ABI (include/volta_backend.h):
+  * capabilities() and apply_gradients() of the Backend trait
+    (src/engine/ir/backend.rs:24-69), whose update is
+    optimizer::apply_gradients (src/engine/ir/optimizer.rs:36-178);
+  * compile(), execute_value() and execute_terminal() for MLP graphs, through
+    the library's plan cache (plan_cache.rs:8-51), with a small Graph /
+    ExecutionPlan mirror (graph.rs, execution_plan.rs) and the reference's
+    lower_model_to_graph (lowering.rs:87-140) to build them.
 
-The same RtOptimizer drives libvolta_hip.so (device pointers) and the CPU
-oracle (host pointers, tests only).  Parameters and gradients are keyed by
-integer ids as the reference keys them by ValueId; the state follows a fixed
-list of ids.
+The same classes drive libvolta_hip.so (device pointers) and the CPU oracle
+(host pointers, tests only).  Parameters and gradients are keyed by integer
+ids as the reference keys them by ValueId; the state follows a fixed list of
+ids.
 """
 from __future__ import annotations
 
@@ -46,6 +51,31 @@ class OptimizerError(RuntimeError):
     """OptimizerError (optimizer.rs:95-98): the reference's message."""
 
 
+OPS = {"other": 0, "input": 1, "parameter": 2, "output": 3, "matmul": 4, "add": 5, "gemm": 6, "relu": 7,
+       "sigmoid": 8, "gelu": 9, "softmax": 10}
+DETERMINISM = {"strict": 0, "balanced": 1, "fast": 2}
+
+
+class RtNode(C.Structure):
+    _fields_ = [("op", C.c_int32), ("output", C.c_int32), ("in0", C.c_int32), ("in1", C.c_int32),
+                ("in2", C.c_int32), ("binding", C.c_int32), ("alpha", C.c_float), ("beta", C.c_float)]
+
+
+class RtBinding(C.Structure):
+    _fields_ = [("rows", C.c_int64), ("cols", C.c_int64)]
+
+
+class RtGraph(C.Structure):
+    _fields_ = [("n_nodes", C.c_int32), ("nodes", C.POINTER(RtNode)), ("n_ordered", C.c_int32),
+                ("ordered_nodes", C.POINTER(C.c_int32)), ("n_bindings", C.c_int32),
+                ("bindings", C.POINTER(RtBinding)), ("graph_fingerprint", C.c_uint64),
+                ("shape_signature_hash", C.c_uint64), ("peak_bytes", C.c_int64)]
+
+
+class RtCompiled(C.Structure):
+    _fields_ = [("schedule_len", C.c_int64), ("peak_bytes", C.c_int64), ("fingerprint", C.c_uint64)]
+
+
 _SIGS = {
     "volta_rt_optimizer_new": (C.c_void_p, [C.c_int32, C.POINTER(C.c_int64)]),
     "volta_rt_optimizer_free": (None, [C.c_void_p]),
@@ -55,6 +85,13 @@ _SIGS = {
     "volta_rt_get_state": (C.c_int32, [C.c_void_p, C.c_int32, C.c_int32, C.POINTER(C.c_float)]),
     "volta_rt_last_error": (C.c_char_p, []),
     "volta_rt_capabilities_get": (None, [C.POINTER(RtCapabilities)]),
+    "volta_rt_compile": (C.c_int32, [C.POINTER(RtGraph), C.c_int32, C.POINTER(RtCompiled)]),
+    "volta_rt_execute_value": (C.c_int32, [C.POINTER(RtGraph), C.c_int32, C.c_int32, C.POINTER(C.c_void_p),
+                                           C.c_void_p, C.c_int64, C.POINTER(C.c_int64)]),
+    "volta_rt_execute_terminal": (C.c_int32, [C.POINTER(RtGraph), C.c_int32, C.POINTER(C.c_void_p), C.c_void_p,
+                                              C.c_int64, C.POINTER(C.c_int64)]),
+    "volta_rt_clear_plan_cache": (None, []),
+    "volta_rt_compile_count": (C.c_int64, []),
 }
 
 
@@ -114,16 +151,181 @@ def capabilities(cdll: C.CDLL) -> Dict[str, int]:
     return {f: int(getattr(out, f)) for f, _ in RtCapabilities._fields_}
 
 
+# ---------------------------------------------------------------------------
+# Graph execution
+# ---------------------------------------------------------------------------
+class BackendError(RuntimeError):
+    """BackendError (backend.rs:19-22): the library's message."""
+
+
+class Graph:
+    """Graph (graph.rs) as far as MLP graphs use it: add_op returns the
+    ValueId the node defines (ValueIds are handed out in order, one per
+    node); bind_input_shape / bind_parameter_shape record shapes by name.
+
+    add_op("input", name=...), ("parameter", name=...), ("matmul", a, b),
+    ("add", a, b), ("gemm", lhs, rhs, bias_or_None, alpha=1.0, beta=1.0),
+    ("relu"|"sigmoid"|"gelu"|"softmax"|"output", a), or ("other", ...) for an
+    op the backends do not lower."""
+
+    def __init__(self):
+        self.nodes = []  # (op, operands, name, alpha, beta)
+        self.shapes = {}
+
+    def add_op(self, op: str, *operands, name: Optional[str] = None, alpha: float = 1.0, beta: float = 1.0) -> int:
+        if op not in OPS:
+            raise ValueError(f"unknown op {op!r}")
+        self.nodes.append((op, tuple(-1 if o is None else int(o) for o in operands), name, float(alpha),
+                           float(beta)))
+        return len(self.nodes) - 1
+
+    def bind_input_shape(self, name: str, shape: Sequence[int]) -> None:
+        self.shapes[name] = tuple(int(d) for d in shape)
+
+    bind_parameter_shape = bind_input_shape
+
+    def last_value_id(self) -> int:
+        return len(self.nodes) - 1
+
+
+def lower_model_to_graph(graph: Graph, layers: Sequence[int], activation: str, input_val: int,
+                         apply_final_activation: bool) -> int:
+    """LoweringContext::lower_model_to_graph (lowering.rs:87-140): per layer
+    Parameter weight_{in}_{out} [in, out], Parameter bias_{out} [1, out],
+    MatMul, Add; Relu or Sigmoid after hidden layers (other activations add
+    nothing there); Softmax after the last layer when asked and the
+    activation is softmax.  Returns the last value."""
+    cur = input_val
+    for i in range(len(layers) - 1):
+        fi, fo = int(layers[i]), int(layers[i + 1])
+        w = graph.add_op("parameter", name=f"weight_{fi}_{fo}")
+        b = graph.add_op("parameter", name=f"bias_{fo}")
+        cur = graph.add_op("add", graph.add_op("matmul", cur, w), b)
+        if i != len(layers) - 2:
+            if activation == "relu":
+                cur = graph.add_op("relu", cur)
+            elif activation == "sigmoid":
+                cur = graph.add_op("sigmoid", cur)
+        elif apply_final_activation and activation == "softmax":
+            cur = graph.add_op("softmax", cur)
+    return cur
+
+
+def _fnv(values) -> int:
+    h = 1469598103934665603
+    for v in values:
+        for byte in int(v).to_bytes(8, "little", signed=True):
+            h = ((h ^ byte) * 1099511628211) & 0xFFFFFFFFFFFFFFFF
+    return h
+
+
+class ExecutionPlan:
+    """What the backend reads of ExecutionPlan (execution_plan.rs): the
+    schedule, graph_fingerprint, shape_signature_hash and peak_bytes.  This
+    mirror schedules in graph order (a topological order: every operand is
+    defined by an earlier node) and takes FNV-1a hashes of the nodes and of
+    the bound shapes as the two fingerprints; a Rust caller passes the
+    reference's own values (fingerprint.rs:7)."""
+
+    def __init__(self, graph: Graph, ordered_nodes: Optional[Sequence[int]] = None, peak_bytes: int = 0):
+        self.ordered_nodes = list(range(len(graph.nodes))) if ordered_nodes is None else list(ordered_nodes)
+        self.graph_fingerprint = _fnv(v for op, args, name, a, b in graph.nodes
+                                      for v in (OPS[op], len(args), *args, hash(name or "") & 0xFFFF))
+        self.shape_signature_hash = _fnv(d for name in sorted(graph.shapes) for d in graph.shapes[name])
+        self.peak_bytes = int(peak_bytes)
+
+
+def build_execution_plan(graph: Graph) -> ExecutionPlan:
+    return ExecutionPlan(graph)
+
+
+class GraphTables:
+    """A Graph + ExecutionPlan as the volta_rt_graph tables (one binding per
+    distinct Input/Parameter name, in order of first appearance)."""
+
+    def __init__(self, graph: Graph, plan: ExecutionPlan):
+        self.names = []
+        index = {}
+        nodes = (RtNode * len(graph.nodes))()
+        for i, (op, args, name, alpha, beta) in enumerate(graph.nodes):
+            n = nodes[i]
+            n.op, n.output, n.alpha, n.beta = OPS[op], i, alpha, beta
+            ins = list(args) + [-1] * (3 - len(args))
+            n.in0, n.in1, n.in2 = ins[:3]
+            n.binding = -1
+            if op in ("input", "parameter"):
+                if name not in index:
+                    if name not in graph.shapes:
+                        raise BackendError(f"no shape bound for '{name}'")
+                    index[name] = len(self.names)
+                    self.names.append(name)
+                n.binding = index[name]
+        binds = (RtBinding * max(1, len(self.names)))()
+        for i, name in enumerate(self.names):
+            shape = graph.shapes[name]
+            binds[i].rows, binds[i].cols = (1, shape[0]) if len(shape) == 1 else shape
+        order = (C.c_int32 * len(plan.ordered_nodes))(*plan.ordered_nodes)
+        self._keep = (nodes, binds, order)
+        self.c = RtGraph(len(graph.nodes), nodes, len(plan.ordered_nodes), order, len(self.names), binds,
+                         plan.graph_fingerprint, plan.shape_signature_hash, plan.peak_bytes)
+
+    def pointers(self, addresses: Dict[str, int]):
+        missing = [n for n in self.names if n not in addresses]
+        if missing:
+            raise BackendError(f"Missing parameter: '{missing[0]}'")
+        return (C.c_void_p * max(1, len(self.names)))(*[int(addresses[n]) for n in self.names])
+
+
+class GraphLibrary:
+    """volta_rt_compile / execute_value / execute_terminal of one library on
+    raw addresses (device for libvolta_hip.so, host for the oracle)."""
+
+    def __init__(self, cdll: C.CDLL):
+        self.lib = bind(cdll)
+
+    def compile(self, graph: Graph, plan: ExecutionPlan, determinism: int = 0) -> Dict[str, int]:
+        t = GraphTables(graph, plan)
+        out = RtCompiled()
+        if self.lib.volta_rt_compile(C.byref(t.c), determinism, C.byref(out)) != 0:
+            raise BackendError(self.lib.volta_rt_last_error().decode())
+        return {"schedule_len": out.schedule_len, "peak_bytes": out.peak_bytes, "fingerprint": out.fingerprint}
+
+    def execute(self, graph: Graph, plan: ExecutionPlan, target: Optional[int], addresses: Dict[str, int],
+                out_addr: int, capacity: int, determinism: int = 0):
+        """Runs execute_value (target given) or execute_terminal (None);
+        returns the value's shape."""
+        t = GraphTables(graph, plan)
+        ptrs = t.pointers(addresses)
+        shape = (C.c_int64 * 2)()
+        if target is None:
+            rc = self.lib.volta_rt_execute_terminal(C.byref(t.c), determinism, ptrs, out_addr, capacity, shape)
+        else:
+            rc = self.lib.volta_rt_execute_value(C.byref(t.c), determinism, int(target), ptrs, out_addr, capacity,
+                                                 shape)
+        if rc != 0:
+            raise BackendError(self.lib.volta_rt_last_error().decode())
+        return int(shape[0]), int(shape[1])
+
+    def clear_plan_cache(self) -> None:
+        self.lib.volta_rt_clear_plan_cache()
+
+    def compile_count(self) -> int:
+        return int(self.lib.volta_rt_compile_count())
+
+
 class HipBackend:
-    """The HIP backend's side of the Backend trait for training updates:
-    capabilities() and apply_gradients(parameters, gradients, config, state)
+    """The HIP backend's side of the Backend trait (backend.rs:24-69):
+    capabilities(); apply_gradients(parameters, gradients, config, state)
     with parameters/gradients as {id: DeviceArray} (gradients may omit ids,
-    as the reference skips parameters without a gradient)."""
+    as the reference skips parameters without a gradient); compile(),
+    execute_value() and execute_terminal() of MLP graphs with the context's
+    inputs and parameters as {name: DeviceArray}."""
 
     def __init__(self, lib=None):
         from volta_amd import load_hip
 
         self.lib = lib or load_hip()
+        self.graphs = GraphLibrary(self.lib.lib)
 
     def capabilities(self) -> Dict[str, int]:
         return capabilities(self.lib.lib)
@@ -144,3 +346,31 @@ class HipBackend:
                                      f"{g.host.shape}")
         state.apply(cfg, [parameters[i].ptr for i in state.ids],
                     [gradients[i].ptr if i in gradients else None for i in state.ids])
+
+    def compile(self, graph: Graph, plan: ExecutionPlan, determinism: int = 0) -> Dict[str, int]:
+        """Backend::compile through compile_or_get_cached."""
+        return self.graphs.compile(graph, plan, determinism)
+
+    def execute_value(self, graph: Graph, plan: ExecutionPlan, target: int, context: Dict[str, "object"],
+                      determinism: int = 0) -> np.ndarray:
+        """The value `target` as a host array of its [rows, cols] shape."""
+        return self._execute(graph, plan, target, context, determinism)
+
+    def execute_terminal(self, graph: Graph, plan: ExecutionPlan, context: Dict[str, "object"],
+                         determinism: int = 0) -> np.ndarray:
+        return self._execute(graph, plan, None, context, determinism)
+
+    def _execute(self, graph, plan, target, context, determinism):
+        from volta_amd import DeviceArray
+
+        # every value of an MLP chain fits rows x the widest bound dimension
+        shapes = [graph.shapes[n] for n in GraphTables(graph, plan).names]
+        rows = max((s[0] for s in shapes if len(s) == 2), default=1)
+        cap = max([rows * max(max(s) for s in shapes)] + [int(np.prod(s)) for s in shapes]) if shapes else 1
+        out = DeviceArray(np.zeros(cap, np.float32), self.lib)
+        try:
+            r, c = self.graphs.execute(graph, plan, target, {k: v.ptr for k, v in context.items()}, out.ptr, cap,
+                                       determinism)
+            return out.numpy()[: r * c].reshape(r, c)
+        finally:
+            out.free()

@@ -25,9 +25,9 @@ BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libvolta_hip.so")
 
 SOURCES = ["gemm.hip", "skinny.hip", "step_kernels.hip", "extras.hip", "runtime.hip", "test_hooks.hip", "rt_optimizer.hip",
-           "spec.cpp", "vt_frontend.cpp"]
+           "rt_graph.hip", "rt_lower.cpp", "spec.cpp", "vt_frontend.cpp"]
 HEADERS = ["gemm.h", "skinny.h", "step_kernels.h", "extras.h", "device_common.h", "recorder.h", "spec.h",
-           "narrow_dw.h", "out_head.h", "vt_frontend.h"]
+           "narrow_dw.h", "out_head.h", "vt_frontend.h", "rt_lower.h"]
 CLI = os.path.join(PKG, "volta-hip")
 CLI_SOURCES = ["volta_hip_cli.cpp", "vt_frontend.cpp", "spec.cpp"]
 CXX = os.environ.get("CXX", "g++")

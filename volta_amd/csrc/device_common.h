@@ -29,8 +29,11 @@ struct DevScalars {
 // Hidden activations, mlp_train_rust_codegen.rs:563-596 (forward) and
 // :893-916 (derivative).  Same expression order as the reference; the
 // library is built with -ffp-contract=off so nothing is fused into FMAs.
-// kIdentity marks the linear output layer.
+// kIdentity marks the linear output layer.  kRtSigmoid is the runtime
+// interpreter's sigmoid (kernels/activations.rs:82-90), used by graph
+// execution: the same 1/(1+e^-x) for x >= 0, e^x/(1+e^x) below.
 constexpr int kIdentity = -1;
+constexpr int kRtSigmoid = 16;
 
 __device__ __forceinline__ float d_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
 
@@ -38,6 +41,11 @@ __device__ __forceinline__ float act_forward(int act, float x) {
   switch (act) {
     case VOLTA_ACT_RELU: return x > 0.0f ? x : 0.0f;
     case VOLTA_ACT_SIGMOID: return d_sigmoid(x);
+    case kRtSigmoid: {
+      if (x >= 0.0f) return 1.0f / (1.0f + expf(-x));
+      const float e = expf(x);
+      return e / (1.0f + e);
+    }
     case VOLTA_ACT_TANH: return tanhf(x);
     case VOLTA_ACT_LEAKY_RELU: return x > 0.0f ? x : 0.01f * x;
     case VOLTA_ACT_SILU: return x * d_sigmoid(x);

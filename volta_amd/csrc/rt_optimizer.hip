@@ -347,6 +347,11 @@ void launch_apply(VoltaRtOptimizer* h, const RtArgs& a) {
 
 }  // namespace
 
+namespace volta {
+// volta_rt_last_error's text for the graph-execution calls (rt_graph.hip).
+void rt_set_error(const std::string& m) { g_rt_err = m; }
+}  // namespace volta
+
 extern "C" {
 
 VoltaRtOptimizer* volta_rt_optimizer_new(int32_t n, const int64_t* counts) {
