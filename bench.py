@@ -53,7 +53,15 @@ WORKLOADS = {
     "c4_256": (MlpSpec([512, 1024, 1024, 512, 256, 1], "silu", "sgd"), 256, 0.01),
     "c4_1024": (MlpSpec([512, 1024, 1024, 512, 256, 1], "silu", "sgd"), 1024, 0.01),
     "c5": (MlpSpec([1024, 4096, 4096, 1024, 10], "relu", "adagrad", "ce", eps=1e-10), 4096, 1e-2),
+    # the codegen extras on the headline topology, as the reference's own
+    # benchmark scripts set them (examples/bench_layernorm.vt,
+    # bench_dropout.vt: SGD, lr 0.01, B=64), and all three together
+    "x_layernorm": (MlpSpec([512, 1024, 1024, 512, 256, 1], "relu", "sgd", layernorm=True), 64, 0.01),
+    "x_dropout": (MlpSpec([512, 1024, 1024, 512, 256, 1], "relu", "sgd", dropout_p=0.2), 64, 0.01),
+    "x_all": (MlpSpec([512, 1024, 1024, 512, 256, 1], "relu", "adam", layernorm=True, dropout_p=0.2,
+                      clip_grad=1.0), 64, 1e-3),
 }
+EXTRAS_WORKLOADS = ("x_layernorm", "x_dropout", "x_all")
 
 # Reference's own published CPU figure for the headline topology with Adam
 # (docs/BENCHMARKS.md:87; 6-core x86, MKL; different input pattern).
@@ -611,6 +619,20 @@ def main():
     if not a.no_profile:
         line["runtime_optimizer"] = run_rt_optimizer()
         log(f"runtime optimizer: {line['runtime_optimizer']}")
+        # the extras launch structure (not paired; 3-4 more launches per
+        # hidden layer), on the headline topology
+        line["extras_path"] = []
+        for x in EXTRAS_WORKLOADS:
+            x_spec, x_B, x_lr, x_res = run_gpu(x, max(50, a.steps // 4), max(10, a.warmup // 4))
+            row = {"workload": x, "layernorm": bool(x_spec.layernorm), "dropout_p": x_spec.dropout_p,
+                   "clip_grad": x_spec.clip_grad, "optimizer": x_spec.optimizer, "batch": x_B,
+                   "ms_per_step": round(x_res["ms_per_step"], 5),
+                   "samples_per_s": round(x_res["samples_per_s"], 2), "launches": len(x_res["kernels"]),
+                   "kernel_sum_ms": round(x_res["kernel_sum_ms"], 5),
+                   "slowest": max(({"kernel": r["kernel"], "ms": round(r["ms"], 5)} for r in x_res["kernels"]),
+                                  key=lambda r: r["ms"])}
+            line["extras_path"].append(row)
+            log(f"{x}: {row['ms_per_step']:.4f} ms/step, {row['launches']} launches")
     if a.secondary and a.secondary != "none":
         s_steps = max(5, a.steps // 20)
         s_spec, s_B, s_lr, s_res = run_gpu(a.secondary, s_steps, max(2, a.warmup // 10),

@@ -6,11 +6,16 @@
 //   :888-892) -- every element's draw is found by jumping the LCG ahead, so
 //   the mask does not depend on the launch shape;
 //   gradient clipping by the global norm of the deltas (:936-955).
-// Row statistics (LayerNorm mean/variance, the backward's row means) are
-// sequential f32 sums by one thread per row, as in the reference; column
-// sums are sequential over the batch, one thread per column.  The global
-// norm of the clip is a fixed-order tree (it differs from the reference's
-// sequential sum only in rounding).
+// Row statistics (the softmax maximum and sum, LayerNorm mean/variance, the
+// backward's row means and the softmax dot product) are block reductions
+// over one row per 256-thread block: each thread folds its column-strided
+// elements in column order, then a fixed butterfly per wave and the four
+// waves in order -- deterministic, and different from the reference's
+// sequential f32 sums only in rounding (the maximum is exact: the fold keeps
+// the reference's first-maximum rule, so NaN handling matches too).  Column
+// sums over the batch (dgamma, dbeta) are four interleaved batch-order sums
+// added in a fixed order.  The global norm of the clip is a fixed-order tree
+// as well.
 #include <algorithm>
 
 #include "extras.h"
@@ -38,56 +43,76 @@ __device__ __forceinline__ uint64_t lcg_jump(uint64_t s, uint64_t m) {
   return ra * s + rc;
 }
 
+// Sum of v over the 256 threads of the block, the same value in every
+// thread: a fixed butterfly per wave, then the four waves in order.  `part`
+// is 4 floats of LDS; the block must be converged.
+__device__ __forceinline__ float block_sum(float v, float* part) {
+  v = wave_sum(v);
+  __syncthreads();  // earlier readers of part are done
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return ((part[0] + part[1]) + part[2]) + part[3];
+}
+
+// The reference's first maximum of a row (mx = row[0]; mx = row[j] if
+// row[j] > mx, :727-733) over the block: threads fold their strided columns
+// (thread 0 starting from row[0], the others from -inf), then partial maxima
+// are combined lowest columns first with the same strict comparison, so the
+// result -- including a NaN in row[0] -- is the sequential one.
+__device__ __forceinline__ float block_first_max(const float* row, int c, float* part) {
+  float mx = threadIdx.x == 0 ? row[0] : -INFINITY;
+  for (int j = threadIdx.x == 0 ? 256 : threadIdx.x; j < c; j += 256)
+    if (row[j] > mx) mx = row[j];
+  // lane l combines with lane l + off, keeping the lower lane's value unless
+  // the higher one is strictly greater
+  for (int off = 1; off < 64; off <<= 1) {
+    const float o = __shfl_down(mx, off, kWave);
+    if ((threadIdx.x & (2 * off - 1)) == 0 && o > mx) mx = o;
+  }
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  float m = part[0];
+  for (int w = 1; w < 4; ++w)
+    if (part[w] > m) m = part[w];
+  return m;
+}
+
 __global__ void __launch_bounds__(256) hidden_fwd_kernel(HiddenFwdArgs a) {
-  __shared__ float stat[4];
+  __shared__ float part[4];
   const int b = blockIdx.x, c = a.c;
   float* row = a.act + (size_t)b * c;
   if (a.softmax) {
-    // :727-740: first maximum (strict >), exp(pre - max), sum in column
-    // order, times 1/sum
-    if (threadIdx.x == 0) {
-      float mx = row[0];
-      for (int j = 1; j < c; ++j)
-        if (row[j] > mx) mx = row[j];
-      stat[2] = mx;
+    // :727-740: first maximum (strict >), exp(pre - max), their sum, times
+    // 1/sum
+    const float mx = block_first_max(row, c, part);
+    float s = 0.0f;
+    for (int j = threadIdx.x; j < c; j += blockDim.x) {
+      const float e = expf(row[j] - mx);
+      row[j] = e;
+      s = s + e;
     }
-    __syncthreads();
-    const float mx = stat[2];
-    for (int j = threadIdx.x; j < c; j += blockDim.x) row[j] = expf(row[j] - mx);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float sum = 0.0f;
-      for (int j = 0; j < c; ++j) sum = sum + row[j];
-      stat[3] = 1.0f / sum;
-    }
-    __syncthreads();
-    const float inv = stat[3];
+    const float inv = 1.0f / block_sum(s, part);
     for (int j = threadIdx.x; j < c; j += blockDim.x) row[j] = row[j] * inv;
     __syncthreads();
   }
   float mu = 0.0f, is = 0.0f;
   if (a.gamma) {
-    if (threadIdx.x == 0) {
-      float m = 0.0f;
-      for (int j = 0; j < c; ++j) m = m + row[j];
-      m = m / (float)c;
-      float var = 0.0f;
-      for (int j = 0; j < c; ++j) {
-        const float d = row[j] - m;
-        var = var + d * d;
-      }
-      var = var / (float)c;
-      const float s = 1.0f / sqrtf(var + 1e-5f);
-      if (a.mu) {
-        a.mu[b] = m;
-        a.inv_std[b] = s;
-      }
-      stat[0] = m;
-      stat[1] = s;
+    // :745-760: mean, then the mean of squared deviations
+    float s = 0.0f;
+    for (int j = threadIdx.x; j < c; j += blockDim.x) s = s + row[j];
+    mu = block_sum(s, part) / (float)c;
+    float v = 0.0f;
+    for (int j = threadIdx.x; j < c; j += blockDim.x) {
+      const float d = row[j] - mu;
+      v = v + d * d;
     }
-    __syncthreads();
-    mu = stat[0];
-    is = stat[1];
+    const float var = block_sum(v, part) / (float)c;
+    is = 1.0f / sqrtf(var + 1e-5f);
+    if (a.mu && threadIdx.x == 0) {
+      a.mu[b] = mu;
+      a.inv_std[b] = is;
+    }
   }
   const uint64_t base = a.mask ? a.scalars->rng : 0;
   for (int j = threadIdx.x; j < c; j += blockDim.x) {
@@ -109,21 +134,32 @@ __global__ void __launch_bounds__(256) hidden_fwd_kernel(HiddenFwdArgs a) {
 }
 
 // LayerNorm gradient columns: dgamma[j] = sum_b dout*xhat, dbeta[j] =
-// sum_b dout, xhat recomputed from the output as (y - beta)/(gamma + 1e-12).
+// sum_b dout, xhat recomputed from the output as (y - beta)/(gamma + 1e-12)
+// (:829-838).  A block covers 64 columns; wave w sums rows b = w, w + 4, ...
+// in batch order (its loads unrolled eight rows deep), and the four wave
+// partials are added in wave order.
 __global__ void __launch_bounds__(256) ln_bwd_cols_kernel(HiddenBwdArgs a) {
-  const int j = blockIdx.x * blockDim.x + threadIdx.x;
-  if (j >= a.c) return;
-  const float g = a.gamma[j], be = a.beta[j];
+  __shared__ float pg[4][64], pb[4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int j = blockIdx.x * 64 + lane;
+  const int jj = j < a.c ? j : a.c - 1;  // loads stay in bounds; the store is guarded
+  const float g = a.gamma[jj], be = a.beta[jj];
   float dg = 0.0f, db = 0.0f;
-  for (int b = 0; b < a.B; ++b) {
-    const size_t k = (size_t)b * a.c + j;
+#pragma unroll 8
+  for (int b = w; b < a.B; b += 4) {
+    const size_t k = (size_t)b * a.c + jj;
     const float xh = (a.act[k] - be) / (g + 1e-12f);
     const float dout = a.delta[k];
     dg = dg + dout * xh;
     db = db + dout;
   }
-  a.dgamma[j] = dg;
-  a.dbeta[j] = db;
+  pg[w][lane] = dg;
+  pb[w][lane] = db;
+  __syncthreads();
+  if (w == 0 && j < a.c) {
+    a.dgamma[j] = ((pg[0][lane] + pg[1][lane]) + pg[2][lane]) + pg[3][lane];
+    a.dbeta[j] = ((pb[0][lane] + pb[1][lane]) + pb[2][lane]) + pb[3][lane];
+  }
 }
 
 // Row pass: LayerNorm backward (row means of d_xhat and d_xhat*xhat by
@@ -131,27 +167,23 @@ __global__ void __launch_bounds__(256) ln_bwd_cols_kernel(HiddenBwdArgs a) {
 // derivative takes the pre-activation (the output is no longer relu(pre));
 // sigmoid/tanh take the layer output as the reference does.
 __global__ void __launch_bounds__(256) hidden_bwd_rows_kernel(HiddenBwdArgs a) {
-  __shared__ float stat[3];
+  __shared__ float part[4];
   const int b = blockIdx.x, c = a.c;
   float* d = a.delta + (size_t)b * c;
   const float* y = a.act + (size_t)b * c;
   float sum_d = 0.0f, sum_dxh = 0.0f, is = 0.0f;
   if (a.gamma) {
-    if (threadIdx.x == 0) {
-      float s1 = 0.0f, s2 = 0.0f;
-      for (int j = 0; j < c; ++j) {
-        const float g = a.gamma[j];
-        const float xh = (y[j] - a.beta[j]) / (g + 1e-12f);
-        const float dout = d[j];
-        s1 = s1 + dout * g;
-        s2 = s2 + dout * g * xh;
-      }
-      stat[0] = s1 / (float)c;
-      stat[1] = s2 / (float)c;
+    // :840-860: row means of d_xhat and d_xhat * xhat
+    float s1 = 0.0f, s2 = 0.0f;
+    for (int j = threadIdx.x; j < c; j += blockDim.x) {
+      const float g = a.gamma[j];
+      const float xh = (y[j] - a.beta[j]) / (g + 1e-12f);
+      const float dout = d[j];
+      s1 = s1 + dout * g;
+      s2 = s2 + dout * g * xh;
     }
-    __syncthreads();
-    sum_d = stat[0];
-    sum_dxh = stat[1];
+    sum_d = block_sum(s1, part) / (float)c;
+    sum_dxh = block_sum(s2, part) / (float)c;
     is = a.inv_std[b];
   }
   const float* pre = a.pre + (size_t)b * c;
@@ -171,15 +203,11 @@ __global__ void __launch_bounds__(256) hidden_bwd_rows_kernel(HiddenBwdArgs a) {
     d[j] = x;
   }
   if (a.act_kind == VOLTA_ACT_SOFTMAX) {
-    // :898-906: dot(d, y) in column order, then d = y * (d - dot)
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float dot = 0.0f;
-      for (int j = 0; j < c; ++j) dot = dot + d[j] * y[j];
-      stat[2] = dot;
-    }
-    __syncthreads();
-    const float dot = stat[2];
+    // :898-906: dot(d, y), then d = y * (d - dot); every thread reads back
+    // only the columns it wrote above
+    float s = 0.0f;
+    for (int j = threadIdx.x; j < c; j += blockDim.x) s = s + d[j] * y[j];
+    const float dot = block_sum(s, part);
     for (int j = threadIdx.x; j < c; j += blockDim.x) d[j] = y[j] * (d[j] - dot);
   }
 }
@@ -254,7 +282,7 @@ hipError_t launch_hidden_bwd(const HiddenBwdArgs& a, float* gamma, float* beta, 
                              hipStream_t st) {
   const int cb = (a.c + 255) / 256;
   if (a.gamma) {
-    hipLaunchKernelGGL(ln_bwd_cols_kernel, dim3(cb), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(ln_bwd_cols_kernel, dim3((a.c + 63) / 64), dim3(256), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

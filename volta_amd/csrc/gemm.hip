@@ -1979,21 +1979,29 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus, bool 
   return p;
 }
 
-// Bias update from db[n] = sum_b delta[b][n], b ascending (:931-933), for
-// steps whose dW launches run without the fused column sums (gradient
-// clipping forms db from the deltas before they are scaled, :936-955).
+// Bias update from db[n] = sum_b delta[b][n] (:931-933), for steps whose
+// dW launches run without the fused column sums (gradient clipping forms db
+// from the deltas before they are scaled, :936-955).  A block covers 64
+// columns; wave w sums rows b = w, w + 4, ... in batch order (loads unrolled
+// eight rows deep), and the four partials are added in wave order.
 __global__ void __launch_bounds__(256) bias_update_kernel(EpiArgs e, const float* __restrict__ delta, int B, int N) {
-  const int n = blockIdx.x * blockDim.x + threadIdx.x;
-  if (n >= N) return;
+  __shared__ float part[4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int n = blockIdx.x * 64 + lane;
+  const int nn = n < N ? n : N - 1;  // loads stay in bounds; the update is guarded
   float db = 0.0f;
-  for (int b = 0; b < B; ++b) db = db + delta[(size_t)b * N + n];
-  apply_bias_update(e, n, N, db, adam_rcp_of(e));
+#pragma unroll 8
+  for (int b = w; b < B; b += 4) db = db + delta[(size_t)b * N + nn];
+  part[w][lane] = db;
+  __syncthreads();
+  if (w == 0 && n < N)
+    apply_bias_update(e, n, N, ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane], adam_rcp_of(e));
 }
 
 hipError_t launch_bias_update(const EpiArgs& e, const float* delta, int B, int N, hipStream_t st) {
   if (!e.b || !e.scalars || !delta || B < 1 || N < 1) return hipErrorInvalidValue;
   if (e.opt != VOLTA_OPT_SGD && (!e.bm || (e.opt == VOLTA_OPT_ADAM && !e.bv))) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(bias_update_kernel, dim3((N + 255) / 256), dim3(256), 0, st, e, delta, B, N);
+  hipLaunchKernelGGL(bias_update_kernel, dim3((N + 63) / 64), dim3(256), 0, st, e, delta, B, N);
   return hipGetLastError();
 }
 
