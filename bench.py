@@ -20,7 +20,10 @@ The JSON line also carries:
   cpu_baseline  the CPU oracle (C++ restatement of Volta's compile-train step,
                 OpenMP GEMMs) on this host's cores, on a bounded sample;
   runtime_optimizer  the runtime optimizer (Backend::apply_gradients path,
-                include/volta_backend.h) over C5's parameter tensors, Adam.
+                include/volta_backend.h) over C5's parameter tensors, Adam;
+  graph_execution    the runtime's inference graph of the C5 and C2 models
+                through Backend::execute_terminal (include/volta_backend.h);
+  extras_path   the codegen extras' launch structure on the C2 topology.
 """
 from __future__ import annotations
 
@@ -290,6 +293,49 @@ def run_rt_optimizer(name="c5", kind="adam", reps=20):
     return out
 
 
+def run_rt_graph(name="c5", rows=4096, reps=20):
+    """Graph execution (volta_rt_execute_terminal, Backend::execute_terminal
+    of the reference's runtime) of the inference graph the reference's
+    executor builds for a workload's model (lower_model_to_graph,
+    executor.rs:827-857) over `rows` resident input rows: one GEMM launch per
+    layer (bias + activation in the epilogue) and a synchronize per call."""
+    from volta_amd import DeviceArray
+    from volta_amd.backend import Graph, GraphLibrary, build_execution_plan, lower_model_to_graph
+
+    spec, _, _ = WORKLOADS[name]
+    lib = load_hip()
+    g = Graph()
+    x = g.add_op("input", name="input")
+    lower_model_to_graph(g, spec.sizes, spec.activation, x, True)
+    g.bind_input_shape("input", [rows, spec.sizes[0]])
+    rng = np.random.default_rng(3)
+    vals = {"input": rng.standard_normal((rows, spec.sizes[0])).astype(np.float32)}
+    for r, c in spec.shapes():
+        g.bind_parameter_shape(f"weight_{r}_{c}", [r, c])
+        g.bind_parameter_shape(f"bias_{c}", [1, c])
+        vals[f"weight_{r}_{c}"] = (rng.uniform(-1, 1, (r, c)) * np.sqrt(6.0 / r)).astype(np.float32)
+        vals[f"bias_{c}"] = np.zeros((1, c), np.float32)
+    plan = build_execution_plan(g)
+    dev = {k: DeviceArray(v, lib) for k, v in vals.items()}
+    cap = rows * spec.sizes[-1]
+    out = DeviceArray(np.zeros(cap, np.float32), lib)
+    gl = GraphLibrary(lib.lib)
+    addr = {k: d.ptr for k, d in dev.items()}
+    gl.execute(g, plan, None, addr, out.ptr, cap)  # compile + device state, warm-up
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        gl.execute(g, plan, None, addr, out.ptr, cap)
+    dt = (time.perf_counter() - t0) / reps
+    flops = sum(2.0 * rows * r * c for r, c in spec.shapes())
+    res = {"workload": name, "rows": rows, "layers": list(spec.sizes), "activation": spec.activation,
+           "ms_per_call": round(dt * 1e3, 4), "samples_per_s": round(rows / dt, 1),
+           "tflops": round(flops / dt / 1e12, 2), "frac_mfma": round(flops / dt / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
+           "note": "synchronous call (host tables, plan-cache lookup, launches, stream synchronize)"}
+    for d in list(dev.values()) + [out]:
+        d.free()
+    return res
+
+
 CPU_REF_SO = os.path.join(ROOT, "oracle", "_ref", "libvolta_cpu_ref.so")
 
 
@@ -549,6 +595,9 @@ def main():
     ap.add_argument("--secondary", default="c5", help="second workload in the same line, or 'none'")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-profile", action="store_true", help="skip the per-kernel profile")
+    ap.add_argument("--no-extra-legs", action="store_true",
+                    help="skip the runtime optimizer, graph execution and extras-path measurements (profiler runs "
+                         "whose dispatches are split into the two workloads' steps)")
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
                     or len(os.sched_getaffinity(0)), help="threads of the CPU baseline's all-cores leg")
     ap.add_argument("--graph-dispatch", choices=("nodes", "packets"), default="nodes",
@@ -616,23 +665,6 @@ def main():
     if not a.no_cpu:
         line["cpu_baseline"], line["cpu_baseline_legs"] = run_cpu(a.config, a.cpu_threads)
         line["cpu_host"] = host_cpu()
-    if not a.no_profile:
-        line["runtime_optimizer"] = run_rt_optimizer()
-        log(f"runtime optimizer: {line['runtime_optimizer']}")
-        # the extras launch structure (not paired; 3-4 more launches per
-        # hidden layer), on the headline topology
-        line["extras_path"] = []
-        for x in EXTRAS_WORKLOADS:
-            x_spec, x_B, x_lr, x_res = run_gpu(x, max(50, a.steps // 4), max(10, a.warmup // 4))
-            row = {"workload": x, "layernorm": bool(x_spec.layernorm), "dropout_p": x_spec.dropout_p,
-                   "clip_grad": x_spec.clip_grad, "optimizer": x_spec.optimizer, "batch": x_B,
-                   "ms_per_step": round(x_res["ms_per_step"], 5),
-                   "samples_per_s": round(x_res["samples_per_s"], 2), "launches": len(x_res["kernels"]),
-                   "kernel_sum_ms": round(x_res["kernel_sum_ms"], 5),
-                   "slowest": max(({"kernel": r["kernel"], "ms": round(r["ms"], 5)} for r in x_res["kernels"]),
-                                  key=lambda r: r["ms"])}
-            line["extras_path"].append(row)
-            log(f"{x}: {row['ms_per_step']:.4f} ms/step, {row['launches']} launches")
     if a.secondary and a.secondary != "none":
         s_steps = max(5, a.steps // 20)
         s_spec, s_B, s_lr, s_res = run_gpu(a.secondary, s_steps, max(2, a.warmup // 10),
@@ -652,6 +684,25 @@ def main():
         if not a.no_cpu:
             sec["cpu_baseline"], _ = run_cpu(a.secondary, a.cpu_threads, full_protocol=False)
         line["secondary"] = sec
+    if not a.no_profile and not a.no_extra_legs:
+        line["runtime_optimizer"] = run_rt_optimizer()
+        log(f"runtime optimizer: {line['runtime_optimizer']}")
+        line["graph_execution"] = [run_rt_graph("c5", 4096), run_rt_graph("c2", 64)]
+        log(f"graph execution: {line['graph_execution']}")
+        # the extras launch structure (not paired; 3-4 more launches per
+        # hidden layer), on the headline topology
+        line["extras_path"] = []
+        for x in EXTRAS_WORKLOADS:
+            x_spec, x_B, x_lr, x_res = run_gpu(x, max(50, a.steps // 4), max(10, a.warmup // 4))
+            row = {"workload": x, "layernorm": bool(x_spec.layernorm), "dropout_p": x_spec.dropout_p,
+                   "clip_grad": x_spec.clip_grad, "optimizer": x_spec.optimizer, "batch": x_B,
+                   "ms_per_step": round(x_res["ms_per_step"], 5),
+                   "samples_per_s": round(x_res["samples_per_s"], 2), "launches": len(x_res["kernels"]),
+                   "kernel_sum_ms": round(x_res["kernel_sum_ms"], 5),
+                   "slowest": max(({"kernel": r["kernel"], "ms": round(r["ms"], 5)} for r in x_res["kernels"]),
+                                  key=lambda r: r["ms"])}
+            line["extras_path"].append(row)
+            log(f"{x}: {row['ms_per_step']:.4f} ms/step, {row['launches']} launches")
     print(json.dumps(line), flush=True)
     return 0
 
