@@ -5,13 +5,13 @@
  * and top-level numeric variables; every other statement of the language
  * (print, infer, fn, if, for, loop, save, load, ...) is parsed structurally
  * and noted, not run: the reference's interpreter runs it before compiling,
- * and it does not change the generated library.  Resolves the first model declared the way
- * compile-train does (layers and activation from the model block; the
- * optimizer from the last train statement naming the model, else the
- * model's own, else SGD; autopilot rules when a train statement names
- * none, autopilot.rs:143-160) and applies the compile-train guards
- * (executor.rs:3147-3189) plus this library's limits (no dropout,
- * LayerNorm, gradient clipping or hidden softmax yet). */
+ * and it does not change the generated library.  Resolves the first model
+ * declared the way compile-train does (layers and activation from the model
+ * block; the optimizer from the last train statement naming the model, else
+ * the model's own, else SGD; autopilot rules when a train statement names
+ * none, autopilot.rs:143-160; dropout and LayerNorm from the model block and
+ * clip_grad from the last train statement that sets it) and applies the
+ * compile-train guards (executor.rs:3147-3189). */
 #ifndef VOLTA_VT_H
 #define VOLTA_VT_H
 
