@@ -159,6 +159,12 @@ struct DwGroup {
   int start[kMaxDwGroup + 1] = {};  // first workgroup of product i after the narrow ones; start[n] = total
   int narrow_blocks = 0;            // 0: no narrow dW
   NarrowDwArgs nd{};
+  // the step's loss, when the output launch deferred it (launch_out_layer_dx
+  // with defer_loss): workgroup 0 adds the partials in block order
+  const float* loss_partials = nullptr;
+  int loss_blocks = 0;
+  float loss_denom = 1.0f;
+  DevScalars* loss_scalars = nullptr;
 };
 bool dw_group_supported(const DwGroup& d);
 hipError_t dw_group_launch(const DwGroup& d, hipStream_t st, Recorder* rec, const char* label, double flops,

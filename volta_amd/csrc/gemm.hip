@@ -1830,6 +1830,8 @@ template <int NMAX>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) dw_group_kernel(DwGroup d) {
   __shared__ __attribute__((aligned(16))) float lds[kDwLds];
   int b = blockIdx.x;
+  if (b == 0 && threadIdx.x == 0 && d.loss_partials)
+    deferred_loss_finish(d.loss_scalars, d.loss_partials, d.loss_blocks, d.loss_denom);
   if (b < d.narrow_blocks) {
     narrow_dw_block<NMAX>(d.nd, b, lds);
     return;
@@ -1844,6 +1846,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) d
 
 bool dw_group_supported(const DwGroup& d) {
   if (d.n < 1 || d.n > kMaxDwGroup || d.start[0] != 0) return false;
+  if (d.loss_partials && (!d.loss_scalars || d.loss_blocks < 1 || d.loss_blocks > kOutDxMaxBlocks)) return false;
   for (int i = 0; i < d.n; ++i) {
     const GemmArgs& a = d.g[i];
     if (a.epi.kind != EPI_DW_OPT || !dw_smallk_ok(a, GEMM_TN)) return false;

@@ -201,19 +201,36 @@ __device__ __forceinline__ float out_dx_row(const OutLayerArgs& p, const float* 
 // The step's loss from the per-block partials (blocks of kOutDxRows rows,
 // all loads issued together, added in block order), then the step counter
 // and the arrival ticket reset; run by the one thread that arrived last.
-__device__ __forceinline__ void out_dx_finish(const OutLayerArgs& p, int nblocks, const StepNext& next) {
+__device__ __forceinline__ float out_dx_loss_sum(const float* partials, int nblocks) {
   float part[kOutDxMaxBlocks];
 #pragma unroll
-  for (int b = 0; b < kOutDxMaxBlocks; ++b) part[b] = p.partials[min(b, nblocks - 1)];
+  for (int b = 0; b < kOutDxMaxBlocks; ++b) part[b] = partials[min(b, nblocks - 1)];
   float total = part[0];
 #pragma unroll
   for (int b = 1; b < kOutDxMaxBlocks; ++b) {
     const float t = total + part[b];
     total = b < nblocks ? t : total;
   }
-  const float denom = p.loss == VOLTA_LOSS_MSE ? (float)(p.B * p.N) : (float)p.B;
-  step_finish(p.scalars, next, p.bc_table != nullptr, total / denom);
+  return total;
+}
+
+__device__ __forceinline__ float out_dx_loss_denom(const OutLayerArgs& p) {
+  return p.loss == VOLTA_LOSS_MSE ? (float)(p.B * p.N) : (float)p.B;
+}
+
+__device__ __forceinline__ void out_dx_finish(const OutLayerArgs& p, int nblocks, const StepNext& next) {
+  step_finish(p.scalars, next, p.bc_table != nullptr, out_dx_loss_sum(p.partials, nblocks) / out_dx_loss_denom(p));
   *p.loss_counter = 0u;
+}
+
+// The deferred form: the loss of the partials an earlier output launch
+// stored (launch_out_layer_dx with defer_loss), the same sum in block order,
+// and its non-finite flag; the step counter was advanced by that launch.
+__device__ __forceinline__ void deferred_loss_finish(DevScalars* sc, const float* partials, int nblocks,
+                                                     float denom) {
+  const float loss = out_dx_loss_sum(partials, nblocks) / denom;
+  sc->loss = loss;
+  if (!(fabsf(loss) <= 3.402823466e38f)) atomicOr(&sc->flags, (uint32_t)VOLTA_STATUS_NONFINITE_LOSS);
 }
 
 }  // namespace volta

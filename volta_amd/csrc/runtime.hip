@@ -220,6 +220,150 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
     a.counters = h->counters;
     a.epi.scalars = h->scalars;
   };
+  // Operations of the backward pass (:819-993): the grouped dW launch of a
+  // small-batch step is built from them before the forward, every other
+  // backward launch after it.
+  const int sopt = s.optimizer == VOLTA_OPT_SGD ? 2 : s.optimizer == VOLTA_OPT_ADAGRAD ? 4 : 6;
+  // dX_i as a GEMM (i > 0 and not the narrow output layer)
+  auto make_dx = [&](int i, float* ws) {
+    const LayerPlan& lp = h->layers[i];
+    PairOp o;
+    o.kind = PAIR_GEMM;
+    o.plan = lp.dx;
+    GemmArgs& a = o.args;
+    base_args(a);
+    a.partial = ws;
+    a.A = h->delta[i];
+    a.lda = lp.c;
+    a.B = h->params + lp.w_off;
+    a.ldb = lp.c;
+    a.M = B;
+    a.N = lp.r;
+    a.K = lp.c;
+    a.epi.kind = EPI_DX_ACT;
+    a.epi.act = s.activation;
+    a.epi.ldc = lp.r;
+    a.epi.out = h->delta[i - 1];
+    a.epi.aux_act = h->act[i];
+    a.epi.aux_pre = h->pre[i - 1];
+    return o;
+  };
+  // dW_i = act_i^T delta_i with db_i = column sums of delta_i and the
+  // optimizer update of W_i and b_i (GEMM epilogue, or the narrow kernel for
+  // the output layer).
+  auto make_dw = [&](int i, float* ws) {
+    const LayerPlan& lp = h->layers[i];
+    PairOp o;
+    const int opt = s.optimizer == VOLTA_OPT_ADAMW ? VOLTA_OPT_ADAM : s.optimizer;
+    const float wd = s.optimizer == VOLTA_OPT_ADAMW ? s.weight_decay : 0.0f;
+    if (i == n - 1 && h->narrow_dw) {
+      o.kind = PAIR_NARROW_DW;
+      NarrowDwArgs& d = o.nd;
+      d.act = h->act[i];
+      d.delta = h->delta[i];
+      d.B = B;
+      d.R = lp.r;
+      d.N = lp.c;
+      d.opt = opt;
+      d.w = h->params + lp.w_off;
+      d.b = h->params + lp.b_off;
+      d.m = h->opt_a ? h->opt_a + lp.w_off : nullptr;
+      d.v = h->opt_b ? h->opt_b + lp.w_off : nullptr;
+      d.bm = h->opt_a ? h->opt_a + lp.b_off : nullptr;
+      d.bv = h->opt_b ? h->opt_b + lp.b_off : nullptr;
+      d.grad = h->keep_grads ? h->grads + lp.w_off : nullptr;
+      d.bgrad = h->keep_grads ? h->grads + lp.b_off : nullptr;
+      d.wd = wd;
+      d.b1 = s.beta1;
+      d.b2 = s.beta2;
+      d.eps = s.eps;
+      d.scalars = h->scalars;
+      return o;
+    }
+    o.kind = PAIR_GEMM;
+    o.plan = lp.dw;
+    GemmArgs& a = o.args;
+    base_args(a);
+    a.partial = ws;
+    a.A = h->act[i];
+    a.lda = lp.r;
+    a.B = h->delta[i];
+    a.ldb = lp.c;
+    a.M = lp.r;
+    a.N = lp.c;
+    a.K = B;
+    a.colsum_b = 1;
+    EpiArgs& e = a.epi;
+    e.kind = EPI_DW_OPT;
+    e.ldc = lp.c;
+    e.opt = opt;
+    e.out = h->params + lp.w_off;
+    e.b = h->params + lp.b_off;
+    e.m = h->opt_a ? h->opt_a + lp.w_off : nullptr;
+    e.v = h->opt_b ? h->opt_b + lp.w_off : nullptr;
+    e.bm = h->opt_a ? h->opt_a + lp.b_off : nullptr;
+    e.bv = h->opt_b ? h->opt_b + lp.b_off : nullptr;
+    e.grad = h->keep_grads ? h->grads + lp.w_off : nullptr;
+    e.bgrad = h->keep_grads ? h->grads + lp.b_off : nullptr;
+    e.count = (int64_t)lp.r * lp.c;
+    e.wd = wd;
+    e.b1 = s.beta1;
+    e.b2 = s.beta2;
+    e.eps = s.eps;
+    return o;
+  };
+  // algorithmic figures (flops, bytes) of dX_i and dW_i:
+  //   dX: 4(B*c + r*c + 2*B*r); dW + db + optimizer: 4(B*r + B*c) + 4*s*(r*c + c)
+  //   with s = 2 (SGD), 4 (Adagrad), 6 (Adam/AdamW) beyond the gradient.
+  auto dx_cost = [&](int i) {
+    const LayerPlan& lp = h->layers[i];
+    return std::make_pair(2.0 * B * lp.r * lp.c, 4.0 * ((double)B * lp.c + (double)lp.r * lp.c + 2.0 * B * lp.r));
+  };
+  auto dw_cost = [&](int i) {
+    const LayerPlan& lp = h->layers[i];
+    return std::make_pair(2.0 * B * lp.r * lp.c,
+                          4.0 * ((double)B * lp.r + (double)B * lp.c) + 4.0 * sopt * ((double)lp.r * lp.c + lp.c));
+  };
+  // Small-batch steps run every dW in one grouped launch after the dX
+  // chain.  It is built before the forward so the output launch knows
+  // whether it may leave the step's loss sum to that launch (no arrival
+  // ticket and agent-scope fences in the output launch).
+  DwGroup group;
+  std::string group_label;
+  double group_fl = 0.0, group_by = 0.0;
+  bool group_ok = false, defer_loss = false;
+  if (h->dx_alone) {
+    for (int i = n - 1; i >= 0; --i) {
+      const PairOp o = make_dw(i, h->gemm_ws);
+      if (o.kind == PAIR_NARROW_DW) {
+        group.nd = o.nd;
+        group.narrow_blocks = (o.nd.R + kNarrowRows - 1) / kNarrowRows;
+      } else {
+        group.g[group.n] = o.args;
+        group.g[group.n].k_per_split = o.plan.k_per_split;
+        group.start[group.n + 1] = group.start[group.n] + o.plan.tiles(o.args.M, o.args.N);
+        ++group.n;
+      }
+      char lx[32];
+      std::snprintf(lx, sizeof lx, "dw%d+db+opt", i);
+      group_label += (group_label.empty() ? "" : "|") + std::string(lx);
+      group_fl += dw_cost(i).first;
+      group_by += dw_cost(i).second;
+    }
+    defer_loss = h->dw_group && h->out_mode == OUT_NARROW && h->out_dx_merged && !h->fwd_head;
+    if (defer_loss) {
+      group.loss_partials = h->loss_partials;
+      group.loss_blocks = out_layer_dx_blocks(B);
+      group.loss_denom = s.loss == VOLTA_LOSS_MSE ? (float)(B * Ln) : (float)B;
+      group.loss_scalars = h->scalars;
+    }
+    group_ok = h->dw_group && dw_group_supported(group);
+    if (!group_ok && defer_loss) {
+      defer_loss = false;
+      group.loss_partials = nullptr;
+      group_ok = h->dw_group && dw_group_supported(group);
+    }
+  }
   // The narrow output layer's arguments (layer n-1), with its dX_{n-1}
   // fields when that is formed in the same launch.
   auto out_args = [&]() {
@@ -245,6 +389,7 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
       o.dx_pre = h->pre[n - 2];
       o.dx_out = h->delta[n - 2];
       o.loss_counter = h->counters + h->n_counters - 1;
+      o.defer_loss = defer_loss ? 1 : 0;
     }
     return o;
   };
@@ -350,107 +495,6 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
   // optimizer state), and each pair runs after the launch that produced its
   // inputs (delta_i from dX_{i+1}, delta_{i+1} from dX_{i+2}).  A pair the
   // paired kernel does not cover runs as two launches in the same order.
-  const int sopt = s.optimizer == VOLTA_OPT_SGD ? 2 : s.optimizer == VOLTA_OPT_ADAGRAD ? 4 : 6;
-  // dX_i as a GEMM (i > 0 and not the narrow output layer)
-  auto make_dx = [&](int i, float* ws) {
-    const LayerPlan& lp = h->layers[i];
-    PairOp o;
-    o.kind = PAIR_GEMM;
-    o.plan = lp.dx;
-    GemmArgs& a = o.args;
-    base_args(a);
-    a.partial = ws;
-    a.A = h->delta[i];
-    a.lda = lp.c;
-    a.B = h->params + lp.w_off;
-    a.ldb = lp.c;
-    a.M = B;
-    a.N = lp.r;
-    a.K = lp.c;
-    a.epi.kind = EPI_DX_ACT;
-    a.epi.act = s.activation;
-    a.epi.ldc = lp.r;
-    a.epi.out = h->delta[i - 1];
-    a.epi.aux_act = h->act[i];
-    a.epi.aux_pre = h->pre[i - 1];
-    return o;
-  };
-  // dW_i = act_i^T delta_i with db_i = column sums of delta_i and the
-  // optimizer update of W_i and b_i (GEMM epilogue, or the narrow kernel for
-  // the output layer).
-  auto make_dw = [&](int i, float* ws) {
-    const LayerPlan& lp = h->layers[i];
-    PairOp o;
-    const int opt = s.optimizer == VOLTA_OPT_ADAMW ? VOLTA_OPT_ADAM : s.optimizer;
-    const float wd = s.optimizer == VOLTA_OPT_ADAMW ? s.weight_decay : 0.0f;
-    if (i == n - 1 && h->narrow_dw) {
-      o.kind = PAIR_NARROW_DW;
-      NarrowDwArgs& d = o.nd;
-      d.act = h->act[i];
-      d.delta = h->delta[i];
-      d.B = B;
-      d.R = lp.r;
-      d.N = lp.c;
-      d.opt = opt;
-      d.w = h->params + lp.w_off;
-      d.b = h->params + lp.b_off;
-      d.m = h->opt_a ? h->opt_a + lp.w_off : nullptr;
-      d.v = h->opt_b ? h->opt_b + lp.w_off : nullptr;
-      d.bm = h->opt_a ? h->opt_a + lp.b_off : nullptr;
-      d.bv = h->opt_b ? h->opt_b + lp.b_off : nullptr;
-      d.grad = h->keep_grads ? h->grads + lp.w_off : nullptr;
-      d.bgrad = h->keep_grads ? h->grads + lp.b_off : nullptr;
-      d.wd = wd;
-      d.b1 = s.beta1;
-      d.b2 = s.beta2;
-      d.eps = s.eps;
-      d.scalars = h->scalars;
-      return o;
-    }
-    o.kind = PAIR_GEMM;
-    o.plan = lp.dw;
-    GemmArgs& a = o.args;
-    base_args(a);
-    a.partial = ws;
-    a.A = h->act[i];
-    a.lda = lp.r;
-    a.B = h->delta[i];
-    a.ldb = lp.c;
-    a.M = lp.r;
-    a.N = lp.c;
-    a.K = B;
-    a.colsum_b = 1;
-    EpiArgs& e = a.epi;
-    e.kind = EPI_DW_OPT;
-    e.ldc = lp.c;
-    e.opt = opt;
-    e.out = h->params + lp.w_off;
-    e.b = h->params + lp.b_off;
-    e.m = h->opt_a ? h->opt_a + lp.w_off : nullptr;
-    e.v = h->opt_b ? h->opt_b + lp.w_off : nullptr;
-    e.bm = h->opt_a ? h->opt_a + lp.b_off : nullptr;
-    e.bv = h->opt_b ? h->opt_b + lp.b_off : nullptr;
-    e.grad = h->keep_grads ? h->grads + lp.w_off : nullptr;
-    e.bgrad = h->keep_grads ? h->grads + lp.b_off : nullptr;
-    e.count = (int64_t)lp.r * lp.c;
-    e.wd = wd;
-    e.b1 = s.beta1;
-    e.b2 = s.beta2;
-    e.eps = s.eps;
-    return o;
-  };
-  // algorithmic figures (flops, bytes) of dX_i and dW_i:
-  //   dX: 4(B*c + r*c + 2*B*r); dW + db + optimizer: 4(B*r + B*c) + 4*s*(r*c + c)
-  //   with s = 2 (SGD), 4 (Adagrad), 6 (Adam/AdamW) beyond the gradient.
-  auto dx_cost = [&](int i) {
-    const LayerPlan& lp = h->layers[i];
-    return std::make_pair(2.0 * B * lp.r * lp.c, 4.0 * ((double)B * lp.c + (double)lp.r * lp.c + 2.0 * B * lp.r));
-  };
-  auto dw_cost = [&](int i) {
-    const LayerPlan& lp = h->layers[i];
-    return std::make_pair(2.0 * B * lp.r * lp.c,
-                          4.0 * ((double)B * lp.r + (double)B * lp.c) + 4.0 * sopt * ((double)lp.r * lp.c + lp.c));
-  };
   auto run_single = [&](const PairOp& o, const char* lbl, std::pair<double, double> cost) -> bool {
     if (o.kind == PAIR_NARROW_DW) {
       VOLTA_CHECK(launch_narrow_dw(o.nd, st));
@@ -581,27 +625,8 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
       std::snprintf(lx, sizeof lx, "dx%d", i);
       if (!run_single(make_dx(i, ws0), lx, dx_cost(i))) return false;
     }
-    DwGroup d;
-    std::string lab;
-    double fl = 0.0, by = 0.0;
-    for (int i = n - 1; i >= 0; --i) {
-      const PairOp o = make_dw(i, ws0);
-      if (o.kind == PAIR_NARROW_DW) {
-        d.nd = o.nd;
-        d.narrow_blocks = (o.nd.R + kNarrowRows - 1) / kNarrowRows;
-      } else {
-        d.g[d.n] = o.args;
-        d.g[d.n].k_per_split = o.plan.k_per_split;
-        d.start[d.n + 1] = d.start[d.n] + o.plan.tiles(o.args.M, o.args.N);
-        ++d.n;
-      }
-      std::snprintf(lx, sizeof lx, "dw%d+db+opt", i);
-      lab += (lab.empty() ? "" : "|") + std::string(lx);
-      fl += dw_cost(i).first;
-      by += dw_cost(i).second;
-    }
-    if (h->dw_group && dw_group_supported(d)) {
-      VOLTA_CHECK(dw_group_launch(d, st, rec, lab.c_str(), fl, by));
+    if (group_ok) {
+      VOLTA_CHECK(dw_group_launch(group, st, rec, group_label.c_str(), group_fl, group_by));
       return true;
     }
     // one launch each (VOLTA_NO_PAIR, or a narrow dW whose staged deltas

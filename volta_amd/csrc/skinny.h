@@ -28,6 +28,10 @@ struct OutLayerArgs {
   const float* dx_pre;      // its pre-activation [B x K] (null when not kept)
   float* dx_out;            // delta_{n-2} [B x K]
   unsigned* loss_counter;   // arrival ticket of the blocks (zero between launches)
+  // launch_out_layer_dx only: 1 = leave the loss sum to a later launch (the
+  // dW group of the step): the blocks only store their partials, block 0
+  // advances the step counter, and no arrival ticket is taken
+  int defer_loss;
 };
 
 struct NarrowDwArgs {

@@ -148,9 +148,10 @@ __global__ void __launch_bounds__(kOutDxRows * 64) out_layer_dx_kernel(OutLayerA
     __syncthreads();
   }
   // the next step counter and its bias corrections, in case this block
-  // finishes last (nothing else in the launch writes them)
+  // finishes last (nothing else in the launch writes them); with the loss
+  // deferred, block 0 alone reads and advances the counter
   StepNext next{};
-  if (threadIdx.x == 0) next = step_prefetch(p.scalars, p.bc_table, p.bc_len);
+  if (threadIdx.x == 0 && (!p.defer_loss || blockIdx.x == 0)) next = step_prefetch(p.scalars, p.bc_table, p.bc_len);
   const float row_loss = out_dx_row<NMAX, WL>(p, w_lds, blockIdx.x * kOutDxRows + wave);
   if (lane == 0) wave_loss[wave] = row_loss;
   __syncthreads();
@@ -158,6 +159,16 @@ __global__ void __launch_bounds__(kOutDxRows * 64) out_layer_dx_kernel(OutLayerA
     float sb = wave_loss[0];
     for (int w = 1; w < kOutDxRows; ++w) sb = sb + wave_loss[w];
     p.partials[blockIdx.x] = sb;
+    if (p.defer_loss) {
+      // a later launch of the step adds the partials (deferred_loss_finish):
+      // no agent-scope fence or ticket here
+      if (blockIdx.x == 0 && p.bc_table) {
+        p.scalars->t = next.t;
+        p.scalars->bc1 = next.bc.x;
+        p.scalars->bc2 = next.bc.y;
+      }
+      return;
+    }
     __threadfence();
     last_block = atomicAdd(p.loss_counter, 1u) == gridDim.x - 1 ? 1u : 0u;
     if (last_block) {
@@ -175,7 +186,7 @@ bool out_layer_dx_supported(int B, int K, int N) {
 }
 
 hipError_t launch_out_layer_dx(const OutLayerArgs& p, hipStream_t st) {
-  if (!out_layer_dx_supported(p.B, p.K, p.N) || !p.partials || !p.loss_counter || !p.dx_out)
+  if (!out_layer_dx_supported(p.B, p.K, p.N) || !p.partials || (!p.loss_counter && !p.defer_loss) || !p.dx_out)
     return hipErrorInvalidValue;
   const dim3 grid(out_layer_dx_blocks(p.B)), block(kOutDxRows * 64);
   const bool wl = p.N > 1;
