@@ -34,7 +34,7 @@ __global__ void __launch_bounds__(1024) out_layer_kernel(OutLayerArgs p, int row
   // rows per group and k per lane per chunk, sized to stay within the 128
   // registers a 1024-thread block allows
   constexpr int RG = NMAX >= 16 ? 1 : 4;
-  constexpr int C = NMAX >= 16 ? (WL ? 4 : 2) : 4;
+  constexpr int C = NMAX >= 16 ? (WL ? 16 : 2) : 4;
   __shared__ float wave_loss[16];
   extern __shared__ float w_lds[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -102,11 +102,19 @@ __global__ void __launch_bounds__(1024) out_layer_kernel(OutLayerArgs p, int row
   }
 }
 
-// Sum the per-block losses in block order and finish the step's loss.
+// Sum the per-block losses in block order and finish the step's loss.  The
+// wave loads every partial at once (lane l: blocks l, l + 64, ...) into LDS,
+// then lane 0 adds them in block order.
+constexpr int kLossFinishMax = 4096;
 __global__ void __launch_bounds__(64) loss_finish_kernel(OutLayerArgs p, int blocks) {
+  __shared__ float part[kLossFinishMax];
+  const bool staged = blocks <= kLossFinishMax;
+  if (staged)
+    for (int b = threadIdx.x; b < blocks; b += 64) part[b] = p.partials[b];
+  __syncthreads();
   if (threadIdx.x != 0) return;
-  float s = p.partials[0];
-  for (int b = 1; b < blocks; ++b) s = s + p.partials[b];
+  float s = staged ? part[0] : p.partials[0];
+  for (int b = 1; b < blocks; ++b) s = s + (staged ? part[b] : p.partials[b]);
   const float denom = p.loss == VOLTA_LOSS_MSE ? (float)(p.B * p.N) : (float)p.B;
   step_epilogue(p.scalars, p.bc_table, p.bc_len, s / denom);
 }
