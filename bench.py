@@ -584,7 +584,7 @@ def trace_summary(trace_csv, bench_json):
     return 0
 
 
-def main():
+def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     # 2000 C2 steps = 0.12 s timed after 12 ms of warm-up: shorter runs of the
@@ -610,7 +610,7 @@ def main():
                     help="only print HBM bytes per launch from rocprofv3 counter passes (no GPU)")
     ap.add_argument("--trace-summary", nargs=2, metavar=("TRACE_CSV", "BENCH_JSON"),
                     help="only print per-launch durations from a rocprofv3 kernel trace of a bench run (no GPU)")
-    a = ap.parse_args()
+    a = ap.parse_args(argv)
     if a.traffic_table:
         return traffic_table(*a.traffic_table)
     if a.trace_summary:
