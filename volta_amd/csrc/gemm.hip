@@ -1278,16 +1278,16 @@ __device__ __forceinline__ void dw_smallk_tile(const GemmArgs& args, int blk, fl
     store_slice();
     __syncthreads();
     if (do_db && tid < kDwT) {
-      // batch order; each batch of 16 reads is issued before its first add
-      // (16 registers, not the slice's 64: the kernel's occupancy)
+      // batch order; each batch of 8 reads is issued before its first add
+      // (8 registers, not the slice's 64: the kernel's occupancy)
       const int kn = min(kDwK, K - k0);
 #pragma unroll
-      for (int k1 = 0; k1 < kDwK; k1 += 16) {
-        float col[16];
+      for (int k1 = 0; k1 < kDwK; k1 += 8) {
+        float col[8];
 #pragma unroll
-        for (int kk = 0; kk < 16; ++kk) col[kk] = lb[(k1 + kk) * kDwS + tid];
+        for (int kk = 0; kk < 8; ++kk) col[kk] = lb[(k1 + kk) * kDwS + tid];
 #pragma unroll
-        for (int kk = 0; kk < 16; ++kk) {
+        for (int kk = 0; kk < 8; ++kk) {
           const float t = db + col[kk];
           db = k1 + kk < kn ? t : db;
         }
@@ -1833,7 +1833,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) d
   if (b == 0 && threadIdx.x == 0 && d.loss_partials)
     deferred_loss_finish(d.loss_scalars, d.loss_partials, d.loss_blocks, d.loss_denom);
   if (b < d.narrow_blocks) {
-    narrow_dw_block<NMAX>(d.nd, b, lds);
+    narrow_dw_block<NMAX, true>(d.nd, b, lds);
     return;
   }
   b -= d.narrow_blocks;

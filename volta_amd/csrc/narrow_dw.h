@@ -44,11 +44,19 @@ __host__ __device__ inline int narrow_lds_floats_n(int B, int N) {
 // (16 a thread for each of up to four 64-row chunks a round) and wave 0's
 // optimizer state; the staged deltas are read from LDS in batches before
 // the multiplies, and guards are selects.
-template <int NMAX>
+// KU (64-row chunks whose loads one round issues together), SB (deltas a
+// thread holds while staging them), DBC (the bias column's reads issued
+// before their adds) and the batch of staged deltas read before the
+// multiplies trade registers for memory latency: the stand-alone launches
+// keep the widest settings; the grouped dW launch, whose small-K tiles share
+// its register budget, takes the narrow ones (LEAN).
+template <int NMAX, bool LEAN = false>
 __device__ __forceinline__ void narrow_dw_block(const NarrowDwArgs& p, int block, float* lds) {
   constexpr int kQ = 16;  // batch rows per wave per 64-row chunk
-  constexpr int kU = 4;   // 64-row chunks whose loads one round issues together
-  constexpr int kDBatch = NMAX == 1 ? 16 : NMAX <= 4 ? 8 : 2;  // batch rows per LDS read batch
+  constexpr int kU = LEAN ? 1 : 4;  // 64-row chunks whose loads one round issues together
+  constexpr int kSB = LEAN ? 4 : kNarrowStage;  // deltas per staging batch
+  constexpr int kDBatch = LEAN ? (NMAX == 1 ? 8 : NMAX <= 4 ? 4 : 2)
+                               : (NMAX == 1 ? 16 : NMAX <= 4 ? 8 : 2);  // batch rows per LDS read batch
   const int B = p.B, N = p.N, R = p.R;
   const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
   const int j = block * kNarrowRows + lane;
@@ -58,13 +66,24 @@ __device__ __forceinline__ void narrow_dw_block(const NarrowDwArgs& p, int block
   const int BN = B * N;
   float* sdelta = lds;
   float* part = lds + (BN + 3) / 4 * 4;  // part[(q*NMAX + k)*64 + lane]
-  // staged deltas: at most kNarrowStage per thread (B <= kNarrowMaxB, N <= 16)
-  float dst[kNarrowStage];
+  // staged deltas: at most kNarrowStage per thread (B <= kNarrowMaxB, N <=
+  // 16), kSB at a time; the first batch's loads go before the activations'
+  float dst[kSB];
+  auto stage_load = [&](int i0) {
 #pragma unroll
-  for (int i = 0; i < kNarrowStage; ++i) {
-    if (i * kNarrowThreads >= BN) break;  // block-uniform
-    dst[i] = p.delta[min(tid + i * kNarrowThreads, BN - 1)];
-  }
+    for (int i = 0; i < kSB; ++i) {
+      if ((i0 + i) * kNarrowThreads >= BN) break;  // block-uniform
+      dst[i] = p.delta[min(tid + (i0 + i) * kNarrowThreads, BN - 1)];
+    }
+  };
+  auto stage_store = [&](int i0) {
+#pragma unroll
+    for (int i = 0; i < kSB; ++i) {
+      if ((i0 + i) * kNarrowThreads >= BN) break;
+      if (tid + (i0 + i) * kNarrowThreads < BN) sdelta[tid + (i0 + i) * kNarrowThreads] = dst[i];
+    }
+  };
+  stage_load(0);
   // activations of a round: chunk u holds batch rows b0 + 64u + 16q + c
   float a[kU][kQ];
   auto load_round = [&](int b0) {
@@ -95,10 +114,10 @@ __device__ __forceinline__ void narrow_dw_block(const NarrowDwArgs& p, int block
   const float bs2 = (adam && p.b ? p.bv : pb)[kb];
   const float lr = p.scalars->lr;
   const AdamRcp rc = adam_rcp(p.scalars->bc1, p.scalars->bc2);
-#pragma unroll
-  for (int i = 0; i < kNarrowStage; ++i) {
-    if (i * kNarrowThreads >= BN) break;
-    if (tid + i * kNarrowThreads < BN) sdelta[tid + i * kNarrowThreads] = dst[i];
+  stage_store(0);
+  for (int i0 = kSB; i0 < kNarrowStage && i0 * kNarrowThreads < BN; i0 += kSB) {
+    stage_load(i0);
+    stage_store(i0);
   }
   __syncthreads();
 
@@ -169,7 +188,7 @@ __device__ __forceinline__ void narrow_dw_block(const NarrowDwArgs& p, int block
     const int k = threadIdx.x;
     // four interleaved accumulators; each chunk's reads are issued before
     // its first add
-    constexpr int kDbChunk = 64;
+    constexpr int kDbChunk = LEAN ? 16 : 64;
     float dba[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int b0 = 0; b0 < B; b0 += kDbChunk) {
       float d[kDbChunk];
