@@ -5,7 +5,8 @@
 //   inverted dropout with masks from the reference's LCG (:774-788,
 //   :888-892) -- every element's draw is found by jumping the LCG ahead, so
 //   the mask does not depend on the launch shape;
-//   gradient clipping by the global norm of the deltas (:936-955).
+//   gradient clipping by the global norm of the deltas (:936-955): partial
+//   sums of squares, then one pass that forms the factor and scales.
 // Row statistics (the softmax maximum and sum, LayerNorm mean/variance, the
 // backward's row means and the softmax dot product) are block reductions
 // over one row per 256-thread block: each thread folds its column-strided
@@ -251,17 +252,20 @@ __global__ void __launch_bounds__(256) clip_partials_kernel(ClipArgs a) {
   if (threadIdx.x == 0) a.partials[blockIdx.x] = wave_part[0] + wave_part[1] + wave_part[2] + wave_part[3];
 }
 
-__global__ void clip_finish_kernel(ClipArgs a) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  float gsq = 0.0f;
-  for (int k = 0; k < kClipBlocks; ++k) gsq = gsq + a.partials[k];
-  const float gnorm = sqrtf(gsq);
-  a.scalars->clip_scale = gnorm > a.clip ? a.clip / gnorm : 1.0f;
-}
-
-// delta *= scale for every layer (x * 1.0f is x, so no test of scale < 1).
+// The clip factor from the partial sums of squares (every block forms the
+// same sum: one partial per thread, a fixed butterfly per wave, the four
+// waves in order; block 0 records it), then delta *= scale for every layer
+// (x * 1.0f is x, so no test of scale < 1).
+static_assert(kClipBlocks == 256, "one partial per thread of the apply block");
 __global__ void __launch_bounds__(256) clip_apply_kernel(ClipArgs a) {
-  const float scale = a.scalars->clip_scale;
+  __shared__ float wave_part[4];
+  float v = wave_sum(a.partials[threadIdx.x]);
+  if ((threadIdx.x & 63) == 0) wave_part[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float gsq = ((wave_part[0] + wave_part[1]) + wave_part[2]) + wave_part[3];
+  const float gnorm = sqrtf(gsq);
+  const float scale = gnorm > a.clip ? a.clip / gnorm : 1.0f;
+  if (blockIdx.x == 0 && threadIdx.x == 0) a.scalars->clip_scale = scale;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int i = 0; i < a.n; ++i) {
     float* d = a.delta[i];
@@ -307,9 +311,6 @@ hipError_t launch_clip(const ClipArgs& a, hipStream_t st) {
   }
   hipLaunchKernelGGL(clip_partials_kernel, dim3(kClipBlocks), dim3(256), 0, st, a);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(clip_finish_kernel, dim3(1), dim3(64), 0, st, a);
-  e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int blocks = (int)std::min<int64_t>((total + 255) / 256, 2048);
   hipLaunchKernelGGL(clip_apply_kernel, dim3(blocks), dim3(256), 0, st, a);
