@@ -115,6 +115,7 @@ struct Handle {
   float* scratch = nullptr;    // this device's static scratch (allocation-free inference)
   bool dx_alone = false;       // small-batch backward: dX launches alone, dW products grouped
   bool dw_group = false;       // ... in one launch (off with VOLTA_NO_PAIR)
+  bool ext_dw_group = false;   // codegen extras: phase 2's dW products in one launch likewise
   size_t infer_ws_floats = 0;
   SegTable segs{};
   std::vector<LayerPlan> layers;
@@ -592,15 +593,44 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
       for (int i = 0; i < n; ++i) cnt += (double)B * h->L[i + 1];
       VOLTA_CHECK(mark(rec, "clip", 3.0 * cnt, 12.0 * cnt));
     }
-    for (int i = n - 1; i >= 0; --i) {
+    // phase 2: every dW (W only when clipping: b_i took its update above)
+    auto ext_dw = [&](int i) {
       PairOp o = make_dw(i, ws0);
       if (h->ext_clip) {
         o.args.colsum_b = 0;
         o.args.epi.b = nullptr;
         o.nd.b = nullptr;
       }
+      return o;
+    };
+    if (h->ext_dw_group) {
+      DwGroup d;
+      std::string lab;
+      double fl = 0.0, by = 0.0;
+      for (int i = n - 1; i >= 0; --i) {
+        const PairOp o = ext_dw(i);
+        if (o.kind == PAIR_NARROW_DW) {
+          d.nd = o.nd;
+          d.narrow_blocks = (o.nd.R + kNarrowRows - 1) / kNarrowRows;
+        } else {
+          d.g[d.n] = o.args;
+          d.g[d.n].k_per_split = o.plan.k_per_split;
+          d.start[d.n + 1] = d.start[d.n] + o.plan.tiles(o.args.M, o.args.N);
+          ++d.n;
+        }
+        std::snprintf(lx, sizeof lx, h->ext_clip ? "dw%d+opt" : "dw%d+db+opt", i);
+        lab += (lab.empty() ? "" : "|") + std::string(lx);
+        fl += dw_cost(i).first;
+        by += dw_cost(i).second;
+      }
+      if (dw_group_supported(d)) {
+        VOLTA_CHECK(dw_group_launch(d, st, rec, lab.c_str(), fl, by));
+        return true;
+      }
+    }
+    for (int i = n - 1; i >= 0; --i) {
       std::snprintf(lx, sizeof lx, h->ext_clip ? "dw%d+opt" : "dw%d+db+opt", i);
-      if (!run_single(o, lx, dw_cost(i))) return false;
+      if (!run_single(ext_dw(i), lx, dw_cost(i))) return false;
     }
     return true;
   }
@@ -813,15 +843,18 @@ static bool build(Handle* h) {
   // count, and the dW products share one launch after them (VOLTA_NO_PAIR:
   // one launch each, same plans, same bits).
   int n_small = 0;
-  bool all_small = !h->extras() && n >= 2;
+  bool all_small = n >= 2;
   for (int i = 0; i < n; ++i) {
     if (i == n - 1 && h->narrow_dw) continue;
     all_small = all_small && h->layers[i].dw.tile == TILE_DW_SMALLK;
     ++n_small;
   }
-  h->dx_alone = all_small && n_small <= kMaxDwGroup;
+  h->dx_alone = !h->extras() && all_small && n_small <= kMaxDwGroup;
   h->dw_group = h->dx_alone && h->pair_backward;
-  if (h->dx_alone)
+  // The extras step runs its dX products alone anyway and its dW products
+  // after every delta: those share one launch under the same conditions.
+  h->ext_dw_group = h->extras() && all_small && n_small <= kMaxDwGroup && !(np && *np && *np != '0');
+  if (h->dx_alone || h->ext_dw_group)
     for (int i = 1; i < n; ++i) {
       LayerPlan& lp = h->layers[i];
       if (lp.dx.tile == TILE_SMALLM) lp.dx.waves = gemm_smallm_waves(false, B, lp.r, h->num_cus);
