@@ -128,11 +128,13 @@ __global__ void __launch_bounds__(64) loss_finish_kernel(OutLayerArgs p, int blo
 //                                    for the lane's k = lane + 64c (j ascending,
 //                                    outer_dx_kernel's order)
 // Everything but the loss is row-local.  The block's row losses are added in
-// row order into partials[b]; the last block to finish (integer ticket)
-// adds the partials in block order and records the step's loss, the
-// non-finite flag and the Adam step counter (step_epilogue).  A separate
-// one-block output launch plus the outer-product dX launch cost more: one
-// CU for 64 rows, and a dependent launch between them.
+// row order into partials[b].  With defer_loss (the small-batch step, whose
+// grouped dW launch adds the partials later) block 0 only advances the Adam
+// step counter; otherwise the last block to finish (integer ticket, an
+// agent-scope release and acquire) adds the partials in block order and
+// records the step's loss, the non-finite flag and the step counter.  A
+// separate one-block output launch plus the outer-product dX launch cost
+// more: one CU for 64 rows, and a dependent launch between them.
 
 template <int NMAX, bool WL>
 __global__ void __launch_bounds__(kOutDxRows * 64) out_layer_dx_kernel(OutLayerArgs p) {
