@@ -435,6 +435,9 @@ NARROW_HEAD_CASES = {
     "w_lds_b37": (MlpSpec([96, 256, 1], "tanh", "sgd"), 37, 0.01),
     # staged W, width 10, more than one output-layer block (B > 256)
     "w_lds_b300": (MlpSpec([64, 128, 10], "silu", "sgd", "ce"), 300, 0.05),
+    # the small-batch structure with CE: dX alone, every dW (the narrow one
+    # of width 10 too) in one grouped launch, the loss summed by that launch
+    "grouped_ce_b64": (MlpSpec([64, 128, 64, 10], "relu", "sgd", "ce"), 64, 0.05),
 }
 
 
@@ -453,6 +456,49 @@ def test_narrow_output_layer_paths(name):
     ok, mx, _ = close_enough(lh, lo)
     assert ok, f"{name}: losses differ, max abs {mx:.3e}"
     assert_params_close(wh, bh, wo, bo, name)
+
+
+def test_deferred_loss_and_step_counter():
+    """In the small-batch structure the output launch leaves the loss sum to
+    the grouped dW launch and only advances the Adam step counter: after k
+    steps the counter reads k, and every step's loss equals the separate
+    launches' (VOLTA_NO_PAIR=1, where the output launch sums the loss itself
+    under its arrival ticket) bit for bit, and the oracle's first-step loss
+    within rel 1e-4."""
+    spec, B = MlpSpec([64, 96, 48, 4], "relu", "adam"), 64
+    say(f"deferred loss: {spec.text()} B={B}")
+    ws, bs, batches = config_inputs(spec, B, seed=8)
+    X, Y = batches[0]
+
+    def run(env):
+        old = {k: os.environ.get(k) for k in env}
+        os.environ.update(env)
+        try:
+            t = Trainer(load_hip(), spec, B)
+        finally:
+            for k, v in old.items():
+                if v is None:
+                    os.environ.pop(k, None)
+                else:
+                    os.environ[k] = v
+        t.set_all_params(ws, bs)
+        losses = []
+        for _ in range(5):
+            t.step(X, Y, 1e-3)
+            losses.append(t.loss())
+        _, step = t.get_state()
+        st = t.status()
+        t.close()
+        return np.array(losses, np.float32), step, st
+
+    grouped, step, st = run({})
+    separate, step2, st2 = run({"VOLTA_NO_PAIR": "1"})
+    assert st == 0 and st2 == 0
+    assert step == 5 and step2 == 5
+    np.testing.assert_array_equal(grouped, separate)
+    lo, _, _, _ = run_steps(load_oracle(), spec, B, ws, bs, batches, 1e-3, 1)
+    ok, mx, _ = close_enough(grouped[:1], lo)
+    assert ok, f"first-step loss {grouped[0]} vs oracle {lo[0]}"
 
 
 def _flat_f64(lib, t, spec):
