@@ -157,6 +157,29 @@ def test_gemm_big_tile_integer_exact(layout, M, N, K):
 
 
 @pytest.mark.parametrize("layout", [0, 1, 2], ids=["NN", "NT", "TN"])
+def test_gemm_big_tile_unaligned_output(layout):
+    """An output 4 bytes past a 16-byte boundary: the epilogue takes its
+    4-byte stores (the MN-contiguous B operands' interleaved columns included)
+    and writes the same bits as into an aligned output."""
+    M, N, K = 512, 512, 256
+    say(f"gemm big tile unaligned output layout={layout}")
+    rng = np.random.default_rng(23 + layout)
+    A = rng.standard_normal((K, M) if layout == 2 else (M, K)).astype(np.float32)
+    B = rng.standard_normal((N, K) if layout == 1 else (K, N)).astype(np.float32)
+    aligned = _gemm(layout, A, B, M, N, K, tile=TILE_BIG)
+    lib = load_hip()
+    dA, dB = DeviceArray(A), DeviceArray(B)
+    dC = DeviceArray(np.zeros(M * N + 1, np.float32))
+    rc = lib.lib.volta_hip_gemm(layout, dA.ptr, dB.ptr, dC.ptr + 4, M, N, K, TILE_BIG, 0)
+    assert rc == 0, lib.last_error()
+    got = dC.numpy()
+    for d in (dA, dB, dC):
+        d.free()
+    assert got[0] == 0.0
+    np.testing.assert_array_equal(got[1:].reshape(M, N), aligned)
+
+
+@pytest.mark.parametrize("layout", [0, 1, 2], ids=["NN", "NT", "TN"])
 def test_gemm_big_tile_float_bound(layout):
     """Random fp32 operands at a C5-like shape: within 2 K eps |A||B| of the
     float64 product."""

@@ -304,6 +304,106 @@ __device__ __forceinline__ void block_epilogue(const EpiArgs& e, const floatx16&
   }
 }
 
+// Four consecutive floats: one 16-byte access when V4 (the caller checked
+// the alignment), else four 4-byte ones.
+template <bool V4>
+__device__ __forceinline__ floatx4 load4(const float* p) {
+  if constexpr (V4) return *reinterpret_cast<const floatx4*>(p);
+  else return floatx4{p[0], p[1], p[2], p[3]};
+}
+template <bool V4>
+__device__ __forceinline__ void store4(float* p, const floatx4& x) {
+  if constexpr (V4) {
+    *reinterpret_cast<floatx4*>(p) = x;
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) p[q] = x[q];
+  }
+}
+
+// Epilogue of four 32x32 blocks j = 0..3 whose columns interleave: block j's
+// column of the lane is n4 + j, so the lane holds four consecutive columns of
+// each of its 16 rows m_base + 8*(v/4) + (v%4) (the 256x256 tile with an
+// MN-contiguous B operand; exact tiles, every row and column in range).
+// Rows go four at a time, every load of a group issued before its stores,
+// with 16-byte accesses when V4 -- the same per-element arithmetic as
+// block_epilogue.
+template <int EPI, bool V4>
+__device__ __forceinline__ void quad_epilogue(const EpiArgs& e, const floatx16& a0, const floatx16& a1,
+                                              const floatx16& a2, const floatx16& a3, int m_base, int n4) {
+  static_assert(EPI == EPI_STORE || EPI == EPI_BIAS_ACT || EPI == EPI_DW_OPT, "no interleaved form");
+  const uint32_t ldc = (uint32_t)e.ldc;
+  auto off = [&](int v) { return (uint32_t)(m_base + 8 * (v >> 2) + (v & 3)) * ldc + (uint32_t)n4; };
+  auto val = [&](int v) { return floatx4{a0[v], a1[v], a2[v], a3[v]}; };
+  if constexpr (EPI == EPI_STORE) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) store4<V4>(e.out + off(v), val(v));
+  } else if constexpr (EPI == EPI_BIAS_ACT) {
+    const floatx4 b = load4<V4>(e.bias + n4);
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      floatx4 x = val(v), y;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        x[q] = x[q] + b[q];  // pre = act_i W_i + b_i (:716-724)
+        y[q] = act_forward(e.act, x[q]);  // act_{i+1} = f(pre) (:725-743)
+      }
+      if (e.pre) store4<V4>(e.pre + off(v), x);
+      store4<V4>(e.out + off(v), y);
+    }
+  } else {
+    const float lr = e.scalars->lr;
+    const bool has1 = e.opt != VOLTA_OPT_SGD, has2 = e.opt == VOLTA_OPT_ADAM || e.opt == VOLTA_OPT_ADAMW;
+    const AdamRcp rc = has2 ? adam_rcp(e.scalars->bc1, e.scalars->bc2) : AdamRcp{};
+    const uint32_t vec_end = (uint32_t)(e.count - e.count % 8);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      floatx4 w[4], s1[4], s2[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint32_t o = off(4 * r + t);
+        w[t] = load4<V4>(e.out + o);
+        s1[t] = has1 ? load4<V4>(e.m + o) : floatx4{};
+        s2[t] = has2 ? load4<V4>(e.v + o) : floatx4{};
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int v = 4 * r + t;
+        const uint32_t o = off(v);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float g = val(v)[q];
+          if (e.opt == VOLTA_OPT_SGD) {
+            w[t][q] = w[t][q] + (-lr) * g;  // sgd_fused_tn: W = 1*W + (-lr) * (act_i^T delta_i)  (:321-324)
+          } else if (e.opt == VOLTA_OPT_ADAGRAD) {
+            float a = w[t][q], b = s1[t][q];
+            adagrad_elem(&a, &b, g, lr, e.eps);
+            w[t][q] = a, s1[t][q] = b;
+          } else {
+            float a = w[t][q], b = s1[t][q], c = s2[t][q];
+            adam_elem(&a, &b, &c, g, o + q >= vec_end, lr, rc, e.b1, e.b2, e.eps, e.wd);
+            w[t][q] = a, s1[t][q] = b, s2[t][q] = c;
+          }
+        }
+        store4<V4>(e.out + o, w[t]);
+        if (has1) store4<V4>(e.m + o, s1[t]);
+        if (has2) store4<V4>(e.v + o, s2[t]);
+        if (e.grad) store4<V4>(e.grad + o, val(v));
+      }
+    }
+  }
+}
+
+// Whether every buffer the interleaved epilogue touches takes 16-byte
+// accesses at column multiples of 4.
+__device__ __forceinline__ bool quad_aligned(const EpiArgs& e, int epi) {
+  auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  bool ok = e.ldc % 4 == 0 && a16(e.out);
+  if (epi == EPI_BIAS_ACT) ok = ok && a16(e.bias) && a16(e.pre);
+  if (epi == EPI_DW_OPT) ok = ok && a16(e.m) && a16(e.v) && a16(e.grad);
+  return ok;
+}
+
 // Adam's bias-correction reciprocals when the epilogue runs Adam/AdamW.
 __device__ __forceinline__ AdamRcp adam_rcp_of(const EpiArgs& e) {
   return e.opt == VOLTA_OPT_ADAM || e.opt == VOLTA_OPT_ADAMW ? adam_rcp(e.scalars->bc1, e.scalars->bc2) : AdamRcp{};
@@ -422,6 +522,9 @@ __device__ __forceinline__ void loss_tile(const EpiArgs& e, const float* z, int 
     }
   }
 }
+
+// Split-K planes whose loads the last slice of a tile issues together.
+constexpr int kInkPlanes = 4;
 
 // EPI is the epilogue kind (compile time, so each launch carries only its
 // own epilogue).  INK selects how a split-K launch is reduced: false -- each
@@ -590,42 +693,69 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& args, int bx, int by, 
     if constexpr (!INK) {
       return;  // splitk_reduce finishes
     } else {
-      __threadfence();
+      // Release this slice's plane and take the tile's ticket; the slice
+      // that arrives last adds the planes in slice order -- its own from
+      // its registers -- exactly as splitk_reduce adds them, then runs the
+      // epilogue.  Per 32x32 block every plane's loads are issued before
+      // the first add (kInkPlanes at a time), so the reduction waits one
+      // memory latency per block and chunk rather than one per register.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
       __syncthreads();
       if (tid == 0) {
-        const unsigned ticket = atomicAdd(&args.counters[bx], 1u);
+        const unsigned ticket = __hip_atomic_fetch_add(&args.counters[bx], 1u, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT);
         lds_small[BM] = ticket == (unsigned)gy - 1u ? 1.0f : 0.0f;
       }
       __syncthreads();
       if (lds_small[BM] == 0.0f) return;
-      __threadfence();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       const float* planes = args.partial;
+      static_for_blocks<0, T::TM, T::TN>([&](auto I, auto J) {
+        constexpr int i = decltype(I)::value, j = decltype(J)::value;
+        const int n = n0 + wn * WN + j * 32 + l32;
+        const int nc = n < N ? n : N - 1;  // clamped: every load in bounds, unused values discarded
+        float s[16];
 #pragma unroll
-      for (int i = 0; i < T::TM; ++i)
+        for (int v = 0; v < 16; ++v) s[v] = 0.0f;
+        for (int z0 = 0; z0 < gy; z0 += kInkPlanes) {
+          float p[kInkPlanes][16];
 #pragma unroll
-        for (int j = 0; j < T::TN; ++j) {
-          const int n = n0 + wn * WN + j * 32 + l32;
+          for (int q = 0; q < kInkPlanes; ++q) {
+            const int z = z0 + q < gy ? z0 + q : gy - 1;
+            const float* src = planes + (size_t)z * plane + nc;
+            if (z != by) {
 #pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int m = m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-            if (m < M && n < N) {
-              const size_t off = (size_t)m * N + n;
-              float s = planes[off];
-              for (int z = 1; z < gy; ++z) s = s + planes[z * plane + off];
-              acc[i][j][v] = s;
+              for (int v = 0; v < 16; ++v) {
+                const int m = m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                p[q][v] = src[(size_t)(m < M ? m : M - 1) * N];
+              }
+            } else {
+#pragma unroll
+              for (int v = 0; v < 16; ++v) p[q][v] = acc[i][j][v];
+            }
+          }
+#pragma unroll
+          for (int q = 0; q < kInkPlanes; ++q) {
+            const int z = z0 + q;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              const float t = z == 0 ? p[q][v] : s[v] + p[q][v];
+              s[v] = z < gy ? t : s[v];
             }
           }
         }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = s[v];
+        __builtin_amdgcn_sched_barrier(0);
+      });
       if (cs_owner) {
 #pragma unroll
         for (int j = 0; j < T::TN; ++j) {
           const int n = n0 + wn * WN + j * 32 + l32;
-          if (n < N) {
-            const size_t off = (size_t)M * N + n;
-            float s = planes[off];
-            for (int z = 1; z < gy; ++z) s = s + planes[z * plane + off];
-            cs[j] = s;
-          }
+          const float* src = planes + (size_t)M * N + (n < N ? n : N - 1);
+          float s = by == 0 ? cs[j] : src[0];
+          for (int z = 1; z < gy; ++z) s = s + (z == by ? cs[j] : src[(size_t)z * plane]);
+          cs[j] = s;
         }
       }
       if (tid == 0) args.counters[bx] = 0u;
@@ -728,12 +858,17 @@ gemm_f32_mfma(GemmArgs args) {
 // workgroup barrier).
 //
 // LDS layouts.  K-contiguous tile [256 rows][32 k] in 16-byte chunks: (row
-// r, k-quad q) at chunk r*8 + (q ^ (r & 7)), so the fragment reads of 8
-// consecutive rows at one k-quad hit 8 distinct 4-bank groups (each load
-// instruction fills 64 consecutive chunks: 8 rows, their k-quads permuted,
-// from 8 whole 128-byte row segments).  MN-contiguous tile [32 k][256]: one
-// k row of 256 floats per load instruction; a lane's four k values of a
-// column are four 4-byte reads, conflict-free across consecutive columns.
+// r, k-quad q) at chunk r*8 + (q ^ ((r >> 1) & 7)), so the fragment reads of
+// 16 consecutive rows at one k-quad hit all 16 four-bank groups of the 64
+// banks (rows 2m and 2m+1 lie in opposite halves, m = 0..7 permutes the
+// quads); each load instruction fills 64 consecutive chunks: 8 rows, their
+// k-quads permuted, from 8 whole 128-byte row segments.  MN-contiguous tile
+// [32 k][256]: one k row of 256 floats per load instruction.  An
+// MN-contiguous A operand is read as four 4-byte reads per fragment (a
+// lane's four k of one row), conflict-free across consecutive rows; an
+// MN-contiguous B operand as one 16-byte read per MFMA step (big_bq: four
+// consecutive columns of one k, one per accumulator block), 16 lanes
+// covering 256 consecutive bytes.
 //
 // Exact tiles only (M, N multiples of 256, K of 64, 16-byte aligned rows and
 // bases): every load is in bounds without a guard; gemm_plan checks.
@@ -746,7 +881,7 @@ typedef __attribute__((address_space(3))) void* LdsVoidPtr;
 // Issue this wave's 4 of the 32 one-kilobyte load instructions of an operand
 // tile (rows row0.., k k0..k0+31) into `tile`; `wave` (0..7) is wave-uniform.
 // Instruction j = wave + 8t fills chunks 64j..64j+63: K-contiguous, rows
-// 8j..8j+7 (lane: row 8j + lane/8, k-quad (lane & 7) ^ (row & 7));
+// 8j..8j+7 (lane: row 8j + lane/8, k-quad (lane & 7) ^ ((row >> 1) & 7));
 // MN-contiguous, k row j.  32-bit element offsets (big_tile_fits bounds the
 // operands).
 template <bool KC>
@@ -755,7 +890,7 @@ __device__ __forceinline__ void big_load(const float* __restrict__ p, int ld, in
   uint32_t off, step;
   if constexpr (KC) {
     const int r = wave * 8 + (lane >> 3);
-    const int q = (lane & 7) ^ ((lane >> 3) & 7);
+    const int q = (lane & 7) ^ ((r >> 1) & 7);  // rows 64t apart share the swizzle
     off = (uint32_t)(row0 + r) * (uint32_t)ld + (uint32_t)(k0 + 4 * q);
     step = 64u * (uint32_t)ld;
   } else {
@@ -768,18 +903,28 @@ __device__ __forceinline__ void big_load(const float* __restrict__ p, int ld, in
                                      0, 0);
 }
 
-// The 4 operands (k = 8g + 4h + s) of lane (row, h) for k-group g.
+// The 4 operands (k = 8g + 4h + s) of lane (row, h) for k-group g.  (For an
+// MN-contiguous B operand the tile reads big_bq instead.)
 template <bool KC>
 __device__ __forceinline__ floatx4 big_frag(const float* tile, int row, int h, int g) {
   if constexpr (KC) {
     const int q = 2 * g + h;
-    return *reinterpret_cast<const floatx4*>(tile + 4 * (row * 8 + (q ^ (row & 7))));
+    return *reinterpret_cast<const floatx4*>(tile + 4 * (row * 8 + (q ^ ((row >> 1) & 7))));
   } else {
     floatx4 f;
 #pragma unroll
     for (int s = 0; s < 4; ++s) f[s] = tile[(8 * g + 4 * h + s) * kBigBM + row];
     return f;
   }
+}
+
+// MN-contiguous B operand, one 16-byte read per MFMA step: lane (c, h) takes
+// columns 4c..4c+3 of k row 8g + 4h + s, the B operands of its four 32x32
+// blocks j = 0..3 at step s -- block j's column of lane c is 4c + j.  The k
+// of every product is unchanged (8g + 4h + s), so each output sums the same
+// products in the same order as the one-block-per-32-columns mapping.
+__device__ __forceinline__ floatx4 big_bq(const float* tile, int col4, int h, int g, int s) {
+  return *reinterpret_cast<const floatx4*>(tile + (8 * g + 4 * h + s) * kBigBM + col4);
 }
 
 template <bool A_KC, bool B_KC, int EPI>
@@ -812,6 +957,16 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
+  // Column of block j held by lane l32 (B MN-contiguous: 4 l32 + j, big_bq).
+  auto col = [&](int j) { return B_KC ? j * 32 + l32 : 4 * l32 + j; };
+  // B fragment t of k-group g: K-contiguous, block t's four steps; MN-
+  // contiguous, step t's four blocks.
+  auto b_frag = [&](const float* b_s, int t, int g) {
+    if constexpr (B_KC) return big_frag<true>(b_s, wn * WN + t * 32 + l32, h, g);
+    else return big_bq(b_s, wn * WN + 4 * l32, h, g, t);
+  };
+  static_assert(TN == 4, "the MN-contiguous B reads cover four blocks per step");
+
   // One stage: the fragments of k-group g + 1 are read from LDS before the
   // 32 MFMAs of group g are issued, so their latency hides behind the
   // matrix work; the wave's priority is raised while it issues MFMAs.
@@ -820,7 +975,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
 #pragma unroll
     for (int i = 0; i < TM; ++i) fa_n[i] = big_frag<A_KC>(a_s, wm * WM + i * 32 + l32, h, 0);
 #pragma unroll
-    for (int j = 0; j < TN; ++j) fb_n[j] = big_frag<B_KC>(b_s, wn * WN + j * 32 + l32, h, 0);
+    for (int t = 0; t < TN; ++t) fb_n[t] = b_frag(b_s, t, 0);
 #pragma unroll
     for (int g = 0; g < kBigBK / 8; ++g) {
       floatx4 fa[TM], fb[TN];
@@ -832,7 +987,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
 #pragma unroll
         for (int i = 0; i < TM; ++i) fa_n[i] = big_frag<A_KC>(a_s, wm * WM + i * 32 + l32, h, g + 1);
 #pragma unroll
-        for (int j = 0; j < TN; ++j) fb_n[j] = big_frag<B_KC>(b_s, wn * WN + j * 32 + l32, h, g + 1);
+        for (int t = 0; t < TN; ++t) fb_n[t] = b_frag(b_s, t, g + 1);
       }
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_setprio(1);
@@ -842,14 +997,14 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], B_KC ? fb[j][s] : fb[s][j], acc[i][j], 0, 0, 0);
       __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_sched_barrier(0);
       if (kColsum && colsum) {
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
-          for (int s = 0; s < 4; ++s) cs[j] = cs[j] + fb[j][s];
+          for (int s = 0; s < 4; ++s) cs[j] = cs[j] + (B_KC ? fb[j][s] : fb[s][j]);
       }
     }
   };
@@ -884,16 +1039,29 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
   }
   const bool cs_owner = kColsum && colsum && h == 0;
   const EpiArgs& e = args.epi;
-  static_for_blocks<0, TM, TN>([&](auto I, auto J) {
-    constexpr int i = decltype(I)::value, j = decltype(J)::value;
-    block_epilogue<EPI>(e, acc[i][j], m0 + wm * WM + i * 32 + 4 * h, n0 + wn * WN + j * 32 + l32, M, N);
-    __builtin_amdgcn_sched_barrier(0);
-  });
+  if constexpr (B_KC) {
+    static_for_blocks<0, TM, TN>([&](auto I, auto J) {
+      constexpr int i = decltype(I)::value, j = decltype(J)::value;
+      block_epilogue<EPI>(e, acc[i][j], m0 + wm * WM + i * 32 + 4 * h, n0 + wn * WN + col(j), M, N);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  } else {
+    // the lane's four blocks of a row hold four consecutive columns
+    const bool v4 = quad_aligned(e, EPI);
+    const int n4 = n0 + wn * WN + 4 * l32;
+    static_for_blocks<0, TM, 1>([&](auto I, auto) {
+      constexpr int i = decltype(I)::value;
+      const int mb = m0 + wm * WM + i * 32 + 4 * h;
+      if (v4) quad_epilogue<EPI, true>(e, acc[i][0], acc[i][1], acc[i][2], acc[i][3], mb, n4);
+      else quad_epilogue<EPI, false>(e, acc[i][0], acc[i][1], acc[i][2], acc[i][3], mb, n4);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  }
   if constexpr (kColsum) {
     if (cs_owner && e.b) {
       const AdamRcp rc = adam_rcp_of(e);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) apply_bias_update(e, n0 + wn * WN + j * 32 + l32, N, cs[j], rc);
+      for (int j = 0; j < TN; ++j) apply_bias_update(e, n0 + wn * WN + col(j), N, cs[j], rc);
     }
   }
 }
