@@ -323,17 +323,17 @@ __device__ __forceinline__ void store4(float* p, const floatx4& x) {
 
 // Epilogue of four 32x32 blocks j = 0..3 whose columns interleave: block j's
 // column of the lane is n4 + j, so the lane holds four consecutive columns of
-// each of its 16 rows m_base + 8*(v/4) + (v%4) (the 256x256 tile with an
-// MN-contiguous B operand; exact tiles, every row and column in range).
-// Rows go four at a time, every load of a group issued before its stores,
-// with 16-byte accesses when V4 -- the same per-element arithmetic as
-// block_epilogue.
-template <int EPI, bool V4>
+// each of its 16 rows m_base + RS*(8*(v/4) + (v%4)) (the 256x256 tile with an
+// MN-contiguous B operand, RS = 2 where the A operand's rows interleave too;
+// exact tiles, every row and column in range).  Rows go four at a time,
+// every load of a group issued before its stores, with 16-byte accesses
+// when V4 -- the same per-element arithmetic as block_epilogue.
+template <int EPI, bool V4, int RS>
 __device__ __forceinline__ void quad_epilogue(const EpiArgs& e, const floatx16& a0, const floatx16& a1,
                                               const floatx16& a2, const floatx16& a3, int m_base, int n4) {
   static_assert(EPI == EPI_STORE || EPI == EPI_BIAS_ACT || EPI == EPI_DW_OPT, "no interleaved form");
   const uint32_t ldc = (uint32_t)e.ldc;
-  auto off = [&](int v) { return (uint32_t)(m_base + 8 * (v >> 2) + (v & 3)) * ldc + (uint32_t)n4; };
+  auto off = [&](int v) { return (uint32_t)(m_base + RS * (8 * (v >> 2) + (v & 3))) * ldc + (uint32_t)n4; };
   auto val = [&](int v) { return floatx4{a0[v], a1[v], a2[v], a3[v]}; };
   if constexpr (EPI == EPI_STORE) {
 #pragma unroll
@@ -927,6 +927,14 @@ __device__ __forceinline__ floatx4 big_bq(const float* tile, int col4, int h, in
   return *reinterpret_cast<const floatx4*>(tile + (8 * g + 4 * h + s) * kBigBM + col4);
 }
 
+// MN-contiguous A operand likewise, one 8-byte read per MFMA step: lane
+// (r, h) takes rows 2r and 2r+1 of k row 8g + 4h + s, the A operands of its
+// two 32x32 row blocks i = 0, 1 -- block i's row of lane r is 2r + i.
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ floatx2 big_aq(const float* tile, int row2, int h, int g, int s) {
+  return *reinterpret_cast<const floatx2*>(tile + (8 * g + 4 * h + s) * kBigBM + row2);
+}
+
 template <bool A_KC, bool B_KC, int EPI>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) gemm_big(GemmArgs args) {
   __shared__ __attribute__((aligned(16))) float lds_a0[kBigTileFloats];
@@ -957,8 +965,25 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  // Column of block j held by lane l32 (B MN-contiguous: 4 l32 + j, big_bq).
+  // Column of block j held by lane l32 (B MN-contiguous: 4 l32 + j, big_bq);
+  // first row of block i held by lane half h (A MN-contiguous: rows
+  // interleave, block i's MFMA row r is 2r + i, big_aq).
   auto col = [&](int j) { return B_KC ? j * 32 + l32 : 4 * l32 + j; };
+  auto row_base = [&](int i) { return m0 + wm * WM + (A_KC ? i * 32 + 4 * h : i + 8 * h); };
+  constexpr int kRowStride = A_KC ? 1 : 2;
+  static_assert(TM == 2, "the MN-contiguous A reads cover two blocks per step");
+  // A fragment t of k-group g: K-contiguous, block t's four steps; MN-
+  // contiguous, steps 2t and 2t+1 of both blocks ({s0 i0, s0 i1, s1 i0, s1 i1}).
+  auto a_frag = [&](const float* a_s, int t, int g) {
+    if constexpr (A_KC) {
+      return big_frag<true>(a_s, wm * WM + t * 32 + l32, h, g);
+    } else {
+      const floatx2 x = big_aq(a_s, wm * WM + 2 * l32, h, g, 2 * t);
+      const floatx2 y = big_aq(a_s, wm * WM + 2 * l32, h, g, 2 * t + 1);
+      return floatx4{x[0], x[1], y[0], y[1]};
+    }
+  };
+  auto a_op = [&](const floatx4* fa, int i, int s) { return A_KC ? fa[i][s] : fa[s >> 1][2 * (s & 1) + i]; };
   // B fragment t of k-group g: K-contiguous, block t's four steps; MN-
   // contiguous, step t's four blocks.
   auto b_frag = [&](const float* b_s, int t, int g) {
@@ -973,7 +998,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
   auto compute = [&](const float* a_s, const float* b_s) {
     floatx4 fa_n[TM], fb_n[TN];
 #pragma unroll
-    for (int i = 0; i < TM; ++i) fa_n[i] = big_frag<A_KC>(a_s, wm * WM + i * 32 + l32, h, 0);
+    for (int t = 0; t < TM; ++t) fa_n[t] = a_frag(a_s, t, 0);
 #pragma unroll
     for (int t = 0; t < TN; ++t) fb_n[t] = b_frag(b_s, t, 0);
 #pragma unroll
@@ -985,7 +1010,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
       for (int j = 0; j < TN; ++j) fb[j] = fb_n[j];
       if (g + 1 < kBigBK / 8) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i) fa_n[i] = big_frag<A_KC>(a_s, wm * WM + i * 32 + l32, h, g + 1);
+        for (int t = 0; t < TM; ++t) fa_n[t] = a_frag(a_s, t, g + 1);
 #pragma unroll
         for (int t = 0; t < TN; ++t) fb_n[t] = b_frag(b_s, t, g + 1);
       }
@@ -997,7 +1022,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], B_KC ? fb[j][s] : fb[s][j], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a_op(fa, i, s), B_KC ? fb[j][s] : fb[s][j], acc[i][j], 0,
+                                                             0, 0);
       __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_sched_barrier(0);
       if (kColsum && colsum) {
@@ -1040,9 +1066,10 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
   const bool cs_owner = kColsum && colsum && h == 0;
   const EpiArgs& e = args.epi;
   if constexpr (B_KC) {
+    static_assert(A_KC, "every layout with a K-contiguous B has a K-contiguous A");
     static_for_blocks<0, TM, TN>([&](auto I, auto J) {
       constexpr int i = decltype(I)::value, j = decltype(J)::value;
-      block_epilogue<EPI>(e, acc[i][j], m0 + wm * WM + i * 32 + 4 * h, n0 + wn * WN + col(j), M, N);
+      block_epilogue<EPI>(e, acc[i][j], row_base(i), n0 + wn * WN + col(j), M, N);
       __builtin_amdgcn_sched_barrier(0);
     });
   } else {
@@ -1051,9 +1078,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
     const int n4 = n0 + wn * WN + 4 * l32;
     static_for_blocks<0, TM, 1>([&](auto I, auto) {
       constexpr int i = decltype(I)::value;
-      const int mb = m0 + wm * WM + i * 32 + 4 * h;
-      if (v4) quad_epilogue<EPI, true>(e, acc[i][0], acc[i][1], acc[i][2], acc[i][3], mb, n4);
-      else quad_epilogue<EPI, false>(e, acc[i][0], acc[i][1], acc[i][2], acc[i][3], mb, n4);
+      if (v4) quad_epilogue<EPI, true, kRowStride>(e, acc[i][0], acc[i][1], acc[i][2], acc[i][3], row_base(i), n4);
+      else quad_epilogue<EPI, false, kRowStride>(e, acc[i][0], acc[i][1], acc[i][2], acc[i][3], row_base(i), n4);
       __builtin_amdgcn_sched_barrier(0);
     });
   }
