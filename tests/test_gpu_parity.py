@@ -156,6 +156,37 @@ def test_gemm_big_tile_integer_exact(layout, M, N, K):
     np.testing.assert_array_equal(got, (Am.astype(np.int64) @ Bm.astype(np.int64)).astype(np.float32))
 
 
+KGROUP_CASES = [  # (tile, groups, M, N, K): ragged K, M and N included
+    (0, 2, 130, 70, 300), (0, 4, 96, 64, 1000), (0, 4, 64, 200, 202), (1, 2, 256, 384, 520), (1, 2, 200, 130, 64),
+]
+
+
+@pytest.mark.parametrize("layout", [0, 1, 2], ids=["NN", "NT", "TN"])
+@pytest.mark.parametrize("tile,groups,M,N,K", KGROUP_CASES)
+def test_gemm_kgroups_exact_and_equal_to_split_launches(layout, tile, groups, M, N, K):
+    """K split over groups of one workgroup's waves (the partial tiles added
+    through LDS): exact on integer operands, and on random operands
+    bit-identical to the same slices as split-K launches with the reduce
+    kernel (both add the slices in order)."""
+    if groups == 4 and layout == 2:
+        groups = 2  # dW products take at most two groups
+    say(f"gemm K groups tile={tile} groups={groups} layout={layout} M={M} N={N} K={K}")
+    rng = np.random.default_rng(M + 3 * N + 5 * K + layout)
+    a_shape = (K, M) if layout == 2 else (M, K)
+    b_shape = (N, K) if layout == 1 else (K, N)
+    Ai = rng.integers(-4, 5, a_shape).astype(np.float32)
+    Bi = rng.integers(-4, 5, b_shape).astype(np.float32)
+    Am = Ai.T if layout == 2 else Ai
+    Bm = Bi.T if layout == 1 else Bi
+    want = (Am.astype(np.int64) @ Bm.astype(np.int64)).astype(np.float32)
+    np.testing.assert_array_equal(_gemm(layout, Ai, Bi, M, N, K, tile=tile, splits=-groups), want)
+    A = rng.standard_normal(a_shape).astype(np.float32)
+    B = rng.standard_normal(b_shape).astype(np.float32)
+    grouped = _gemm(layout, A, B, M, N, K, tile=tile, splits=-groups)
+    split = _gemm(layout, A, B, M, N, K, tile=tile, splits=groups)
+    np.testing.assert_array_equal(grouped, split)
+
+
 @pytest.mark.parametrize("layout", [0, 1, 2], ids=["NN", "NT", "TN"])
 def test_gemm_big_tile_unaligned_output(layout):
     """An output 4 bytes past a 16-byte boundary: the epilogue takes its
@@ -773,6 +804,26 @@ def test_paired_backward_launches_bit_identical(name):
     for a, b in zip(p1, p2):
         np.testing.assert_array_equal(a, b)
     for a, b in zip(b1, b2):
+        np.testing.assert_array_equal(a, b)
+
+
+KGROUP_STEP_CASES = {
+    "c4_b1024": (MlpSpec([512, 1024, 1024, 512, 256, 1], "silu", "sgd"), 1024, 0.01),
+    "ragged_b900": (MlpSpec([300, 700, 500, 3], "tanh", "adam"), 900, 1e-3),
+}
+
+
+@pytest.mark.parametrize("name", sorted(KGROUP_STEP_CASES))
+def test_kgroups_steps_bit_identical(name):
+    """Split-K products with their slices on groups of one workgroup's waves
+    (VOLTA_KGROUPS=1) give the same bits as the split launches and their
+    reduce kernel: losses, parameters, activations and deltas after 3 steps."""
+    spec, B, lr = KGROUP_STEP_CASES[name]
+    say(f"K groups {name}")
+    l1, p1, b1 = _run_with_env({"VOLTA_KGROUPS": "0"}, spec, B, lr, 3)
+    l2, p2, b2 = _run_with_env({"VOLTA_KGROUPS": "1"}, spec, B, lr, 3)
+    np.testing.assert_array_equal(l1, l2)
+    for a, b in zip(p1 + b1, p2 + b2):
         np.testing.assert_array_equal(a, b)
 
 

@@ -207,13 +207,14 @@ __device__ __forceinline__ void apply_epilogue(const EpiArgs& e, int m, int n, f
 struct DwState {
   float w[16], s1[16], s2[16];
 
-  __device__ __forceinline__ void load(const EpiArgs& e, int m_base, int n, int M, int N) {
+  // Registers v_lo <= v < v_hi only (the others are neither loaded nor stored).
+  __device__ __forceinline__ void load(const EpiArgs& e, int m_base, int n, int M, int N, int v_lo, int v_hi) {
     const uint32_t n32 = (uint32_t)n, ldc = (uint32_t)e.ldc;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int m = m_base + 8 * (v >> 2) + (v & 3);
       const uint32_t o = (uint32_t)m * ldc + n32;
-      const bool ok = m < M && n < N;
+      const bool ok = m < M && n < N && v >= v_lo && v < v_hi;
       w[v] = ok ? e.out[o] : 0.0f;
       s1[v] = ok && e.opt != VOLTA_OPT_SGD ? e.m[o] : 0.0f;
       s2[v] = ok && (e.opt == VOLTA_OPT_ADAM || e.opt == VOLTA_OPT_ADAMW) ? e.v[o] : 0.0f;
@@ -221,7 +222,8 @@ struct DwState {
   }
 
   // Caller guarantees n < N.
-  __device__ __forceinline__ void update_store(const EpiArgs& e, const floatx16& acc, int m_base, int n, int M) {
+  __device__ __forceinline__ void update_store(const EpiArgs& e, const floatx16& acc, int m_base, int n, int M,
+                                               int v_lo, int v_hi) {
     const float lr = e.scalars->lr;
     const uint32_t n32 = (uint32_t)n, ldc = (uint32_t)e.ldc;
     auto row = [&](int v) { return m_base + 8 * (v >> 2) + (v & 3); };
@@ -243,7 +245,7 @@ struct DwState {
     }
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      if (row(v) < M) {
+      if (row(v) < M && v >= v_lo && v < v_hi) {
         e.out[off(v)] = w[v];
         if (e.opt != VOLTA_OPT_SGD) e.m[off(v)] = s1[v];
         if (e.opt == VOLTA_OPT_ADAM || e.opt == VOLTA_OPT_ADAMW) e.v[off(v)] = s2[v];
@@ -254,21 +256,22 @@ struct DwState {
 };
 
 // Epilogue for the 16 accumulators a lane holds of one 32x32 block: column n,
-// rows m_base + 8*(v/4) + (v%4).  All loads are issued before any store so
-// the memory accesses of the 16 elements overlap (the element-by-element
-// form serialises them, since the compiler cannot prove the buffers
-// disjoint).
+// rows m_base + 8*(v/4) + (v%4), registers v_lo <= v < v_hi of them.  All
+// loads are issued before any store so the memory accesses of the elements
+// overlap (the element-by-element form serialises them, since the compiler
+// cannot prove the buffers disjoint).
 template <int EPI>
 __device__ __forceinline__ void block_epilogue(const EpiArgs& e, const floatx16& acc, int m_base, int n, int M,
-                                               int N) {
+                                               int N, int v_lo = 0, int v_hi = 16) {
   if (n >= N) return;
   auto row = [&](int v) { return m_base + 8 * (v >> 2) + (v & 3); };
+  auto mine = [&](int v) { return v >= v_lo && v < v_hi; };
   if constexpr (EPI == EPI_BIAS_ACT) {
     const float b = e.bias[n];
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int m = row(v);
-      if (m < M) {
+      if (m < M && mine(v)) {
         const size_t idx = (size_t)m * e.ldc + n;
         const float x = acc[v] + b;  // pre = act_i W_i + b_i (:716-724)
         if (e.pre) e.pre[idx] = x;
@@ -283,23 +286,23 @@ __device__ __forceinline__ void block_epilogue(const EpiArgs& e, const floatx16&
     for (int v = 0; v < 16; ++v) {
       const int m = row(v);
       const size_t idx = (size_t)m * e.ldc + n;
-      y[v] = m < M ? e.aux_act[idx] : 0.0f;
-      p[v] = m < M ? pp[idx] : 0.0f;
+      y[v] = m < M && mine(v) ? e.aux_act[idx] : 0.0f;
+      p[v] = m < M && mine(v) ? pp[idx] : 0.0f;
     }
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int m = row(v);
-      if (m < M) e.out[(size_t)m * e.ldc + n] = acc[v] * act_derivative(e.act, p[v], y[v]);
+      if (m < M && mine(v)) e.out[(size_t)m * e.ldc + n] = acc[v] * act_derivative(e.act, p[v], y[v]);
     }
   } else if constexpr (EPI == EPI_DW_OPT) {
     DwState st;
-    st.load(e, m_base, n, M, N);
-    st.update_store(e, acc, m_base, n, M);
+    st.load(e, m_base, n, M, N, v_lo, v_hi);
+    st.update_store(e, acc, m_base, n, M, v_lo, v_hi);
   } else {
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int m = row(v);
-      if (m < M) e.out[(size_t)m * e.ldc + n] = acc[v];
+      if (m < M && mine(v)) e.out[(size_t)m * e.ldc + n] = acc[v];
     }
   }
 }
@@ -534,17 +537,29 @@ constexpr int kInkPlanes = 4;
 // The tile body is a device function of the block coordinates (bx = output
 // tile, by = K slice of gy) and of its LDS (two A buffers, two B buffers,
 // BM + 2 floats), so a launch may also run it beside another operation.
-template <int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, bool VEC, int EPI, bool INK>
+//
+// KG > 1 splits K inside the workgroup instead (gy = 1): KG groups of the
+// tile's waves, group z taking K slice z (k_per_split each) with its own two
+// A and two B buffers (lds_a0: KG x 2 A buffers, lds_b0 right after it: KG x
+// 2 B buffers).  Every group runs as many stages as group 0, computing only
+// inside its slice, so the workgroup barriers match.  The partial tiles are
+// then added through the (free) operand LDS in slice order -- the sum
+// splitk_reduce forms over KG planes -- each group finishing 16/KG of every
+// block's 16 accumulator rows, and the epilogue runs on those rows.
+template <int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, bool VEC, int EPI, bool INK, int KG = 1>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& args, int bx, int by, int gy, float* lds_a0,
                                           float* lds_b0, float* lds_small) {
   using T = Tile<BM, BN, BK, WM, WN>;
   constexpr int THREADS = T::kThreads;
   using LA = LdsTile<BM, BK, A_KC>;
   using LB = LdsTile<BN, BK, B_KC>;
-  auto lds_a = [&](int i) { return lds_a0 + i * LA::kFloats; };
-  auto lds_b = [&](int i) { return lds_b0 + i * LB::kFloats; };
+  static_assert(KG == 1 || (EPI != EPI_LOSS && !INK), "K groups finish whole tiles in their own epilogue");
+  const int grp = KG > 1 ? (int)threadIdx.x / THREADS : 0;  // workgroup-uniform per wave
+  float* const lds_x = lds_a0;  // the K groups' exchange area (all operand buffers)
+  auto lds_a = [&](int i) { return lds_a0 + (grp * 2 + i) * LA::kFloats; };
+  auto lds_b = [&](int i) { return lds_b0 + (grp * 2 + i) * LB::kFloats; };
 
-  const int tid = threadIdx.x;
+  const int tid = KG > 1 ? (int)threadIdx.x % THREADS : (int)threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave / T::kWavesN;
@@ -560,8 +575,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& args, int bx, int by, 
   const int tn = bx % tiles_n;
   const int m0 = tm * BM, n0 = tn * BN;
 
-  const int kbeg = by * args.k_per_split;
+  const int kbeg = (KG > 1 ? grp : by) * args.k_per_split;
   const int kend = min(args.K, kbeg + args.k_per_split);
+  // Stages: a K group runs as many as group 0 (whose slice is the longest).
+  const int n_stages = KG > 1 ? (min(args.K, args.k_per_split) + BK - 1) / BK : (kend - kbeg + BK - 1) / BK;
   // Column sums of B over k (dW's db = sum_b delta), taken from the MFMA B
   // fragments the waves already hold: the first row of waves (wm == 0) of
   // the first row of tiles adds its fragments in k order per lane half,
@@ -631,23 +648,29 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& args, int bx, int by, 
     }
   };
 
-  if (kbeg < kend) {
-    la.load(args.A, args.lda, M, kend, m0, kbeg, tid);
-    lb.load(args.B, args.ldb, N, kend, n0, kbeg, tid);
-    la.store(lds_a(0), tid);
-    lb.store(lds_b(0), tid);
+  if (n_stages > 0) {
+    if (kbeg < kend) {
+      la.load(args.A, args.lda, M, kend, m0, kbeg, tid);
+      lb.load(args.B, args.ldb, N, kend, n0, kbeg, tid);
+      la.store(lds_a(0), tid);
+      lb.store(lds_b(0), tid);
+    }
     __syncthreads();
 
     int buf = 0;
-    for (int k0 = kbeg; k0 < kend; k0 += BK) {
+    for (int st = 0; st < n_stages; ++st) {
+      const int k0 = kbeg + st * BK;
+      const bool active = KG == 1 || k0 < kend;  // a K group past its slice only meets the barriers
       const bool more = k0 + BK < kend;
       if (more) {
         la.load(args.A, args.lda, M, kend, m0, k0 + BK, tid);
         lb.load(args.B, args.ldb, N, kend, n0, k0 + BK, tid);
       }
-      __builtin_amdgcn_s_setprio(1);
-      compute_stage(lds_a(buf), lds_b(buf), [] {});
-      __builtin_amdgcn_s_setprio(0);
+      if (active) {
+        __builtin_amdgcn_s_setprio(1);
+        compute_stage(lds_a(buf), lds_b(buf), [] {});
+        __builtin_amdgcn_s_setprio(0);
+      }
       if (more) {
         la.store(lds_a(buf ^ 1), tid);
         lb.store(lds_b(buf ^ 1), tid);
@@ -663,7 +686,46 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& args, int bx, int by, 
 #pragma unroll
     for (int j = 0; j < T::TN; ++j) cs[j] = cs[j] + __shfl_xor(cs[j], 32, kWave);
   }
-  const bool cs_owner = kColsum && colsum && h == 0;
+  const bool cs_owner = kColsum && colsum && h == 0 && grp == 0;
+
+  // Accumulator rows (registers v) this group finishes.
+  const int v_lo = grp * 16 / KG, v_hi = (grp + 1) * 16 / KG;
+  if constexpr (KG > 1) {
+    // Slot of (group z, this wave, block (i, j), register v): lane-minor, so
+    // a wave's 64 lanes write and read 256 consecutive bytes.
+    constexpr int kBlocks = T::TM * T::TN;
+    constexpr int kWavesG = THREADS / kWave;
+    static_assert(KG * (BM * BN + BN) <= 2 * KG * (LA::kFloats + LB::kFloats), "exchange does not fit");
+    auto slot = [&](int z, int b, int v) { return lds_x + (((z * kWavesG + wave) * kBlocks + b) * 16 + v) * kWave + lane; };
+    float* const cs_x = lds_x + KG * BM * BN;  // column sums of group z: cs_x[z * BN + column]
+#pragma unroll
+    for (int b = 0; b < kBlocks; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        if (v < v_lo || v >= v_hi) *slot(grp, b, v) = acc[b / T::TN][b % T::TN][v];
+    if (kColsum && colsum && h == 0 && grp > 0) {
+#pragma unroll
+      for (int j = 0; j < T::TN; ++j) cs_x[grp * BN + wn * WN + j * 32 + l32] = cs[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < kBlocks; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        if (v >= v_lo && v < v_hi) {
+          const float own = acc[b / T::TN][b % T::TN][v];
+          float sum = grp == 0 ? own : *slot(0, b, v);
+#pragma unroll
+          for (int z = 1; z < KG; ++z) sum = sum + (z == grp ? own : *slot(z, b, v));
+          acc[b / T::TN][b % T::TN][v] = sum;
+        }
+    if (cs_owner) {
+#pragma unroll
+      for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+        for (int z = 1; z < KG; ++z) cs[j] = cs[j] + cs_x[z * BN + wn * WN + j * 32 + l32];
+    }
+  }
 
   // Accumulator register v of lane (h, l32) in block (i, j) holds row
   // 8*(v/4) + 4*h + (v%4), column l32 of that 32x32 block.
@@ -789,7 +851,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& args, int bx, int by, 
     // accumulators at run time and put them in scratch memory.
     static_for_blocks<0, T::TM, T::TN>([&](auto I, auto J) {
       constexpr int i = decltype(I)::value, j = decltype(J)::value;
-      block_epilogue<EPI>(e, acc[i][j], m0 + wm * WM + i * 32 + 4 * h, n0 + wn * WN + j * 32 + l32, M, N);
+      block_epilogue<EPI>(e, acc[i][j], m0 + wm * WM + i * 32 + 4 * h, n0 + wn * WN + j * 32 + l32, M, N, v_lo,
+                          v_hi);
       // one block's loads at a time: hoisting the next block's loads
       // above these stores would raise the register count (occupancy)
       // of the whole kernel
@@ -844,6 +907,19 @@ gemm_f32_mfma(GemmArgs args) {
   __shared__ float lds_small[BM + 2];
   const int bx = xcd_tile(blockIdx.x, (args.M + BM - 1) / BM, (args.N + BN - 1) / BN);
   gemm_tile<BM, BN, BK, WM, WN, A_KC, B_KC, VEC, EPI, INK>(args, bx, blockIdx.y, gridDim.y, lds_a, lds_b, lds_small);
+}
+
+// The tile with K split over KG groups of its waves inside the workgroup
+// (gemm_tile with KG): one launch, no partial planes, the same sums as KG
+// slices reduced by splitk_reduce.  One workgroup per CU (the operand LDS
+// of KG groups), KG waves per SIMD.
+template <int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, bool VEC, int EPI, int KG>
+__global__ void __launch_bounds__(KG * (BM / WM) * (BN / WN) * 64) __attribute__((amdgpu_waves_per_eu(2)))
+gemm_f32_mfma_kg(GemmArgs args) {
+  constexpr int kLa = LdsTile<BM, BK, A_KC>::kFloats, kLb = LdsTile<BN, BK, B_KC>::kFloats;
+  __shared__ __attribute__((aligned(16))) float lds[2 * KG * (kLa + kLb)];
+  const int bx = xcd_tile(blockIdx.x, (args.M + BM - 1) / BM, (args.N + BN - 1) / BN);
+  gemm_tile<BM, BN, BK, WM, WN, A_KC, B_KC, VEC, EPI, false, KG>(args, bx, 0, 1, lds, lds + 2 * KG * kLa, nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -1642,9 +1718,33 @@ __global__ void __launch_bounds__(256) splitk_reduce(GemmArgs a, int splits) {
 // ---------------------------------------------------------------------------
 // Host-side dispatch.
 // ---------------------------------------------------------------------------
-template <int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, int EPI>
-static hipError_t launch_epi(const GemmArgs& a, bool vec, int splits, bool ink, hipStream_t st) {
+template <int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, int EPI, int KG>
+static hipError_t launch_kg(const GemmArgs& a, bool vec, hipStream_t st) {
   using T = Tile<BM, BN, BK, WM, WN>;
+  const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+  if (vec) hipLaunchKernelGGL((gemm_f32_mfma_kg<BM, BN, BK, WM, WN, A_KC, B_KC, true, EPI, KG>), dim3(tiles),
+                              dim3(KG * T::kThreads), 0, st, a);
+  else hipLaunchKernelGGL((gemm_f32_mfma_kg<BM, BN, BK, WM, WN, A_KC, B_KC, false, EPI, KG>), dim3(tiles),
+                          dim3(KG * T::kThreads), 0, st, a);
+  return hipGetLastError();
+}
+
+template <int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, int EPI>
+static hipError_t launch_epi(const GemmArgs& a, bool vec, int splits, bool ink, hipStream_t st, int kg = 1) {
+  using T = Tile<BM, BN, BK, WM, WN>;
+  // K groups where their operand LDS fits the CU's 160 KB
+  constexpr int kStageFloats = LdsTile<BM, BK, A_KC>::kFloats + LdsTile<BN, BK, B_KC>::kFloats;
+  if constexpr (EPI != EPI_LOSS && BK == 32) {
+    if constexpr (2 * 2 * kStageFloats * 4 <= 160 * 1024) {
+      if (kg == 2) return launch_kg<BM, BN, BK, WM, WN, A_KC, B_KC, EPI, 2>(a, vec, st);
+    }
+    // (four groups: 16 waves, 128 registers a lane -- too few for the
+    // optimizer epilogue's state, which would spill)
+    if constexpr (2 * 4 * kStageFloats * 4 <= 160 * 1024 && 4 * T::kThreads <= 1024 && EPI != EPI_DW_OPT) {
+      if (kg == 4) return launch_kg<BM, BN, BK, WM, WN, A_KC, B_KC, EPI, 4>(a, vec, st);
+    }
+  }
+  if (kg != 1) return hipErrorInvalidValue;
   const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   dim3 grid(tiles, splits), block(T::kThreads);
   if (ink) {
@@ -1660,23 +1760,27 @@ static hipError_t launch_epi(const GemmArgs& a, bool vec, int splits, bool ink, 
 // Valid (layout, epilogue) pairs of the step: NN with BIAS_ACT / LOSS /
 // STORE, NT with DX_ACT / STORE, TN with DW_OPT / STORE.
 template <int BM, int BN, int BK, int WM, int WN>
-static hipError_t launch_cfg(const GemmArgs& a, int layout, bool vec, int splits, bool ink, hipStream_t st) {
+static hipError_t launch_cfg(const GemmArgs& a, int layout, bool vec, int splits, bool ink, hipStream_t st,
+                             int kg = 1) {
   const int k = a.epi.kind;
   switch (layout) {
     case GEMM_NN:
-      if (k == EPI_BIAS_ACT) return launch_epi<BM, BN, BK, WM, WN, true, false, EPI_BIAS_ACT>(a, vec, splits, ink, st);
-      if (k == EPI_STORE) return launch_epi<BM, BN, BK, WM, WN, true, false, EPI_STORE>(a, vec, splits, ink, st);
+      if (k == EPI_BIAS_ACT)
+        return launch_epi<BM, BN, BK, WM, WN, true, false, EPI_BIAS_ACT>(a, vec, splits, ink, st, kg);
+      if (k == EPI_STORE) return launch_epi<BM, BN, BK, WM, WN, true, false, EPI_STORE>(a, vec, splits, ink, st, kg);
       if constexpr (BM * (BN + 1) <= 2 * LdsTile<BM, BK, true>::kFloats) {
-        if (k == EPI_LOSS) return launch_epi<BM, BN, BK, WM, WN, true, false, EPI_LOSS>(a, vec, splits, true, st);
+        if (k == EPI_LOSS && kg == 1)
+          return launch_epi<BM, BN, BK, WM, WN, true, false, EPI_LOSS>(a, vec, splits, true, st);
       }
       break;
     case GEMM_NT:
-      if (k == EPI_DX_ACT) return launch_epi<BM, BN, BK, WM, WN, true, true, EPI_DX_ACT>(a, vec, splits, ink, st);
-      if (k == EPI_STORE) return launch_epi<BM, BN, BK, WM, WN, true, true, EPI_STORE>(a, vec, splits, ink, st);
+      if (k == EPI_DX_ACT) return launch_epi<BM, BN, BK, WM, WN, true, true, EPI_DX_ACT>(a, vec, splits, ink, st, kg);
+      if (k == EPI_STORE) return launch_epi<BM, BN, BK, WM, WN, true, true, EPI_STORE>(a, vec, splits, ink, st, kg);
       break;
     case GEMM_TN:
-      if (k == EPI_DW_OPT) return launch_epi<BM, BN, BK, WM, WN, false, false, EPI_DW_OPT>(a, vec, splits, ink, st);
-      if (k == EPI_STORE) return launch_epi<BM, BN, BK, WM, WN, false, false, EPI_STORE>(a, vec, splits, ink, st);
+      if (k == EPI_DW_OPT)
+        return launch_epi<BM, BN, BK, WM, WN, false, false, EPI_DW_OPT>(a, vec, splits, ink, st, kg);
+      if (k == EPI_STORE) return launch_epi<BM, BN, BK, WM, WN, false, false, EPI_STORE>(a, vec, splits, ink, st, kg);
       break;
   }
   return hipErrorInvalidValue;
@@ -1844,10 +1948,22 @@ hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& args_in, hipStream_t s
     if ((err = hipGetLastError()) != hipSuccess) return err;
     return mark(rec, label, 2.0 * a.M * a.N * a.K, bytes);
   }
+  if (p.kgroups > 1) {
+    // K groups inside the workgroup: every group's slice starts inside K
+    const bool ok = p.splits == 1 && a.epi.kind != EPI_LOSS && (p.kgroups == 2 || p.kgroups == 4) &&
+                    (p.kgroups == 2 || (p.tile == TILE_64x64 && a.epi.kind != EPI_DW_OPT)) && (size_t)(p.kgroups - 1) * p.k_per_split < (size_t)a.K &&
+                    (size_t)p.kgroups * p.k_per_split >= (size_t)a.K && p.k_per_split % 32 == 0;
+    if (!ok) return hipErrorInvalidValue;
+  }
   switch (p.tile) {
-    case TILE_64x64: err = launch_cfg<64, 64, 32, 32, 32>(a, p.layout, p.vec, p.splits, ink, st); break;
-    case TILE_128x128: err = launch_cfg<128, 128, 32, 64, 64>(a, p.layout, p.vec, p.splits, ink, st); break;
-    case TILE_64x64_K64: err = launch_cfg<64, 64, 64, 32, 32>(a, p.layout, p.vec, p.splits, ink, st); break;
+    case TILE_64x64: err = launch_cfg<64, 64, 32, 32, 32>(a, p.layout, p.vec, p.splits, ink, st, p.kgroups); break;
+    case TILE_128x128:
+      err = launch_cfg<128, 128, 32, 64, 64>(a, p.layout, p.vec, p.splits, ink, st, p.kgroups);
+      break;
+    case TILE_64x64_K64:
+      if (p.kgroups != 1) return hipErrorInvalidValue;
+      err = launch_cfg<64, 64, 64, 32, 32>(a, p.layout, p.vec, p.splits, ink, st);
+      break;
     default: return hipErrorInvalidValue;
   }
   if (err != hipSuccess) return err;
@@ -2172,6 +2288,19 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus, bool 
     p.tile = TILE_DW_SMALLK;
     p.splits = 1;
     p.k_per_split = K;
+  }
+  // Opt-in (VOLTA_KGROUPS=1): a split of up to 2 slices (4 on the 64x64
+  // tile but for dW) runs inside one workgroup instead, the slices on groups
+  // of its waves (gemm_tile's K groups): no partial planes, no reduce
+  // launch, the same sums -- but slower here (C5 4.63 -> 4.64 ms, C4 B=1024
+  // 0.282 -> 0.289 ms): the groups meet at every stage's barrier, where two
+  // 4-wave workgroups per CU cover each other's, and a grid of fewer tiles
+  // than CUs runs on fewer CUs.  Only where the epilogue is per element.
+  const char* kg = std::getenv("VOLTA_KGROUPS");
+  const int kg_max = p.tile == TILE_64x64 && layout != GEMM_TN ? 4 : p.tile == TILE_64x64 || p.tile == TILE_128x128 ? 2 : 1;
+  if (kg && *kg == '1' && small_m && !p.inkernel_reduce && p.splits > 1 && p.splits <= kg_max) {
+    p.kgroups = p.splits;
+    p.splits = 1;
   }
   return p;
 }

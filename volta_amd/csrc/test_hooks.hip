@@ -34,7 +34,9 @@ int32_t volta_hip_calibration_copy(void* dst, const void* src, int64_t bytes, in
 }
 
 // C[M x N] = op(A) op(B) for layout GEMM_NN / GEMM_NT / GEMM_TN (see gemm.h).
-// force_tile < 0 and force_splits <= 0 select the runtime's own plan.
+// force_tile < 0 and force_splits == 0 select the runtime's own plan;
+// force_splits > 0 splits K over that many launch slices (reduced by a
+// second kernel), force_splits = -G over G groups of one workgroup's waves.
 int32_t volta_hip_gemm(int32_t layout, const float* A, const float* B, float* Cm, int32_t M, int32_t N,
                        int32_t K, int32_t force_tile, int32_t force_splits) {
   using namespace volta;
@@ -59,7 +61,12 @@ int32_t volta_hip_gemm(int32_t layout, const float* A, const float* B, float* Cm
     set_last_error("volta_hip_gemm: unknown tile");
     return -1;
   }
-  if (force_tile >= 0) p.tile = force_tile;
+  if (force_tile >= 0 && force_tile != p.tile) {
+    // the plan's K groups (if any) become split launches on another tile
+    p.tile = force_tile;
+    p.splits *= p.kgroups;
+    p.kgroups = 1;
+  }
   if (p.tile == TILE_SMALLM && p.waves == 0) {  // forced onto a shape planned otherwise
     const char* w = std::getenv("VOLTA_SMALLM_WAVES");
     p.waves = layout == GEMM_NT || (w && std::atoi(w) == 4) ? 4 : (w && std::atoi(w) == 16) ? 16 : 8;
@@ -68,11 +75,13 @@ int32_t volta_hip_gemm(int32_t layout, const float* A, const float* B, float* Cm
     p.splits = 1;
     p.k_per_split = K;
   }
-  if (force_splits > 0) {
-    int kps = (K + force_splits - 1) / force_splits;
+  if (force_splits != 0) {
+    const int g = force_splits > 0 ? force_splits : -force_splits;
+    int kps = (K + g - 1) / g;
     kps = (kps + 31) / 32 * 32;
     p.k_per_split = kps;
-    p.splits = (K + kps - 1) / kps;
+    p.splits = force_splits > 0 ? (K + kps - 1) / kps : 1;
+    p.kgroups = force_splits > 0 ? 1 : (K + kps - 1) / kps;
   }
   float* ws = nullptr;
   unsigned* counters = nullptr;
