@@ -2136,8 +2136,11 @@ static hipError_t reduce_after(const PairOp& o, hipStream_t st) {
 // workgroups [start[i], start[i+1]) after them.
 static_assert(sizeof(DwGroup) <= 4000, "DwGroup is passed by value as a kernel argument (4 KiB limit)");
 
+// Five waves per SIMD (at most 96 registers) where the narrow part's state
+// fits them (NMAX <= 4); the 16-wide narrow dW needs more (at 96 it spilled
+// 27 registers), so four.
 template <int NMAX>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) dw_group_kernel(DwGroup d) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NMAX <= 4 ? 5 : 3))) dw_group_kernel(DwGroup d) {
   __shared__ __attribute__((aligned(16))) float lds[kDwLds];
   int b = blockIdx.x;
   if (b == 0 && threadIdx.x == 0 && d.loss_partials)

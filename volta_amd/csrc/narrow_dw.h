@@ -161,9 +161,12 @@ __device__ __forceinline__ void narrow_dw_block(const NarrowDwArgs& p, int block
   if (own) {
     const int64_t count = (int64_t)R * N;
     const int64_t vec_end = count - count % 8;
+    // columns k >= N are skipped by a guard, not a break: a loop with a
+    // data-dependent exit around this body was left rolled (the registers
+    // then indexed at run time, in scratch memory)
 #pragma unroll
     for (int k = 0; k < NMAX; ++k) {
-      if (k >= N) break;
+      if (k >= N) continue;
       const int64_t idx = (int64_t)j * N + k;
       if (sgd) {
         const float nlr = -lr;
@@ -176,7 +179,7 @@ __device__ __forceinline__ void narrow_dw_block(const NarrowDwArgs& p, int block
     }
 #pragma unroll
     for (int k = 0; k < NMAX; ++k) {
-      if (k >= N) break;
+      if (k >= N) continue;
       const size_t idx = (size_t)j * N + k;
       if (p.grad) p.grad[idx] = acc[k];
       p.w[idx] = w[k];
