@@ -302,6 +302,22 @@ def test_gemm_splitk_matches(splits):
     assert np.all(np.abs(got - want) <= bound)
 
 
+@pytest.mark.parametrize("splits", [17, 32, 40])
+@pytest.mark.parametrize("layout", [0, 2], ids=["NN", "TN"])
+def test_gemm_many_planes_narrow_exact(splits, layout):
+    """More split-K planes than the reduce kernel loads at once, on a product
+    10 columns wide (the reduce's one-column form, as for the output layer's
+    dW at large batch): exact on integer operands."""
+    say(f"gemm {splits} planes layout={layout}")
+    M, N, K = 96, 10, 32 * splits
+    rng = np.random.default_rng(splits + layout)
+    A = rng.integers(-4, 5, (K, M) if layout == 2 else (M, K)).astype(np.float32)
+    B = rng.integers(-4, 5, (K, N)).astype(np.float32)
+    got = _gemm(layout, A, B, M, N, K, tile=0, splits=splits)
+    Am = A.T if layout == 2 else A
+    np.testing.assert_array_equal(got, (Am.astype(np.int64) @ B.astype(np.int64)).astype(np.float32))
+
+
 @pytest.mark.parametrize("kind,wd,count", [("adam", 0.0, 1000), ("adamw", 0.01, 1029), ("adam", 0.0, 5),
                                            ("adagrad", 0.0, 3001)])
 def test_optimizer_kernel_bit_exact(kind, wd, count):

@@ -1674,6 +1674,17 @@ __global__ void __launch_bounds__(256) splitk_reduce(GemmArgs a, int splits) {
 #pragma unroll
           for (int q = 0; q < W; ++q) s[q] = s[q] + p[z][q];
         }
+    } else if constexpr (W == 1) {
+      // kReduceUnroll planes' loads at a time, added in plane order (the
+      // narrow products split K the most)
+      s[0] = a.partial[idx];
+      for (int z0 = 1; z0 < splits; z0 += kReduceUnroll) {
+        float p[kReduceUnroll];
+#pragma unroll
+        for (int z = 0; z < kReduceUnroll; ++z) p[z] = a.partial[(size_t)min(z0 + z, splits - 1) * plane + idx];
+#pragma unroll
+        for (int z = 0; z < kReduceUnroll; ++z) s[0] = z0 + z < splits ? s[0] + p[z] : s[0];
+      }
     } else {
 #pragma unroll
       for (int q = 0; q < W; ++q) s[q] = a.partial[idx + q];
