@@ -397,9 +397,9 @@ __device__ __forceinline__ void quad_epilogue(const EpiArgs& e, const floatx16& 
   }
 }
 
-// Whether every buffer the interleaved epilogue touches takes 16-byte
-// accesses at column multiples of 4.
-__device__ __forceinline__ bool quad_aligned(const EpiArgs& e, int epi) {
+// Whether every buffer the interleaved epilogue (or the four-wide reduce)
+// touches takes 16-byte accesses at column multiples of 4.
+__host__ __device__ __forceinline__ bool quad_aligned(const EpiArgs& e, int epi) {
   auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
   bool ok = e.ldc % 4 == 0 && a16(e.out);
   if (epi == EPI_BIAS_ACT) ok = ok && a16(e.bias) && a16(e.pre);
@@ -1715,6 +1715,35 @@ __global__ void __launch_bounds__(256) splitk_reduce(GemmArgs a, int splits) {
         }
 #pragma unroll
         for (int q = 0; q < W; ++q) e.out[o + q] = s[q] * act_derivative(e.act, pr[q], y[q]);
+      } else if constexpr (EPI == EPI_DW_OPT && W == 4) {
+        // the four elements' W and optimizer state loaded together (16-byte
+        // accesses: launch_reduce checked the alignment), then the same
+        // per-element update as apply_epilogue, then the stores -- instead
+        // of one dependent load-update-store per element
+        const float lr = e.scalars->lr;
+        const bool has1 = e.opt != VOLTA_OPT_SGD, has2 = e.opt == VOLTA_OPT_ADAM || e.opt == VOLTA_OPT_ADAMW;
+        floatx4 w = *reinterpret_cast<const floatx4*>(e.out + o);
+        floatx4 s1 = has1 ? *reinterpret_cast<const floatx4*>(e.m + o) : floatx4{};
+        floatx4 s2 = has2 ? *reinterpret_cast<const floatx4*>(e.v + o) : floatx4{};
+        const int64_t vec_end = e.count - e.count % 8;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (e.opt == VOLTA_OPT_SGD) {
+            w[q] = w[q] + (-lr) * s[q];  // sgd_fused_tn: W = 1*W + (-lr) * (act_i^T delta_i)  (:321-324)
+          } else if (e.opt == VOLTA_OPT_ADAGRAD) {
+            float a = w[q], b = s1[q];
+            adagrad_elem(&a, &b, s[q], lr, e.eps);
+            w[q] = a, s1[q] = b;
+          } else {
+            float a = w[q], b = s1[q], c = s2[q];
+            adam_elem(&a, &b, &c, s[q], (int64_t)(o + q) >= vec_end, lr, rc, e.b1, e.b2, e.eps, e.wd);
+            w[q] = a, s1[q] = b, s2[q] = c;
+          }
+        }
+        if (e.grad) *reinterpret_cast<floatx4*>(e.grad + o) = floatx4{s[0], s[1], s[2], s[3]};
+        *reinterpret_cast<floatx4*>(e.out + o) = w;
+        if (has1) *reinterpret_cast<floatx4*>(e.m + o) = s1;
+        if (has2) *reinterpret_cast<floatx4*>(e.v + o) = s2;
       } else {
 #pragma unroll
         for (int q = 0; q < W; ++q) apply_epilogue<EPI>(e, m, n + q, s[q], rc);
@@ -1800,7 +1829,7 @@ static hipError_t launch_cfg(const GemmArgs& a, int layout, bool vec, int splits
 template <int EPI>
 static hipError_t launch_reduce(const GemmArgs& a, int splits, hipStream_t st) {
   const size_t total = (size_t)a.M * a.N + (EPI == EPI_DW_OPT && a.colsum_b ? a.N : 0);
-  const bool v4 = a.N % 4 == 0 && a.epi.ldc % 4 == 0;
+  const bool v4 = a.N % 4 == 0 && a.epi.ldc % 4 == 0 && (EPI != EPI_DW_OPT || quad_aligned(a.epi, EPI));
   const size_t items = v4 ? total / 4 : total;
   const int blocks = (int)std::min<size_t>((items + 255) / 256, 1 << 20);
   if (v4) hipLaunchKernelGGL((splitk_reduce<EPI, 4>), dim3(blocks), dim3(256), 0, st, a, splits);
