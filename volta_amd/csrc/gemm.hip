@@ -403,6 +403,7 @@ __host__ __device__ __forceinline__ bool quad_aligned(const EpiArgs& e, int epi)
   auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
   bool ok = e.ldc % 4 == 0 && a16(e.out);
   if (epi == EPI_BIAS_ACT) ok = ok && a16(e.bias) && a16(e.pre);
+  if (epi == EPI_DX_ACT) ok = ok && a16(e.aux_act) && a16(e.aux_pre);
   if (epi == EPI_DW_OPT) ok = ok && a16(e.m) && a16(e.v) && a16(e.grad);
   return ok;
 }
@@ -1699,22 +1700,35 @@ __global__ void __launch_bounds__(256) splitk_reduce(GemmArgs a, int splits) {
         float b[W];
 #pragma unroll
         for (int q = 0; q < W; ++q) b[q] = e.bias[n + q];
+        float x[W], y[W];
 #pragma unroll
         for (int q = 0; q < W; ++q) {
-          const float v = s[q] + b[q];  // pre = act_i W_i + b_i (:716-724)
-          if (e.pre) e.pre[o + q] = v;
-          e.out[o + q] = act_forward(e.act, v);
+          x[q] = s[q] + b[q];  // pre = act_i W_i + b_i (:716-724)
+          y[q] = act_forward(e.act, x[q]);
+        }
+        if constexpr (W == 4) {  // 16-byte stores (launch_reduce checked the alignment)
+          if (e.pre) *reinterpret_cast<floatx4*>(e.pre + o) = floatx4{x[0], x[1], x[2], x[3]};
+          *reinterpret_cast<floatx4*>(e.out + o) = floatx4{y[0], y[1], y[2], y[3]};
+        } else {
+          if (e.pre) e.pre[o] = x[0];
+          e.out[o] = y[0];
         }
       } else if constexpr (EPI == EPI_DX_ACT) {
         const float* pp = e.aux_pre ? e.aux_pre : e.aux_act;
-        float y[W], pr[W];
+        float y[W], pr[W], d[W];
+        if constexpr (W == 4) {
+          const floatx4 y4 = *reinterpret_cast<const floatx4*>(e.aux_act + o);
+          const floatx4 p4 = *reinterpret_cast<const floatx4*>(pp + o);
 #pragma unroll
-        for (int q = 0; q < W; ++q) {
-          y[q] = e.aux_act[o + q];
-          pr[q] = pp[o + q];
+          for (int q = 0; q < W; ++q) y[q] = y4[q], pr[q] = p4[q];
+        } else {
+          y[0] = e.aux_act[o];
+          pr[0] = pp[o];
         }
 #pragma unroll
-        for (int q = 0; q < W; ++q) e.out[o + q] = s[q] * act_derivative(e.act, pr[q], y[q]);
+        for (int q = 0; q < W; ++q) d[q] = s[q] * act_derivative(e.act, pr[q], y[q]);
+        if constexpr (W == 4) *reinterpret_cast<floatx4*>(e.out + o) = floatx4{d[0], d[1], d[2], d[3]};
+        else e.out[o] = d[0];
       } else if constexpr (EPI == EPI_DW_OPT && W == 4) {
         // the four elements' W and optimizer state loaded together (16-byte
         // accesses: launch_reduce checked the alignment), then the same
@@ -1829,7 +1843,7 @@ static hipError_t launch_cfg(const GemmArgs& a, int layout, bool vec, int splits
 template <int EPI>
 static hipError_t launch_reduce(const GemmArgs& a, int splits, hipStream_t st) {
   const size_t total = (size_t)a.M * a.N + (EPI == EPI_DW_OPT && a.colsum_b ? a.N : 0);
-  const bool v4 = a.N % 4 == 0 && a.epi.ldc % 4 == 0 && (EPI != EPI_DW_OPT || quad_aligned(a.epi, EPI));
+  const bool v4 = a.N % 4 == 0 && a.epi.ldc % 4 == 0 && (EPI == EPI_STORE || quad_aligned(a.epi, EPI));
   const size_t items = v4 ? total / 4 : total;
   const int blocks = (int)std::min<size_t>((items + 255) / 256, 1 << 20);
   if (v4) hipLaunchKernelGGL((splitk_reduce<EPI, 4>), dim3(blocks), dim3(256), 0, st, a, splits);
