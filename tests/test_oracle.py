@@ -20,7 +20,8 @@ import numpy as np
 import pytest
 
 from tests.oracle_lib import load_ref_shim
-from volta_amd.abi import HEADER_SYMBOLS, MlpSpec, Trainer, fptr
+from volta_amd.abi import (BUF_DELTA, BUF_DROPOUT_MASK, BUF_LN_BETA, BUF_LN_GAMMA, HEADER_SYMBOLS, MlpSpec, Trainer,
+                           fptr)
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 GOLDEN = json.load(open(os.path.join(HERE, "golden", "train_step_golden.json")))["cases"]
@@ -603,6 +604,139 @@ def test_f64_layernorm_gradient_matches_finite_differences(oracle, act):
             wm[li][a, b] -= h
             fd = (loss_at(wp) - loss_at(wm)) / (2 * (np.float64(wp[li][a, b]) - np.float64(ws[li][a, b])))
             assert abs(fd - grad[a, b]) <= 2e-3 * max(1.0, abs(fd)), (li, a, b, fd, grad[a, b])
+
+
+def _buf64(oracle, t, kind, layer, n):
+    out = np.zeros(n, np.float64)
+    got = oracle.lib.volta_oracle_debug_buffer_f64(t.h, kind, layer, out.ctypes.data_as(C.POINTER(C.c_double)))
+    assert got == n, (kind, layer, got)
+    return out
+
+
+def _textbook_layernorm(a):
+    """Per-row standardisation with eps 1e-5 (gamma 1, beta 0): x-hat and
+    1/sigma."""
+    mu = a.mean(axis=1, keepdims=True)
+    var = ((a - mu) ** 2).mean(axis=1, keepdims=True)
+    inv = 1.0 / np.sqrt(var + np.float64(np.float32(1e-5)))
+    return (a - mu) * inv, inv
+
+
+@pytest.mark.parametrize("act", ["sigmoid", "tanh"])
+def test_f64_sigmoid_tanh_layernorm_derivative_at_the_layernorm_output(oracle, act):
+    """Sigmoid/tanh followed by LayerNorm (mlp_train_rust_codegen.rs:908-914):
+    the reference multiplies the LayerNorm backward by the activation's
+    derivative written in its output -- y(1 - y), 1 - y^2 -- evaluated at the
+    LayerNorm output y, not at the activation's own output.  With one hidden
+    layer, no dropout and B = 1 its LayerNorm backward is the textbook one, so
+    the hidden delta must equal the true gradient with respect to the
+    pre-activation (central differences of the fp64 twin's loss over b_0)
+    times g(y_j) / f'(z_j), unit by unit -- z the pre-activation, y the
+    textbook LayerNorm of f(z).  The true derivative would fail: the ratio
+    is far from 1 here."""
+    spec = MlpSpec([4, 6, 2], act, "sgd", layernorm=True)
+    rng = np.random.default_rng(31)
+    ws = [rng.uniform(-0.9, 0.9, (r, c)).astype(np.float32) for r, c in spec.shapes()]
+    bs = [rng.uniform(-0.3, 0.3, c).astype(np.float32) for _, c in spec.shapes()]
+    X = rng.standard_normal((1, 4)).astype(np.float32)
+    Y = rng.standard_normal((1, 2)).astype(np.float32)
+
+    def loss_at(b0):
+        t = oracle_trainer(oracle, spec, 1, f64=True)
+        t.set_all_params(ws, [b0] + bs[1:])
+        t.step(X, Y, 0.0)
+        v = float(oracle.lib.volta_oracle_loss_f64(t.h))
+        t.close()
+        return v
+
+    t = oracle_trainer(oracle, spec, 1, f64=True)
+    t.set_all_params(ws, bs)
+    t.step(X, Y, 0.0)
+    delta = _buf64(oracle, t, BUF_DELTA, 0, 6)
+    t.close()
+    z = (X.astype(np.float64) @ ws[0].astype(np.float64) + bs[0])[0]
+    a = 1.0 / (1.0 + np.exp(-z)) if act == "sigmoid" else np.tanh(z)
+    fprime = a * (1.0 - a) if act == "sigmoid" else 1.0 - a * a
+    y = _textbook_layernorm(a[None, :])[0][0]
+    g = y * (1.0 - y) if act == "sigmoid" else 1.0 - y * y
+    assert np.abs(g / fprime - 1.0).max() > 0.1
+    for j in range(6):
+        bp, bm = bs[0].copy(), bs[0].copy()
+        bp[j] += np.float32(1e-4)
+        bm[j] -= np.float32(1e-4)
+        fd = (loss_at(bp) - loss_at(bm)) / (np.float64(bp[j]) - np.float64(bm[j]))
+        want = fd * g[j] / fprime[j]
+        assert abs(delta[j] - want) <= 1e-5 * abs(want) + 1e-9, (j, delta[j], want, fd)
+
+
+def test_f64_layernorm_then_dropout_backward(oracle):
+    """LayerNorm followed by dropout (:742-790 forward, :829-880 backward):
+    the reference runs the LayerNorm backward on the gradient with respect
+    to the dropout output g, with x-hat recomputed from the stored output
+    after dropout d = s * mask * x-hat (s = 1/(1-p)), then applies the mask,
+    then ReLU's derivative; dgamma = g * d and dbeta = g.  Pinned with one
+    hidden layer and B = 1 against quantities fixed independently: the mask
+    (the LCG written out with Python integers), the textbook LayerNorm
+    forward, and g itself -- for a kept unit g = u / s with u the true
+    gradient over beta (central differences of the fp64 twin's loss, which is
+    quadratic in beta, so they are exact), and each dropped unit's outgoing
+    weights are set to a kept unit's so its g is that unit's.  The textbook
+    order (mask first, x-hat from the LayerNorm output) gives another delta
+    here."""
+    H, p = 8, 0.3
+    spec = MlpSpec([4, H, 2], "relu", "sgd", layernorm=True, dropout_p=p)
+    keep, _ = _lcg_keep(H, p)  # B = 1: the first step's mask of the hidden layer
+    kept, dropped = np.flatnonzero(keep), np.flatnonzero(~keep)
+    assert kept.size and dropped.size
+    rng = np.random.default_rng(41)
+    ws = [rng.uniform(-0.8, 0.8, (r, c)).astype(np.float32) for r, c in spec.shapes()]
+    bs = [rng.uniform(-0.2, 0.4, c).astype(np.float32) for _, c in spec.shapes()]
+    partner = {int(j): int(kept[i % kept.size]) for i, j in enumerate(dropped)}
+    for j, k in partner.items():
+        ws[1][j] = ws[1][k]
+    X = rng.standard_normal((1, 4)).astype(np.float32)
+    Y = rng.standard_normal((1, 2)).astype(np.float32)
+    s = np.float64(np.float32(1.0) / (np.float32(1.0) - np.float32(p)))  # the reference's f32 literal
+
+    def run(beta, lr):
+        t = oracle_trainer(oracle, spec, 1, f64=True)
+        t.set_all_params(ws, bs)
+        t.set_state(np.concatenate([np.ones(H, np.float32), beta.astype(np.float32)]), 0)
+        t.set_dropout_rng(12345678)
+        t.step(X, Y, lr)
+        return t
+
+    u = np.zeros(H)
+    for j in range(H):
+        bp, bm = np.zeros(H, np.float32), np.zeros(H, np.float32)
+        bp[j], bm[j] = np.float32(1e-2), np.float32(-1e-2)
+        lv = []
+        for beta in (bp, bm):
+            t = run(beta, 0.0)
+            lv.append(float(oracle.lib.volta_oracle_loss_f64(t.h)))
+            t.close()
+        u[j] = (lv[0] - lv[1]) / (np.float64(bp[j]) - np.float64(bm[j]))
+    assert np.abs(u[dropped]).max() < 1e-12  # a dropped unit does not reach the loss
+    g = np.zeros(H)
+    g[kept] = u[kept] / s
+    for j, k in partner.items():
+        g[j] = g[k]
+    z = (X.astype(np.float64) @ ws[0].astype(np.float64) + bs[0])[0]
+    xhat, inv = _textbook_layernorm(np.maximum(z, 0.0)[None, :])
+    xhat, inv = xhat[0], float(inv[0, 0])
+    d = s * keep * xhat
+    want = keep * s * inv * (g - g.mean() - d * (g * d).mean()) * (z > 0)
+    t = run(np.zeros(H, np.float32), 1.0)
+    np.testing.assert_array_equal(_buf64(oracle, t, BUF_DROPOUT_MASK, 0, H), keep.astype(np.float64))
+    delta = _buf64(oracle, t, BUF_DELTA, 0, H)
+    dgamma = 1.0 - _buf64(oracle, t, BUF_LN_GAMMA, 0, H)
+    dbeta = -_buf64(oracle, t, BUF_LN_BETA, 0, H)
+    t.close()
+    np.testing.assert_allclose(delta, want, rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(dbeta, g, rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(dgamma, g * d, rtol=1e-9, atol=1e-12)
+    textbook = keep * inv * ((s * keep * g) - (s * keep * g).mean() - xhat * (s * keep * g * xhat).mean()) * (z > 0)
+    assert np.abs(textbook - want).max() > 1e-3 * np.abs(want).max()
 
 
 def test_oracle_clip_scales_dw_but_not_db(oracle):
