@@ -140,8 +140,9 @@ struct Handle {
 
   // --- host side -------------------------------------------------------------
   float* h_params = nullptr;  // pinned mirror returned by get_params
-  float* h_stage_x = nullptr;
-  void* h_stage_y = nullptr;
+  float* h_stage_x = nullptr;   // pinned [X | gap | Y] (one allocation)
+  void* h_stage_y = nullptr;    // its Y part, stage_y_off bytes in
+  size_t stage_y_off = 0;
   hipEvent_t stage_free = nullptr;  // staging buffers may be overwritten
   static constexpr int kLrSlots = 64;
   float* h_lr = nullptr;
@@ -165,7 +166,6 @@ Handle::~Handle() {
   if (stage_free) (void)hipEventDestroy(stage_free);
   if (h_params) (void)hipHostFree(h_params);
   if (h_stage_x) (void)hipHostFree(h_stage_x);
-  if (h_stage_y) (void)hipHostFree(h_stage_y);
   if (h_lr) (void)hipHostFree(h_lr);
   if (bc_table) (void)hipFree(bc_table);
   if (infer_x) (void)hipFree(infer_x);
@@ -880,7 +880,11 @@ static bool build(Handle* h) {
   h->act.assign(n + 1, nullptr);
   h->pre.assign(n, nullptr);
   h->delta.assign(n, nullptr);
-  for (int i = 0; i <= n; ++i) req((void**)&h->act[i], (size_t)B * h->L[i] * 4);
+  // the targets right after act_0, 256-byte aligned, with the same gap as in
+  // the pinned staging buffer: a host-staged step copies both in one transfer
+  req((void**)&h->act[0], (size_t)B * h->L[0] * 4);
+  req(&h->target, s.loss == VOLTA_LOSS_MSE ? (size_t)B * h->L[n] * 4 : (size_t)B * 4);
+  for (int i = 1; i <= n; ++i) req((void**)&h->act[i], (size_t)B * h->L[i] * 4);
   for (int i = 0; i < n - 1; ++i)
     if (act_needs_pre(s.activation) || h->hidden_ext()) req((void**)&h->pre[i], (size_t)B * h->L[i + 1] * 4);
   h->ln_g.assign(n, nullptr);
@@ -904,7 +908,6 @@ static bool build(Handle* h) {
   }
   if (h->ext_clip) req((void**)&h->clip_partials, kClipBlocks * 4);
   for (int i = 0; i < n; ++i) req((void**)&h->delta[i], (size_t)B * h->L[i + 1] * 4);
-  req(&h->target, s.loss == VOLTA_LOSS_MSE ? (size_t)B * h->L[n] * 4 : (size_t)B * 4);
   if (ws_floats) req((void**)&h->gemm_ws, ws_floats * 4);
   req((void**)&h->counters, (size_t)h->n_counters * sizeof(unsigned));
   req((void**)&h->loss_partials,
@@ -923,8 +926,11 @@ static bool build(Handle* h) {
 
   // Host side: pinned parameter mirror, input staging, lr slots.
   VOLTA_CHECK(hipHostMalloc((void**)&h->h_params, (size_t)h->flat * 4, hipHostMallocDefault));
-  VOLTA_CHECK(hipHostMalloc((void**)&h->h_stage_x, (size_t)B * h->L[0] * 4, hipHostMallocDefault));
-  VOLTA_CHECK(hipHostMalloc(&h->h_stage_y, (size_t)B * std::max(h->L[n], 1) * 4, hipHostMallocDefault));
+  // [X | gap | Y], laid out as act_0 and the targets are in the arena
+  h->stage_y_off = align_up((size_t)B * h->L[0] * 4, 256);
+  VOLTA_CHECK(hipHostMalloc((void**)&h->h_stage_x, h->stage_y_off + (size_t)B * std::max(h->L[n], 1) * 4,
+                            hipHostMallocDefault));
+  h->h_stage_y = reinterpret_cast<char*>(h->h_stage_x) + h->stage_y_off;
   VOLTA_CHECK(hipHostMalloc((void**)&h->h_lr, Handle::kLrSlots * sizeof(float), hipHostMallocDefault));
   VOLTA_CHECK(hipEventCreateWithFlags(&h->stage_free, hipEventDisableTiming));
   for (auto& e : h->lr_ev) VOLTA_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
@@ -1050,8 +1056,10 @@ static bool stage_inputs(Handle* h, const float* X, const void* Y, size_t ybytes
   VOLTA_CHECK(hipEventSynchronize(h->stage_free));
   std::memcpy(h->h_stage_x, X, xbytes);
   std::memcpy(h->h_stage_y, Y, ybytes);
-  VOLTA_CHECK(hipMemcpyAsync(h->act[0], h->h_stage_x, xbytes, hipMemcpyHostToDevice, h->stream));
-  VOLTA_CHECK(hipMemcpyAsync(h->target, h->h_stage_y, ybytes, hipMemcpyHostToDevice, h->stream));
+  // act_0 and the targets are adjacent in the arena as in the staging buffer
+  // (the gap is copied too): one host-to-device transfer per step
+  if (static_cast<char*>(h->target) != reinterpret_cast<char*>(h->act[0]) + h->stage_y_off) return false;
+  VOLTA_CHECK(hipMemcpyAsync(h->act[0], h->h_stage_x, h->stage_y_off + ybytes, hipMemcpyHostToDevice, h->stream));
   VOLTA_CHECK(hipEventRecord(h->stage_free, h->stream));
   return true;
 }
