@@ -1000,6 +1000,70 @@ def test_resident_batch_step_device():
     b.close()
 
 
+def test_host_and_device_steps_interleaved():
+    """Host-staged steps (the caller overwriting its X/Y right after each
+    call; X and Y travel in one transfer), steps on the resident buffers,
+    steps from other device buffers and a hyperparameter change (a new
+    graph) in between: bit-identical to the same inputs as plain host steps
+    on a second handle, act_0 holds the last step's batch, and the
+    trajectory is within rel 1e-4 of the oracle's."""
+    say("host-staged and device steps interleaved")
+    hip = load_hip()
+    spec, B = MlpSpec([24, 48, 32, 6], "tanh", "adam"), 16
+    ws, bs = data.he_uniform(5, spec.sizes)
+    rng = np.random.default_rng(17)
+    batches = [(rng.standard_normal((B, 24)).astype(np.float32), rng.standard_normal((B, 6)).astype(np.float32))
+               for _ in range(4)]
+    a = Trainer(hip, spec, B)
+    b = Trainer(hip, spec, B)
+    o = Trainer(load_oracle(), spec, B)
+    for t in (a, b, o):
+        t.set_all_params(ws, bs)
+    dev = [(DeviceArray(X), DeviceArray(Y)) for X, Y in batches]
+    plan = ["h0", "h1", "r", "h2", "h3", "d1", "r", "h0", "hp", "h2", "r", "d3", "h1"]
+    last = None
+    for k, op in enumerate(plan):
+        if op == "hp":  # new hyperparameters: the step graph captured again
+            for t in (a, b, o):
+                t.set_hparams(0.8, 0.99, 1e-7, 0.0)
+            continue
+        if op == "r":  # the resident batch again
+            xp, yp = a.batch_buffers()
+            assert a.step_device(xp, yp, 1e-3) == 0
+            X, Y = last
+        elif op[0] == "d":  # another device buffer pair, copied into the resident buffers
+            i = int(op[1])
+            assert a.step_device(dev[i][0].ptr, dev[i][1].ptr, 1e-3) == 0
+            X, Y = batches[i]
+        else:
+            i = int(op[1])
+            Xc, Yc = batches[i][0].copy(), batches[i][1].copy()
+            a.step(Xc, Yc, 1e-3)
+            Xc[:] = np.nan  # the caller reuses its buffers at once
+            Yc[:] = np.nan
+            X, Y = batches[i]
+        last = (X, Y)
+        b.step(X, Y, 1e-3)
+        o.step(X, Y, 1e-3)
+        la, lb, lo = a.loss(), b.loss(), o.loss()
+        assert la == lb, (k, op, la, lb)
+        assert abs(la - lo) <= 1e-4 * abs(lo) + 1e-5, (k, op, la, lo)
+    from volta_amd.abi import BUF_ACT
+    np.testing.assert_array_equal(a.debug_buffer(BUF_ACT, 0).reshape(B, 24), last[0])
+    assert a.status() == 0 and b.status() == 0
+    wa, ba = a.get_params()
+    wb, bb = b.get_params()
+    for p, q in zip(wa + ba, wb + bb):
+        np.testing.assert_array_equal(p, q)
+    wo, bo = o.get_params()
+    assert_params_close(wa, ba, wo, bo, "interleaved steps")
+    for t in (a, b, o):
+        t.close()
+    for d in dev:
+        d[0].free()
+        d[1].free()
+
+
 def test_state_roundtrip_resumes_bit_identically():
     say("state roundtrip")
     hip = load_hip()
