@@ -641,6 +641,15 @@ def main(argv=None):
         os.environ["HSA_ENABLE_INTERRUPT"] = "0"
     else:
         os.environ.pop("HSA_ENABLE_INTERRUPT", None)
+    # The CPU legs run first, before this process's first HIP call: once the
+    # HSA runtime has started with polled completion signals, its event
+    # thread spins on a host core and an all-cores OpenMP step slows many
+    # times over (C2 4.4 -> 160-180 ms on 16 threads).
+    cpu_primary = cpu_secondary = None
+    if not a.no_cpu:
+        cpu_primary = run_cpu(a.config, a.cpu_threads)
+        if a.secondary and a.secondary != "none":
+            cpu_secondary, _ = run_cpu(a.secondary, a.cpu_threads, full_protocol=False)
     spec, B, lr, res = run_gpu(a.config, a.steps, a.warmup, want_profile=not a.no_profile)
     log(f"{a.config}: {res['ms_per_step']:.4f} ms/step, {res['samples_per_s']:.0f} samples/s")
     line = {
@@ -674,8 +683,8 @@ def main(argv=None):
                            for r in res["kernels"]]
     if a.config in PUBLISHED_CPU:
         line["reference_published_cpu"] = PUBLISHED_CPU[a.config]
-    if not a.no_cpu:
-        line["cpu_baseline"], line["cpu_baseline_legs"] = run_cpu(a.config, a.cpu_threads)
+    if cpu_primary:
+        line["cpu_baseline"], line["cpu_baseline_legs"] = cpu_primary
         line["cpu_host"] = host_cpu()
     if a.secondary and a.secondary != "none":
         s_steps = max(5, a.steps // 20)
@@ -693,8 +702,8 @@ def main(argv=None):
             sec["roofline"] = s_res["roofline"]
             sec["kernels"] = [{k: (round(v, 5) if isinstance(v, float) else v) for k, v in r.items()}
                               for r in s_res["kernels"]]
-        if not a.no_cpu:
-            sec["cpu_baseline"], _ = run_cpu(a.secondary, a.cpu_threads, full_protocol=False)
+        if cpu_secondary:
+            sec["cpu_baseline"] = cpu_secondary
         line["secondary"] = sec
     if not a.no_profile and not a.no_extra_legs:
         line["runtime_optimizer"] = run_rt_optimizer()
