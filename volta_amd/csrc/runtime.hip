@@ -1311,6 +1311,27 @@ int32_t volta_hip_time_kernel(VoltaTrainHandle* vh, int32_t index, int32_t reps,
   if (!h || index < 0 || reps <= 0 || !avg_ms) return -1;
   double total[2] = {0.0, 0.0};
   std::string lab;
+  // Every timed step is preceded by about 0.2 ms of graph-replayed steps, so
+  // the host has enqueued the timed step's launches (a few microseconds of
+  // host work each) before the GPU reaches them: the launch then starts when
+  // its predecessor ends, as in a replayed step, and its interval holds no
+  // host enqueue time, which the back-to-back marker pair would not see.
+  int prelude = 1;
+  {
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    float step_ms = 0.0f;
+    const bool ok = hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess &&
+                    hipEventRecord(e0, h->stream) == hipSuccess && volta::launch_step(h) &&
+                    hipEventRecord(e1, h->stream) == hipSuccess && hipStreamSynchronize(h->stream) == hipSuccess &&
+                    hipEventElapsedTime(&step_ms, e0, e1) == hipSuccess;
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (!ok) {
+      volta::set_last_error("volta_hip_time_kernel: step timing failed");
+      return -1;
+    }
+    prelude = std::min(8, std::max(1, (int)std::ceil(0.2 / std::max(step_ms, 1e-3f))));
+  }
   for (int r = 0; r < 2 * reps; ++r) {
     const bool empty = r % 2 == 1;
     volta::Recorder rec;
@@ -1318,6 +1339,8 @@ int32_t volta_hip_time_kernel(VoltaTrainHandle* vh, int32_t index, int32_t reps,
     rec.target = index;
     rec.empty = empty;
     float ms = 0.0f;
+    for (int k = 0; k < prelude; ++k)
+      if (!volta::launch_step(h)) return -1;
     if (hipEventCreate(&rec.before) != hipSuccess || hipEventCreate(&rec.after) != hipSuccess ||
         (index == 0 && hipEventRecord(rec.before, h->stream) != hipSuccess) ||
         (index == 0 && empty && hipEventRecord(rec.after, h->stream) != hipSuccess)) {
