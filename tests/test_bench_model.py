@@ -9,17 +9,17 @@ import pytest
 import bench
 
 # (GFLOP, MB) per step, as the survey tabulates them for every BASELINE config
-SURVEY_STEP = {
+MODEL_STEP_FIGURES = {
     "c1": (0.185, 15.0), "c2": (0.789, 93.6), "c3": (2.282, 258.0), "c4_128": (1.577, 64.4),
     "c4_256": (3.155, 77.4), "c4_1024": (12.618, 155.3), "c5": (584.4, 2115),
 }
 
 
-@pytest.mark.parametrize("name", sorted(SURVEY_STEP))
+@pytest.mark.parametrize("name", sorted(MODEL_STEP_FIGURES))
 def test_step_model_matches_survey(name):
     spec, B, _ = bench.WORKLOADS[name]
     fl, by = bench.survey_step_cost(spec, B)
-    gf, mb = SURVEY_STEP[name]
+    gf, mb = MODEL_STEP_FIGURES[name]
     assert round(fl / 1e9, 3 if gf < 100 else 1) == gf
     assert round(by / 1e6, 1 if mb < 1000 else 0) == mb
     assert bench.gemm_flops(spec, B) == pytest.approx(fl, rel=1e-12)
