@@ -28,9 +28,12 @@ namespace {
 constexpr uint64_t kLcgA = 6364136223846793005ULL;
 constexpr uint64_t kLcgC = 1442695040888963407ULL;
 
-// State after m draws from s: the affine map s -> A*s + C applied m times,
-// composed by squaring (maps of one LCG commute).
-__device__ __forceinline__ uint64_t lcg_jump(uint64_t s, uint64_t m) {
+// The affine map s -> A*s + C of m draws, composed by squaring (maps of one
+// LCG commute).
+struct LcgMap {
+  uint64_t a, c;
+};
+__device__ __forceinline__ LcgMap lcg_map(uint64_t m) {
   uint64_t a = kLcgA, c = kLcgC, ra = 1, rc = 0;
   while (m) {
     if (m & 1) {
@@ -41,7 +44,13 @@ __device__ __forceinline__ uint64_t lcg_jump(uint64_t s, uint64_t m) {
     a = a * a;
     m >>= 1;
   }
-  return ra * s + rc;
+  return {ra, rc};
+}
+
+// State after m draws from s.
+__device__ __forceinline__ uint64_t lcg_jump(uint64_t s, uint64_t m) {
+  const LcgMap f = lcg_map(m);
+  return f.a * s + f.c;
 }
 
 // Sum of v over the 256 threads of the block, the same value in every
@@ -115,7 +124,16 @@ __global__ void __launch_bounds__(256) hidden_fwd_kernel(HiddenFwdArgs a) {
       a.inv_std[b] = is;
     }
   }
-  const uint64_t base = a.mask ? a.scalars->rng : 0;
+  // Element k = b*c + j of the layer draws state jump(base, offset + k + 1):
+  // the thread's first element by one jump from the stream, its next ones
+  // (blockDim.x apart) by the map of blockDim.x draws -- the same states as
+  // a jump per element.
+  uint64_t st = 0;
+  LcgMap stride{1, 0};
+  if (a.mask) {
+    st = lcg_jump(a.scalars->rng, a.rng_offset + (uint64_t)b * c + threadIdx.x + 1);
+    stride = lcg_map(blockDim.x);
+  }
   for (int j = threadIdx.x; j < c; j += blockDim.x) {
     float x = row[j];
     if (a.gamma) {
@@ -124,11 +142,11 @@ __global__ void __launch_bounds__(256) hidden_fwd_kernel(HiddenFwdArgs a) {
     }
     if (a.mask) {
       const uint64_t k = (uint64_t)b * c + j;
-      const uint64_t s = lcg_jump(base, a.rng_offset + k + 1);
-      const float r = (float)(s >> 33) / 2147483648.0f;
+      const float r = (float)(st >> 33) / 2147483648.0f;
       const uint8_t keep = r >= a.p ? 1 : 0;
       a.mask[k] = keep;
       x = x * ((float)keep * a.keep_scale);
+      st = stride.a * st + stride.c;
     }
     row[j] = x;
   }
