@@ -186,6 +186,31 @@ def test_misaligned_bindings_take_the_elementwise_path(rows):
     assert_close(aligned, want, "aligned")
 
 
+def test_big_tile_layer_into_unaligned_output():
+    """A 4096-row graph whose last layer runs on the 256x256 tile with its
+    bias epilogue, written straight into the caller's output: an output 4
+    bytes off a 16-byte boundary (the epilogue's 4-byte path) holds the same
+    bits as an aligned one."""
+    layers, rows = [1024, 4096, 4096], 4096
+    say("big-tile layer into an unaligned output")
+    g = model_graph(layers, "relu", rows)
+    plan = build_execution_plan(g)
+    b = Bound(mlp_values(layers, rows, 13))
+    lib = GraphLibrary(load_hip().lib)
+    n = rows * layers[-1]
+    outs = []
+    for off in (0, 1):
+        out = DeviceArray(np.zeros(n + 1, F32))
+        try:
+            r, c = lib.execute(g, plan, None, b.addr, out.ptr + 4 * off, n)
+            assert (r, c) == (rows, layers[-1])
+            outs.append(out.numpy()[off:off + n].copy())
+        finally:
+            out.free()
+    assert np.isfinite(outs[0]).all() and (outs[0] > 0).any()
+    np.testing.assert_array_equal(outs[1], outs[0])
+
+
 def test_repeated_runs_bit_identical_and_cache_reused():
     layers = [128, 256, 256, 10]
     g = model_graph(layers, "softmax", 96)
