@@ -2330,7 +2330,15 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus, bool 
   // B=1024 both tiles are slower than the 64x64 family (0.45 vs 0.30 ms).
   const char* sm = std::getenv("VOLTA_SMALLM_MAX_M");
   const int small_max = sm && *sm ? std::atoi(sm) : 256;
-  if (small_m && (layout == GEMM_NN || layout == GEMM_NT) && p.splits > 1 && M <= small_max) {
+  // ... except a dX product (NT) with a long reduction: there the 16x16
+  // tiles' operand re-reads from L2 cost more than the split's reduce launch
+  // (C3's dX_1, 64 x 2048 x 2048: 18.4 us on the small-M tile against
+  // 7.3 + 2.2 us split).  VOLTA_NT_SPLIT_MIN sets the M*K threshold (with
+  // K >= 1024); 0 keeps every such product on the small-M tile.
+  const char* ns = std::getenv("VOLTA_NT_SPLIT_MIN");
+  const long nt_split_min = ns && *ns ? std::atol(ns) : 131072L;
+  const bool nt_long = layout == GEMM_NT && nt_split_min > 0 && K >= 1024 && (long)M * K >= nt_split_min;
+  if (small_m && (layout == GEMM_NN || layout == GEMM_NT) && p.splits > 1 && M <= small_max && !nt_long) {
     p.tile = TILE_SMALLM;
     p.splits = 1;
     p.k_per_split = K;
