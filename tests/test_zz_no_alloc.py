@@ -55,14 +55,16 @@ def test_noalloc_infer_matches_infer(name):
 
 
 def test_noalloc_rejects_workspace_beyond_scratch():
-    """With the split-K planner asked for 8 workgroups per CU, a 1024x1024
-    product with K=4096 splits K 16 ways: 16 x 1025 x 1024 floats of partial
-    planes, above the 64 MiB scratch.  The call is refused on the host with
-    a message naming both sizes; nothing is launched."""
+    """With the split-K planner asked for 8 workgroups per CU and 128x128
+    tiles from 2^20 outputs, a 1024x1024 product with K=4096 splits K 16
+    ways: 16 x 1025 x 1024 floats of partial planes, above the 64 MiB
+    scratch.  The call is refused on the host with a message naming both
+    sizes; nothing is launched."""
     lib = load_hip()
     spec = MlpSpec([4096, 1024, 10], "relu", "sgd", "ce")
-    old = os.environ.get("VOLTA_SPLITK_WGS_PER_CU")
-    os.environ["VOLTA_SPLITK_WGS_PER_CU"] = "8"
+    env = {"VOLTA_SPLITK_WGS_PER_CU": "8", "VOLTA_TILE128_MIN_MN": str(1 << 20)}
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
     try:
         t = Trainer(lib, spec, 1024)
         dX = DeviceArray(np.zeros((1024, 4096), np.float32), lib)
@@ -70,10 +72,11 @@ def test_noalloc_rejects_workspace_beyond_scratch():
         rc = lib.lib.volta_train_infer_device_noalloc(t.h, dX.ptr, 1024, dO.ptr)
         msg = lib.last_error()
     finally:
-        if old is None:
-            os.environ.pop("VOLTA_SPLITK_WGS_PER_CU", None)
-        else:
-            os.environ["VOLTA_SPLITK_WGS_PER_CU"] = old
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
     assert rc == -1
     assert "split-K workspace" in msg and str(16 << 22) in msg, msg
     t.clear_status()

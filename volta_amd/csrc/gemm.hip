@@ -2125,7 +2125,13 @@ bool pair_supported(const PairOp& a, const PairOp& b) {
              o.plan.waves == 4 && smallm_vec_ok(o.args, GEMM_NT);
     if (o.plan.tile == TILE_DW_SMALLK)
       return o.plan.splits == 1 && o.args.epi.kind == EPI_DW_OPT && dw_smallk_ok(o.args, GEMM_TN);
-    return o.plan.tile == TILE_64x64 && o.plan.vec && !o.plan.inkernel_reduce &&
+    // GemmOp64 runs K slice blk / tiles of ceil(K / k_per_split) and the
+    // pair launches tiles * splits blocks, so the two must agree: a plan
+    // whose slices run as K groups inside one workgroup (kgroups > 1,
+    // splits 1) launches on its own.
+    const int kps = std::max(o.plan.k_per_split, 1);
+    return o.plan.tile == TILE_64x64 && o.plan.vec && !o.plan.inkernel_reduce && o.plan.kgroups == 1 &&
+           (o.args.K + kps - 1) / kps == o.plan.splits &&
            ((o.plan.layout == GEMM_NT && o.args.epi.kind == EPI_DX_ACT) ||
             (o.plan.layout == GEMM_TN && o.args.epi.kind == EPI_DW_OPT)) &&
            (o.plan.splits == 1 || o.args.partial) &&
@@ -2289,10 +2295,16 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus, bool 
   GemmPlan p;
   p.layout = layout;
   p.vec = vec;
-  // 128x128 tiles only where there is enough K to amortise them; a short K
-  // (dW at small batch) is epilogue bound and wants the 4x larger grid.
-  p.tile = ((size_t)M * N >= (size_t)1024 * 1024 && M >= 128 && N >= 128 && K > 256) ? TILE_128x128
-                                                                                      : TILE_64x64;
+  // 128x128 tiles only where there is enough K to amortise them (a short K,
+  // dW at small batch, is epilogue bound and wants the 4x larger grid) and
+  // where their grid has a tile per CU (M*N >= 256 * 128^2 = 4M outputs):
+  // below that the 64x64 grid needs a quarter of the K split and its reduce
+  // reads a quarter of the planes (C4 B=1024, 1024 x 1024 products: 0.280 ->
+  // 0.256 ms/step; C5's 4096 x 1024 products keep 128x128, 4.61 against
+  // 4.87 ms/step).  VOLTA_TILE128_MIN_MN changes the threshold.
+  const char* t128 = std::getenv("VOLTA_TILE128_MIN_MN");
+  const size_t mn128 = t128 && *t128 ? (size_t)std::atoll(t128) : (size_t)4096 * 1024;
+  p.tile = ((size_t)M * N >= mn128 && M >= 128 && N >= 128 && K > 256) ? TILE_128x128 : TILE_64x64;
   const char* sb = std::getenv("VOLTA_SMALL_BK");
   if (p.tile == TILE_64x64 && sb && std::atoi(sb) == 64) p.tile = TILE_64x64_K64;
   if (big_tile_fits(layout, M, N, K, vec, num_cus)) {
@@ -2358,9 +2370,11 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus, bool 
   // tile but for dW) runs inside one workgroup instead, the slices on groups
   // of its waves (gemm_tile's K groups): no partial planes, no reduce
   // launch, the same sums -- but slower here (C5 4.63 -> 4.64 ms, C4 B=1024
-  // 0.282 -> 0.289 ms): the groups meet at every stage's barrier, where two
-  // 4-wave workgroups per CU cover each other's, and a grid of fewer tiles
-  // than CUs runs on fewer CUs.  Only where the epilogue is per element.
+  // 0.282 -> 0.289 ms with 128x128 tiles for its 1024-wide products): the
+  // groups meet at every stage's barrier, where two 4-wave workgroups per CU
+  // cover each other's, and a grid of fewer tiles than CUs runs on fewer
+  // CUs.  Only where the epilogue is per element; such a product launches
+  // on its own, never in a paired launch.
   const char* kg = std::getenv("VOLTA_KGROUPS");
   const int kg_max = p.tile == TILE_64x64 && layout != GEMM_TN ? 4 : p.tile == TILE_64x64 || p.tile == TILE_128x128 ? 2 : 1;
   if (kg && *kg == '1' && small_m && !p.inkernel_reduce && p.splits > 1 && p.splits <= kg_max) {
