@@ -832,15 +832,20 @@ KGROUP_STEP_CASES = {
 @pytest.mark.parametrize("name", sorted(KGROUP_STEP_CASES))
 def test_kgroups_steps_bit_identical(name):
     """Split-K products with their slices on groups of one workgroup's waves
-    (VOLTA_KGROUPS=1) give the same bits as the split launches and their
-    reduce kernel: losses, parameters, activations and deltas after 3 steps."""
+    -- everywhere they apply (VOLTA_KGROUPS=1) and where the planner takes
+    them by default (the variable unset: C4 B=1024's two 1024-wide forward
+    products) -- give the same bits as the split launches and their reduce
+    kernel (VOLTA_KGROUPS=0): losses, parameters, activations and deltas
+    after 3 steps."""
     spec, B, lr = KGROUP_STEP_CASES[name]
     say(f"K groups {name}")
+    assert "VOLTA_KGROUPS" not in os.environ
     l1, p1, b1 = _run_with_env({"VOLTA_KGROUPS": "0"}, spec, B, lr, 3)
-    l2, p2, b2 = _run_with_env({"VOLTA_KGROUPS": "1"}, spec, B, lr, 3)
-    np.testing.assert_array_equal(l1, l2)
-    for a, b in zip(p1 + b1, p2 + b2):
-        np.testing.assert_array_equal(a, b)
+    for env in ({"VOLTA_KGROUPS": "1"}, {}):
+        l2, p2, b2 = _run_with_env(env, spec, B, lr, 3)
+        np.testing.assert_array_equal(l1, l2)
+        for a, b in zip(p1 + b1, p2 + b2):
+            np.testing.assert_array_equal(a, b)
 
 
 OUT_DX_CASES = {

@@ -2366,18 +2366,23 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus, bool 
     p.splits = 1;
     p.k_per_split = K;
   }
-  // Opt-in (VOLTA_KGROUPS=1): a split of up to 2 slices (4 on the 64x64
+  // K groups (gemm_tile's KG): a split of up to 2 slices (4 on the 64x64
   // tile but for dW) runs inside one workgroup instead, the slices on groups
-  // of its waves (gemm_tile's K groups): no partial planes, no reduce
-  // launch, the same sums -- but slower here (C5 4.63 -> 4.64 ms, C4 B=1024
-  // 0.282 -> 0.289 ms with 128x128 tiles for its 1024-wide products): the
-  // groups meet at every stage's barrier, where two 4-wave workgroups per CU
-  // cover each other's, and a grid of fewer tiles than CUs runs on fewer
-  // CUs.  Only where the epilogue is per element; such a product launches
+  // of its waves: no partial planes, no reduce launch, the same sums.  By
+  // default only for a forward product on 64x64 tiles split in two whose
+  // grid already has a tile per CU (C4 B=1024's fwd0 and fwd1: 17.4 -> 17.3
+  // and 28.5 -> 26.9 us against split + reduce, one launch fewer each).
+  // Elsewhere slower: a grid of fewer tiles than CUs then runs on fewer CUs
+  // (C4 B=1024 dX_3 7.7 -> 9.7 us), four groups meet at every stage's
+  // barrier (fwd2 17.8 -> 25.8 us), and 128x128 tiles lose their second
+  // workgroup per CU (C5 4.63 -> 4.64 ms).  VOLTA_KGROUPS=1 takes them
+  // wherever they apply, 0 nowhere.  Only where the epilogue is per element
+  // (small_m is false for the loss-head product); such a product launches
   // on its own, never in a paired launch.
   const char* kg = std::getenv("VOLTA_KGROUPS");
   const int kg_max = p.tile == TILE_64x64 && layout != GEMM_TN ? 4 : p.tile == TILE_64x64 || p.tile == TILE_128x128 ? 2 : 1;
-  if (kg && *kg == '1' && small_m && !p.inkernel_reduce && p.splits > 1 && p.splits <= kg_max) {
+  const bool kg_auto = !(kg && *kg) && layout == GEMM_NN && p.tile == TILE_64x64 && p.splits == 2 && tiles >= num_cus;
+  if (((kg && *kg == '1') || kg_auto) && small_m && !p.inkernel_reduce && p.splits > 1 && p.splits <= kg_max) {
     p.kgroups = p.splits;
     p.splits = 1;
   }
