@@ -834,7 +834,7 @@ def test_kgroups_steps_bit_identical(name):
     """Split-K products with their slices on groups of one workgroup's waves
     -- everywhere they apply (VOLTA_KGROUPS=1) and where the planner takes
     them by default (the variable unset: C4 B=1024's two 1024-wide forward
-    products) -- give the same bits as the split launches and their reduce
+    products and its dX_1) -- give the same bits as the split launches and their reduce
     kernel (VOLTA_KGROUPS=0): losses, parameters, activations and deltas
     after 3 steps."""
     spec, B, lr = KGROUP_STEP_CASES[name]

@@ -2369,19 +2369,23 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus, bool 
   // K groups (gemm_tile's KG): a split of up to 2 slices (4 on the 64x64
   // tile but for dW) runs inside one workgroup instead, the slices on groups
   // of its waves: no partial planes, no reduce launch, the same sums.  By
-  // default only for a forward product on 64x64 tiles split in two whose
-  // grid already has a tile per CU (C4 B=1024's fwd0 and fwd1: 17.4 -> 17.3
-  // and 28.5 -> 26.9 us against split + reduce, one launch fewer each).
-  // Elsewhere slower: a grid of fewer tiles than CUs then runs on fewer CUs
-  // (C4 B=1024 dX_3 7.7 -> 9.7 us), four groups meet at every stage's
-  // barrier (fwd2 17.8 -> 25.8 us), and 128x128 tiles lose their second
-  // workgroup per CU (C5 4.63 -> 4.64 ms).  VOLTA_KGROUPS=1 takes them
-  // wherever they apply, 0 nowhere.  Only where the epilogue is per element
-  // (small_m is false for the loss-head product); such a product launches
-  // on its own, never in a paired launch.
+  // default only for a product on 64x64 tiles split in two whose grid
+  // already has a tile per CU, forward or a dX with K >= 1024 (C4 B=1024's
+  // fwd0 and fwd1: 17.4 -> 17.3 and 28.5 -> 26.9 us against split + reduce,
+  // one launch fewer each; dX_1 alone in 26.1 us where the paired dX_1 |
+  // dW_2 launch and its reduces took 47.5 us, dW_2 alone 16.9).  Elsewhere
+  // slower: a grid of fewer tiles than CUs then runs on fewer CUs (C4
+  // B=1024 dX_3 7.7 -> 9.7 us), four groups meet at every stage's barrier
+  // (fwd2 17.8 -> 25.8 us), the dW pairs and a short-K dX pair are faster
+  // paired, and 128x128 tiles lose their second workgroup per CU (C5 4.63
+  // -> 4.64 ms).  VOLTA_KGROUPS=1 takes them wherever they apply, 0
+  // nowhere.  Only where the epilogue is per element (small_m is false for
+  // the loss-head product); such a product launches on its own, never in a
+  // paired launch.
   const char* kg = std::getenv("VOLTA_KGROUPS");
   const int kg_max = p.tile == TILE_64x64 && layout != GEMM_TN ? 4 : p.tile == TILE_64x64 || p.tile == TILE_128x128 ? 2 : 1;
-  const bool kg_auto = !(kg && *kg) && layout == GEMM_NN && p.tile == TILE_64x64 && p.splits == 2 && tiles >= num_cus;
+  const bool kg_auto = !(kg && *kg) && (layout == GEMM_NN || (layout == GEMM_NT && K >= 1024)) &&
+                       p.tile == TILE_64x64 && p.splits == 2 && tiles >= num_cus;
   if (((kg && *kg == '1') || kg_auto) && small_m && !p.inkernel_reduce && p.splits > 1 && p.splits <= kg_max) {
     p.kgroups = p.splits;
     p.splits = 1;
