@@ -920,9 +920,10 @@ def test_forward_head_launch_bit_identical(name):
     say(f"forward + output head launch {name}")
     n = len(spec.sizes) - 1
     fused = f"fwd{n - 2}+fwd{n - 1}+loss+dx{n - 1}"
-    # the fused launch's forward tile has 8 waves: both runs use 8
-    sep_env = {"VOLTA_FWD_HEAD": "0", "VOLTA_SMALLM_WAVES": "8"}
-    fused_env = {"VOLTA_FWD_HEAD": "1", "VOLTA_SMALLM_WAVES": "8"}
+    # the fused launch's forward tile has 8 waves: both runs use 8 (and the
+    # output launch stays apart from dX_{n-2})
+    sep_env = {"VOLTA_FWD_HEAD": "0", "VOLTA_SMALLM_WAVES": "8", "VOLTA_NO_TAIL": "1"}
+    fused_env = {"VOLTA_FWD_HEAD": "1", "VOLTA_SMALLM_WAVES": "8", "VOLTA_NO_TAIL": "1"}
     lab_sep = _launch_labels(sep_env, spec, B)
     lab_fused = _launch_labels(fused_env, spec, B)
     assert fused in lab_fused and fused not in lab_sep
@@ -933,6 +934,39 @@ def test_forward_head_launch_bit_identical(name):
     for a, b in zip(p1, p2):
         np.testing.assert_array_equal(a, b)
     for a, b in zip(b1, b2):
+        np.testing.assert_array_equal(a, b)
+
+
+TAIL_CASES = {
+    "c1": (MlpSpec([256, 512, 512, 256, 1], "relu", "sgd"), 64, 0.01),
+    "c2": (MlpSpec([512, 1024, 1024, 512, 256, 1], "relu", "adam"), 64, 1e-3),
+    "c4_b128": (MlpSpec([512, 1024, 1024, 512, 256, 1], "silu", "sgd"), 128, 0.01),  # pre-activation read
+    "gelu_b37": (MlpSpec([96, 512, 512, 1], "gelu", "sgd"), 37, 0.01),  # strips of 16, 16 and 5 rows
+    "tanh_b200": (MlpSpec([64, 256, 256, 1], "tanh", "adam"), 200, 1e-3),  # 13 strips, the last of 8 rows
+}
+
+
+@pytest.mark.parametrize("name", sorted(TAIL_CASES))
+def test_output_launch_with_next_dx_bit_identical(name):
+    """The output layer (loss head, dX_{n-1}) and the dX_{n-2} product in one
+    launch (gemm_smallm_tail: every workgroup forms its strip's row deltas
+    and the product's A operand in registers; the default where dX_{n-2}
+    runs on the 16-wave small-M tile) against the two launches
+    (VOLTA_NO_TAIL=1): one launch fewer, and losses, parameters, activations
+    and deltas after 4 steps bit-identical (same per-row code, same loss
+    partials in the same order, same product order)."""
+    spec, B, lr = TAIL_CASES[name]
+    say(f"output launch + dX_(n-2) {name}")
+    n = len(spec.sizes) - 1
+    fused = f"fwd{n - 1}+loss+dx{n - 1}+dx{n - 2}"
+    lab_sep = _launch_labels({"VOLTA_NO_TAIL": "1"}, spec, B)
+    lab_fused = _launch_labels({"VOLTA_NO_TAIL": "0"}, spec, B)
+    assert fused in lab_fused and fused not in lab_sep, (lab_sep, lab_fused)
+    assert len(lab_fused) == len(lab_sep) - 1
+    l1, p1, b1 = _run_with_env({"VOLTA_NO_TAIL": "1"}, spec, B, lr, 4)
+    l2, p2, b2 = _run_with_env({"VOLTA_NO_TAIL": "0"}, spec, B, lr, 4)
+    np.testing.assert_array_equal(l1, l2)
+    for a, b in zip(p1 + b1, p2 + b2):
         np.testing.assert_array_equal(a, b)
 
 

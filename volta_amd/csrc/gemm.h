@@ -118,6 +118,10 @@ hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& a, hipStream_t st, Rec
 // fields and loss ticket) in one launch; strip_counters: one zeroed
 // counter per 16 rows of the batch (at least (M + 15) / 16 of the
 // n_counters), left zero.
+// The one-column output layer (loss head, dX_{n-1}) and the dX_{n-2}
+// product planned as `p` in one launch (gemm_smallm_tail; loss deferred).
+bool tail_supported(const GemmPlan& p, const GemmArgs& a, const OutLayerArgs& o);
+hipError_t launch_smallm_tail(const GemmPlan& p, const GemmArgs& a, const OutLayerArgs& o, hipStream_t st);
 bool fwd_head_supported(const GemmPlan& p, const GemmArgs& a, const OutLayerArgs& o, int n_counters);
 hipError_t launch_fwd_head(const GemmPlan& p, const GemmArgs& a, const OutLayerArgs& o, unsigned* strip_counters,
                            int n_counters, hipStream_t st);

@@ -1228,13 +1228,36 @@ __device__ __forceinline__ void smallm_coords(int blk, int tiles_m, int tiles_n,
   }
 }
 
+// The A operand of the dX product below a one-column output layer, formed
+// in registers (smallm_tile with AH > 0): A(m, k) = (0 + d[m - m0] * W[k]) *
+// f'(pre[m][k], act[m][k]) -- the row of delta_{n-2} that out_dx_row stores,
+// from the same operands in the same order.  args.A then holds act_{n-1}
+// (lda its row stride); `pre` is read only for AH == 2 (else f' takes act
+// for both).  With `dx_out` set (workgroup-uniform) the tile also stores
+// the A values it forms: its rows of delta_{n-2}, every element once.
+struct SmallHead {
+  const float* pre = nullptr;  // pre-activation of layer n-2 [M x lda]
+  const float* w = nullptr;    // W_{n-1} [K x 1]
+  const float* d = nullptr;    // the tile's 16 row deltas delta_{n-1} (LDS)
+  float* dx_out = nullptr;     // delta_{n-2} [M x lda], or null
+  int act = 0;                 // activation of layer n-2
+};
+struct SmallNoPre {
+  __device__ void operator()() const {}
+};
+
 // NW waves per workgroup (4, or 8 for a stand-alone launch), each taking
-// one NW-th of the K range.
-template <bool B_KC, bool VEC, int EPI, int NW>
-__device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float* lds) {
+// one NW-th of the K range.  With AH > 0 every wave calls `pre` once, after
+// its first chunk's loads are issued and before any product term; the row
+// deltas hd.d are read after it.
+template <bool B_KC, bool VEC, int EPI, int NW, int AH = 0, class Pre = SmallNoPre>
+__device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float* lds,
+                                            const SmallHead& hd = SmallHead{}, Pre pre = Pre{}) {
   static_assert(NW == 4 || NW == 8 || NW == 16, "wave trees for 4, 8 or 16 partial tiles");
-  // 16-wave workgroups (four waves per SIMD) hold a quarter chunk per wave
-  constexpr int CH = NW == 16 ? kSmallChunk / 4 : kSmallChunk;
+  static_assert(AH == 0 || (B_KC && VEC && EPI == EPI_DX_ACT), "head operand: NT dX product, 16-byte rows");
+  // 16-wave workgroups (four waves per SIMD), and the head operand's three
+  // streams, hold a quarter chunk per wave
+  constexpr int CH = NW == 16 || AH > 0 ? kSmallChunk / 4 : kSmallChunk;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int M = args.M, N = args.N, K = args.K;
@@ -1251,6 +1274,8 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
   // (row 0 / column 0 stand in for rows and columns outside the matrix)
   const float* pa = args.A + (size_t)(row_ok ? m0 + r : 0) * lda;
   const float* pb = B_KC ? args.B + (size_t)(col_ok ? n0 + r : 0) * ldb : args.B + (col_ok ? n0 + r : 0);
+  const float* pp = AH == 2 ? hd.pre + (size_t)(row_ok ? m0 + r : 0) * lda : pa;
+  floatx4 fp[AH == 2 ? CH : 1], fw[AH > 0 ? CH : 1];  // head operand: pre-activation, W_{n-1}
 
   // A chunk's loads: per group unconditional within the lane (k clamped
   // into the wave's range), keeping the raw values; compute() replaces those
@@ -1266,6 +1291,8 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
       if (VEC) {  // K % 4 == 0 and every range bound is a multiple of 4
         const int kl = min(k, kend - 4);
         fa[g] = *reinterpret_cast<const floatx4*>(pa + kl);
+        if constexpr (AH == 2) fp[g] = *reinterpret_cast<const floatx4*>(pp + kl);
+        if constexpr (AH > 0) fw[g] = *reinterpret_cast<const floatx4*>(hd.w + kl);
         if (B_KC) {
           fb[g] = *reinterpret_cast<const floatx4*>(pb + kl);
         } else {
@@ -1303,15 +1330,30 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
 #pragma unroll
   for (int c = 0; c < 4; ++c) acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
   static_assert(kSmallChunk % 4 == 0, "a chunk must hold whole rounds of the four accumulators");
+  float dr = 0.0f;  // head operand: delta_{n-1} of the lane's row
   auto compute = [&](const floatx4(&fa)[CH], const floatx4(&fb)[CH], int kc) {
 #pragma unroll
     for (int g = 0; g < CH; ++g) {
       if (kc + 16 * g < kend) {  // wave-uniform
         const int k = kc + 16 * g + 4 * q;
+        floatx4 xa;  // head operand: the lane's four A values of the group
+        if constexpr (AH > 0) {
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const float av = fa[g][s];
+            float pv = av;
+            if constexpr (AH == 2) pv = fp[g][s];
+            xa[s] = (0.0f + dr * fw[g][s]) * act_derivative(hd.act, pv, av);
+          }
+          if (hd.dx_out && k < kend && row_ok)
+            *reinterpret_cast<floatx4*>(hd.dx_out + (size_t)(m0 + r) * lda + k) = xa;
+        }
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
           const bool in = VEC ? k < kend : k + s < kend;
-          const float x = in && row_ok ? fa[g][s] : 0.0f;
+          float x;
+          if constexpr (AH > 0) x = in && row_ok ? xa[s] : 0.0f;
+          else x = in && row_ok ? fa[g][s] : 0.0f;
           const float y = in && col_ok ? fb[g][s] : 0.0f;
           acc[g & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, y, acc[g & 3], 0, 0, 0);
         }
@@ -1322,9 +1364,19 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
   // small-batch product of the step): all its loads are in flight together,
   // then its MFMAs run.  Longer ranges take one memory latency per chunk.
   floatx4 fa[CH], fb[CH];
-  for (int kc = kbeg; kc < kend; kc += 16 * CH) {
-    load(fa, fb, kc);
-    compute(fa, fb, kc);
+  if constexpr (AH > 0) {
+    if (kbeg < kend) load(fa, fb, kbeg);
+    pre();  // every wave, once
+    dr = hd.d[r];
+    for (int kc = kbeg; kc < kend; kc += 16 * CH) {
+      if (kc != kbeg) load(fa, fb, kc);
+      compute(fa, fb, kc);
+    }
+  } else {
+    for (int kc = kbeg; kc < kend; kc += 16 * CH) {
+      load(fa, fb, kc);
+      compute(fa, fb, kc);
+    }
   }
 
   // Partial tiles to LDS: row (wave, v) holds register v of every lane.
@@ -1431,6 +1483,64 @@ gemm_smallm_head(GemmArgs args, OutLayerArgs p, unsigned* strip_counters) {
       out_dx_finish(p, nblocks, next);
     }
   }
+}
+
+// The one-column output layer with its loss head and dX_{n-1} (out_dx_row),
+// and the dX product below it (dX_{n-2} on the 16-wave small-M tile), in
+// one launch: one dependent launch fewer than out_layer_dx_kernel followed
+// by that product.  The product's A operand, delta_{n-2}, is row-local:
+// every workgroup forms the deltas delta_{n-1} of its 16-row strip (one row
+// per wave, the output launch's own per-row code, nothing stored) and then
+// A from act_{n-1}, W_{n-1} and the pre-activation in registers
+// (SmallHead), so no workgroup waits for another.  The strip's first column
+// tile (tn == 0) also stores what the output launch stores -- z and
+// delta_{n-1}, the rows of delta_{n-2} that the dW launch reads (the A
+// values as it forms them), the loss partials of the strip's four 4-row
+// blocks (the output launch's blocks, added in the same order) -- and
+// strip 0's advances the step counter; the loss sum is left to the step's
+// dW launch (defer_loss).  Parameters, activations, deltas and the loss
+// equal the two-launch path's bit for bit.
+template <bool HP>
+__global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4)))
+gemm_smallm_tail(GemmArgs args, OutLayerArgs p) {
+  constexpr int NW = 16;
+  __shared__ float lds[SmallLds<NW>::kFloats];
+  __shared__ float d_rows[16];
+  __shared__ float row_loss[16];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tiles_m = (args.M + 15) / 16, tiles_n = (args.N + 15) / 16;
+  int tm, tn;
+  smallm_coords<1>(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const bool writer = tn == 0;  // workgroup-uniform
+  auto head = [&]() {
+    StepNext next{};
+    if (writer && tm == 0 && tid == 0) next = step_prefetch(p.scalars, p.bc_table, p.bc_len);
+    const float l = out_dx_row<1, false>(p, nullptr, 16 * tm + wave, writer, false, d_rows + wave);
+    if (lane == 0) row_loss[wave] = l;
+    __syncthreads();
+    if (writer && tid == 0) {
+      const int nblocks = (p.B + kOutDxRows - 1) / kOutDxRows;
+#pragma unroll
+      for (int g = 0; g < 16 / kOutDxRows; ++g) {
+        const int b = (16 / kOutDxRows) * tm + g;
+        float sb = row_loss[kOutDxRows * g];
+        for (int w = 1; w < kOutDxRows; ++w) sb = sb + row_loss[kOutDxRows * g + w];
+        if (b < nblocks) p.partials[b] = sb;
+      }
+      if (tm == 0 && p.bc_table) {
+        p.scalars->t = next.t;
+        p.scalars->bc1 = next.bc.x;
+        p.scalars->bc2 = next.bc.y;
+      }
+    }
+  };
+  SmallHead hd;
+  hd.pre = HP ? p.dx_pre : nullptr;
+  hd.w = p.W;
+  hd.d = d_rows;
+  hd.dx_out = writer ? p.dx_out : nullptr;
+  hd.act = p.dx_act;
+  smallm_tile<true, true, EPI_DX_ACT, NW, HP ? 2 : 1>(args, blockIdx.x, lds, hd, head);
 }
 
 // ---------------------------------------------------------------------------
@@ -1940,6 +2050,31 @@ hipError_t launch_fwd_head(const GemmPlan& p, const GemmArgs& args_in, const Out
   const dim3 grid(((a.M + 15) / 16) * ((a.N + 15) / 16));
   if (p.vec) hipLaunchKernelGGL(gemm_smallm_head<true>, grid, dim3(512), 0, st, a, o, strip_counters);
   else hipLaunchKernelGGL(gemm_smallm_head<false>, grid, dim3(512), 0, st, a, o, strip_counters);
+  return hipGetLastError();
+}
+
+// `a` is the dX_{n-2} product as planned (its A, delta_{n-2}, is replaced
+// by the head operand); `o` the output launch's arguments with its dX.
+bool tail_supported(const GemmPlan& p, const GemmArgs& a, const OutLayerArgs& o) {
+  const auto al = [](const void* q) { return ((uintptr_t)q & 15u) == 0; };
+  GemmArgs h = a;
+  h.A = o.act;
+  h.lda = o.K;
+  return p.tile == TILE_SMALLM && p.layout == GEMM_NT && p.splits == 1 && p.vec && p.waves == 16 &&
+         a.epi.kind == EPI_DX_ACT && o.N == 1 && o.B == a.M && o.K == a.K && o.B >= 1 && o.B <= kNarrowMaxB &&
+         o.defer_loss && o.partials && o.scalars && o.dx_out && al(o.dx_out) && o.act && o.W && al(o.W) &&
+         (!o.dx_pre || al(o.dx_pre)) && smallm_vec_ok(h, GEMM_NT);
+}
+
+hipError_t launch_smallm_tail(const GemmPlan& p, const GemmArgs& args_in, const OutLayerArgs& o, hipStream_t st) {
+  if (!tail_supported(p, args_in, o)) return hipErrorInvalidValue;
+  GemmArgs a = args_in;
+  a.A = o.act;
+  a.lda = o.K;
+  a.k_per_split = p.k_per_split;
+  const dim3 grid(((a.M + 15) / 16) * ((a.N + 15) / 16));
+  if (o.dx_pre) hipLaunchKernelGGL(gemm_smallm_tail<true>, grid, dim3(1024), 0, st, a, o);
+  else hipLaunchKernelGGL(gemm_smallm_tail<false>, grid, dim3(1024), 0, st, a, o);
   return hipGetLastError();
 }
 

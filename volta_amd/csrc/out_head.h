@@ -143,8 +143,13 @@ constexpr int kOutDxMaxBlocks = (kNarrowMaxB + kOutDxRows - 1) / kOutDxRows;
 // + b, the loss head (z and delta_{n-1} stored by lane 0), and the row of
 // delta_{n-2} = (delta_{n-1} W^T) * f'(layer n-2).  Returns the row's loss
 // (0 for m >= B, whose loads are clamped and whose results are not stored).
+// With `store_head` false (wave-uniform) z and delta_{n-1} are not stored,
+// with `store_dx` false the row of delta_{n-2} is neither formed nor
+// stored; `d_row`, when given, receives the row's delta_{n-1} from lane 0
+// (also for m >= B).
 template <int NMAX, bool WL>
-__device__ __forceinline__ float out_dx_row(const OutLayerArgs& p, const float* w_lds, int m) {
+__device__ __forceinline__ float out_dx_row(const OutLayerArgs& p, const float* w_lds, int m, bool store_head = true,
+                                            bool store_dx = true, float* d_row = nullptr) {
   constexpr int C = 4;
   const int lane = threadIdx.x & 63;
   const int N = p.N, K = p.K;
@@ -165,10 +170,14 @@ __device__ __forceinline__ float out_dx_row(const OutLayerArgs& p, const float* 
   for (int j = 0; j < NMAX; ++j) z[0][j] = z[0][j] + bias[j];
   float d[NMAX];
   const float row_loss = head_delta<NMAX>(p, z[0], y, lab, d);
-  if (has && lane == 0) (void)head_row<NMAX>(p, z[0], y, lab, m);
+  if (d_row && lane == 0) {
+#pragma unroll
+    for (int j = 0; j < NMAX; ++j) d_row[j] = d[j];
+  }
+  if (has && store_head && lane == 0) (void)head_row<NMAX>(p, z[0], y, lab, m);
 
   // delta_{n-2} of this row
-  if (has) {
+  if (has && store_dx) {
     const float* act = p.act + (size_t)m * K;
     const float* pre = p.dx_pre ? p.dx_pre + (size_t)m * K : act;
     float* out = p.dx_out + (size_t)m * K;

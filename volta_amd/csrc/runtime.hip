@@ -105,6 +105,7 @@ struct Handle {
   bool narrow_dx = false;     // dX of the output layer as an outer product (L[n] <= 16)
   bool out_dx_merged = false; // ... formed by the output layer's own launch (out_layer_dx_kernel)
   bool fwd_head = false;      // ... and that launch folded into the last hidden forward launch (opt-in)
+  bool tail_merge = false;    // ... or that launch and dX_{n-2} in one (gemm_smallm_tail; VOLTA_NO_TAIL=1: off)
   bool narrow_dw = false;     // dW of the output layer by narrow_dw_kernel
   bool keep_grads = false;    // also store dW/db in `grads` (VOLTA_KEEP_GRADS=1)
   DevScalars* scalars = nullptr;
@@ -402,6 +403,13 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
            (h->out_dx_merged ? 4.0 * (double)B * lp.r : 0.0);
   };
   bool head_done = false;  // the output layer ran in the last hidden forward launch
+  // The output launch and dX_{n-2} in one launch when the product runs on
+  // the 16-wave small-M tile and the loss sum is left to the dW group.
+  bool tail = false;
+  if (h->tail_merge && defer_loss && h->out_mode == OUT_NARROW) {
+    const PairOp t = make_dx(n - 2, h->gemm_ws);
+    tail = tail_supported(t.plan, t.args, out_args());
+  }
   // Forward (:702-789); the output layer also runs the loss head (:792-798).
   for (int i = 0; i < n; ++i) {
     const LayerPlan& lp = h->layers[i];
@@ -410,6 +418,14 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
     if (last && h->out_mode == OUT_NARROW) {
       const OutLayerArgs o = out_args();
       const double fb = out_bytes();
+      if (tail) {
+        // ... and dX_{n-2}, whose A operand each workgroup forms from its rows
+        const PairOp t = make_dx(n - 2, h->gemm_ws);
+        VOLTA_CHECK(launch_smallm_tail(t.plan, t.args, o, st));
+        std::snprintf(label, sizeof label, "fwd%d+loss+dx%d+dx%d", i, i, i - 1);
+        VOLTA_CHECK(mark(rec, label, 4.0 * B * lp.r * lp.c + dx_cost(n - 2).first, fb + dx_cost(n - 2).second));
+        continue;
+      }
       if (h->out_dx_merged) {
         // the output layer's dX_{n-1} in the same launch (row-local)
         VOLTA_CHECK(launch_out_layer_dx(o, st));
@@ -652,6 +668,7 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
     // then every dW product in one launch -- dW_i only needs act_i and
     // delta_i, and dX_i has read W_i before that launch updates it.
     for (int i = n - 2; i >= 1; --i) {
+      if (i == n - 2 && tail) continue;  // ran with the output launch
       std::snprintf(lx, sizeof lx, "dx%d", i);
       if (!run_single(make_dx(i, ws0), lx, dx_cost(i))) return false;
     }
@@ -817,6 +834,8 @@ static bool build(Handle* h) {
   // (0.0402 -> 0.0384 ms).
   const char* fh = std::getenv("VOLTA_FWD_HEAD");
   h->fwd_head = h->out_dx_merged && Ln == 1 && fh && *fh && *fh != '0';
+  const char* nt = std::getenv("VOLTA_NO_TAIL");
+  h->tail_merge = h->out_dx_merged && !h->fwd_head && Ln == 1 && n >= 3 && !(nt && *nt && *nt != '0');
   h->narrow_dw = Ln <= 16 && B <= kNarrowMaxB;
   size_t ws_floats = 0;
   int max_tiles = 1;
