@@ -1254,10 +1254,10 @@ template <bool B_KC, bool VEC, int EPI, int NW, int AH = 0, class Pre = SmallNoP
 __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float* lds,
                                             const SmallHead& hd = SmallHead{}, Pre pre = Pre{}) {
   static_assert(NW == 4 || NW == 8 || NW == 16, "wave trees for 4, 8 or 16 partial tiles");
-  static_assert(AH == 0 || (B_KC && VEC && EPI == EPI_DX_ACT), "head operand: NT dX product, 16-byte rows");
-  // 16-wave workgroups (four waves per SIMD), and the head operand's three
-  // streams, hold a quarter chunk per wave
-  constexpr int CH = NW == 16 || AH > 0 ? kSmallChunk / 4 : kSmallChunk;
+  static_assert(AH == 0 || (B_KC && VEC && EPI == EPI_DX_ACT && NW == 16),
+                "head operand: NT dX product, 16-byte rows, 16 waves");
+  // 16-wave workgroups (four waves per SIMD) hold a quarter chunk per wave
+  constexpr int CH = NW == 16 ? kSmallChunk / 4 : kSmallChunk;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int M = args.M, N = args.N, K = args.K;
@@ -1485,14 +1485,17 @@ gemm_smallm_head(GemmArgs args, OutLayerArgs p, unsigned* strip_counters) {
   }
 }
 
-// The one-column output layer with its loss head and dX_{n-1} (out_dx_row),
-// and the dX product below it (dX_{n-2} on the 16-wave small-M tile), in
-// one launch: one dependent launch fewer than out_layer_dx_kernel followed
-// by that product.  The product's A operand, delta_{n-2}, is row-local:
-// every workgroup forms the deltas delta_{n-1} of its 16-row strip (one row
-// per wave, the output launch's own per-row code, nothing stored) and then
-// A from act_{n-1}, W_{n-1} and the pre-activation in registers
-// (SmallHead), so no workgroup waits for another.  The strip's first column
+// The one-column output layer with its loss head and dX_{n-1}, and the dX
+// product below it (dX_{n-2} on the 16-wave small-M tile), in one launch:
+// one dependent launch fewer than out_layer_dx_kernel followed by that
+// product.  The product's A operand, delta_{n-2}, is row-local: every
+// workgroup forms the deltas delta_{n-1} of its 16-row strip (one row per
+// wave with the output launch's own per-row arithmetic, out_head_rows) and
+// then A from act_{n-1}, W_{n-1} and the pre-activation in registers
+// (SmallHead), so no workgroup waits for another.  (Where dX_{n-2} takes
+// 4-wave workgroups -- a grid above one workgroup per CU -- the same launch
+// with four rows per wave is slower than the two launches: C3 0.088 ->
+// 0.095 ms, C4 B=256 0.101 -> 0.104 ms.)  The strip's first column
 // tile (tn == 0) also stores what the output launch stores -- z and
 // delta_{n-1}, the rows of delta_{n-2} that the dW launch reads (the A
 // values as it forms them), the loss partials of the strip's four 4-row
@@ -1504,6 +1507,7 @@ template <bool HP>
 __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4)))
 gemm_smallm_tail(GemmArgs args, OutLayerArgs p) {
   constexpr int NW = 16;
+  constexpr int RG = 16 / NW;  // strip rows per wave
   __shared__ float lds[SmallLds<NW>::kFloats];
   __shared__ float d_rows[16];
   __shared__ float row_loss[16];
@@ -1515,8 +1519,15 @@ gemm_smallm_tail(GemmArgs args, OutLayerArgs p) {
   auto head = [&]() {
     StepNext next{};
     if (writer && tm == 0 && tid == 0) next = step_prefetch(p.scalars, p.bc_table, p.bc_len);
-    const float l = out_dx_row<1, false>(p, nullptr, 16 * tm + wave, writer, false, d_rows + wave);
-    if (lane == 0) row_loss[wave] = l;
+    int rows[RG];
+    float ls[RG];
+#pragma unroll
+    for (int g = 0; g < RG; ++g) rows[g] = 16 * tm + RG * wave + g;
+    out_head_rows<RG>(p, rows, writer, d_rows + RG * wave, ls);
+    if (lane == 0) {
+#pragma unroll
+      for (int g = 0; g < RG; ++g) row_loss[RG * wave + g] = ls[g];
+    }
     __syncthreads();
     if (writer && tid == 0) {
       const int nblocks = (p.B + kOutDxRows - 1) / kOutDxRows;

@@ -143,13 +143,8 @@ constexpr int kOutDxMaxBlocks = (kNarrowMaxB + kOutDxRows - 1) / kOutDxRows;
 // + b, the loss head (z and delta_{n-1} stored by lane 0), and the row of
 // delta_{n-2} = (delta_{n-1} W^T) * f'(layer n-2).  Returns the row's loss
 // (0 for m >= B, whose loads are clamped and whose results are not stored).
-// With `store_head` false (wave-uniform) z and delta_{n-1} are not stored,
-// with `store_dx` false the row of delta_{n-2} is neither formed nor
-// stored; `d_row`, when given, receives the row's delta_{n-1} from lane 0
-// (also for m >= B).
 template <int NMAX, bool WL>
-__device__ __forceinline__ float out_dx_row(const OutLayerArgs& p, const float* w_lds, int m, bool store_head = true,
-                                            bool store_dx = true, float* d_row = nullptr) {
+__device__ __forceinline__ float out_dx_row(const OutLayerArgs& p, const float* w_lds, int m) {
   constexpr int C = 4;
   const int lane = threadIdx.x & 63;
   const int N = p.N, K = p.K;
@@ -170,14 +165,10 @@ __device__ __forceinline__ float out_dx_row(const OutLayerArgs& p, const float* 
   for (int j = 0; j < NMAX; ++j) z[0][j] = z[0][j] + bias[j];
   float d[NMAX];
   const float row_loss = head_delta<NMAX>(p, z[0], y, lab, d);
-  if (d_row && lane == 0) {
-#pragma unroll
-    for (int j = 0; j < NMAX; ++j) d_row[j] = d[j];
-  }
-  if (has && store_head && lane == 0) (void)head_row<NMAX>(p, z[0], y, lab, m);
+  if (has && lane == 0) (void)head_row<NMAX>(p, z[0], y, lab, m);
 
   // delta_{n-2} of this row
-  if (has && store_dx) {
+  if (has) {
     const float* act = p.act + (size_t)m * K;
     const float* pre = p.dx_pre ? p.dx_pre + (size_t)m * K : act;
     float* out = p.dx_out + (size_t)m * K;
@@ -205,6 +196,42 @@ __device__ __forceinline__ float out_dx_row(const OutLayerArgs& p, const float* 
     }
   }
   return has ? row_loss : 0.0f;
+}
+
+// Rows rows[g] (g < RG) of a one-column output layer computed together by
+// one wave, as out_dx_row computes each (wave_rows adds every row in the
+// same k order whatever RG, then the same loss head): the row deltas
+// delta_{n-1} go to d_rows[g] (lane 0; also for rows >= B), the row losses
+// to losses[g] (0 for rows >= B), and with `store_head` (wave-uniform) z and
+// delta_{n-1} are stored.  delta_{n-2} is not formed.
+template <int RG>
+__device__ __forceinline__ void out_head_rows(const OutLayerArgs& p, const int* rows, bool store_head, float* d_rows,
+                                              float* losses) {
+  const int lane = threadIdx.x & 63;
+  const bool mse = p.loss == VOLTA_LOSS_MSE;
+  const float bias = p.bias[0];
+  int wr[RG];
+  float y[RG][1];
+  int lab[RG];
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    const bool has = rows[g] < p.B;
+    const int mc = has ? rows[g] : p.B - 1;
+    wr[g] = has ? rows[g] : -1;
+    y[g][0] = mse ? p.y[mc] : 0.0f;
+    lab[g] = mse ? 0 : p.labels[mc];
+  }
+  float z[RG][1];
+  wave_rows<1, RG, 4, false>(p, nullptr, wr, z);
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    z[g][0] = z[g][0] + bias;
+    float d[1];
+    const float l = head_delta<1>(p, z[g], y[g], lab[g], d);
+    if (lane == 0) d_rows[g] = d[0];
+    losses[g] = wr[g] >= 0 ? l : 0.0f;
+    if (wr[g] >= 0 && store_head && lane == 0) (void)head_row<1>(p, z[g], y[g], lab[g], rows[g]);
+  }
 }
 
 // The step's loss from the per-block partials (blocks of kOutDxRows rows,
