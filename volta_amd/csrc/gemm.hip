@@ -1234,7 +1234,9 @@ __device__ __forceinline__ void smallm_coords(int blk, int tiles_m, int tiles_n,
 // from the same operands in the same order.  args.A then holds act_{n-1}
 // (lda its row stride); `pre` is read only for AH == 2 (else f' takes act
 // for both).  With `dx_out` set (workgroup-uniform) the tile also stores
-// the A values it forms: its rows of delta_{n-2}, every element once.
+// the A values it forms, its rows of delta_{n-2}, every element once: the
+// last chunk's after the tile's last barrier (no wait inside the tile
+// covers those stores), earlier chunks' as they are formed.
 struct SmallHead {
   const float* pre = nullptr;  // pre-activation of layer n-2 [M x lda]
   const float* w = nullptr;    // W_{n-1} [K x 1]
@@ -1247,12 +1249,13 @@ struct SmallNoPre {
 };
 
 // NW waves per workgroup (4, or 8 for a stand-alone launch), each taking
-// one NW-th of the K range.  With AH > 0 every wave calls `pre` once, after
-// its first chunk's loads are issued and before any product term; the row
-// deltas hd.d are read after it.
-template <bool B_KC, bool VEC, int EPI, int NW, int AH = 0, class Pre = SmallNoPre>
+// one NW-th of the K range.  With AH > 0 every thread calls `pre` once,
+// after its first chunk's loads are issued and before any product term (the
+// row deltas hd.d are read after it), and `post` once, after the tile's last
+// barrier.
+template <bool B_KC, bool VEC, int EPI, int NW, int AH = 0, class Pre = SmallNoPre, class Post = SmallNoPre>
 __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float* lds,
-                                            const SmallHead& hd = SmallHead{}, Pre pre = Pre{}) {
+                                            const SmallHead& hd = SmallHead{}, Pre pre = Pre{}, Post post = Post{}) {
   static_assert(NW == 4 || NW == 8 || NW == 16, "wave trees for 4, 8 or 16 partial tiles");
   static_assert(AH == 0 || (B_KC && VEC && EPI == EPI_DX_ACT && NW == 16),
                 "head operand: NT dX product, 16-byte rows, 16 waves");
@@ -1331,7 +1334,8 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
   for (int c = 0; c < 4; ++c) acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
   static_assert(kSmallChunk % 4 == 0, "a chunk must hold whole rounds of the four accumulators");
   float dr = 0.0f;  // head operand: delta_{n-1} of the lane's row
-  auto compute = [&](const floatx4(&fa)[CH], const floatx4(&fb)[CH], int kc) {
+  // (the head operand's A values replace the chunk's act values in fa)
+  auto compute = [&](floatx4(&fa)[CH], const floatx4(&fb)[CH], int kc) {
 #pragma unroll
     for (int g = 0; g < CH; ++g) {
       if (kc + 16 * g < kend) {  // wave-uniform
@@ -1345,8 +1349,7 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
             if constexpr (AH == 2) pv = fp[g][s];
             xa[s] = (0.0f + dr * fw[g][s]) * act_derivative(hd.act, pv, av);
           }
-          if (hd.dx_out && k < kend && row_ok)
-            *reinterpret_cast<floatx4*>(hd.dx_out + (size_t)(m0 + r) * lda + k) = xa;
+          fa[g] = xa;
         }
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
@@ -1364,6 +1367,18 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
   // small-batch product of the step): all its loads are in flight together,
   // then its MFMAs run.  Longer ranges take one memory latency per chunk.
   floatx4 fa[CH], fb[CH];
+  // head operand: store chunk kc's A values (rows of delta_{n-2})
+  auto store_a = [&](int kc) {
+    if constexpr (AH > 0) {
+      if (!hd.dx_out || !row_ok) return;
+#pragma unroll
+      for (int g = 0; g < CH; ++g) {
+        const int k = kc + 16 * g + 4 * q;
+        if (kc + 16 * g < kend && k < kend) *reinterpret_cast<floatx4*>(hd.dx_out + (size_t)(m0 + r) * lda + k) = fa[g];
+      }
+    }
+  };
+  int last_kc = -1;
   if constexpr (AH > 0) {
     if (kbeg < kend) load(fa, fb, kbeg);
     pre();  // every wave, once
@@ -1371,6 +1386,8 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
     for (int kc = kbeg; kc < kend; kc += 16 * CH) {
       if (kc != kbeg) load(fa, fb, kc);
       compute(fa, fb, kc);
+      if (kc + 16 * CH < kend) store_a(kc);
+      else last_kc = kc;
     }
   } else {
     for (int kc = kbeg; kc < kend; kc += 16 * CH) {
@@ -1384,6 +1401,10 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
   for (int v = 0; v < 4; ++v)
     lds[(wave * 4 + v) * kSmallRedStride + lane] = (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]);
   __syncthreads();
+  if constexpr (AH > 0) {
+    if (last_kc >= 0) store_a(last_kc);
+    post();
+  }
   // Element (i, j) of the tile: lane 16*(i/4) + j, register i%4 of each
   // wave; the waves' values added as (w0 + w1) + (w2 + w3) (then the same
   // for w4..w7, and the two halves).  Threads 0..255 hold one element each.
@@ -1492,44 +1513,48 @@ gemm_smallm_head(GemmArgs args, OutLayerArgs p, unsigned* strip_counters) {
 // workgroup forms the deltas delta_{n-1} of its 16-row strip (one row per
 // wave with the output launch's own per-row arithmetic, out_head_rows) and
 // then A from act_{n-1}, W_{n-1} and the pre-activation in registers
-// (SmallHead), so no workgroup waits for another.  (Where dX_{n-2} takes
-// 4-wave workgroups -- a grid above one workgroup per CU -- the same launch
-// with four rows per wave is slower than the two launches: C3 0.088 ->
-// 0.095 ms, C4 B=256 0.101 -> 0.104 ms.)  The strip's first column
-// tile (tn == 0) also stores what the output launch stores -- z and
+// (SmallHead), so no workgroup waits for another.  The strip's first
+// column tile (tn == 0) also stores what the output launch stores -- z and
 // delta_{n-1}, the rows of delta_{n-2} that the dW launch reads (the A
 // values as it forms them), the loss partials of the strip's four 4-row
 // blocks (the output launch's blocks, added in the same order) -- and
-// strip 0's advances the step counter; the loss sum is left to the step's
-// dW launch (defer_loss).  Parameters, activations, deltas and the loss
-// equal the two-launch path's bit for bit.
+// strip 0's advances the step counter, all after the tile's last barrier,
+// so no wait of the tile covers them; the loss sum is left to the step's
+// dW launch (defer_loss).  MSE only (z and delta_{n-1} are stored without
+// the CE label check).  Parameters, activations, deltas and the loss equal
+// the two-launch path's bit for bit.  (Where dX_{n-2} takes 4-wave
+// workgroups -- a grid above one workgroup per CU -- the same launch with
+// four rows per wave is slower than the two launches: C3 0.088 -> 0.095 ms,
+// C4 B=256 0.101 -> 0.104 ms.)
 template <bool HP>
 __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4)))
 gemm_smallm_tail(GemmArgs args, OutLayerArgs p) {
   constexpr int NW = 16;
-  constexpr int RG = 16 / NW;  // strip rows per wave
   __shared__ float lds[SmallLds<NW>::kFloats];
-  __shared__ float d_rows[16];
-  __shared__ float row_loss[16];
+  __shared__ float z_rows[16], d_rows[16], row_loss[16];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int tiles_m = (args.M + 15) / 16, tiles_n = (args.N + 15) / 16;
   int tm, tn;
   smallm_coords<1>(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const bool writer = tn == 0;  // workgroup-uniform
+  // row 16*tm + wave of the strip: z, delta_{n-1} and the loss to LDS
   auto head = [&]() {
-    StepNext next{};
-    if (writer && tm == 0 && tid == 0) next = step_prefetch(p.scalars, p.bc_table, p.bc_len);
-    int rows[RG];
-    float ls[RG];
-#pragma unroll
-    for (int g = 0; g < RG; ++g) rows[g] = 16 * tm + RG * wave + g;
-    out_head_rows<RG>(p, rows, writer, d_rows + RG * wave, ls);
-    if (lane == 0) {
-#pragma unroll
-      for (int g = 0; g < RG; ++g) row_loss[RG * wave + g] = ls[g];
-    }
+    const int rows[1] = {16 * tm + wave};
+    float ls[1];
+    out_head_rows<1>(p, rows, z_rows + wave, d_rows + wave, ls);
+    if (lane == 0) row_loss[wave] = ls[0];
     __syncthreads();
-    if (writer && tid == 0) {
+  };
+  // the output launch's stores of this strip (first column tile only)
+  auto tail_stores = [&]() {
+    if (!writer) return;
+    if (tid < 16) {
+      const int m = 16 * tm + tid;
+      if (m < p.B) {
+        p.out[m] = z_rows[tid];
+        p.delta[m] = d_rows[tid];
+      }
+    } else if (tid == 64) {
       const int nblocks = (p.B + kOutDxRows - 1) / kOutDxRows;
 #pragma unroll
       for (int g = 0; g < 16 / kOutDxRows; ++g) {
@@ -1539,6 +1564,7 @@ gemm_smallm_tail(GemmArgs args, OutLayerArgs p) {
         if (b < nblocks) p.partials[b] = sb;
       }
       if (tm == 0 && p.bc_table) {
+        const StepNext next = step_prefetch(p.scalars, p.bc_table, p.bc_len);
         p.scalars->t = next.t;
         p.scalars->bc1 = next.bc.x;
         p.scalars->bc2 = next.bc.y;
@@ -1551,7 +1577,7 @@ gemm_smallm_tail(GemmArgs args, OutLayerArgs p) {
   hd.d = d_rows;
   hd.dx_out = writer ? p.dx_out : nullptr;
   hd.act = p.dx_act;
-  smallm_tile<true, true, EPI_DX_ACT, NW, HP ? 2 : 1>(args, blockIdx.x, lds, hd, head);
+  smallm_tile<true, true, EPI_DX_ACT, NW, HP ? 2 : 1>(args, blockIdx.x, lds, hd, head, tail_stores);
 }
 
 // ---------------------------------------------------------------------------
@@ -2073,7 +2099,8 @@ bool tail_supported(const GemmPlan& p, const GemmArgs& a, const OutLayerArgs& o)
   h.lda = o.K;
   return p.tile == TILE_SMALLM && p.layout == GEMM_NT && p.splits == 1 && p.vec && p.waves == 16 &&
          a.epi.kind == EPI_DX_ACT && o.N == 1 && o.B == a.M && o.K == a.K && o.B >= 1 && o.B <= kNarrowMaxB &&
-         o.defer_loss && o.partials && o.scalars && o.dx_out && al(o.dx_out) && o.act && o.W && al(o.W) &&
+         o.loss == VOLTA_LOSS_MSE && o.defer_loss && o.partials && o.scalars && o.dx_out && al(o.dx_out) && o.act &&
+         o.W && al(o.W) &&
          (!o.dx_pre || al(o.dx_pre)) && smallm_vec_ok(h, GEMM_NT);
 }
 

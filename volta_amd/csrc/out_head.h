@@ -200,26 +200,22 @@ __device__ __forceinline__ float out_dx_row(const OutLayerArgs& p, const float* 
 
 // Rows rows[g] (g < RG) of a one-column output layer computed together by
 // one wave, as out_dx_row computes each (wave_rows adds every row in the
-// same k order whatever RG, then the same loss head): the row deltas
-// delta_{n-1} go to d_rows[g] (lane 0; also for rows >= B), the row losses
-// to losses[g] (0 for rows >= B), and with `store_head` (wave-uniform) z and
-// delta_{n-1} are stored.  delta_{n-2} is not formed.
+// same k order whatever RG, then the same loss head), MSE only: lane 0
+// writes each row's z to z_rows[g] and its delta_{n-1} to d_rows[g] (also
+// for rows >= B), and every lane gets the row losses in losses[g] (0 for
+// rows >= B).  Nothing is stored to global memory.
 template <int RG>
-__device__ __forceinline__ void out_head_rows(const OutLayerArgs& p, const int* rows, bool store_head, float* d_rows,
+__device__ __forceinline__ void out_head_rows(const OutLayerArgs& p, const int* rows, float* z_rows, float* d_rows,
                                               float* losses) {
   const int lane = threadIdx.x & 63;
-  const bool mse = p.loss == VOLTA_LOSS_MSE;
   const float bias = p.bias[0];
   int wr[RG];
   float y[RG][1];
-  int lab[RG];
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
     const bool has = rows[g] < p.B;
-    const int mc = has ? rows[g] : p.B - 1;
     wr[g] = has ? rows[g] : -1;
-    y[g][0] = mse ? p.y[mc] : 0.0f;
-    lab[g] = mse ? 0 : p.labels[mc];
+    y[g][0] = p.y[has ? rows[g] : p.B - 1];
   }
   float z[RG][1];
   wave_rows<1, RG, 4, false>(p, nullptr, wr, z);
@@ -227,10 +223,12 @@ __device__ __forceinline__ void out_head_rows(const OutLayerArgs& p, const int* 
   for (int g = 0; g < RG; ++g) {
     z[g][0] = z[g][0] + bias;
     float d[1];
-    const float l = head_delta<1>(p, z[g], y[g], lab[g], d);
-    if (lane == 0) d_rows[g] = d[0];
+    const float l = head_delta<1>(p, z[g], y[g], 0, d);
+    if (lane == 0) {
+      z_rows[g] = z[g][0];
+      d_rows[g] = d[0];
+    }
     losses[g] = wr[g] >= 0 ? l : 0.0f;
-    if (wr[g] >= 0 && store_head && lane == 0) (void)head_row<1>(p, z[g], y[g], lab[g], rows[g]);
   }
 }
 
