@@ -19,10 +19,12 @@ HIP_LIB = os.path.join(PKG_DIR, "libvolta_hip.so")
 _F = C.POINTER(C.c_float)
 
 # Kernel-level entry points of libvolta_hip.so used by the GPU tests; they
-# take device pointers and run synchronously.
+# take device pointers and run synchronously (volta_hip_gemm_plan makes no
+# device call: the CPU tests use it).
 HIP_EXTRA = {
     "volta_hip_gemm": (C.c_int32, [C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p,
                                    C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32]),
+    "volta_hip_gemm_plan": (C.c_int32, [C.c_int32] * 7 + [C.POINTER(C.c_int32)]),
     "volta_hip_arena_bytes": (C.c_int64, [C.c_void_p]),
     "volta_hip_optimizer": (C.c_int32, [C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64]
                             + [C.c_float] * 7),

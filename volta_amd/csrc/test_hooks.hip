@@ -37,6 +37,27 @@ int32_t volta_hip_calibration_copy(void* dst, const void* src, int64_t bytes, in
 // force_tile < 0 and force_splits == 0 select the runtime's own plan;
 // force_splits > 0 splits K over that many launch slices (reduced by a
 // second kernel), force_splits = -G over G groups of one workgroup's waves.
+// The planner's choice for one product (gemm_plan; host code only, no
+// device call): out[0..5] = tile (GemmTile), splits, k_per_split, kgroups,
+// waves, vec.  `small_m` as the step passes it (0 for the loss-head
+// product).  Test use.
+int32_t volta_hip_gemm_plan(int32_t layout, int32_t M, int32_t N, int32_t K, int32_t vec, int32_t num_cus,
+                            int32_t small_m, int32_t* out) {
+  using namespace volta;
+  if (layout < GEMM_NN || layout > GEMM_TN || M <= 0 || N <= 0 || K <= 0 || num_cus <= 0 || !out) {
+    set_last_error("volta_hip_gemm_plan: bad arguments");
+    return -1;
+  }
+  const GemmPlan p = gemm_plan(layout, M, N, K, vec != 0, num_cus, small_m != 0);
+  out[0] = p.tile;
+  out[1] = p.splits;
+  out[2] = p.k_per_split;
+  out[3] = p.kgroups;
+  out[4] = p.waves;
+  out[5] = p.vec ? 1 : 0;
+  return 0;
+}
+
 int32_t volta_hip_gemm(int32_t layout, const float* A, const float* B, float* Cm, int32_t M, int32_t N,
                        int32_t K, int32_t force_tile, int32_t force_splits) {
   using namespace volta;
