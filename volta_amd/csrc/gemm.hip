@@ -1530,6 +1530,7 @@ template <bool HP>
 __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4)))
 gemm_smallm_tail(GemmArgs args, OutLayerArgs p) {
   constexpr int NW = 16;
+  static_assert(16 % kOutDxRows == 0, "a strip holds whole loss blocks of the output launch");
   __shared__ float lds[SmallLds<NW>::kFloats];
   __shared__ float z_rows[16], d_rows[16], row_loss[16];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
