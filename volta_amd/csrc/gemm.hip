@@ -1235,8 +1235,8 @@ __device__ __forceinline__ void smallm_coords(int blk, int tiles_m, int tiles_n,
 // (lda its row stride); `pre` is read only for AH == 2 (else f' takes act
 // for both).  With `dx_out` set (workgroup-uniform) the tile also stores
 // the A values it forms, its rows of delta_{n-2}, every element once: the
-// last chunk's after the tile's last barrier (no wait inside the tile
-// covers those stores), earlier chunks' as they are formed.
+// last chunk's after the tile's last barrier (from the operand registers
+// they replace), earlier chunks' as they are formed.
 struct SmallHead {
   const float* pre = nullptr;  // pre-activation of layer n-2 [M x lda]
   const float* w = nullptr;    // W_{n-1} [K x 1]
@@ -1518,9 +1518,9 @@ gemm_smallm_head(GemmArgs args, OutLayerArgs p, unsigned* strip_counters) {
 // delta_{n-1}, the rows of delta_{n-2} that the dW launch reads (the A
 // values as it forms them), the loss partials of the strip's four 4-row
 // blocks (the output launch's blocks, added in the same order) -- and
-// strip 0's advances the step counter, all after the tile's last barrier,
-// so no wait of the tile covers them; the loss sum is left to the step's
-// dW launch (defer_loss).  MSE only (z and delta_{n-1} are stored without
+// strip 0's advances the step counter, all after the tile's last barrier
+// (off the path from the row heads to the product); the loss sum is left
+// to the step's dW launch (defer_loss).  MSE only (z and delta_{n-1} are stored without
 // the CE label check).  Parameters, activations, deltas and the loss equal
 // the two-launch path's bit for bit.  (Where dX_{n-2} takes 4-wave
 // workgroups -- a grid above one workgroup per CU -- the same launch with
