@@ -1160,6 +1160,8 @@ INFER_CASES = [
     (MlpSpec([512, 1024, 1024, 512, 256, 1], "relu", "adam"), 64, (64, 17, 200)),
     (MlpSpec([64, 96, 40], "gelu", "sgd", "ce"), 32, (32, 5, 70)),
     (MlpSpec([1024, 4096, 10], "silu", "adagrad", "ce"), 256, (256, 3, 300)),
+    # 1024-row chunks: the 1024-wide products take K groups (64x64 tiles, both K slices in one workgroup)
+    (MlpSpec([512, 1024, 1024, 1], "silu", "sgd"), 1024, (1024, 1500)),
 ]
 
 
