@@ -1244,7 +1244,7 @@ struct SmallHead {
   float* dx_out = nullptr;     // delta_{n-2} [M x lda], or null
   int act = 0;                 // activation of layer n-2
 };
-struct SmallNoPre {
+struct SmallNoop {
   __device__ void operator()() const {}
 };
 
@@ -1253,7 +1253,7 @@ struct SmallNoPre {
 // after its first chunk's loads are issued and before any product term (the
 // row deltas hd.d are read after it), and `post` once, after the tile's last
 // barrier.
-template <bool B_KC, bool VEC, int EPI, int NW, int AH = 0, class Pre = SmallNoPre, class Post = SmallNoPre>
+template <bool B_KC, bool VEC, int EPI, int NW, int AH = 0, class Pre = SmallNoop, class Post = SmallNoop>
 __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float* lds,
                                             const SmallHead& hd = SmallHead{}, Pre pre = Pre{}, Post post = Post{}) {
   static_assert(NW == 4 || NW == 8 || NW == 16, "wave trees for 4, 8 or 16 partial tiles");
