@@ -231,6 +231,15 @@ int64_t volta_train_state_size(VoltaTrainHandle* h);
  *                        only where the backward needs it -- leaky ReLU,
  *                        SiLU, GELU, softmax, LayerNorm or dropout) */
 #define VOLTA_BUF_PRE 7
+/*   VOLTA_BUF_LN_DGAMMA  dgamma_i [L[i+1]], i = 0..n-2 (spec.layernorm): the
+ *                        LayerNorm scale gradient the step applied (:843-887)
+ *   VOLTA_BUF_LN_DBETA   dbeta_i  [L[i+1]]
+ *   VOLTA_BUF_CLIP_SCALE one float (layer ignored): the factor the step
+ *                        multiplied every delta by (spec.clip_grad > 0; 1
+ *                        when the norm was within the limit, :936-955) */
+#define VOLTA_BUF_LN_DGAMMA 8
+#define VOLTA_BUF_LN_DBETA 9
+#define VOLTA_BUF_CLIP_SCALE 10
 int64_t volta_train_debug_buffer(VoltaTrainHandle* h, int32_t kind, int32_t layer, float* out);
 int32_t volta_train_get_state(VoltaTrainHandle* h, float* state, int64_t* step);
 int32_t volta_train_set_state(VoltaTrainHandle* h, const float* state, int64_t step);
@@ -257,16 +266,19 @@ int32_t volta_train_set_hparams(VoltaTrainHandle* h, float beta1, float beta2, f
 int32_t volta_train_infer(VoltaTrainHandle* h, const float* X, int64_t rows, float* out);
 
 /* Allocation-free variant of volta_train_infer.  No counterpart in the
- * reference: it is for callers that cannot allocate device memory (code
- * under stream capture, serving loops, harnesses that forbid hipMalloc).
+ * reference: it is for callers that cannot allocate device memory (serving
+ * loops, harnesses that forbid hipMalloc).
  * X [rows x L0] and out [rows x Ln] are 16-byte aligned device buffers; the
  * forward runs on the handle's weights and activation buffers with its
  * split-K partial planes in a static 64 MiB device array per GPU (held from
  * library load to process end); rows whose plan needs more are rejected
  * with an error.  Nothing is allocated, freed or synchronized: the launches
- * are enqueued on the handle's stream (volta_train_sync before reading
- * out).  Calls that overlap on one GPU share that GPU's scratch and race.
- * Returns 0, or -1 with volta_train_last_error() set. */
+ * are enqueued on the handle's own stream, not on a stream of the caller,
+ * so a caller's stream capture does not record them and nothing orders
+ * them after the caller's work: finish the work that writes X first (e.g.
+ * synchronize the stream that produced it), and call volta_train_sync
+ * before reading out.  Calls that overlap on one GPU share that GPU's
+ * scratch and race.  Returns 0, or -1 with volta_train_last_error() set. */
 int32_t volta_train_infer_device_noalloc(VoltaTrainHandle* h, const float* X, int64_t rows, float* out);
 
 /* The inference library's entry point (codegen/inner.rs:198; contract
@@ -278,6 +290,20 @@ int32_t volta_train_infer_device_noalloc(VoltaTrainHandle* h, const float* X, in
  * volta_train_last_error() says why. */
 int32_t volta_infer_bind(VoltaTrainHandle* h);
 void volta_infer(const float* input, int64_t in_n, float* output, int64_t out_n);
+
+/* The model of an inference library made by `volta-hip compile` (the
+ * reference's `volta compile`, main.rs:158-215 -> executor.rs:1684-1744,
+ * whose library embeds the trained weights, codegen/inner.rs:190-262): the
+ * forward graph lower_model_to_graph builds (lowering.rs:87-140) -- each
+ * layer MatMul by W_i then Add of b_i; hidden layers followed by ReLU when
+ * hidden_act is VOLTA_ACT_RELU, by nothing when it is -1 -- with the
+ * parameters `params` ([W_0 | b_0 | W_1 | b_1 | ...], host float32, W_i
+ * row-major [L_i x L_i+1]) copied to the device.  Run it with
+ * volta_train_infer (any row count, host buffers); release it with
+ * volta_train_free.  Returns NULL, with volta_train_last_error() set, on bad
+ * arguments, no device, or a device failure. */
+VoltaTrainHandle* volta_infer_model_create(int32_t n_sizes, const int32_t* sizes, int32_t hidden_act,
+                                           const float* params);
 
 #ifdef __cplusplus
 }

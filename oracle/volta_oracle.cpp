@@ -215,6 +215,11 @@ struct Net {
   uint64_t dropout_rng = 12345678ULL;  // alloc: dropout_rng: 12345678u64 (:553)
   uint64_t adam_step = 0;
   T last_loss = T(0);
+  T clip_scale = T(1);  // factor the last step applied to the deltas (clipping)
+  // inference model of a `volta compile` library whose graph has no hidden
+  // activation (lower_model_to_graph drops all but Relu/Sigmoid,
+  // lowering.rs:121-129)
+  bool linear_hidden = false;
 
   void alloc(const volta_mlp_spec& s, int batch) {
     spec = s;
@@ -265,7 +270,8 @@ struct Net {
       if (!last) {
         T* a = act[i + 1].data();
         const size_t cnt = (size_t)B * c;
-        if (spec.activation == VOLTA_ACT_SOFTMAX) softmax_fwd(dst, a, c);
+        if (linear_hidden) std::copy(dst, dst + cnt, a);
+        else if (spec.activation == VOLTA_ACT_SOFTMAX) softmax_fwd(dst, a, c);
         else
           for (size_t k = 0; k < cnt; ++k) a[k] = act_fwd<T>(spec.activation, dst[k]);
         if (spec.layernorm) layernorm_fwd(i);
@@ -535,6 +541,7 @@ struct Net {
       const T gnorm = std::sqrt(gsq);
       const T cv = T(spec.clip_grad);
       const T scale = gnorm > cv ? cv / gnorm : T(1);
+      clip_scale = scale;
       if (scale < T(1))
         for (int i = 0; i < n; ++i)
           for (T& v : delta[i]) v = v * scale;
@@ -921,6 +928,14 @@ static int64_t debug_buffer(Net<T>& f, int kind, int layer, O* out) {
       return f.spec.layernorm && layer >= 0 && layer < f.n - 1 ? copy_out(f.ln_g[layer], out) : -1;
     case VOLTA_BUF_LN_BETA:
       return f.spec.layernorm && layer >= 0 && layer < f.n - 1 ? copy_out(f.ln_b[layer], out) : -1;
+    case VOLTA_BUF_LN_DGAMMA:
+      return f.spec.layernorm && layer >= 0 && layer < f.n - 1 ? copy_out(f.ln_dg[layer], out) : -1;
+    case VOLTA_BUF_LN_DBETA:
+      return f.spec.layernorm && layer >= 0 && layer < f.n - 1 ? copy_out(f.ln_db[layer], out) : -1;
+    case VOLTA_BUF_CLIP_SCALE:
+      if (!(f.spec.clip_grad > 0.0f)) return -1;
+      out[0] = (O)f.clip_scale;
+      return 1;
     case VOLTA_BUF_DROPOUT_MASK:
       if (!(f.spec.dropout_p > 0.0f) || layer < 0 || layer >= f.n - 1) return -1;
       for (size_t k = 0; k < f.mask[layer].size(); ++k) out[k] = (O)f.mask[layer][k];
@@ -1061,6 +1076,30 @@ int32_t volta_train_infer(VoltaTrainHandle* vh, const float* X, int64_t rows, fl
   if (h->precision == 64) infer_rows(h->d, X, rows, out);
   else infer_rows(h->f, X, rows, out);
   return 0;
+}
+
+// The inference model of a `volta compile` library: the forward graph of
+// lower_model_to_graph (lowering.rs:87-140) with ReLU hidden layers
+// (hidden_act VOLTA_ACT_RELU) or none (-1), parameters [W_0|b_0|W_1|...].
+VoltaTrainHandle* volta_infer_model_create(int32_t n_sizes, const int32_t* sizes, int32_t hidden_act,
+                                           const float* params) {
+  if (n_sizes < 2 || n_sizes > VOLTA_MAX_LAYER_SIZES || !sizes || !params ||
+      (hidden_act != VOLTA_ACT_RELU && hidden_act != -1)) {
+    set_last_error("volta_infer_model_create: bad arguments");
+    return nullptr;
+  }
+  volta_mlp_spec s;
+  volta_mlp_spec_default(&s, n_sizes, sizes, VOLTA_ACT_RELU, VOLTA_OPT_SGD, VOLTA_LOSS_MSE);
+  VoltaTrainHandle* vh = volta_train_init_spec(&s, 64);
+  if (!vh) return nullptr;
+  H(vh)->f.linear_hidden = hidden_act == -1;
+  const float* p = params;
+  for (int i = 0; i + 1 < n_sizes; ++i) {
+    const int64_t r = sizes[i], c = sizes[i + 1];
+    volta_train_set_params(vh, i, p, p + r * c);
+    p += r * c + c;
+  }
+  return vh;
 }
 
 // The CPU library's memory is host memory: the allocation-free variant is

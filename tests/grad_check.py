@@ -278,3 +278,236 @@ def bits_equal(a, b):
     a = np.ascontiguousarray(a, np.float32).ravel()
     b = np.ascontiguousarray(b, np.float32).ravel()
     return a.shape == b.shape and bool(np.array_equal(a.view(np.uint32), b.view(np.uint32)))
+
+
+# ---------------------------------------------------------------------------
+# Steps with the codegen extras (LayerNorm, dropout, gradient clipping,
+# softmax hidden rows; mlp_train_rust_codegen.rs:727-788, :829-955).
+#
+# The step order there: phase 1 for i = n-1 .. 0 runs, on a hidden layer,
+# LayerNorm backward (dgamma/dbeta as batch sums of the upstream gradient g
+# and of g * xhat, xhat recomputed from the layer's stored output as
+# (y - beta) / (gamma + 1e-12), then gamma/beta -= lr * grad), the dropout
+# mask and f'; then db_i = sum_b delta_i; then delta_{i-1} = delta_i W_i^T.
+# The clip scales every delta by s = clip / ||delta|| when the norm exceeds
+# clip; phase 2 forms dW_i = act_i^T delta_i from the scaled deltas.  So db
+# comes from the unscaled deltas and dW from the scaled ones.
+#
+# Checks on the candidate's own operands (bounds as above): every forward
+# product, the loss gradient, dW_i (2 B eps), db_i over the unscaled deltas
+# (delta / s), dgamma/dbeta as batch sums of g = delta_{i+1,unscaled}
+# W_{i+1}^T (and of g * xhat), and s against clip / ||delta||.  Against the
+# fp64 twin: every forward product, dW_i, db_i, dgamma and dbeta by the
+# triangle bounds on the measured operand deviations; the dropout masks
+# bit for bit; and the hidden activations and deltas, whose LayerNorm /
+# softmax row arithmetic has no closed elementwise bound here, by their
+# distance from the twin measured against the fp32 oracle's own distance
+# from it for the same step (norm within 4x plus 16 eps of the twin's norm,
+# largest element within 8x plus 16 eps of the largest).
+# ---------------------------------------------------------------------------
+
+class ExtBuffers(StepBuffers):
+    """StepBuffers plus the extras' buffers: dgamma/dbeta and gamma/beta
+    (after the step) of each hidden layer with LayerNorm, the dropout masks
+    and the clip scale (1.0 without clipping).  `delta` holds the deltas as
+    the step left them (scaled by the clip)."""
+
+    def __init__(self, base: StepBuffers, dg, dbe, gamma, beta, mask, scale):
+        super().__init__(base.act, base.delta, base.pre, base.dw, base.db)
+        self.dg, self.dbe, self.gamma, self.beta, self.mask, self.scale = dg, dbe, gamma, beta, mask, scale
+
+
+def _ext_parts(get, spec, B):
+    from volta_amd.abi import BUF_CLIP_SCALE, BUF_DROPOUT_MASK, BUF_LN_BETA, BUF_LN_DBETA, BUF_LN_DGAMMA, \
+        BUF_LN_GAMMA
+    nh, L = spec.n_layers - 1, spec.sizes
+    ln = bool(spec.layernorm)
+    dg = [get(BUF_LN_DGAMMA, i, (L[i + 1],)) for i in range(nh)] if ln else []
+    dbe = [get(BUF_LN_DBETA, i, (L[i + 1],)) for i in range(nh)] if ln else []
+    gam = [get(BUF_LN_GAMMA, i, (L[i + 1],)) for i in range(nh)] if ln else []
+    bet = [get(BUF_LN_BETA, i, (L[i + 1],)) for i in range(nh)] if ln else []
+    mask = [get(BUF_DROPOUT_MASK, i, (B, L[i + 1])) for i in range(nh)] if spec.dropout_p > 0 else []
+    scale = float(get(BUF_CLIP_SCALE, 0, (1,))[0]) if spec.clip_grad > 0 else 1.0
+    return dg, dbe, gam, bet, mask, scale
+
+
+def read_candidate_ext(t, spec, B) -> ExtBuffers:
+    """read_candidate plus the extras' buffers, through
+    volta_train_debug_buffer (the HIP library, or the fp32 oracle)."""
+    base = read_candidate(t, spec, B)
+
+    def get(kind, i, shape):
+        return t.debug_buffer(kind, i).astype(np.float64).reshape(shape)
+    return ExtBuffers(base, *_ext_parts(get, spec, B))
+
+
+def read_twin_ext(orc, t, spec, B) -> ExtBuffers:
+    """read_twin plus the extras' buffers, unrounded."""
+    base = read_twin(orc, t, spec, B)
+    fn = orc.lib.volta_oracle_debug_buffer_f64
+
+    def get(kind, i, shape):
+        out = np.zeros(int(np.prod(shape)), np.float64)
+        if fn(t.h, kind, i, out.ctypes.data_as(_D)) != out.size:
+            raise RuntimeError(f"fp64 twin has no buffer {kind} of layer {i}")
+        return out.reshape(shape)
+    return ExtBuffers(base, *_ext_parts(get, spec, B))
+
+
+def _norm(x):
+    return float(np.sqrt(np.sum(np.square(np.asarray(x, np.float64)))))
+
+
+def check_against_yardstick(rep, name, got, want, yard):
+    """Distance of `got` from the twin's `want`, against the fp32 oracle's
+    (`yard`) distance from it on the same step: norm within 4x the oracle's
+    plus 16 eps of the twin's norm, largest element within 8x the oracle's
+    largest plus 16 eps of the twin's largest."""
+    got, want, yard = (np.asarray(x, np.float64) for x in (got, want, yard))
+    e_got, e_yard = got - want, yard - want
+    n_bound = 4.0 * _norm(e_yard) + 16 * EPS * _norm(want) + 1e-37
+    m_bound = 8.0 * float(np.max(np.abs(e_yard), initial=0.0)) + 16 * EPS * float(np.max(np.abs(want), initial=0.0)) \
+        + 1e-37
+    n_got, m_got = _norm(e_got), float(np.max(np.abs(e_got), initial=0.0))
+    ratio = max(n_got / n_bound, m_got / m_bound)
+    bad = int(n_got > n_bound) + int(m_got > m_bound)
+    rep.rows.append((name, ratio, bad, 2))
+    if bad:
+        rep.failures.append(f"{rep.label} {name}: distance from fp64 {n_got:.3e} (norm) / {m_got:.3e} (max) "
+                            f"against the fp32 oracle's {_norm(e_yard):.3e} / "
+                            f"{float(np.max(np.abs(e_yard), initial=0.0)):.3e}")
+
+
+def clip_sum_terms(spec, B):
+    """Sequential terms per thread in the clip's sum of squares (the library
+    cuts the deltas into 256 chunks of 256 threads, then two fixed trees)."""
+    total = B * sum(spec.sizes[1:])
+    chunk = -(-total // 256)
+    return -(-chunk // 256)
+
+
+def check_step_ext(orc, spec, B, X, Y, W0, b0, g0, be0, cand: ExtBuffers, twin: ExtBuffers, yard: ExtBuffers,
+                   label, clip_terms=None) -> Report:
+    """All checks of one extras step.  W0/b0/g0/be0: the parameters and
+    LayerNorm gamma/beta the step started from; yard: the fp32 oracle's
+    buffers of the same step (the yardstick of the row-operation checks);
+    clip_terms: the longest run of sequential additions in the candidate's
+    sum of squares for the clip (default: the HIP library's)."""
+    n, L = spec.n_layers, spec.sizes
+    rep = Report(label)
+    W = [np.asarray(w, np.float64).reshape(L[i], L[i + 1]) for i, w in enumerate(W0)]
+    bvec = [np.asarray(b, np.float64) for b in b0]
+    aW = [np.abs(w) for w in W]
+    ln = bool(spec.layernorm)
+
+    rep.check("act0 (input)", cand.act[0], np.asarray(X, np.float64).reshape(B, L[0]), np.zeros((B, L[0])))
+    for i in range(n):
+        r = L[i]
+        A_c, A_t = cand.act[i], twin.act[i]
+        rnd = 2 * (r + 1) * EPS * (np.abs(A_c) @ aW[i] + np.abs(bvec[i]))
+        zdev = np.abs(A_c - A_t) @ aW[i] + rnd
+        z_own = A_c @ W[i] + bvec[i]
+        if i == n - 1:
+            rep.check(f"fwd{i} local (output)", cand.act[n], z_own, rnd)
+            rep.check(f"fwd{i} vs fp64 (output)", cand.act[n], twin.act[n], zdev)
+        else:
+            rep.check(f"fwd{i} local (pre)", cand.pre[i], z_own, rnd)
+            rep.check(f"fwd{i} vs fp64 (pre)", cand.pre[i], twin.pre[i], zdev)
+            check_against_yardstick(rep, f"fwd{i} vs fp64 (act, row ops)", cand.act[i + 1], twin.act[i + 1],
+                                    yard.act[i + 1])
+    for i, (mc, mt) in enumerate(zip(cand.mask, twin.mask)):
+        rep.check(f"dropout mask {i}", mc, mt, np.zeros_like(mt))
+
+    # the clip scale and the unscaled deltas (delta / s; the division adds
+    # one rounding of the product delta * s)
+    s_c, s_t = cand.scale, twin.scale
+    Du_c = [d / s_c for d in cand.delta]
+    Du_t = [d / s_t for d in twin.delta]
+    Du_y = [d / yard.scale for d in yard.delta]
+    if spec.clip_grad > 0:
+        gsq = sum(float(np.sum(d * d)) for d in Du_c)
+        own = float(np.float32(spec.clip_grad)) / np.sqrt(gsq) if np.sqrt(gsq) > np.float32(spec.clip_grad) else 1.0
+        m = clip_sum_terms(spec, B) if clip_terms is None else clip_terms
+        rep.check("clip scale local", np.array([s_c]), np.array([own]), np.array([own * (m + 24) * EPS]))
+
+    # loss gradient (unscaled)
+    Ln = L[n]
+    yh_c, yh_t = cand.act[n], twin.act[n]
+    if spec.loss == "mse":
+        Yv = np.asarray(Y, np.float64).reshape(B, Ln)
+        scale = 2.0 / (B * Ln)
+        rnd = 10 * EPS * scale * (np.abs(yh_c) + np.abs(Yv))
+        rep.check("loss grad local", Du_c[n - 1], scale * (yh_c - Yv), rnd)
+        rep.check("loss grad vs fp64", Du_c[n - 1], Du_t[n - 1], scale * np.abs(yh_c - yh_t) + rnd)
+    else:
+        lab = np.asarray(Y).reshape(B)
+        z = yh_c - yh_c.max(axis=1, keepdims=True)
+        p = np.exp(z)
+        p /= p.sum(axis=1, keepdims=True)
+        onehot = np.zeros((B, Ln))
+        onehot[np.arange(B), lab] = 1.0
+        rnd = (4 * Ln + 18) * EPS / B * np.ones((B, Ln))
+        rep.check("loss grad local", Du_c[n - 1], (p - onehot) / B, rnd)
+        dz = np.abs(yh_c - yh_t).max(axis=1, keepdims=True)
+        rep.check("loss grad vs fp64", Du_c[n - 1], Du_t[n - 1], dz / B + rnd)
+
+    for i in range(n - 1, 0, -1):
+        check_against_yardstick(rep, f"delta{i - 1} vs fp64", Du_c[i - 1], Du_t[i - 1], Du_y[i - 1])
+
+    # LayerNorm parameter gradients of hidden layer i: g = delta_{i+1} W_{i+1}^T
+    # (the upstream gradient, before LayerNorm's backward rewrote it)
+    if ln:
+        for i in range(n - 1):
+            c2 = L[i + 2]
+            G_c = Du_c[i + 1] @ W[i + 1].T
+            G_t = Du_t[i + 1] @ W[i + 1].T
+            # fp32 summation of c2 terms, plus the delta / s reconstruction
+            G_rnd = (2 * c2 + 1) * EPS * (np.abs(Du_c[i + 1]) @ aW[i + 1].T)
+            gam = np.asarray(g0[i], np.float64)
+            bet = np.asarray(be0[i], np.float64)
+            den = gam + float(np.float32(1e-12))
+            xh_c = (cand.act[i + 1] - bet) / den
+            xh_t = (twin.act[i + 1] - bet) / den
+            xh_rnd = 3 * EPS * np.abs(xh_c) + EPS * (np.abs(cand.act[i + 1]) + np.abs(bet)) / np.abs(den)
+            rnd_b = (G_rnd + 2 * B * EPS * np.abs(G_c)).sum(axis=0)
+            rep.check(f"dbeta{i} local", cand.dbe[i], G_c.sum(axis=0), rnd_b + 1e-37)
+            rep.check(f"dbeta{i} vs fp64", cand.dbe[i], twin.dbe[i],
+                      np.abs(G_c - G_t).sum(axis=0) + rnd_b + 1e-37)
+            P_c = G_c * xh_c
+            rnd_g = (G_rnd * np.abs(xh_c) + np.abs(G_c) * xh_rnd + (2 * B + 2) * EPS * np.abs(P_c)).sum(axis=0)
+            rep.check(f"dgamma{i} local", cand.dg[i], P_c.sum(axis=0), rnd_g + 1e-37)
+            rep.check(f"dgamma{i} vs fp64", cand.dg[i], twin.dg[i],
+                      (np.abs(G_c - G_t) * np.abs(xh_c) + np.abs(G_t) * np.abs(xh_c - xh_t)).sum(axis=0)
+                      + rnd_g + 1e-37)
+
+    # dW_i from the scaled deltas, db_i from the unscaled ones
+    for i in range(n):
+        A_c, A_t = cand.act[i], twin.act[i]
+        D_c, D_t = cand.delta[i], twin.delta[i]
+        rnd = 2 * B * EPS * (np.abs(A_c).T @ np.abs(D_c))
+        rep.check(f"dw{i} local", cand.dw[i], A_c.T @ D_c, rnd + 1e-37)
+        rep.check(f"dw{i} vs fp64", cand.dw[i], twin.dw[i],
+                  np.abs(A_c - A_t).T @ np.abs(D_c) + np.abs(A_t).T @ np.abs(D_c - D_t) + rnd + 1e-37)
+        rnd_b = (2 * B + 2) * EPS * np.abs(Du_c[i]).sum(axis=0)
+        rep.check(f"db{i} local", cand.db[i], Du_c[i].sum(axis=0), rnd_b + 1e-37)
+        rep.check(f"db{i} vs fp64", cand.db[i], twin.db[i], np.abs(Du_c[i] - Du_t[i]).sum(axis=0) + rnd_b + 1e-37)
+    return rep
+
+
+def expected_update_ext(orc, spec, lr, t_next, W0, b0, state0, dw, db, g0, be0, dg, dbe):
+    """expected_update plus LayerNorm's SGD step of gamma/beta
+    (gamma -= lr * dgamma, :884-885) written into the state's tail
+    ([gamma_i | beta_i] per hidden layer after the optimizer's moments)."""
+    n, L = spec.n_layers, spec.sizes
+    per = sum(L[i] * L[i + 1] + L[i + 1] for i in range(n))
+    k = {"adam": 2, "adamw": 2, "adagrad": 1}[spec.optimizer] * per
+    st0 = np.asarray(state0, np.float32)
+    W, bb, head = expected_update(orc, spec, lr, t_next, W0, b0, st0[:k], dw, db)
+    tail = []
+    lr32 = np.float32(lr)
+    for i in range(len(g0)):
+        g = np.asarray(g0[i], np.float32) - lr32 * np.asarray(dg[i], np.float32)
+        b = np.asarray(be0[i], np.float32) - lr32 * np.asarray(dbe[i], np.float32)
+        tail += [g.astype(np.float32), b.astype(np.float32)]
+    st = np.concatenate([head] + tail).astype(np.float32) if tail else head
+    return W, bb, st

@@ -115,3 +115,63 @@ def test_teacher_forced_step_gradients(name, k):
         assert gc.bits_equal(W1[i], We[i]), f"W{i} differs from the oracle's update of the HIP gradient"
         assert gc.bits_equal(b1[i], be[i]), f"b{i} differs from the oracle's update of the HIP gradient"
     assert gc.bits_equal(st1, ste), "optimizer state differs from the oracle's update of the HIP gradient"
+
+
+@pytest.mark.parametrize("step", [25, 50])
+def test_c5_late_step_gradients_from_hip_state(step):
+    """C5 (B=4096, softmax-CE, Adagrad eps 1e-10) over its 50 steps
+    the HIP run's own parameters and Adagrad
+    sums after step-1 steps, then step `step` checked as above -- every
+    product against the fp32 summation bound and the fp64 twin's step from
+    the same state, and the update bit-equal to the oracle's Adagrad applied
+    to the HIP gradients.  Teacher-forced from the HIP state, so no 50-step
+    CPU trajectory is needed."""
+    from tests.test_oracle import oracle_trainer
+
+    name = "c5_wide_ce_adagrad_b4096"
+    spec, B, lr, _ = CONFIGS[name]
+    say(f"gradient parity {name} step {step} from the HIP run's state")
+    ws, bs, batches = config_inputs(spec, B)
+    X, Y = batches[0]
+    orc = load_oracle()
+    old = os.environ.get("VOLTA_KEEP_GRADS")
+    os.environ["VOLTA_KEEP_GRADS"] = "1"
+    try:
+        th = Trainer(load_hip(), spec, B)
+    finally:
+        if old is None:
+            os.environ.pop("VOLTA_KEEP_GRADS", None)
+        else:
+            os.environ["VOLTA_KEEP_GRADS"] = old
+    th.set_all_params(ws, bs)
+    for _ in range(step - 1):
+        th.step(X, Y, lr)
+    assert th.status() == 0
+    W0, b0 = th.get_params()
+    W0 = [w.copy() for w in W0]
+    b0 = [b.copy() for b in b0]
+    st0, t0 = th.get_state()
+    th.step(X, Y, lr)
+    assert th.status() == 0, f"HIP step status {th.status()}"
+    say(f"  {step} hip steps done; fp64 twin step")
+    tt = oracle_trainer(orc, spec, B, f64=True)
+    tt.set_all_params(W0, b0)
+    tt.set_state(st0, t0)
+    tt.step(X, Y, lr)
+    cand = gc.read_candidate(th, spec, B)
+    twin = gc.read_twin(orc, tt, spec, B)
+    W1, b1 = th.get_params()
+    st1, t1 = th.get_state()
+    th.close()
+    tt.close()
+
+    say("  product checks")
+    rep = gc.check_step(orc, spec, B, X, Y, W0, b0, cand, twin, f"step {step}")
+    say(rep.summary())
+    assert not rep.failures, "\n".join(rep.failures)
+    say("  optimizer on the HIP gradients")
+    We, be, ste = gc.expected_update(orc, spec, lr, t1, W0, b0, st0, cand.dw, cand.db)
+    for i in range(spec.n_layers):
+        assert gc.bits_equal(W1[i], We[i]), f"W{i} differs from the oracle's update of the HIP gradient"
+        assert gc.bits_equal(b1[i], be[i]), f"b{i} differs from the oracle's update of the HIP gradient"
+    assert gc.bits_equal(st1, ste), "Adagrad sums differ from the oracle's update of the HIP gradient"

@@ -802,3 +802,43 @@ def test_division_by_a_constant_through_double_is_the_fp32_quotient():
         want = x / c
         got = (x.astype(np.float64) * (1.0 / c.astype(np.float64))).astype(np.float32)
     np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("hidden_act", [0, -1], ids=["relu", "linear"])
+def test_oracle_inference_model_graph(oracle, hidden_act):
+    """volta_infer_model_create (the `volta compile` library's model): the
+    graph of lower_model_to_graph (lowering.rs:87-140) -- x W_i + b_i per
+    layer, ReLU after each hidden layer (hidden_act VOLTA_ACT_RELU = 0) or
+    nothing (-1) -- on the embedded [W_0|b_0|W_1|b_1|...] parameters.
+    Against the float64 numpy forward within the fp32 summation bound
+    2(K+1) eps |x||W| + |b| per layer (with the bound carried through the
+    later layers), and a ReLU model differs from the linear one."""
+    sizes = [24, 40, 33, 5]
+    rng = np.random.default_rng(8)
+    ws = [rng.standard_normal((sizes[i], sizes[i + 1])).astype(np.float32) / 4 for i in range(3)]
+    bs = [rng.standard_normal(sizes[i + 1]).astype(np.float32) for i in range(3)]
+    blob = np.concatenate([np.concatenate([w.ravel(), b]) for w, b in zip(ws, bs)]).astype(np.float32)
+    arr = (C.c_int32 * 4)(*sizes)
+    F = C.POINTER(C.c_float)
+    h = oracle.lib.volta_infer_model_create(4, arr, hidden_act, blob.ctypes.data_as(F))
+    assert h
+    rows = 70  # more rows than the model's 64-row chunk
+    X = rng.standard_normal((rows, sizes[0])).astype(np.float32)
+    out = np.zeros((rows, sizes[-1]), np.float32)
+    assert oracle.lib.volta_train_infer(h, X.ctypes.data_as(F), rows, out.ctypes.data_as(F)) == 0
+    oracle.lib.volta_train_free(h)
+    eps = 2.0 ** -24
+    a = X.astype(np.float64)
+    err = np.zeros_like(a)
+    for i in range(3):
+        W = ws[i].astype(np.float64)
+        z = a @ W + bs[i]
+        err = err @ np.abs(W) + 2 * (sizes[i] + 1) * eps * (np.abs(a) @ np.abs(W) + np.abs(bs[i]))
+        if i < 2 and hidden_act == 0:
+            z = np.maximum(z, 0.0)
+        a = z
+    assert np.all(np.abs(out - a) <= err * (1 + 1e-6) + 1e-30)
+    # the two graphs differ (the ReLU is applied or not)
+    relu_differs = np.any(np.maximum(X.astype(np.float64) @ ws[0] + bs[0], 0) != X.astype(np.float64) @ ws[0] + bs[0])
+    assert relu_differs
+    assert oracle.lib.volta_infer_model_create(4, arr, 3, blob.ctypes.data_as(F)) is None  # tanh: refused

@@ -280,3 +280,123 @@ def test_cli_check_and_compile_train(tmp_path):
                        capture_output=True, text=True)
     assert r.returncode == 0 and (tmp_path / "x.so.c").exists()
     assert subprocess.run([CLI, "frobnicate", str(vt)], capture_output=True).returncode == 2
+
+
+INFER_VT = "model m\n    layers 4 3 2\n    activation {act}\n\ndataset d\n    batch 2\n\ntrain m on d\n    epochs 1\n" \
+           "    optimizer rmsprop\n"
+
+
+def _rodata(path):
+    """The bytes of a shared library's .rodata section."""
+    import tempfile
+
+    with tempfile.NamedTemporaryFile(suffix=".bin") as f:
+        subprocess.run(["objcopy", "-O", "binary", "--only-section=.rodata", str(path), f.name], check=True)
+        return open(f.name, "rb").read()
+
+
+def test_compile_flags_as_the_reference_checks_them(tmp_path):
+    """compile's arguments (main.rs:541-586): -o once and not a flag,
+    --cpu-target portable|native, no other flag, exactly one file."""
+    vt = tmp_path / "m.vt"
+    vt.write_text(INFER_VT.format(act="relu"))
+    cases = [
+        (["--cpu-target", "fast"], "'compile --cpu-target' accepts only 'portable' or 'native', got 'fast'"),
+        (["-o"], "'compile -o' requires an output path"),
+        (["-o", "--rust"], "'compile -o' requires an output path"),
+        (["-o", "a.so", "-o", "b.so"], "'compile' accepts '-o' at most once"),
+        (["--rust"], "'compile' does not accept flag '--rust'"),
+        ([str(vt)], "'compile' expects exactly one .vt file"),
+    ]
+    for extra, msg in cases:
+        r = subprocess.run([CLI, "compile", str(vt)] + extra, capture_output=True, text=True)
+        assert r.returncode == 2 and msg in r.stderr, (extra, r.stderr)
+    r = subprocess.run([CLI, "compile"], capture_output=True, text=True)
+    assert r.returncode == 2 and "'compile' expects a .vt file path" in r.stderr
+
+
+@pytest.mark.parametrize("act,ok", [("relu", True), ("gelu", True), ("tanh", True), ("sigmoid", False),
+                                    ("softmax", False)])
+def test_compile_resolution(tmp_path, act, ok):
+    """The inference graph of lower_model_to_graph (lowering.rs:87-140): ReLU
+    hidden layers for 'relu', linear for the activations it drops (noted);
+    'sigmoid' and 'softmax' fail as the reference's inference codegen fails
+    on Sigmoid / Softmax nodes (codegen/inner.rs:395-399).  No compile-train
+    optimizer guard applies (the script trains with RMSProp here)."""
+    import numpy as np
+
+    vt = tmp_path / "m.vt"
+    vt.write_text(INFER_VT.format(act=act))
+    w = tmp_path / "m.f32"
+    np.arange(4 * 3 + 3 + 3 * 2 + 2, dtype=np.float32).tofile(w)
+    r = subprocess.run([CLI, "compile", str(vt), "--weights", str(w)], capture_output=True, text=True)
+    if not ok:
+        assert r.returncode == 1 and "Unsupported op in codegen" in r.stderr, r.stderr
+        return
+    assert r.returncode == 0, r.stderr
+    assert r.stdout.startswith(f"Compiled: {tmp_path / 'm.so'} (cpu-target=portable)")
+    assert ("no activation for '%s'" % act in r.stdout) == (act != "relu")
+
+
+def test_compile_requires_weights_and_checks_their_size(tmp_path):
+    import numpy as np
+
+    vt = tmp_path / "m.vt"
+    vt.write_text(INFER_VT.format(act="relu"))
+    r = subprocess.run([CLI, "compile", str(vt)], capture_output=True, text=True)
+    assert r.returncode == 1 and "Model 'm' has no weights" in r.stderr
+    w = tmp_path / "m.f32"
+    np.zeros(5, np.float32).tofile(w)
+    r = subprocess.run([CLI, "compile", str(vt), "--weights", str(w)], capture_output=True, text=True)
+    assert r.returncode == 1 and "holds 20 bytes" in r.stderr and "needs 92" in r.stderr
+
+
+def test_compile_library_embeds_weights_and_exports_volta_infer(tmp_path):
+    """The generated library carries the weights file's bytes in its
+    read-only data (the reference embeds its trained weights as constant
+    globals, codegen/inner.rs:251-260) -- also from a path holding a quote,
+    a backslash and a newline -- and exports volta_infer.  Without a GPU the
+    first call writes nothing and names the reason."""
+    import numpy as np
+
+    vt = tmp_path / "m.vt"
+    vt.write_text(INFER_VT.format(act="relu"))
+    blob = np.random.default_rng(3).standard_normal(4 * 3 + 3 + 3 * 2 + 2).astype(np.float32)
+    w = tmp_path / 'w"e\\ir\nd.f32'
+    blob.tofile(w)
+    out = tmp_path / "inf.so"
+    r = subprocess.run([CLI, "compile", str(vt), "--weights", str(w), "-o", str(out)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    assert blob.tobytes() in _rodata(out)
+    lib = C.CDLL(str(out))
+    assert hasattr(lib, "volta_infer")
+    F = C.POINTER(C.c_float)
+    lib.volta_infer.argtypes = [F, C.c_int64, F, C.c_int64]
+    lib.volta_infer_last_error.restype = C.c_char_p
+    X = np.ones(4, np.float32)
+    y = np.full(2, 5.0, np.float32)
+    lib.volta_infer(X.ctypes.data_as(F), 4, y.ctypes.data_as(F), 2)
+    if lib.volta_infer_last_error():  # no GPU here
+        assert (y == 5.0).all() and b"HIP" in lib.volta_infer_last_error()
+
+
+def test_compile_train_weights_rounded_as_the_reference_literals(tmp_path):
+    """compile-train --weights embeds each value as the reference's C-path
+    loader holds it: printed f"{v:.8}f" (mlp_train_codegen.rs:393-405) and
+    read back as the nearest float32 -- values below 5e-9 become 0, and
+    others move by up to 5e-9."""
+    import numpy as np
+
+    vt = tmp_path / "m.vt"
+    vt.write_text("model m\n    layers 4 3 2\n")
+    blob = np.random.default_rng(4).standard_normal(4 * 3 + 3 + 3 * 2 + 2).astype(np.float32)
+    blob[:4] = [1e-9, -3e-9, 0.123456789, 2.0 ** -9 * 63]
+    w = tmp_path / "m.f32"
+    blob.tofile(w)
+    r = subprocess.run([CLI, "compile-train", str(vt), "--weights", str(w), "-o", str(tmp_path / "t.so")],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    want = np.array([np.float32(f"{float(v):.8f}") for v in blob], np.float32)
+    assert want[0] == 0 and want[1] == 0 and want[2] == np.float32(0.12345679)
+    assert want.tobytes() in _rodata(tmp_path / "t.so")
+    assert not (tmp_path / "t.so.weights").exists()

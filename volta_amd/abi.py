@@ -147,6 +147,7 @@ _SIGNATURES = {
     "volta_train_infer_device_noalloc": (C.c_int32, [_P, C.c_void_p, C.c_int64, C.c_void_p]),
     "volta_infer_bind": (C.c_int32, [_P]),
     "volta_infer": (None, [_F, C.c_int64, _F, C.c_int64]),
+    "volta_infer_model_create": (_P, [C.c_int32, C.POINTER(C.c_int32), C.c_int32, _F]),
 }
 
 # include/volta_vt.h (the .vt front end; GPU library only)
@@ -158,6 +159,7 @@ VT_SIGNATURES = {
 
 BUF_ACT, BUF_DELTA, BUF_GRAD_W, BUF_GRAD_B = 0, 1, 2, 3
 BUF_LN_GAMMA, BUF_LN_BETA, BUF_DROPOUT_MASK, BUF_PRE = 4, 5, 6, 7
+BUF_LN_DGAMMA, BUF_LN_DBETA, BUF_CLIP_SCALE = 8, 9, 10
 
 # Every symbol include/volta_train.h declares (checked by the CPU tests).
 HEADER_SYMBOLS = tuple(_SIGNATURES)
@@ -332,7 +334,9 @@ class Trainer:
         count = {BUF_ACT: lambda i: B * sizes[i], BUF_DELTA: lambda i: B * sizes[i + 1],
                  BUF_GRAD_W: lambda i: sizes[i] * sizes[i + 1], BUF_GRAD_B: lambda i: sizes[i + 1],
                  BUF_LN_GAMMA: lambda i: sizes[i + 1], BUF_LN_BETA: lambda i: sizes[i + 1],
-                 BUF_DROPOUT_MASK: lambda i: B * sizes[i + 1], BUF_PRE: lambda i: B * sizes[i + 1]}[kind](layer)
+                 BUF_DROPOUT_MASK: lambda i: B * sizes[i + 1], BUF_PRE: lambda i: B * sizes[i + 1],
+                 BUF_LN_DGAMMA: lambda i: sizes[i + 1], BUF_LN_DBETA: lambda i: sizes[i + 1],
+                 BUF_CLIP_SCALE: lambda i: 1}[kind](layer)
         out = np.zeros(count, np.float32)
         n = self.lib.lib.volta_train_debug_buffer(self.h, kind, layer, fptr(out))
         if n != count:

@@ -133,6 +133,9 @@ struct Handle {
   bool extras() const { return hidden_ext() || ext_clip; }
   // activation of the hidden layers' GEMM epilogue (softmax runs after it)
   int gemm_act() const { return ext_softmax ? kIdentity : spec.activation; }
+  // inference model of a `volta-hip compile` library whose hidden layers
+  // carry no activation (volta_infer_model_create)
+  bool infer_linear = false;
 
   // --- launch sequence -------------------------------------------------------
   bool use_graph = true;
@@ -1013,7 +1016,7 @@ static bool enqueue_forward_into(Handle* h, const std::vector<GemmPlan>& plans, 
     a.N = lp.c;
     a.K = lp.r;
     a.epi.kind = EPI_BIAS_ACT;
-    a.epi.act = last ? kIdentity : h->gemm_act();
+    a.epi.act = last || h->infer_linear ? kIdentity : h->gemm_act();
     a.epi.ldc = lp.c;
     a.epi.out = last ? out : h->act[i + 1];
     a.epi.bias = h->params + lp.b_off;
@@ -1424,6 +1427,17 @@ int64_t volta_train_debug_buffer(VoltaTrainHandle* vh, int32_t kind, int32_t lay
       src = kind == VOLTA_BUF_LN_GAMMA ? h->ln_g[layer] : h->ln_b[layer];
       count = (size_t)h->L[layer + 1];
       break;
+    case VOLTA_BUF_LN_DGAMMA:
+    case VOLTA_BUF_LN_DBETA:
+      if (layer < 0 || layer >= n - 1 || !h->ext_ln) return -1;
+      src = kind == VOLTA_BUF_LN_DGAMMA ? h->ln_dg[layer] : h->ln_db[layer];
+      count = (size_t)h->L[layer + 1];
+      break;
+    case VOLTA_BUF_CLIP_SCALE:
+      if (!h->ext_clip) return -1;
+      src = &h->scalars->clip_scale;
+      count = 1;
+      break;
     case VOLTA_BUF_DROPOUT_MASK: {
       if (layer < 0 || layer >= n - 1 || !h->ext_drop) return -1;
       count = (size_t)B * h->L[layer + 1];
@@ -1663,6 +1677,37 @@ void volta_infer(const float* input, int64_t in_n, float* output, int64_t out_n)
     return;
   }
   (void)volta_train_infer(g_infer_model, input, in_n / L0, output);
+}
+
+// Rows per forward chunk of an inference model (its handle's batch): every
+// call of volta_train_infer runs its rows this many at a time.
+constexpr int32_t kInferModelChunk = 1024;
+
+VoltaTrainHandle* volta_infer_model_create(int32_t n_sizes, const int32_t* sizes, int32_t hidden_act,
+                                           const float* params) {
+  if (n_sizes < 2 || n_sizes > VOLTA_MAX_LAYER_SIZES || !sizes || !params ||
+      (hidden_act != VOLTA_ACT_RELU && hidden_act != -1)) {
+    set_last_error("volta_infer_model_create: bad arguments");
+    return nullptr;
+  }
+  volta_mlp_spec s;
+  volta_mlp_spec_default(&s, n_sizes, sizes, VOLTA_ACT_RELU, VOLTA_OPT_SGD, VOLTA_LOSS_MSE);
+  VoltaTrainHandle* vh = volta_train_init_spec(&s, kInferModelChunk);
+  if (!vh) return nullptr;
+  Handle* h = H(vh);
+  h->infer_linear = hidden_act == -1;
+  const float* p = params;
+  for (int i = 0; i < h->n; ++i) {
+    const int64_t r = h->L[i], c = h->L[i + 1];
+    volta_train_set_params(vh, i, p, p + r * c);
+    p += r * c + c;
+  }
+  if (!volta::sync(h) || h->status != 0) {
+    set_last_error("volta_infer_model_create: device error while copying the parameters");
+    volta_train_free(vh);
+    return nullptr;
+  }
+  return vh;
 }
 
 int32_t volta_train_set_state(VoltaTrainHandle* vh, const float* state, int64_t step) {

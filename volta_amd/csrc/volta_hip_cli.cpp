@@ -1,6 +1,7 @@
-// volta-hip: the command line of the MI355X training library, for the one
-// subcommand of the reference CLI on this path (`volta compile-train`,
-// main.rs:219-274, argument rules main.rs:587-650).
+// volta-hip: the command line of the MI355X training library, for the two
+// subcommands of the reference CLI that make libraries of a model: `volta
+// compile-train` (main.rs:219-274, argument rules main.rs:587-650) and `volta
+// compile` (the inference library, main.rs:158-215, rules main.rs:541-586).
 //
 //   volta-hip check FILE.vt [--rust]
 //       print the training spec compile-train takes from FILE (and notes on
@@ -22,9 +23,19 @@
 //       CPU code generation and has no counterpart on the GPU.
 //       Extensions: --weights embeds trained parameters (raw little-endian
 //       float32, [W_0 | b_0 | W_1 | b_1 | ...], each W_i row-major [L_i x
-//       L_i+1]) and exports volta_train_load_pretrained, the C path's loader
-//       of trained weights (mlp_train_codegen.rs:386-413); --keep-source
-//       keeps the generated C source beside OUT.
+//       L_i+1]) rounded to 8 decimal places as the reference's literals are,
+//       and exports volta_train_load_pretrained, the C path's loader of
+//       trained weights (mlp_train_codegen.rs:386-413); --keep-source keeps
+//       the generated C source beside OUT.
+//   volta-hip compile FILE.vt --weights FILE.f32 [-o OUT] [--cpu-target portable|native]
+//                     [--keep-source]
+//       write the model's inference library: it exports volta_infer(input,
+//       in_n, output, out_n) (codegen/inner.rs:198) with the weights
+//       embedded bit for bit, as the reference embeds its trained weights,
+//       and runs the forward graph lower_model_to_graph builds for the first
+//       model (lowering.rs:87-140) on the GPU.  The reference trains the
+//       model in its interpreter first; this build has no interpreter, so
+//       --weights is required.  OUT defaults to FILE with the extension .so.
 //
 // Exit status: 0 success, 1 compile error (message on stderr), 2 usage.
 #include <unistd.h>
@@ -36,6 +47,7 @@
 #include <fstream>
 #include <sstream>
 #include <string>
+#include <vector>
 
 #include "../../include/volta_train.h"
 #include "vt_frontend.h"
@@ -46,7 +58,9 @@ int usage() {
   std::fprintf(stderr,
                "usage: volta-hip check FILE.vt [--rust]\n"
                "       volta-hip compile-train FILE.vt [-o OUT] [--rust] [--cpu-target portable|native]\n"
-               "                               [--weights FILE.f32] [--keep-source]\n");
+               "                               [--weights FILE.f32] [--keep-source]\n"
+               "       volta-hip compile FILE.vt --weights FILE.f32 [-o OUT] [--cpu-target portable|native]\n"
+               "                         [--keep-source]\n");
   return 2;
 }
 
@@ -87,15 +101,40 @@ std::string c_string(const std::string& s) {
   return o + "\"";
 }
 
-// C source of the per-model library.
-std::string asm_string(const std::string& s) {
+// A file path as the quoted operand of an assembler directive written inside
+// a C string literal: escaped first for the assembler's string syntax (\"
+// and \\, octal escapes for control characters), then that text escaped for
+// C.
+std::string asm_path_in_c(const std::string& path) {
+  std::string a;
+  for (unsigned char c : path) {
+    if (c == '"' || c == '\\') {
+      a += '\\';
+      a += (char)c;
+    } else if (c < 0x20 || c == 0x7f) {
+      char b[8];
+      std::snprintf(b, sizeof b, "\\%03o", c);
+      a += b;
+    } else {
+      a += (char)c;
+    }
+  }
   std::string o;
-  for (char c : s) {
-    if (c == '"' || c == '\\') o += "\\\\";
+  for (char c : a) {
+    if (c == '"' || c == '\\') o += '\\';
     o += c;
   }
   return o;
 }
+
+// The assembler block that places a file's bytes in the library's read-only
+// data under `symbol` (16-byte aligned).
+std::string incbin_block(const std::string& symbol, const std::string& path) {
+  return "__asm__(\".section .rodata\\n.balign 16\\n.type " + symbol + ", @object\\n" + symbol + ":\\n.incbin \\\"" +
+         asm_path_in_c(path) + "\\\"\\n.previous\\n\");\nextern const float " + symbol + "[];\n";
+}
+
+// C source of the per-model library.
 
 std::string generate(const volta::VtTrainPlan& plan, const std::string& vt_path, const std::string& lib_path,
                      const std::string& weights_path) {
@@ -155,9 +194,7 @@ std::string generate(const volta::VtTrainPlan& plan, const std::string& vt_path,
     << "const char* volta_train_last_error(void) { return p_last_error ? p_last_error() : g_error; }\n";
   if (!weights_path.empty()) {
     // trained parameters embedded in the library's read-only data
-    o << "\n__asm__(\".section .rodata\\n.balign 16\\n.type volta_pretrained_blob, @object\\n"
-      << "volta_pretrained_blob:\\n.incbin \\\"" << asm_string(weights_path) << "\\\"\\n.previous\\n\");\n"
-      << "extern const float volta_pretrained_blob[];\n"
+    o << "\n" << incbin_block("volta_pretrained_blob", weights_path)
       << "void volta_train_load_pretrained(void* h) {\n"
       << "  const float* p = volta_pretrained_blob;\n";
     for (int i = 0; i + 1 < s.n_sizes; ++i) {
@@ -167,6 +204,69 @@ std::string generate(const volta::VtTrainPlan& plan, const std::string& vt_path,
     }
     o << "}\n";
   }
+  return o.str();
+}
+
+// C source of a `compile` library: the reference's inference library
+// (codegen/inner.rs:190-262: weights embedded as constant globals, one
+// exported symbol volta_infer(input, in_n, output, out_n)).  The model is
+// created on the GPU at the first call (volta_infer_model_create in
+// libvolta_hip.so, opened with dlopen) and lives until the process ends.
+std::string generate_infer(const volta::VtInferPlan& plan, const std::string& vt_path, const std::string& lib_path,
+                           const std::string& weights_path) {
+  const int n = (int)plan.sizes.size();
+  std::string layers;
+  for (int i = 0; i < n; ++i) layers += (i ? "-" : "") + std::to_string(plan.sizes[i]);
+  std::ostringstream o;
+  o << "/* Inference library for model '" << plan.model << "' from " << vt_path << ",\n"
+    << " * generated by volta-hip compile: layers " << layers << ", hidden layers MatMul + Add"
+    << (plan.relu_hidden ? " + Relu" : "") << ".\n"
+    << " * Exports volta_infer(input, in_n, output, out_n) with the trained weights\n"
+    << " * embedded; the forward runs on the GPU through " << lib_path << ". */\n"
+    << "#include <dlfcn.h>\n#include <pthread.h>\n#include <stdint.h>\n#include <stdio.h>\n\n"
+    << incbin_block("volta_model_blob", weights_path) << "\n"
+    << "static const int32_t kSizes[" << n << "] = {";
+  for (int i = 0; i < n; ++i) o << (i ? ", " : "") << plan.sizes[i];
+  o << "};\n"
+    << "static void* (*p_create)(int32_t, const int32_t*, int32_t, const float*);\n"
+    << "static int32_t (*p_infer)(void*, const float*, int64_t, float*);\n"
+    << "static const char* (*p_last_error)(void);\n"
+    << "static void* g_model;\n"
+    << "static char g_error[512];\n"
+    << "static pthread_once_t g_once = PTHREAD_ONCE_INIT;\n"
+    << "static pthread_mutex_t g_mu = PTHREAD_MUTEX_INITIALIZER;\n\n"
+    << "static void set_error(const char* what, const char* why) {\n"
+    << "  snprintf(g_error, sizeof g_error, \"%s%s\", what, why ? why : \"\");\n}\n\n"
+    << "static void volta_model_open(void) {\n"
+    << "  void* h = dlopen(" << c_string(lib_path) << ", RTLD_NOW | RTLD_LOCAL);\n"
+    << "  if (!h) { set_error(\"volta_infer: \", dlerror()); return; }\n"
+    << "  *(void**)&p_create = dlsym(h, \"volta_infer_model_create\");\n"
+    << "  *(void**)&p_infer = dlsym(h, \"volta_train_infer\");\n"
+    << "  *(void**)&p_last_error = dlsym(h, \"volta_train_last_error\");\n"
+    << "  if (!p_create || !p_infer || !p_last_error) {\n"
+    << "    set_error(\"volta_infer: the GPU library lacks volta_infer_model_create\", 0);\n    return;\n  }\n"
+    << "  g_model = p_create(" << n << ", kSizes, " << (plan.relu_hidden ? VOLTA_ACT_RELU : -1)
+    << ", volta_model_blob);\n"
+    << "  if (!g_model) set_error(\"volta_infer: \", p_last_error());\n"
+    << "}\n\n"
+    << "/* rows = in_n / " << plan.sizes[0] << " input rows, as many as output holds (out_n / "
+    << plan.sizes[n - 1] << "); one row per call is\n"
+    << " * the reference's graph (input bound to [1, " << plan.sizes[0] << "], executor.rs:1718). */\n"
+    << "void volta_infer(const float* input, int64_t in_n, float* output, int64_t out_n) {\n"
+    << "  pthread_once(&g_once, volta_model_open);\n"
+    << "  if (!g_model) return;\n"
+    << "  if (!input || !output || in_n < " << plan.sizes[0] << " || out_n < " << plan.sizes[n - 1] << ") {\n"
+    << "    set_error(\"volta_infer: input must hold a row of " << plan.sizes[0] << " floats and output one of "
+    << plan.sizes[n - 1] << "\", 0);\n    return;\n  }\n"
+    << "  int64_t rows = in_n / " << plan.sizes[0] << ";\n"
+    << "  if (rows > out_n / " << plan.sizes[n - 1] << ") rows = out_n / " << plan.sizes[n - 1] << ";\n"
+    << "  pthread_mutex_lock(&g_mu);\n"
+    << "  if (p_infer(g_model, input, rows, output) != 0) set_error(\"volta_infer: \", p_last_error());\n"
+    << "  else g_error[0] = 0;\n"
+    << "  pthread_mutex_unlock(&g_mu);\n"
+    << "}\n\n"
+    << "/* Why the last volta_infer call wrote nothing (\"\" after a call that wrote its output). */\n"
+    << "const char* volta_infer_last_error(void) { return g_error; }\n";
   return o.str();
 }
 
@@ -234,10 +334,34 @@ int compile_train(const TrainArgs& a) {
     }
     weights_real = w;
   }
+  // The reference's C-path loader embeds each trained value as a decimal
+  // literal with 8 places ("{v:.8}f", mlp_train_codegen.rs:393-405), which
+  // the C compiler rounds back to the nearest float: the library embeds the
+  // same values (%.8f of the float, then strtof), written beside OUT.
+  std::string rounded;
+  if (!weights_real.empty()) {
+    std::ifstream f(weights_real, std::ios::binary);
+    std::vector<float> v((size_t)(std::ifstream(weights_real, std::ios::binary | std::ios::ate).tellg() / 4));
+    f.read(reinterpret_cast<char*>(v.data()), (std::streamsize)(v.size() * 4));
+    for (float& x : v) {
+      char buf[96];
+      std::snprintf(buf, sizeof buf, "%.8f", (double)x);
+      x = std::strtof(buf, nullptr);
+    }
+    rounded = out + ".weights";
+    std::ofstream g(rounded, std::ios::binary);
+    g.write(reinterpret_cast<const char*>(v.data()), (std::streamsize)(v.size() * 4));
+    char rr[PATH_MAX];
+    if (!f || !g || !g.flush() || !realpath(rounded.c_str(), rr)) {
+      std::fprintf(stderr, "compile-train error: cannot write %s\n", rounded.c_str());
+      return 1;
+    }
+    rounded = rr;
+  }
   const std::string csrc = out + ".c";
   {
     std::ofstream f(csrc);
-    f << generate(plan, a.path, lib_real, weights_real);
+    f << generate(plan, a.path, lib_real, rounded);
     if (!f) {
       std::fprintf(stderr, "cannot write %s\n", csrc.c_str());
       return 1;
@@ -247,7 +371,10 @@ int compile_train(const TrainArgs& a) {
   const std::string cmd = std::string(cc && *cc ? cc : "cc") + " -O2 -shared -fPIC -o '" + out + "' '" + csrc +
                           "' -ldl";
   const int rc = std::system(cmd.c_str());
-  if (!a.keep) std::remove(csrc.c_str());
+  if (!a.keep) {
+    std::remove(csrc.c_str());
+    if (!rounded.empty()) std::remove(rounded.c_str());
+  }
   if (rc != 0) {
     std::fprintf(stderr, "compile-train error: C compiler failed: %s\n", cmd.c_str());
     return 1;
@@ -257,6 +384,117 @@ int compile_train(const TrainArgs& a) {
   if (!weights_real.empty()) std::printf("note: trained weights from %s: volta_train_load_pretrained\n",
                                          weights_real.c_str());
   for (const auto& n : plan.notes) std::printf("note: %s\n", n.c_str());
+  return 0;
+}
+
+// OUT of `compile`: Path::with_extension("so") of FILE (executor.rs:1734-1737).
+std::string default_output(const std::string& path, const std::string& ext) {
+  const size_t dot = path.rfind('.'), slash = path.rfind('/');
+  return (dot != std::string::npos && (slash == std::string::npos || dot > slash) ? path.substr(0, dot) : path) + ext;
+}
+
+struct InferArgs {
+  std::string path, out, cpu_target = "portable", weights;
+  bool keep = false;
+};
+
+int compile_infer(const InferArgs& a) {
+  std::string src, err;
+  if (!read_file(a.path, &src)) {
+    std::fprintf(stderr, "cannot read %s\n", a.path.c_str());
+    return 2;
+  }
+  volta::VtInferPlan plan;
+  if (!volta::vt_compile_infer_plan(src, &plan, &err)) {
+    std::fprintf(stderr, "Compile error: %s: %s\n", a.path.c_str(), err.c_str());
+    return 1;
+  }
+  if (a.weights.empty()) {  // executor.rs:1702-1705: the model must carry weights
+    std::fprintf(stderr, "Compile error: Model '%s' has no weights — train it first (this build has no "
+                 "interpreter to train it: pass --weights FILE)\n", plan.model.c_str());
+    return 1;
+  }
+  const std::string out = a.out.empty() ? default_output(a.path, ".so") : a.out;
+  char lib_real[PATH_MAX];
+  const std::string lib = self_dir() + "/libvolta_hip.so";
+  if (!realpath(lib.c_str(), lib_real)) {
+    std::fprintf(stderr, "Compile error: %s not found (build it with python -m volta_amd.build)\n", lib.c_str());
+    return 1;
+  }
+  long long want = 0;
+  for (size_t i = 0; i + 1 < plan.sizes.size(); ++i)
+    want += ((long long)plan.sizes[i] * plan.sizes[i + 1] + plan.sizes[i + 1]) * 4;
+  char w[PATH_MAX];
+  std::ifstream f(a.weights, std::ios::binary | std::ios::ate);
+  if (!f || !realpath(a.weights.c_str(), w)) {
+    std::fprintf(stderr, "Compile error: cannot read weights file %s\n", a.weights.c_str());
+    return 1;
+  }
+  if ((long long)f.tellg() != want) {
+    std::fprintf(stderr, "Compile error: weights file %s holds %lld bytes; model '%s' needs %lld "
+                 "(float32 [W_0 | b_0 | W_1 | b_1 | ...])\n", a.weights.c_str(), (long long)f.tellg(),
+                 plan.model.c_str(), want);
+    return 1;
+  }
+  const std::string csrc = out + ".c";
+  {
+    std::ofstream g(csrc);
+    g << generate_infer(plan, a.path, lib_real, w);
+    if (!g) {
+      std::fprintf(stderr, "cannot write %s\n", csrc.c_str());
+      return 1;
+    }
+  }
+  const char* cc = std::getenv("CC");
+  const std::string cmd = std::string(cc && *cc ? cc : "cc") + " -O2 -shared -fPIC -o '" + out + "' '" + csrc +
+                          "' -ldl -lpthread";
+  const int rc = std::system(cmd.c_str());
+  if (!a.keep) std::remove(csrc.c_str());
+  if (rc != 0) {
+    std::fprintf(stderr, "Compile error: C compiler failed: %s\n", cmd.c_str());
+    return 1;
+  }
+  std::printf("Compiled: %s (cpu-target=%s)\n", out.c_str(), a.cpu_target.c_str());
+  for (const auto& n : plan.notes) std::printf("note: %s\n", n.c_str());
+  return 0;
+}
+
+// compile's arguments, checked as the reference checks them (main.rs:
+// 541-586) plus this tool's --weights and --keep-source.
+int parse_compile(int argc, char** argv, InferArgs* a) {
+  const std::string cmd = "compile";
+  bool have_out = false;
+  for (int i = 2; i < argc; ++i) {
+    const std::string x = argv[i];
+    if (x == "-o") {
+      if (i + 1 >= argc || argv[i + 1][0] == '-') return arg_error("'" + cmd + " -o' requires an output path");
+      if (have_out) return arg_error("'" + cmd + "' accepts '-o' at most once");
+      a->out = argv[++i];
+      have_out = true;
+    } else if (x == "--cpu-target" || x.rfind("--cpu-target=", 0) == 0) {
+      std::string v;
+      if (x == "--cpu-target") {
+        if (i + 1 >= argc) return arg_error("'" + cmd + " --cpu-target' requires 'portable' or 'native'");
+        v = argv[++i];
+      } else {
+        v = x.substr(std::strlen("--cpu-target="));
+      }
+      if (v != "portable" && v != "native")
+        return arg_error("'" + cmd + " --cpu-target' accepts only 'portable' or 'native', got '" + v + "'");
+      a->cpu_target = v;
+    } else if (x == "--keep-source") {
+      a->keep = true;
+    } else if (x == "--weights") {
+      if (i + 1 >= argc) return arg_error("'" + cmd + " --weights' requires a file");
+      a->weights = argv[++i];
+    } else if (!x.empty() && x[0] == '-') {
+      return arg_error("'" + cmd + "' does not accept flag '" + x + "'");
+    } else {
+      if (!a->path.empty()) return arg_error("'" + cmd + "' expects exactly one .vt file");
+      a->path = x;
+    }
+  }
+  if (a->path.empty()) return arg_error("'" + cmd + "' expects a .vt file path");
   return 0;
 }
 
@@ -317,6 +555,11 @@ int main(int argc, char** argv) {
     TrainArgs a;
     const int rc = parse_compile_train(argc, argv, &a);
     return rc ? rc : compile_train(a);
+  }
+  if (cmd == "compile") {
+    InferArgs a;
+    const int rc = parse_compile(argc, argv, &a);
+    return rc ? rc : compile_infer(a);
   }
   return usage();
 }

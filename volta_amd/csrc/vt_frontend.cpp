@@ -249,9 +249,13 @@ struct Statement {
   int line = 0;
 };
 
-}  // namespace
+// The three commands that resolve the first model: compile-train on the C
+// path, compile-train --rust, and compile (the inference library).
+enum PlanMode { PLAN_C, PLAN_RUST, PLAN_INFER };
 
-bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::string* error, bool rust) {
+bool plan_first_model(const std::string& source, PlanMode mode, VtTrainPlan* plan, std::string* act_name,
+                      std::string* error) {
+  const bool rust = mode == PLAN_RUST;
   try {
     const std::vector<Line> lines = lex(source);
     std::vector<Statement> stmts;
@@ -467,7 +471,11 @@ bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::st
                         " epoch(s) first; its --rust library does not take those weights (the generator "
                         "ignores them, mlp_train_rust_codegen.rs:249-251) and starts from the LCG Xavier init "
                         "(seed 42), as this library does");
-      if (out.epochs > 0 && !rust)
+      if (out.epochs > 0 && mode == PLAN_INFER)
+        notes.push_back("the reference trains the model in its interpreter for " + std::to_string(out.epochs) +
+                        " epoch(s) and embeds those weights; this build has no interpreter: compile --weights "
+                        "FILE supplies them");
+      if (out.epochs > 0 && mode == PLAN_C)
         notes.push_back("the reference's C-path library exports volta_train_load_pretrained with the weights "
                         "its interpreter trained for " + std::to_string(out.epochs) +
                         " epoch(s) (mlp_train_codegen.rs:386-413); this build has no interpreter: the library "
@@ -489,7 +497,17 @@ bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::st
         clip = c;
       }
     }
-    if (rust) {
+    if (mode == PLAN_INFER) {
+      // compile: the forward graph of lower_model_to_graph has no dropout
+      // or LayerNorm (lowering.rs:87-140); the optimizer only trained it
+      if (dropout > 0.0 || layernorm)
+        notes.push_back("the reference's inference graph (lowering.rs:87-140) has no dropout or LayerNorm; "
+                        "the inference library follows it");
+      dropout = 0.0;
+      layernorm = false;
+      clip = 0.0;
+      optimizer = "sgd";
+    } else if (rust) {
       // compile-train --rust guard (executor.rs:3174-3189)
       if (!(optimizer == "sgd" || optimizer == "adam" || optimizer == "adamw" || optimizer == "adagrad"))
         throw Fail{"Model '" + model->name + "' requests optimizer '" + optimizer +
@@ -539,11 +557,43 @@ bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::st
     out.rust = rust;
     out.notes = notes;
     *plan = out;
+    if (act_name) *act_name = activation;
     return true;
   } catch (const Fail& f) {
     if (error) *error = f.msg;
     return false;
   }
+}
+
+}  // namespace
+
+bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::string* error, bool rust) {
+  return plan_first_model(source, rust ? PLAN_RUST : PLAN_C, plan, nullptr, error);
+}
+
+bool vt_compile_infer_plan(const std::string& source, VtInferPlan* plan, std::string* error) {
+  VtTrainPlan p;
+  std::string act;
+  if (!plan_first_model(source, PLAN_INFER, &p, &act, error)) return false;
+  // lower_model_to_graph's hidden layers: Relu for "relu", Sigmoid for
+  // "sigmoid", nothing otherwise; the last layer: Softmax for "softmax"
+  // (lowering.rs:121-134).  The inference codegen lowers MatMul, Add and
+  // Relu and refuses Sigmoid and Softmax (codegen/inner.rs:395-399).
+  if (act == "sigmoid" || act == "softmax") {
+    if (error) *error = std::string("Unsupported op in codegen: ") + (act == "sigmoid" ? "Sigmoid" : "Softmax");
+    return false;
+  }
+  plan->model = p.model;
+  plan->sizes.assign(p.spec.sizes, p.spec.sizes + p.spec.n_sizes);
+  plan->activation = act;
+  plan->relu_hidden = act == "relu";
+  plan->trained = p.trained;
+  plan->notes = p.notes;
+  if (!plan->relu_hidden && plan->sizes.size() > 2)
+    plan->notes.push_back("the reference's inference graph applies no activation for '" + act +
+                          "' (lower_model_to_graph emits Relu or Sigmoid only, lowering.rs:121-129): the hidden "
+                          "layers are linear, in the reference's library and in this one");
+  return true;
 }
 
 std::string vt_plan_summary(const VtTrainPlan& p) {

@@ -27,6 +27,24 @@ struct VtTrainPlan {
 // text) on a parse error or an unsupported model.
 bool vt_compile_train_plan(const std::string& source, VtTrainPlan* plan, std::string* error, bool rust = true);
 
+// The model `volta compile` builds an inference library for (main.rs:
+// 158-215 -> executor.rs:1684-1744): the first model's layers, and the
+// hidden activation of the forward graph lower_model_to_graph builds for it
+// (lowering.rs:87-140): ReLU for activation 'relu', none for every other
+// activation the lowering drops.  'sigmoid' (a Sigmoid node) and 'softmax' (a
+// final Softmax node) fail as the reference's inference codegen fails on
+// those ops (codegen/inner.rs:395-399).  No compile-train guard applies: the
+// reference trains the model in its interpreter first.
+struct VtInferPlan {
+  std::string model;
+  std::vector<int> sizes;
+  std::string activation;   // model.activation as written
+  bool relu_hidden = true;  // false: hidden layers without activation
+  bool trained = false;     // a `train` statement names the model
+  std::vector<std::string> notes;
+};
+bool vt_compile_infer_plan(const std::string& source, VtInferPlan* plan, std::string* error);
+
 // One-line description of a plan ("model=... layers=a-b-c activation=...").
 std::string vt_plan_summary(const VtTrainPlan& plan);
 
