@@ -410,11 +410,18 @@ def check_step_ext(orc, spec, B, X, Y, W0, b0, g0, be0, cand: ExtBuffers, twin: 
         if i == n - 1:
             rep.check(f"fwd{i} local (output)", cand.act[n], z_own, rnd)
             rep.check(f"fwd{i} vs fp64 (output)", cand.act[n], twin.act[n], zdev)
-        else:
+        elif cand.pre[i] is not None:
             rep.check(f"fwd{i} local (pre)", cand.pre[i], z_own, rnd)
             rep.check(f"fwd{i} vs fp64 (pre)", cand.pre[i], twin.pre[i], zdev)
             check_against_yardstick(rep, f"fwd{i} vs fp64 (act, row ops)", cand.act[i + 1], twin.act[i + 1],
                                     yard.act[i + 1])
+        else:
+            # no row operation and no stored pre-activation (ReLU, sigmoid,
+            # tanh derive f' from the output): act = f(z) from the GEMM
+            # epilogue, within f's Lipschitz constant of the operand bound
+            lip = LIPSCHITZ.get(spec.activation, 1.0)
+            f_rnd = 16 * EPS * (np.abs(twin.act[i + 1]) + np.abs(twin.pre[i]))
+            rep.check(f"fwd{i} vs fp64 (act)", cand.act[i + 1], twin.act[i + 1], lip * zdev + f_rnd + 1e-37)
     for i, (mc, mt) in enumerate(zip(cand.mask, twin.mask)):
         rep.check(f"dropout mask {i}", mc, mt, np.zeros_like(mt))
 

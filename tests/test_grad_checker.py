@@ -200,6 +200,22 @@ def test_oracle_fp32_passes_extras_checker(name):
     assert _ext_bits_equal(r, _ext_update(r))
 
 
+def test_extras_checker_without_stored_pre_activation():
+    """The HIP library keeps no pre-activation for ReLU with clipping only
+    (the derivative comes from the output): the forward is then checked on
+    the activation output; a 1% error there still fails."""
+    import copy
+
+    r = _ext_step("clip_relu_adam")
+    cand = copy.deepcopy(r["cand"])
+    cand.pre = [None] * len(cand.pre)
+    rep = _ext_check(r, cand)
+    assert not rep.failures, "\n".join(rep.failures)
+    assert any(name.startswith("fwd0 vs fp64 (act)") for name, *_ in rep.rows)
+    cand.act[1] = cand.act[1] * 1.01
+    assert any("fwd0 vs fp64 (act)" in f for f in _ext_check(r, cand).failures)
+
+
 def _ext_mutated(name, mutate):
     import copy
 
