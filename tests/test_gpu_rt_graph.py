@@ -259,3 +259,78 @@ def test_c5_shape_rows_against_oracle():
     gs = model_graph(layers, "softmax", 64)
     want = oracle_value(gs, build_execution_plan(gs), Bound(sub), None)
     assert_close(got[:64], want, "C5 rows 0-63")
+
+
+@pytest.mark.parametrize("layers,activation,rows", [([512, 1024, 1024, 512, 256, 1], "relu", 64),
+                                                    ([64, 128, 128, 10], "softmax", 300),
+                                                    ([1024, 256, 128, 8], "relu", 64)],
+                         ids=["c2_relu_r64", "softmax_r300", "splitk_r64"])
+def test_captured_replays_match_direct_launches(layers, activation, rows):
+    """With VOLTA_RT_GRAPH=1 a call whose bindings and output repeat a
+    recent call's runs as a replay of its launch sequence captured into a
+    hipGraph.  Every replay equals, bit for bit, the same call launched
+    layer by layer (the default), with direct launches, other values' calls
+    and host synchronizations between the replays; a replay reads the
+    bindings' current contents (new input values in the same buffer give
+    the new values' result); more pointer sets than the program keeps
+    graphs for still give the right values."""
+    import os
+
+    say(f"captured graph replays {layers} {activation} rows={rows}")
+    lib = load_hip()
+    gl = GraphLibrary(lib.lib)
+    g = model_graph(layers, activation, rows)
+    plan = build_execution_plan(g)
+    vals = mlp_values(layers, rows, 21)
+    b = Bound(vals)
+    ncols = layers[-1]
+    cap = rows * ncols
+    out = DeviceArray(np.zeros(cap, F32))
+    mid = DeviceArray(np.zeros(rows * layers[1], F32))
+    bias0 = [i for i, op in chain_ids(g) if op == "add"][0]  # layer 0's bias sum [rows x L1]
+    term = gl.prepare(g, plan, None, b.addr, out.ptr, cap)
+    value1 = gl.prepare(g, plan, bias0, b.addr, mid.ptr, rows * layers[1])
+
+    def direct(fn):
+        old = os.environ.pop("VOLTA_RT_GRAPH", None)
+        try:
+            fn()
+        finally:
+            if old is not None:
+                os.environ["VOLTA_RT_GRAPH"] = old
+
+    direct(term)
+    want = out.numpy().copy()
+    direct(value1)
+    want_mid = mid.numpy().copy()
+    os.environ["VOLTA_RT_GRAPH"] = "1"
+    r0 = lib.lib.volta_hip_rt_graph_replays()
+    for k in range(4):
+        term()
+        np.testing.assert_array_equal(out.numpy(), want, err_msg=f"replay {k}")
+        value1()  # another value of the program: its own sequence
+        np.testing.assert_array_equal(mid.numpy(), want_mid, err_msg=f"value replay {k}")
+        direct(term)
+        np.testing.assert_array_equal(out.numpy(), want, err_msg=f"direct launch after replay {k}")
+    assert lib.lib.volta_hip_rt_graph_replays() - r0 >= 6, "the repeated calls did not run as graph replays"
+    # new input values in the same buffer
+    x2 = np.random.default_rng(5).standard_normal((rows, layers[0])).astype(F32)
+    assert lib.lib.volta_hip_copy(b.addr["input"], x2.ctypes.data, x2.nbytes, 1) == 0
+    term()
+    got2 = out.numpy().copy()
+    direct(term)
+    np.testing.assert_array_equal(got2, out.numpy())
+    b2 = dict(vals)
+    b2["input"] = x2
+    assert_close(got2.reshape(rows, ncols), oracle_value(g, plan, Bound(b2), None), "replay on new input")
+    # more output buffers than captured graphs kept per program
+    outs = [DeviceArray(np.zeros(cap, F32)) for _ in range(10)]
+    for rnd in range(2):
+        for o in outs:
+            c = gl.prepare(g, plan, None, b.addr, o.ptr, cap)
+            c()
+            c()
+            np.testing.assert_array_equal(o.numpy(), got2, err_msg=f"eviction round {rnd}")
+    os.environ.pop("VOLTA_RT_GRAPH", None)
+    for d in outs + [out, mid]:
+        d.free()

@@ -35,6 +35,7 @@ HIP_EXTRA = {
     "volta_hip_device_alloc": (C.c_void_p, [C.c_int64]),
     "volta_hip_device_free": (C.c_int32, [C.c_void_p]),
     "volta_hip_copy": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_int64, C.c_int32]),
+    "volta_hip_rt_graph_replays": (C.c_int64, []),
 }
 
 

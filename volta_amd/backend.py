@@ -306,6 +306,29 @@ class GraphLibrary:
             raise BackendError(self.lib.volta_rt_last_error().decode())
         return int(shape[0]), int(shape[1])
 
+    def prepare(self, graph: Graph, plan: ExecutionPlan, target: Optional[int], addresses: Dict[str, int],
+                out_addr: int, capacity: int, determinism: int = 0):
+        """A call of execute_value (target given) or execute_terminal (None)
+        with its tables built once, as a caller that keeps its graph and
+        bindings between calls holds them: returns a function of no
+        arguments that runs the call and raises on an error."""
+        t = GraphTables(graph, plan)
+        ptrs = t.pointers(addresses)
+        shape = (C.c_int64 * 2)()
+        lib = self.lib
+        if target is None:
+            args = (C.byref(t.c), determinism, ptrs, out_addr, capacity, shape)
+            fn = lib.volta_rt_execute_terminal
+        else:
+            args = (C.byref(t.c), determinism, int(target), ptrs, out_addr, capacity, shape)
+            fn = lib.volta_rt_execute_value
+
+        def call():
+            if fn(*args) != 0:
+                raise BackendError(lib.volta_rt_last_error().decode())
+        call.tables = t  # the C tables live as long as the call
+        return call
+
     def clear_plan_cache(self) -> None:
         self.lib.volta_rt_clear_plan_cache()
 
