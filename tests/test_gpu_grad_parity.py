@@ -175,3 +175,20 @@ def test_c5_late_step_gradients_from_hip_state(step):
         assert gc.bits_equal(W1[i], We[i]), f"W{i} differs from the oracle's update of the HIP gradient"
         assert gc.bits_equal(b1[i], be[i]), f"b{i} differs from the oracle's update of the HIP gradient"
     assert gc.bits_equal(st1, ste), "Adagrad sums differ from the oracle's update of the HIP gradient"
+
+
+@pytest.mark.parametrize("name,k", [("c2_mlp512_relu_adam_b64", 0), ("c2_mlp512_relu_adam_b64", 10),
+                                    ("c3_mlp512w_gelu_adamw_b64", 10)])
+def test_wide_dw_group_step_gradients(name, k):
+    """The dW group with 32x64 small-K tiles (VOLTA_DW_GROUP_TN=64; two
+    accumulators per block, so its sums differ in rounding from the 32-wide
+    default): the same gradient-level checks and the bit-equal update."""
+    old = os.environ.get("VOLTA_DW_GROUP_TN")
+    os.environ["VOLTA_DW_GROUP_TN"] = "64"
+    try:
+        test_teacher_forced_step_gradients(name, k)
+    finally:
+        if old is None:
+            os.environ.pop("VOLTA_DW_GROUP_TN", None)
+        else:
+            os.environ["VOLTA_DW_GROUP_TN"] = old

@@ -162,6 +162,7 @@ struct DwGroup {
   int n = 0;                        // small-K dW products (plan TILE_DW_SMALLK)
   GemmArgs g[kMaxDwGroup];
   int start[kMaxDwGroup + 1] = {};  // first workgroup of product i after the narrow ones; start[n] = total
+  int tile_n = 32;                  // columns of the small-K tiles: 32, or 64 (the wide form)
   int narrow_blocks = 0;            // 0: no narrow dW
   NarrowDwArgs nd{};
   // the step's loss, when the output launch deferred it (launch_out_layer_dx
@@ -172,6 +173,8 @@ struct DwGroup {
   DevScalars* loss_scalars = nullptr;
 };
 bool dw_group_supported(const DwGroup& d);
+// Workgroups of product `a` in a group whose small-K tiles are 32 x tile_n.
+int dw_group_tiles(const GemmArgs& a, int tile_n);
 hipError_t dw_group_launch(const DwGroup& d, hipStream_t st, Recorder* rec, const char* label, double flops,
                            double bytes);
 

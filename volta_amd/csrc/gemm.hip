@@ -1611,27 +1611,46 @@ constexpr int kDwK = 64;
 constexpr int kDwS = kDwT + 4;   // LDS row stride of the [k][32] operand slices
 constexpr int kDwDS = kDwT + 1;  // LDS row stride of the dW tile
 constexpr int kDwLds = 2 * kDwK * kDwS + kDwT * kDwDS;
+// The wide form (32x64 tiles of W): a [k][64] B slice, and the dW tile over
+// the A slice once the product has consumed it.
+constexpr int kDwTW = 64;
+constexpr int kDwLdsW = kDwK * kDwS + kDwK * (kDwTW + 4);
+static_assert(kDwT * (kDwTW + 1) <= kDwK * kDwS, "the wide dW tile fits over the A slice");
 
-// `tid` (0..255): the thread's index among the tile's 256.
-template <int EPI>
+// `tid` (0..255): the thread's index among the tile's 256.  TN: the tile's
+// columns, 32 (four float4 loads of W/m/v state per thread's element group)
+// or 64 (the wide form: half the workgroups, each thread owning two float4
+// of W, in rows r and r + 16).  Every element of dW sums the same products
+// in the same order in both forms, so their results are bit-identical.
+template <int EPI, int TN = kDwT>
 __device__ __forceinline__ void dw_smallk_tile(const GemmArgs& args, int blk, float* lds, int tid) {
   static_assert(EPI == EPI_DW_OPT || EPI == EPI_STORE, "epilogues of the dW tile");
+  static_assert(TN == kDwT || TN == kDwTW, "tile widths of the dW tile");
+  constexpr int SB = TN + 4;          // LDS row stride of the B slice
+  constexpr int DS = TN + 1;          // LDS row stride of the dW tile
+  constexpr int NB = TN / 32;         // 16-column blocks per wave
+  constexpr int BIT = TN / 16;        // float4 of the B slice per thread
+  constexpr int CPR = TN / 4;         // float4 per row of the tile
+  constexpr int EIT = kDwT * CPR / 256;  // float4 of W per thread
+  constexpr int RSTEP = 256 / CPR;    // rows between a thread's float4 of W
   const int lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, q = lane >> 4;
   const int wm = wave >> 1, wn = wave & 1;
   const int M = args.M, N = args.N, K = args.K;
-  const int tiles_n = (N + kDwT - 1) / kDwT;
+  const int tiles_n = (N + TN - 1) / TN;
   const int tm = blk / tiles_n, tn = blk % tiles_n;
-  const int m0 = tm * kDwT, n0 = tn * kDwT;
-  float* la = lds;                    // la[kk*kDwS + mm] = A(m0 + mm, k0 + kk)
-  float* lb = lds + kDwK * kDwS;      // lb[kk*kDwS + nn] = B(k0 + kk, n0 + nn)
-  float* ld = lds + 2 * kDwK * kDwS;  // ld[mm*kDwDS + nn] = dW(m0 + mm, n0 + nn)
+  const int m0 = tm * kDwT, n0 = tn * TN;
+  float* la = lds;                // la[kk*kDwS + mm] = A(m0 + mm, k0 + kk)
+  float* lb = lds + kDwK * kDwS;  // lb[kk*SB + nn] = B(k0 + kk, n0 + nn)
+  // ld[mm*DS + nn] = dW(m0 + mm, n0 + nn): after both slices (32 wide), over
+  // the A slice (64 wide)
+  float* ld = TN == kDwT ? lds + 2 * kDwK * kDwS : lds;
   const EpiArgs& e = args.epi;
   const floatx4 zero4 = {0.f, 0.f, 0.f, 0.f};
 
-  // One 64-k slice of both operands: 64 rows of 8 float4 each, two of each
-  // per thread.
-  floatx4 xa[2], xb[2];
+  // One 64-k slice of both operands: 64 rows of 8 float4 of A (two per
+  // thread) and 64 rows of TN/4 float4 of B (TN/16 per thread).
+  floatx4 xa[2], xb[BIT];
   auto load_slice = [&](int k0) {
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
@@ -1639,11 +1658,20 @@ __device__ __forceinline__ void dw_smallk_tile(const GemmArgs& args, int blk, fl
       const int kk = slot >> 3, c4 = (slot & 7) * 4;
       const int k = k0 + kk;
       const bool kok = k < K;
-      const bool aok = kok && m0 + c4 < M, bok = kok && n0 + c4 < N;
+      const bool aok = kok && m0 + c4 < M;
       const size_t ka = kok ? (size_t)k : 0;
       const floatx4 va = *reinterpret_cast<const floatx4*>(args.A + ka * args.lda + (aok ? m0 + c4 : 0));
-      const floatx4 vb = *reinterpret_cast<const floatx4*>(args.B + ka * args.ldb + (bok ? n0 + c4 : 0));
       xa[it] = aok ? va : zero4;
+    }
+#pragma unroll
+    for (int it = 0; it < BIT; ++it) {
+      const int slot = tid + 256 * it;
+      const int kk = slot / CPR, c4 = (slot % CPR) * 4;
+      const int k = k0 + kk;
+      const bool kok = k < K;
+      const bool bok = kok && n0 + c4 < N;
+      const size_t kb = kok ? (size_t)k : 0;
+      const floatx4 vb = *reinterpret_cast<const floatx4*>(args.B + kb * args.ldb + (bok ? n0 + c4 : 0));
       xb[it] = bok ? vb : zero4;
     }
   };
@@ -1653,41 +1681,67 @@ __device__ __forceinline__ void dw_smallk_tile(const GemmArgs& args, int blk, fl
       const int slot = tid + 256 * it;
       const int kk = slot >> 3, c4 = (slot & 7) * 4;
       *reinterpret_cast<floatx4*>(la + kk * kDwS + c4) = xa[it];
-      *reinterpret_cast<floatx4*>(lb + kk * kDwS + c4) = xb[it];
+    }
+#pragma unroll
+    for (int it = 0; it < BIT; ++it) {
+      const int slot = tid + 256 * it;
+      const int kk = slot / CPR, c4 = (slot % CPR) * 4;
+      *reinterpret_cast<floatx4*>(lb + kk * SB + c4) = xb[it];
     }
   };
 
-  // This thread's elements of the tile and, for the first row of tiles,
-  // its column of b_i.
-  const int row = tid >> 3, c4 = (tid & 7) * 4;
-  const int gm = m0 + row, gn = n0 + c4;
-  const bool own = gm < M && gn < N;  // N % 4 == 0: the whole float4 is in range
-  const uint32_t o = own ? (uint32_t)gm * (uint32_t)e.ldc + (uint32_t)gn : 0u;
-  const int bn = n0 + (tid & 31);
+  // This thread's elements of the tile (float4 j in row row0 + j*RSTEP)
+  // and, for the first row of tiles, its column of b_i.
+  const int row0 = tid / CPR, c4 = (tid % CPR) * 4;
+  const int gn = n0 + c4;
+  bool own[EIT];
+  uint32_t o[EIT];
+#pragma unroll
+  for (int j = 0; j < EIT; ++j) {
+    const int gm = m0 + row0 + j * RSTEP;
+    own[j] = gm < M && gn < N;  // N % 4 == 0: the whole float4 is in range
+    o[j] = own[j] ? (uint32_t)gm * (uint32_t)e.ldc + (uint32_t)gn : 0u;
+  }
+  const int bn = n0 + (tid & (TN - 1));
   const bool do_db = EPI == EPI_DW_OPT && args.colsum_b && e.b && tm == 0;
 
   load_slice(0);
   __builtin_amdgcn_sched_barrier(0);
-  floatx4 w4 = zero4, m4 = zero4, v4 = zero4;
+  floatx4 w4[EIT], m4[EIT], v4[EIT];
   BiasState bst;
-  if constexpr (EPI == EPI_DW_OPT) {
-    // SGD/Adagrad read their absent state buffers from W's own address (same lines)
-    const float* pm = e.m ? e.m : e.out;
-    const float* pv = e.v ? e.v : e.out;
-    w4 = *reinterpret_cast<const floatx4*>(e.out + o);
-    m4 = *reinterpret_cast<const floatx4*>(pm + o);
-    v4 = *reinterpret_cast<const floatx4*>(pv + o);
+  // SGD/Adagrad read their absent state buffers from W's own address (same lines)
+  const float* pm = e.m ? e.m : e.out;
+  const float* pv = e.v ? e.v : e.out;
+  // the state loaded before the product (all of it in the 32-wide form; the
+  // wide form's second float4 after it, which keeps the kernel within five
+  // waves per SIMD without spills)
+  constexpr int EARLY = TN == kDwT ? EIT : 1;
+  auto load_state = [&](int j) {
+    w4[j] = *reinterpret_cast<const floatx4*>(e.out + o[j]);
+    m4[j] = *reinterpret_cast<const floatx4*>(pm + o[j]);
+    v4[j] = *reinterpret_cast<const floatx4*>(pv + o[j]);
+  };
+  auto load_bias_state = [&]() {
     const float* pb = e.b ? e.b : e.out;
     const uint32_t ob = e.b && bn < N ? (uint32_t)bn : 0u;
     bst.b = pb[ob];
     bst.m = (e.bm ? e.bm : pb)[ob];
     bst.v = (e.bv ? e.bv : pb)[ob];
+  };
+  if constexpr (EPI == EPI_DW_OPT) {
+#pragma unroll
+    for (int j = 0; j < EARLY; ++j) load_state(j);
+    if constexpr (TN == kDwT) load_bias_state();
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  floatx4 acc[4];
+  // accumulators per block: 16-k group g of a slice adds into acc[nb][g % NACC]
+  constexpr int NACC = TN == kDwT ? 4 : 2;
+  floatx4 acc[NB][NACC];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) acc[c] = zero4;
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int c = 0; c < NACC; ++c) acc[nb][c] = zero4;
   float db = 0.0f;
   for (int k0 = 0; k0 < K; k0 += kDwK) {
     if (k0 > 0) {
@@ -1696,7 +1750,7 @@ __device__ __forceinline__ void dw_smallk_tile(const GemmArgs& args, int blk, fl
     }
     store_slice();
     __syncthreads();
-    if (do_db && tid < kDwT) {
+    if (do_db && tid < TN) {
       // batch order; each batch of 8 reads is issued before its first add
       // (8 registers, not the slice's 64: the kernel's occupancy)
       const int kn = min(kDwK, K - k0);
@@ -1704,7 +1758,7 @@ __device__ __forceinline__ void dw_smallk_tile(const GemmArgs& args, int blk, fl
       for (int k1 = 0; k1 < kDwK; k1 += 8) {
         float col[8];
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk) col[kk] = lb[(k1 + kk) * kDwS + tid];
+        for (int kk = 0; kk < 8; ++kk) col[kk] = lb[(k1 + kk) * SB + tid];
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
           const float t = db + col[kk];
@@ -1718,58 +1772,82 @@ __device__ __forceinline__ void dw_smallk_tile(const GemmArgs& args, int blk, fl
       for (int s = 0; s < 4; ++s) {
         const int kk = 16 * g + 4 * q + s;
         const float a = la[kk * kDwS + wm * 16 + r16];
-        const float b = lb[kk * kDwS + wn * 16 + r16];
-        acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[g], 0, 0, 0);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const float b = lb[kk * SB + (wn * NB + nb) * 16 + r16];
+          acc[nb][g % NACC] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[nb][g % NACC], 0, 0, 0);
+        }
       }
   }
-  // register v of lane (r16, q): dW(wm*16 + 4q + v, wn*16 + r16)
+  if constexpr (EPI == EPI_DW_OPT) {
 #pragma unroll
-  for (int v = 0; v < 4; ++v)
-    ld[(wm * 16 + 4 * q + v) * kDwDS + wn * 16 + r16] = (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]);
+    for (int j = EARLY; j < EIT; ++j) load_state(j);
+    if constexpr (TN != kDwT) load_bias_state();
+  }
+  if constexpr (TN != kDwT) __syncthreads();  // the dW tile goes over the A slice
+  // register v of lane (r16, q) of block nb: dW(wm*16 + 4q + v, (wn*NB + nb)*16 + r16)
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float sum;
+      if constexpr (NACC == 4) sum = (acc[nb][0][v] + acc[nb][1][v]) + (acc[nb][2][v] + acc[nb][3][v]);
+      else sum = acc[nb][0][v] + acc[nb][1][v];
+      ld[(wm * 16 + 4 * q + v) * DS + (wn * NB + nb) * 16 + r16] = sum;
+    }
   __syncthreads();
-  floatx4 g4;
+  floatx4 g4[EIT];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) g4[j] = ld[row * kDwDS + c4 + j];
+  for (int j = 0; j < EIT; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) g4[j][i] = ld[(row0 + j * RSTEP) * DS + c4 + i];
 
   if constexpr (EPI == EPI_STORE) {
-    if (own) *reinterpret_cast<floatx4*>(e.out + o) = g4;
+#pragma unroll
+    for (int j = 0; j < EIT; ++j)
+      if (own[j]) *reinterpret_cast<floatx4*>(e.out + o[j]) = g4[j];
   } else {
-    if (own && e.grad) *reinterpret_cast<floatx4*>(e.grad + o) = g4;
+#pragma unroll
+    for (int j = 0; j < EIT; ++j)
+      if (own[j] && e.grad) *reinterpret_cast<floatx4*>(e.grad + o[j]) = g4[j];
     const float lr = e.scalars->lr;
     const AdamRcp rc = adam_rcp_of(e);
-    float w[4], sm[4], sv[4];
+    const uint32_t vec_end = (uint32_t)(e.count - e.count % 8);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      w[j] = w4[j];
-      sm[j] = m4[j];
-      sv[j] = v4[j];
+    for (int j = 0; j < EIT; ++j) {
+      float w[4], sm[4], sv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        w[i] = w4[j][i];
+        sm[i] = m4[j][i];
+        sv[i] = v4[j][i];
+      }
+      if (e.opt == VOLTA_OPT_SGD) {
+        // sgd_fused_tn: W = 1*W + (-lr) * (act_i^T delta_i)  (:321-324)
+        const float nlr = -lr;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = w[i] + nlr * g4[j][i];
+      } else if (e.opt == VOLTA_OPT_ADAGRAD) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) adagrad_elem(&w[i], &sm[i], g4[j][i], lr, e.eps);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          adam_elem(&w[i], &sm[i], &sv[i], g4[j][i], o[j] + i >= vec_end, lr, rc, e.b1, e.b2, e.eps, e.wd);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        w4[j][i] = w[i];
+        m4[j][i] = sm[i];
+        v4[j][i] = sv[i];
+      }
+      if (own[j]) {
+        *reinterpret_cast<floatx4*>(e.out + o[j]) = w4[j];
+        if (e.opt != VOLTA_OPT_SGD) *reinterpret_cast<floatx4*>(e.m + o[j]) = m4[j];
+        if (e.opt == VOLTA_OPT_ADAM || e.opt == VOLTA_OPT_ADAMW) *reinterpret_cast<floatx4*>(e.v + o[j]) = v4[j];
+      }
     }
-    if (e.opt == VOLTA_OPT_SGD) {
-      // sgd_fused_tn: W = 1*W + (-lr) * (act_i^T delta_i)  (:321-324)
-      const float nlr = -lr;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) w[j] = w[j] + nlr * g4[j];
-    } else if (e.opt == VOLTA_OPT_ADAGRAD) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) adagrad_elem(&w[j], &sm[j], g4[j], lr, e.eps);
-    } else {
-      const uint32_t vec_end = (uint32_t)(e.count - e.count % 8);
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        adam_elem(&w[j], &sm[j], &sv[j], g4[j], o + j >= vec_end, lr, rc, e.b1, e.b2, e.eps, e.wd);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      w4[j] = w[j];
-      m4[j] = sm[j];
-      v4[j] = sv[j];
-    }
-    if (own) {
-      *reinterpret_cast<floatx4*>(e.out + o) = w4;
-      if (e.opt != VOLTA_OPT_SGD) *reinterpret_cast<floatx4*>(e.m + o) = m4;
-      if (e.opt == VOLTA_OPT_ADAM || e.opt == VOLTA_OPT_ADAMW) *reinterpret_cast<floatx4*>(e.v + o) = v4;
-    }
-    if (do_db && tid < kDwT && bn < N) bst.update_store(e, bn, N, db, rc);
+    if (do_db && tid < TN && bn < N) bst.update_store(e, bn, N, db, rc);
   }
 }
 
@@ -2373,9 +2451,9 @@ static_assert(sizeof(DwGroup) <= 4000, "DwGroup is passed by value as a kernel a
 // Five waves per SIMD (at most 96 registers) where the narrow part's state
 // fits them (NMAX <= 4); the 16-wide narrow dW needs more (at 96 it spilled
 // 27 registers), so four.
-template <int NMAX>
+template <int NMAX, int TN>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NMAX <= 4 ? 5 : 3))) dw_group_kernel(DwGroup d) {
-  __shared__ __attribute__((aligned(16))) float lds[kDwLds];
+  __shared__ __attribute__((aligned(16))) float lds[TN == kDwT ? kDwLds : (kDwLdsW > kDwLds ? kDwLdsW : kDwLds)];
   int b = blockIdx.x;
   if (b == 0 && threadIdx.x == 0 && d.loss_partials)
     deferred_loss_finish(d.loss_scalars, d.loss_partials, d.loss_blocks, d.loss_denom);
@@ -2388,17 +2466,21 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NMAX <
 #pragma unroll
   for (int k = 1; k < kMaxDwGroup; ++k)
     if (k < d.n && b >= d.start[k]) i = k;
-  dw_smallk_tile<EPI_DW_OPT>(d.g[i], b - d.start[i], lds, threadIdx.x);
+  dw_smallk_tile<EPI_DW_OPT, TN>(d.g[i], b - d.start[i], lds, threadIdx.x);
+}
+
+int dw_group_tiles(const GemmArgs& a, int tile_n) {
+  return ((a.M + kDwT - 1) / kDwT) * ((a.N + tile_n - 1) / tile_n);
 }
 
 bool dw_group_supported(const DwGroup& d) {
   if (d.n < 1 || d.n > kMaxDwGroup || d.start[0] != 0) return false;
+  if (d.tile_n != kDwT && d.tile_n != kDwTW) return false;
   if (d.loss_partials && (!d.loss_scalars || d.loss_blocks < 1 || d.loss_blocks > kOutDxMaxBlocks)) return false;
   for (int i = 0; i < d.n; ++i) {
     const GemmArgs& a = d.g[i];
     if (a.epi.kind != EPI_DW_OPT || !dw_smallk_ok(a, GEMM_TN)) return false;
-    const int tiles = ((a.M + kDwT - 1) / kDwT) * ((a.N + kDwT - 1) / kDwT);
-    if (d.start[i + 1] - d.start[i] != tiles) return false;
+    if (d.start[i + 1] - d.start[i] != dw_group_tiles(a, d.tile_n)) return false;
   }
   if (d.narrow_blocks) {
     const NarrowDwArgs& p = d.nd;
@@ -2414,9 +2496,15 @@ hipError_t dw_group_launch(const DwGroup& d, hipStream_t st, Recorder* rec, cons
   if (!dw_group_supported(d)) return hipErrorInvalidValue;
   const dim3 grid(d.narrow_blocks + d.start[d.n]);
   const int nn = d.narrow_blocks ? d.nd.N : 1;
-  if (nn <= 1) hipLaunchKernelGGL(dw_group_kernel<1>, grid, dim3(256), 0, st, d);
-  else if (nn <= 4) hipLaunchKernelGGL(dw_group_kernel<4>, grid, dim3(256), 0, st, d);
-  else hipLaunchKernelGGL(dw_group_kernel<16>, grid, dim3(256), 0, st, d);
+  if (d.tile_n == kDwTW) {
+    if (nn <= 1) hipLaunchKernelGGL((dw_group_kernel<1, kDwTW>), grid, dim3(256), 0, st, d);
+    else if (nn <= 4) hipLaunchKernelGGL((dw_group_kernel<4, kDwTW>), grid, dim3(256), 0, st, d);
+    else hipLaunchKernelGGL((dw_group_kernel<16, kDwTW>), grid, dim3(256), 0, st, d);
+  } else {
+    if (nn <= 1) hipLaunchKernelGGL((dw_group_kernel<1, kDwT>), grid, dim3(256), 0, st, d);
+    else if (nn <= 4) hipLaunchKernelGGL((dw_group_kernel<4, kDwT>), grid, dim3(256), 0, st, d);
+    else hipLaunchKernelGGL((dw_group_kernel<16, kDwT>), grid, dim3(256), 0, st, d);
+  }
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   return mark(rec, label, flops, bytes);

@@ -117,6 +117,7 @@ struct Handle {
   bool dx_alone = false;       // small-batch backward: dX launches alone, dW products grouped
   bool dw_group = false;       // ... in one launch (off with VOLTA_NO_PAIR)
   bool ext_dw_group = false;   // codegen extras: phase 2's dW products in one launch likewise
+  int dw_group_tn = 32;        // columns of the group's small-K tiles (VOLTA_DW_GROUP_TN: 32 or 64)
   size_t infer_ws_floats = 0;
   SegTable segs{};
   std::vector<LayerPlan> layers;
@@ -334,6 +335,7 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
   // whether it may leave the step's loss sum to that launch (no arrival
   // ticket and agent-scope fences in the output launch).
   DwGroup group;
+  group.tile_n = h->dw_group_tn;
   std::string group_label;
   double group_fl = 0.0, group_by = 0.0;
   bool group_ok = false, defer_loss = false;
@@ -346,7 +348,7 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
       } else {
         group.g[group.n] = o.args;
         group.g[group.n].k_per_split = o.plan.k_per_split;
-        group.start[group.n + 1] = group.start[group.n] + o.plan.tiles(o.args.M, o.args.N);
+        group.start[group.n + 1] = group.start[group.n] + dw_group_tiles(o.args, h->dw_group_tn);
         ++group.n;
       }
       char lx[32];
@@ -624,6 +626,7 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
     };
     if (h->ext_dw_group) {
       DwGroup d;
+      d.tile_n = h->dw_group_tn;
       std::string lab;
       double fl = 0.0, by = 0.0;
       for (int i = n - 1; i >= 0; --i) {
@@ -634,7 +637,7 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
         } else {
           d.g[d.n] = o.args;
           d.g[d.n].k_per_split = o.plan.k_per_split;
-          d.start[d.n + 1] = d.start[d.n] + o.plan.tiles(o.args.M, o.args.N);
+          d.start[d.n + 1] = d.start[d.n] + dw_group_tiles(o.args, h->dw_group_tn);
           ++d.n;
         }
         std::snprintf(lx, sizeof lx, h->ext_clip ? "dw%d+opt" : "dw%d+db+opt", i);
@@ -876,6 +879,8 @@ static bool build(Handle* h) {
   // The extras step runs its dX products alone anyway and its dW products
   // after every delta: those share one launch under the same conditions.
   h->ext_dw_group = h->extras() && all_small && n_small <= kMaxDwGroup && !(np && *np && *np != '0');
+  const char* gtn = std::getenv("VOLTA_DW_GROUP_TN");
+  if (gtn && *gtn) h->dw_group_tn = std::atoi(gtn) == 64 ? 64 : 32;
   if (h->dx_alone || h->ext_dw_group)
     for (int i = 1; i < n; ++i) {
       LayerPlan& lp = h->layers[i];
