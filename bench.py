@@ -204,7 +204,70 @@ def dominance(row):
     return row["ms"]
 
 
-def run_gpu(name, steps, warmup, want_profile=True):
+PROFILES = os.path.join(ROOT, "profiles")
+
+
+def committed_trace_us(workload, label):
+    """Traced average duration (us) of launch `label` in the committed
+    rocprofv3 kernel-trace summary profiles/kernel_trace_<workload>.txt, or
+    None."""
+    path = os.path.join(PROFILES, f"kernel_trace_{workload}.txt")
+    try:
+        lines = open(path).read().splitlines()
+    except OSError:
+        return None
+    for line in lines:
+        f = line.split()
+        if len(f) >= 4 and not line.startswith("#") and f[3] == label:
+            try:
+                return float(f[0])
+            except ValueError:
+                continue
+    return None
+
+
+def committed_mfma(workload, label):
+    """The committed MFMA counter figures of launch `label`
+    (profiles/mfma_counters.txt): {"counted_flops", "algorithmic_flops",
+    "busy_frac"}, or None."""
+    try:
+        lines = open(os.path.join(PROFILES, "mfma_counters.txt")).read().splitlines()
+    except OSError:
+        return None
+    for line in lines:
+        f = line.split("\t")
+        if len(f) >= 5 and not line.startswith("#") and f[0] == workload and f[1] == label:
+            return {"counted_flops": float(f[2]), "algorithmic_flops": float(f[3]), "busy_frac": float(f[4])}
+    return None
+
+
+def add_committed_fractions(workload, rf):
+    """Beside the roofline's in-step fraction: the fraction on the launch's
+    own fused bytes (hbm-bound launches), on the traced average of the
+    committed kernel trace, and from the committed MFMA counters (mfma-bound
+    launches: the MFMA flops the hardware counted over the in-step time, and
+    the fraction of cycles the MFMA pipes were busy)."""
+    sec = rf["avg_ms"] * 1e-3
+    if rf["bound"] == "hbm":
+        rf["frac_fused_bytes"] = round(rf["fused_model_bytes"] / sec / 1e9 / PEAK_HBM_GBS, 4)
+    t_us = committed_trace_us(workload, rf["kernel"])
+    if t_us:
+        work = rf["algorithmic_bytes"] / 1e9 / PEAK_HBM_GBS if rf["bound"] == "hbm" else \
+            rf["algorithmic_flops"] / 1e12 / PEAK_FP32_MFMA_TFLOPS
+        rf["trace_avg_ms"] = round(t_us * 1e-3, 5)
+        rf["frac_trace"] = round(work / (t_us * 1e-6), 4)
+        rf["trace_source"] = f"profiles/kernel_trace_{workload}.txt"
+    if rf["bound"] == "mfma":
+        m = committed_mfma(workload, rf["kernel"])
+        if m:
+            rf["mfma_counted_flops"] = m["counted_flops"]
+            rf["frac_mfma_counters"] = round(m["counted_flops"] / sec / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4)
+            rf["mfma_busy_frac"] = m["busy_frac"]
+            rf["mfma_source"] = "profiles/mfma_counters.txt"
+    return rf
+
+
+def run_gpu(name, steps, warmup, want_profile=True, count_launches=False):
     spec, B, lr = WORKLOADS[name]
     lib = load_hip()
     ws, bs = data.he_uniform(42, spec.sizes)
@@ -244,10 +307,12 @@ def run_gpu(name, steps, warmup, want_profile=True):
     extra.restype = C.c_int64
     extra.argtypes = [C.c_void_p]
     out["arena_bytes"] = int(extra(t.h))
+    if count_launches:
+        out["launches"] = len(launches(lib, t))
     if want_profile:
         rows = profile(lib, t, ms, spec, B)
         out["kernels"] = rows
-        out["roofline"] = roofline_of(max(rows, key=dominance))
+        out["roofline"] = add_committed_fractions(name, roofline_of(max(rows, key=dominance)))
         tr = measured_traffic(name, out["roofline"]["kernel"])
         if tr:
             out["roofline"]["traffic"] = tr["bytes"]
@@ -351,6 +416,30 @@ def run_rt_graph(name="c5", rows=4096, reps=20):
     for d in list(dev.values()) + [out]:
         d.free()
     return res
+
+
+def run_default_runtime_leg(name, steps, warmup):
+    """The headline workload timed in a child process that runs with HIP's
+    default graph dispatch (recorded packets) and the HSA runtime's default
+    completion waits (interrupts): what a caller of the library that sets no
+    environment gets, resident and host-staged.  Started before this
+    process's first HIP call."""
+    import subprocess
+
+    env = dict(os.environ)
+    env.pop("DEBUG_CLR_GRAPH_PACKET_CAPTURE", None)
+    env.pop("HSA_ENABLE_INTERRUPT", None)
+    cmd = [sys.executable, os.path.abspath(__file__), "--config", name, "--secondary", "none", "--no-cpu",
+           "--no-profile", "--configs", "none", "--no-default-runtime-leg", "--graph-dispatch", "packets",
+           "--hsa-completion", "interrupts", "--steps", str(steps), "--warmup", str(warmup)]
+    r = subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        raise RuntimeError(f"default-runtime leg failed ({r.returncode}): {r.stderr[-2000:]}")
+    j = json.loads([ln for ln in r.stdout.splitlines() if ln.startswith("{")][-1])
+    return {"workload": name, "ms_per_step": j["ms_per_step"], "samples_per_s": j["value"],
+            "host_staged_ms_per_step": j["host_staged_ms_per_step"], "graph_dispatch": "packets (HIP default)",
+            "hsa_completion": "interrupts (HSA default)", "steps": steps,
+            "note": "child process with neither DEBUG_CLR_GRAPH_PACKET_CAPTURE nor HSA_ENABLE_INTERRUPT set"}
 
 
 CPU_REF_SO = os.path.join(ROOT, "oracle", "_ref", "libvolta_cpu_ref.so")
@@ -564,6 +653,49 @@ def traffic_table(pmc_dir, bench_json):
     return 0
 
 
+MI355X_XCDS = 8  # GRBM_GUI_ACTIVE as rocprofv3 reports it: summed over the 8 XCDs
+MI355X_CUS = 256
+
+
+def mfma_table(pmc_csv, bench_json):
+    """Text table of MFMA work per launch from one rocprofv3 --pmc pass with
+    SQ_INSTS_VALU_MFMA_MOPS_F32, SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE
+    over `--no-cpu --no-profile` (launches named from a bench JSON line of
+    the same build), averaged over the last 10 steps of each workload:
+      counted_flops  SQ_INSTS_VALU_MFMA_MOPS_F32 x 512 (the counter counts
+                     fp32 MFMA work in units of 512 flops)
+      algorithmic    the hot-path survey's 2 B r c per product of the launch
+      busy_frac      SQ_VALU_MFMA_BUSY_CYCLES / (4 SIMDs x 256 CUs x
+                     GRBM_GUI_ACTIVE / 8): the share of the launch's active
+                     cycles the MFMA pipes were busy, at the clock the chip ran
+                     (busy cycles per SIMD; the GUI counter summed over the 8
+                     XCDs)."""
+    import csv
+
+    b, labels = _bench_labels(bench_json)
+    res = {b["config"]["workload"]: b}
+    if b.get("secondary"):
+        res[b["secondary"]["workload"]] = b["secondary"]
+    rows = list(csv.DictReader(open(pmc_csv)))
+    per = {}
+    for c in ("SQ_INSTS_VALU_MFMA_MOPS_F32", "SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE"):
+        rc = [r for r in rows if r["Counter_Name"] == c]
+        for wl, lst in _per_launch(rc, labels, lambda r: float(r["Counter_Value"])).items():
+            per[(wl, c)] = [(k, w, sum(v[-10:]) / len(v[-10:])) for k, w, v in lst]
+    out = ["# workload\tlaunch\tcounted_flops\talgorithmic_flops\tbusy_frac\tgui_active_per_xcd\tkernel (workgroups)"]
+    for wl in labels:
+        alg = {k["kernel"]: k.get("survey_flops", 0.0) for k in res[wl]["kernels"]}
+        for p, lab in enumerate(labels[wl]):
+            mops = per[(wl, "SQ_INSTS_VALU_MFMA_MOPS_F32")][p]
+            busy = per[(wl, "SQ_VALU_MFMA_BUSY_CYCLES")][p][2]
+            gui = per[(wl, "GRBM_GUI_ACTIVE")][p][2] / MI355X_XCDS
+            frac = busy / (4 * MI355X_CUS * gui) if gui > 0 else 0.0
+            out.append(f"{wl}\t{lab}\t{mops[2] * 512:.0f}\t{alg.get(lab, 0.0):.0f}\t{frac:.4f}\t{gui:.0f}\t"
+                       f"{mops[0]} ({mops[1]})")
+    print("\n".join(out))
+    return 0
+
+
 def trace_summary(trace_csv, bench_json):
     """Per-launch kernel durations from a rocprofv3 --kernel-trace of one
     bench run, averaged over every whole step the run executed, beside the
@@ -631,11 +763,20 @@ def main(argv=None):
                     help="only print HBM bytes per launch from rocprofv3 counter passes (no GPU)")
     ap.add_argument("--trace-summary", nargs=2, metavar=("TRACE_CSV", "BENCH_JSON"),
                     help="only print per-launch durations from a rocprofv3 kernel trace of a bench run (no GPU)")
+    ap.add_argument("--mfma-table", nargs=2, metavar=("PMC_CSV", "BENCH_JSON"),
+                    help="only print MFMA flops and busy cycles per launch from a rocprofv3 --pmc run (no GPU)")
+    ap.add_argument("--configs", default="c1,c3,c4_128,c4_256,c4_1024",
+                    help="other BASELINE.json configurations reported briefly in the line ('none': skip)")
+    ap.add_argument("--default-runtime-leg", action=argparse.BooleanOptionalAction, default=True,
+                    help="also time the headline in a child process with HIP's default graph dispatch and "
+                         "completion waits (what a caller that sets no environment gets)")
     a = ap.parse_args(argv)
     if a.traffic_table:
         return traffic_table(*a.traffic_table)
     if a.trace_summary:
         return trace_summary(*a.trace_summary)
+    if a.mfma_table:
+        return mfma_table(*a.mfma_table)
     if a.calibration_copy:
         return calibration_copy(a.calibration_copy)
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -667,6 +808,10 @@ def main(argv=None):
         cpu_primary = run_cpu(a.config, a.cpu_threads)
         if a.secondary and a.secondary != "none":
             cpu_secondary, _ = run_cpu(a.secondary, a.cpu_threads, full_protocol=False)
+    default_leg = None
+    if a.default_runtime_leg:
+        default_leg = run_default_runtime_leg(a.config, a.steps, a.warmup)
+        log(f"default runtime leg: {default_leg}")
     spec, B, lr, res = run_gpu(a.config, a.steps, a.warmup, want_profile=not a.no_profile)
     log(f"{a.config}: {res['ms_per_step']:.4f} ms/step, {res['samples_per_s']:.0f} samples/s")
     line = {
@@ -722,6 +867,21 @@ def main(argv=None):
         if cpu_secondary:
             sec["cpu_baseline"] = cpu_secondary
         line["secondary"] = sec
+    if default_leg:
+        line["default_runtime"] = default_leg
+    if a.configs and a.configs != "none":
+        # the other BASELINE.json configurations: step time and launch count
+        line["configs"] = []
+        for c in a.configs.split(","):
+            c_spec, c_B, c_lr, c_res = run_gpu(c, max(100, a.steps // 2), max(20, a.warmup // 2),
+                                               want_profile=False, count_launches=True)
+            row = {"workload": c, "layers": list(c_spec.sizes), "activation": c_spec.activation,
+                   "loss": c_spec.loss, "optimizer": c_spec.optimizer, "batch": c_B,
+                   "ms_per_step": round(c_res["ms_per_step"], 5), "samples_per_s": round(c_res["samples_per_s"], 2),
+                   "mfma_frac_step": round(c_res["mfma_frac_step"], 5), "launches": c_res["launches"],
+                   "host_staged_ms_per_step": c_res["host_staged_ms_per_step"]}
+            line["configs"].append(row)
+            log(f"{c}: {row['ms_per_step']:.4f} ms/step, {row['launches']} launches")
     if not a.no_profile and not a.no_extra_legs:
         line["runtime_optimizer"] = run_rt_optimizer()
         log(f"runtime optimizer: {line['runtime_optimizer']}")

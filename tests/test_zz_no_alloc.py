@@ -15,12 +15,33 @@ from volta_amd.abi import MlpSpec, Trainer
 pytestmark = pytest.mark.gpu
 
 CASES = {
-    # B=1024: fwd0 (1024x1024, K=2048) splits K in 4 on 128x128 tiles, fwd1
-    # (1024x512, K=1024) in 2 on 64x64 tiles: both use the scratch
+    # B=1024 (the forward runs 1024 rows at a time; on a 256-CU MI355X): at
+    # 1024 and 976 rows fwd0 (N=1024, K=2048) runs its two K slices as K
+    # groups of one workgroup (no scratch), fwd1 (N=512, K=1024) splits K in
+    # 4 and the output layer (N=10, K=512) in 8, both through the scratch;
+    # at 700 rows fwd0 splits in 2 as well.  test_splitk_case_reaches_scratch
+    # asserts through the planner that each row count splits some layer.
     "splitk_b1024": (MlpSpec([2048, 1024, 512, 10], "relu", "sgd", "ce"), 1024, (2000, 700)),
     # B=64: small-M tiles, no split (the scratch is not touched); LayerNorm
     "smallm_ln_b64": (MlpSpec([512, 1024, 256, 1], "gelu", "adam", layernorm=True), 64, (130, 50)),
 }
+
+
+def _chunk_rows(rows, B):
+    return [min(B, rows - r0) for r0 in range(0, rows, B)]
+
+
+def test_splitk_case_reaches_scratch():
+    """Every row count of the split-K case runs at least one forward layer
+    with K split over workgroups (partial planes in the scratch), so the
+    bit-equality below covers the scratch path whatever the planner picks."""
+    from tests.test_planner import NN, plan
+
+    spec, B, row_counts = CASES["splitk_b1024"]
+    for rows in row_counts:
+        for m in _chunk_rows(rows, B):
+            splits = [plan(NN, m, c, r)[1] for r, c in spec.shapes()]
+            assert max(splits) > 1, f"rows={rows}: no forward layer splits K at {m} rows ({splits})"
 
 
 def say(msg):
@@ -56,13 +77,16 @@ def test_noalloc_infer_matches_infer(name):
 
 def test_noalloc_rejects_workspace_beyond_scratch():
     """With the split-K planner asked for 8 workgroups per CU and 128x128
-    tiles from 2^20 outputs, a 1024x1024 product with K=4096 splits K 16
-    ways: 16 x 1025 x 1024 floats of partial planes, above the 64 MiB
-    scratch.  The call is refused on the host with a message naming both
-    sizes; nothing is launched."""
+    tiles from 2^20 outputs, a 1024x1024 product with K=4096 splits K 32
+    ways (asserted through the planner): 32 x 1025 x 1024 floats of partial
+    planes, above the 64 MiB scratch.  The call is refused on the host with
+    a message naming both sizes; nothing is launched."""
+    from tests.test_planner import NN, plan
     lib = load_hip()
     spec = MlpSpec([4096, 1024, 10], "relu", "sgd", "ce")
     env = {"VOLTA_SPLITK_WGS_PER_CU": "8", "VOLTA_TILE128_MIN_MN": str(1 << 20)}
+    tile, splits = plan(NN, 1024, 1024, 4096, env=env)[:2]
+    assert tile == 1 and splits == 32, (tile, splits)  # 128x128 tiles, K in 32 slices
     old = {k: os.environ.get(k) for k in env}
     os.environ.update(env)
     try:

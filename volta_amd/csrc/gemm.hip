@@ -2676,7 +2676,9 @@ __global__ void __launch_bounds__(256) bias_update_kernel(EpiArgs e, const float
 
 hipError_t launch_bias_update(const EpiArgs& e, const float* delta, int B, int N, hipStream_t st) {
   if (!e.b || !e.scalars || !delta || B < 1 || N < 1) return hipErrorInvalidValue;
-  if (e.opt != VOLTA_OPT_SGD && (!e.bm || (e.opt == VOLTA_OPT_ADAM && !e.bv))) return hipErrorInvalidValue;
+  // the state apply_bias_update reads: m for Adagrad, m and v for Adam and AdamW
+  const bool adam = e.opt == VOLTA_OPT_ADAM || e.opt == VOLTA_OPT_ADAMW;
+  if (e.opt != VOLTA_OPT_SGD && (!e.bm || (adam && !e.bv))) return hipErrorInvalidValue;
   hipLaunchKernelGGL(bias_update_kernel, dim3((N + 63) / 64), dim3(256), 0, st, e, delta, B, N);
   return hipGetLastError();
 }

@@ -14,8 +14,17 @@
 //   fwd_{n-1} + loss            narrow output kernel (L_n <= 16), GEMM with the
 //                               loss head in its epilogue (<= 64), or GEMM +
 //                               loss kernel: delta_{n-1}, loss, Adam t
-//   dX_{n-1}                    outer product (L_n <= 16) or GEMM NT
-//   dX_i | dW_{i+1}             one paired launch, i = n-2 .. 1
+//   dX_{n-1}                    outer product (L_n <= 16) or GEMM NT; merged
+//                               into the output launch where that is narrow
+// then, when every dW runs on the small-K tile (batch <= 256: C1-C4 up to
+// B=256):
+//   dX_i, i = n-2 .. 1          one launch each, on their own wave count (the
+//                               output launch also forms dX_{n-2} where that
+//                               product runs on 16-wave small-M workgroups)
+//   dW_{n-1} .. dW_0            one grouped launch (dw_group_kernel)
+// and otherwise (larger batches):
+//   dX_i | dW_{i+1}             one paired launch, i = n-2 .. 1 (where both
+//                               fit the paired kernels, else two launches)
 //   dW_1 | dW_0                 one paired launch
 // With LayerNorm, dropout, softmax hidden activations or gradient clipping
 // the backward runs unpaired (enqueue_step's extras branch).
