@@ -8,7 +8,11 @@ ReLU hidden, linear output, MSE, Adam (lr 1e-3, b1 0.9, b2 0.999, eps 1e-8),
 fp32, B=64, X,Y ~ N(0,1), He-uniform weights, zero biases, all from seed 42.
 The same resident batch is used every step (inputs in HBM before timing), as
 Volta's synthetic dataset is a single batch.  One "step" = forward, loss,
-backward and optimizer update = one replay of the captured hipGraph.
+backward and optimizer update = the step's fixed launch sequence, enqueued
+directly (the library's default; the graph_replay leg times the same
+sequence replayed from its captured hipGraph).  The process sets no HIP or
+HSA environment unless asked (--graph-dispatch nodes, --hsa-completion
+polling): the figures are what a caller of the library gets.
 
 Secondary workload (configs[4], "c5"): the wide classifier at B=4096, the
 fp32-MFMA-bound case, reported in the same JSON line under "secondary".
@@ -749,14 +753,16 @@ def main(argv=None):
                          "whose dispatches are split into the two workloads' steps)")
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
                     or len(os.sched_getaffinity(0)), help="threads of the CPU baseline's all-cores leg")
-    ap.add_argument("--graph-dispatch", choices=("nodes", "packets"), default="nodes",
-                    help="how HIP replays the step graph in this process: 'nodes' sets "
+    ap.add_argument("--graph-dispatch", choices=("nodes", "packets"), default="packets",
+                    help="how HIP replays graphs in this process (the step runs as direct launches unless "
+                         "VOLTA_GRAPH=1; the graph-replay leg and graph execution replay graphs): 'packets' "
+                         "leaves HIP's default (recorded kernel packets); 'nodes' sets "
                          "DEBUG_CLR_GRAPH_PACKET_CAPTURE=0 before the first HIP call (nodes dispatched in order "
-                         "as stream launches); 'packets' leaves HIP's default (recorded kernel packets)")
-    ap.add_argument("--hsa-completion", choices=("polling", "interrupts"), default="polling",
-                    help="how this process's HSA runtime waits for GPU completion signals: 'polling' sets "
-                         "HSA_ENABLE_INTERRUPT=0 before the first HIP call (the waiting thread spins); "
-                         "'interrupts' leaves the runtime's default")
+                         "as stream launches)")
+    ap.add_argument("--hsa-completion", choices=("polling", "interrupts"), default="interrupts",
+                    help="how this process's HSA runtime waits for GPU completion signals: 'interrupts' leaves "
+                         "the runtime's default; 'polling' sets HSA_ENABLE_INTERRUPT=0 before the first HIP call "
+                         "(the waiting thread spins)")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB 10 times (scales rocprofv3 HBM counters)")
     ap.add_argument("--traffic-table", nargs=2, metavar=("PMC_DIR", "BENCH_JSON"),
@@ -767,9 +773,13 @@ def main(argv=None):
                     help="only print MFMA flops and busy cycles per launch from a rocprofv3 --pmc run (no GPU)")
     ap.add_argument("--configs", default="c1,c3,c4_128,c4_256,c4_1024",
                     help="other BASELINE.json configurations reported briefly in the line ('none': skip)")
-    ap.add_argument("--default-runtime-leg", action=argparse.BooleanOptionalAction, default=True,
+    ap.add_argument("--default-runtime-leg", action=argparse.BooleanOptionalAction, default=False,
                     help="also time the headline in a child process with HIP's default graph dispatch and "
-                         "completion waits (what a caller that sets no environment gets)")
+                         "completion waits (what a caller that sets no environment gets), for runs that set "
+                         "--graph-dispatch nodes or --hsa-completion polling")
+    ap.add_argument("--graph-replay-leg", action=argparse.BooleanOptionalAction, default=True,
+                    help="also time the headline with its launch sequence replayed from a captured hipGraph "
+                         "(VOLTA_GRAPH=1) instead of enqueued directly")
     a = ap.parse_args(argv)
     if a.traffic_table:
         return traffic_table(*a.traffic_table)
@@ -788,9 +798,11 @@ def main(argv=None):
 
     # The host's choices of HIP's graph replay mode and of how the HSA runtime
     # waits for completion signals; both are read once, at the first HIP
-    # call, so they are set before the library is loaded.  (With node
-    # dispatch the host takes part in each replay: polling shortens its
-    # wake-ups, C2 53.9 -> 53.5 us, C1 42 -> 32 us.)
+    # call, so they are set before the library is loaded.  By default the
+    # bench sets neither (what a caller of the library gets); they matter
+    # for graph replays (with node dispatch the host takes part in each
+    # replay and polling shortens its wake-ups), not for the step's direct
+    # launches.
     if a.graph_dispatch == "nodes":
         os.environ["DEBUG_CLR_GRAPH_PACKET_CAPTURE"] = "0"
     else:
@@ -830,8 +842,10 @@ def main(argv=None):
                 "one resident batch reused every step",
         "config": {"workload": a.config, "layers": list(spec.sizes), "activation": spec.activation,
                    "loss": spec.loss, "optimizer": spec.optimizer, "lr": lr, "batch": B,
-                   "parallelism": "single GPU", "graph_dispatch": a.graph_dispatch,
-                   "hsa_completion": a.hsa_completion},
+                   "parallelism": "single GPU",
+                   "step_launch": "graph replay (VOLTA_GRAPH=1)" if os.environ.get("VOLTA_GRAPH", "0") not in
+                   ("", "0") else "direct launches (the library's default)",
+                   "graph_dispatch": a.graph_dispatch, "hsa_completion": a.hsa_completion},
         "mfma_frac_step": round(res["mfma_frac_step"], 5),
         "gemm_gflop_per_step": round(res["gemm_gflop_per_step"], 4),
         "loss_after": res["loss_after"],
@@ -869,6 +883,20 @@ def main(argv=None):
         line["secondary"] = sec
     if default_leg:
         line["default_runtime"] = default_leg
+    if a.graph_replay_leg and os.environ.get("VOLTA_GRAPH", "0") in ("", "0"):
+        # the same step replayed from its captured hipGraph (VOLTA_GRAPH is
+        # read when a handle is created)
+        os.environ["VOLTA_GRAPH"] = "1"
+        try:
+            _, _, _, g_res = run_gpu(a.config, a.steps, a.warmup, want_profile=False)
+        finally:
+            os.environ.pop("VOLTA_GRAPH", None)
+        line["graph_replay"] = {"workload": a.config, "ms_per_step": round(g_res["ms_per_step"], 5),
+                                "samples_per_s": round(g_res["samples_per_s"], 2),
+                                "host_staged_ms_per_step": g_res["host_staged_ms_per_step"],
+                                "note": "the same launch sequence captured once as a hipGraph and replayed "
+                                        "(VOLTA_GRAPH=1), graph dispatch as config.graph_dispatch"}
+        log(f"graph replay: {line['graph_replay']}")
     if a.configs and a.configs != "none":
         # the other BASELINE.json configurations: step time and launch count
         line["configs"] = []

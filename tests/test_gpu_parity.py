@@ -828,6 +828,32 @@ def test_paired_backward_launches_bit_identical(name):
         np.testing.assert_array_equal(a, b)
 
 
+GRAPH_CASES = {
+    # the small-batch structure (dX chain + dW group), the paired backward of
+    # larger batches, the codegen extras, and a large-tile step
+    "c2": (MlpSpec([512, 1024, 1024, 512, 256, 1], "relu", "adam"), 64, 1e-3),
+    "c4_b1024": (MlpSpec([512, 1024, 1024, 512, 256, 1], "silu", "sgd"), 1024, 0.01),
+    "extras": (MlpSpec([48, 128, 96, 10], "gelu", "adam", layernorm=True, dropout_p=0.2, clip_grad=0.05), 64, 1e-3),
+    "ce_big": (MlpSpec([512, 1024, 512, 10], "relu", "adagrad", "ce", eps=1e-10), 2048, 1e-2),
+}
+
+
+@pytest.mark.parametrize("name", sorted(GRAPH_CASES))
+def test_graph_replay_bit_identical_to_direct_launches(name):
+    """The step's launch sequence replayed from the hipGraph it is captured
+    into once (VOLTA_GRAPH=1) gives the same bits as the same sequence
+    enqueued directly (the default): losses, parameters, activations and
+    deltas after 4 steps, with the Adam step counter and the dropout stream
+    advanced on the device in both."""
+    spec, B, lr = GRAPH_CASES[name]
+    say(f"graph replay vs direct launches {name}")
+    l1, p1, b1 = _run_with_env({"VOLTA_GRAPH": "0"}, spec, B, lr, 4)
+    l2, p2, b2 = _run_with_env({"VOLTA_GRAPH": "1"}, spec, B, lr, 4)
+    np.testing.assert_array_equal(l1, l2)
+    for a, b in zip(p1 + b1, p2 + b2):
+        np.testing.assert_array_equal(a, b)
+
+
 KGROUP_STEP_CASES = {
     "c4_b1024": (MlpSpec([512, 1024, 1024, 512, 256, 1], "silu", "sgd"), 1024, 0.01),
     "ragged_b900": (MlpSpec([300, 700, 500, 3], "tanh", "adam"), 900, 1e-3),
