@@ -76,6 +76,12 @@ PUBLISHED_CPU = {"c2": {"ms_per_step": 4.259, "source": "docs/BENCHMARKS.md:87",
                         "hardware": "Windows 11, 6-core x86-64 CPU, MKL"}}
 
 
+def _env_on(name: str) -> bool:
+    """The library's reading of a switch variable: set, non-empty, not '0'."""
+    v = os.environ.get(name, "")
+    return bool(v) and not v.startswith("0")
+
+
 def gemm_flops(spec: MlpSpec, B: int) -> float:
     """2B*sumW (fwd) + 2B*sumW (dW) + 2B*(sumW - L0*L1) (dX, none for layer 0)."""
     sw = sum(r * c for r, c in spec.shapes())
@@ -724,7 +730,8 @@ def trace_summary(trace_csv, bench_json):
         t_us = trace_of[rf["kernel"]]
         t_frac = (rf["algorithmic_bytes"] / (t_us * 1e-6) / 1e9 / PEAK_HBM_GBS if rf["bound"] == "hbm"
                   else rf["algorithmic_flops"] / (t_us * 1e-6) / 1e12 / PEAK_FP32_MFMA_TFLOPS)
-        out += [f"## workload {wl}: step {r['ms_per_step'] * 1000:.1f} us (plain bench run, graph replay); "
+        mode = b["config"].get("step_launch", "graph replay")
+        out += [f"## workload {wl}: step {r['ms_per_step'] * 1000:.1f} us (plain bench run, {mode}); "
                 f"sum of traced kernel durations per step {tot:.1f} us over {len(lst[0][2])} steps",
                 f"## roofline launch {rf['kernel']} (longest in-step launch): plain run {rf['avg_ms'] * 1000:.2f} us "
                 f"-> {rf['achieved']} {rf['unit']} = {rf['frac'] * 100:.1f}% of {rf['peak']}; traced average "
@@ -843,8 +850,8 @@ def main(argv=None):
         "config": {"workload": a.config, "layers": list(spec.sizes), "activation": spec.activation,
                    "loss": spec.loss, "optimizer": spec.optimizer, "lr": lr, "batch": B,
                    "parallelism": "single GPU",
-                   "step_launch": "graph replay (VOLTA_GRAPH=1)" if os.environ.get("VOLTA_GRAPH", "0") not in
-                   ("", "0") else "direct launches (the library's default)",
+                   "step_launch": "graph replay (VOLTA_GRAPH=1)" if _env_on("VOLTA_GRAPH") and not
+                   _env_on("VOLTA_NO_GRAPH") else "direct launches (the library's default)",
                    "graph_dispatch": a.graph_dispatch, "hsa_completion": a.hsa_completion},
         "mfma_frac_step": round(res["mfma_frac_step"], 5),
         "gemm_gflop_per_step": round(res["gemm_gflop_per_step"], 4),
@@ -883,7 +890,7 @@ def main(argv=None):
         line["secondary"] = sec
     if default_leg:
         line["default_runtime"] = default_leg
-    if a.graph_replay_leg and os.environ.get("VOLTA_GRAPH", "0") in ("", "0"):
+    if a.graph_replay_leg and not _env_on("VOLTA_GRAPH") and not _env_on("VOLTA_NO_GRAPH"):
         # the same step replayed from its captured hipGraph (VOLTA_GRAPH is
         # read when a handle is created)
         os.environ["VOLTA_GRAPH"] = "1"

@@ -1344,7 +1344,7 @@ int32_t volta_hip_profile_step(VoltaTrainHandle* vh, int32_t reps, char* out, in
 
 // Duration of launch `index` of the step: the step's launch sequence is
 // enqueued on the handle's stream with an event before and after that
-// launch only (the other launches run back to back as in the graph), `reps`
+// launch only (the other launches run back to back as in a step), `reps`
 // times; the same is done with the two events recorded back to back at that
 // position.  Writes the mean bracketed time to avg_ms[0], the mean
 // back-to-back (marker) time to avg_ms[1], and the launch's label to
@@ -1355,11 +1355,12 @@ int32_t volta_hip_time_kernel(VoltaTrainHandle* vh, int32_t index, int32_t reps,
   if (!h || index < 0 || reps <= 0 || !avg_ms) return -1;
   double total[2] = {0.0, 0.0};
   std::string lab;
-  // Every timed step is preceded by about 0.2 ms of graph-replayed steps, so
-  // the host has enqueued the timed step's launches (a few microseconds of
-  // host work each) before the GPU reaches them: the launch then starts when
-  // its predecessor ends, as in a replayed step, and its interval holds no
-  // host enqueue time, which the back-to-back marker pair would not see.
+  // Every timed step is preceded by about 0.2 ms of ordinary steps (as
+  // volta_train_step_device runs them), so the host has enqueued the timed
+  // step's launches (a few microseconds of host work each) before the GPU
+  // reaches them: the launch then starts when its predecessor ends, as in a
+  // run of steps, and its interval holds no host enqueue time, which the
+  // back-to-back marker pair would not see.
   int prelude = 1;
   {
     hipEvent_t e0 = nullptr, e1 = nullptr;
