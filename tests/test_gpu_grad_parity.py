@@ -177,14 +177,14 @@ def test_c5_late_step_gradients_from_hip_state(step):
     assert gc.bits_equal(st1, ste), "Adagrad sums differ from the oracle's update of the HIP gradient"
 
 
-@pytest.mark.parametrize("name,k", [("c2_mlp512_relu_adam_b64", 0), ("c2_mlp512_relu_adam_b64", 10),
-                                    ("c3_mlp512w_gelu_adamw_b64", 10)])
-def test_wide_dw_group_step_gradients(name, k):
-    """The dW group with 32x64 small-K tiles (VOLTA_DW_GROUP_TN=64; two
-    accumulators per block, so its sums differ in rounding from the 32-wide
-    default): the same gradient-level checks and the bit-equal update."""
+@pytest.mark.parametrize("name,k,tn", [("c2_mlp512_relu_adam_b64", 0, "32"), ("c2_mlp512_relu_adam_b64", 10, "32"),
+                                       ("c3_mlp512w_gelu_adamw_b64", 10, "64")])
+def test_dw_group_width_forced_step_gradients(name, k, tn):
+    """The dW group with the tile width the library would not pick for the
+    configuration (VOLTA_DW_GROUP_TN: C2 picks 32x64 tiles, C3 32x32): the
+    same gradient-level checks and the bit-equal update."""
     old = os.environ.get("VOLTA_DW_GROUP_TN")
-    os.environ["VOLTA_DW_GROUP_TN"] = "64"
+    os.environ["VOLTA_DW_GROUP_TN"] = tn
     try:
         test_teacher_forced_step_gradients(name, k)
     finally:

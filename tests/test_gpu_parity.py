@@ -854,6 +854,29 @@ def test_graph_replay_bit_identical_to_direct_launches(name):
         np.testing.assert_array_equal(a, b)
 
 
+WIDTH_CASES = {
+    # K = 64, 64 and 256 (one and four 64-k slices); the extras step's group
+    "c2": PAIR_CASES["c2"],
+    "c3": PAIR_CASES["c3"],
+    "c4_b256": (MlpSpec([512, 1024, 1024, 512, 256, 1], "silu", "sgd"), 256, 0.01),
+    "extras": GRAPH_CASES["extras"],
+}
+
+
+@pytest.mark.parametrize("name", sorted(WIDTH_CASES))
+def test_dw_group_tile_widths_bit_identical(name):
+    """The dW group on 32x32 and on 32x64 small-K tiles (VOLTA_DW_GROUP_TN=32
+    and 64; the library picks one per group) gives the same bits: losses,
+    parameters, activations and deltas after 4 steps."""
+    spec, B, lr = WIDTH_CASES[name]
+    say(f"dW group tile widths {name}")
+    l1, p1, b1 = _run_with_env({"VOLTA_DW_GROUP_TN": "32"}, spec, B, lr, 4)
+    l2, p2, b2 = _run_with_env({"VOLTA_DW_GROUP_TN": "64"}, spec, B, lr, 4)
+    np.testing.assert_array_equal(l1, l2)
+    for a, b in zip(p1 + b1, p2 + b2):
+        np.testing.assert_array_equal(a, b)
+
+
 KGROUP_STEP_CASES = {
     "c4_b1024": (MlpSpec([512, 1024, 1024, 512, 256, 1], "silu", "sgd"), 1024, 0.01),
     "ragged_b900": (MlpSpec([300, 700, 500, 3], "tanh", "adam"), 900, 1e-3),

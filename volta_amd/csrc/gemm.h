@@ -162,7 +162,7 @@ struct DwGroup {
   int n = 0;                        // small-K dW products (plan TILE_DW_SMALLK)
   GemmArgs g[kMaxDwGroup];
   int start[kMaxDwGroup + 1] = {};  // first workgroup of product i after the narrow ones; start[n] = total
-  int tile_n = 32;                  // columns of the small-K tiles: 32, or 64 (the wide form)
+  int tile_n = 32;                  // columns of the small-K tiles: 32, or 64 (the wide form, same results)
   int narrow_blocks = 0;            // 0: no narrow dW
   NarrowDwArgs nd{};
   // the step's loss, when the output launch deferred it (launch_out_layer_dx
@@ -175,6 +175,12 @@ struct DwGroup {
 bool dw_group_supported(const DwGroup& d);
 // Workgroups of product `a` in a group whose small-K tiles are 32 x tile_n.
 int dw_group_tiles(const GemmArgs& a, int tile_n);
+// Tile width for group `d` (its products, narrow part and narrow width set;
+// start[] and tile_n not read): 64 when the 32-wide tiles need more than one
+// round of the workgroups the device keeps resident and the 64-wide ones fit
+// in one (residency from the occupancy query of the kernel the launch would
+// run), else 32.  Both widths give bit-identical results.
+int dw_group_pick_tile_n(const DwGroup& d, int num_cus);
 hipError_t dw_group_launch(const DwGroup& d, hipStream_t st, Recorder* rec, const char* label, double flops,
                            double bytes);
 

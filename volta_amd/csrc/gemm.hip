@@ -1597,7 +1597,8 @@ gemm_smallm_tail(GemmArgs args, OutLayerArgs p) {
 //      (clamped address, value selected afterwards), which keeps the
 //      compiler's wait counts exact.
 //   2. wave w computes the 16x16 block (w/2, w%2) on v_mfma_f32_16x16x4f32
-//      in the small-M tile's k order, four accumulators added pairwise.
+//      in the small-M tile's k order, the even and odd 16-k groups of each
+//      slice in two accumulators, added at the end.
 //   3. the dW tile goes through LDS; thread t updates row t/8, columns
 //      4(t%8)..+3 of the tile: one float4 of W, m and v.
 //   4. in the first row of tiles, thread j < 32 forms db_i[n0 + j] as
@@ -1620,8 +1621,10 @@ static_assert(kDwT * (kDwTW + 1) <= kDwK * kDwS, "the wide dW tile fits over the
 // `tid` (0..255): the thread's index among the tile's 256.  TN: the tile's
 // columns, 32 (four float4 loads of W/m/v state per thread's element group)
 // or 64 (the wide form: half the workgroups, each thread owning two float4
-// of W, in rows r and r + 16).  Every element of dW sums the same products
-// in the same order in both forms, so their results are bit-identical.
+// of W, in rows r and r + 16).  Both forms add the 16-k groups of every
+// slice into two accumulators per block (even groups, odd groups) and then
+// the two: every element of dW sums the same products in the same order,
+// so the two forms give bit-identical results.
 template <int EPI, int TN = kDwT>
 __device__ __forceinline__ void dw_smallk_tile(const GemmArgs& args, int blk, float* lds, int tid) {
   static_assert(EPI == EPI_DW_OPT || EPI == EPI_STORE, "epilogues of the dW tile");
@@ -1735,8 +1738,10 @@ __device__ __forceinline__ void dw_smallk_tile(const GemmArgs& args, int blk, fl
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  // accumulators per block: 16-k group g of a slice adds into acc[nb][g % NACC]
-  constexpr int NACC = TN == kDwT ? 4 : 2;
+  // accumulators per block: 16-k group g of a slice adds into acc[nb][g % 2]
+  // (two per block in both widths: the same order, and the wide form stays
+  // within five waves per SIMD)
+  constexpr int NACC = 2;
   floatx4 acc[NB][NACC];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb)
@@ -1790,9 +1795,7 @@ __device__ __forceinline__ void dw_smallk_tile(const GemmArgs& args, int blk, fl
   for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      float sum;
-      if constexpr (NACC == 4) sum = (acc[nb][0][v] + acc[nb][1][v]) + (acc[nb][2][v] + acc[nb][3][v]);
-      else sum = acc[nb][0][v] + acc[nb][1][v];
+      const float sum = acc[nb][0][v] + acc[nb][1][v];
       ld[(wm * 16 + 4 * q + v) * DS + (wn * NB + nb) * 16 + r16] = sum;
     }
   __syncthreads();
@@ -2473,6 +2476,36 @@ int dw_group_tiles(const GemmArgs& a, int tile_n) {
   return ((a.M + kDwT - 1) / kDwT) * ((a.N + tile_n - 1) / tile_n);
 }
 
+// The group kernel a launch of `narrow_n` narrow columns and tile width
+// `tile_n` runs (as dw_group_launch selects it).
+static const void* dw_group_fn(int narrow_n, int tile_n) {
+  if (tile_n == kDwTW) {
+    if (narrow_n <= 1) return reinterpret_cast<const void*>(&dw_group_kernel<1, kDwTW>);
+    if (narrow_n <= 4) return reinterpret_cast<const void*>(&dw_group_kernel<4, kDwTW>);
+    return reinterpret_cast<const void*>(&dw_group_kernel<16, kDwTW>);
+  }
+  if (narrow_n <= 1) return reinterpret_cast<const void*>(&dw_group_kernel<1, kDwT>);
+  if (narrow_n <= 4) return reinterpret_cast<const void*>(&dw_group_kernel<4, kDwT>);
+  return reinterpret_cast<const void*>(&dw_group_kernel<16, kDwT>);
+}
+
+int dw_group_pick_tile_n(const DwGroup& d, int num_cus) {
+  const int nn = d.narrow_blocks ? d.nd.N : 1;
+  int t32 = d.narrow_blocks, t64 = d.narrow_blocks;
+  for (int i = 0; i < d.n; ++i) {
+    t32 += dw_group_tiles(d.g[i], kDwT);
+    t64 += dw_group_tiles(d.g[i], kDwTW);
+  }
+  int r32 = 0, r64 = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&r32, dw_group_fn(nn, kDwT), 256, 0) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&r64, dw_group_fn(nn, kDwTW), 256, 0) != hipSuccess ||
+      r32 < 1 || r64 < 1) {
+    (void)hipGetLastError();
+    return kDwT;
+  }
+  return t32 > r32 * num_cus && t64 <= r64 * num_cus ? kDwTW : kDwT;
+}
+
 bool dw_group_supported(const DwGroup& d) {
   if (d.n < 1 || d.n > kMaxDwGroup || d.start[0] != 0) return false;
   if (d.tile_n != kDwT && d.tile_n != kDwTW) return false;
@@ -2496,6 +2529,7 @@ hipError_t dw_group_launch(const DwGroup& d, hipStream_t st, Recorder* rec, cons
   if (!dw_group_supported(d)) return hipErrorInvalidValue;
   const dim3 grid(d.narrow_blocks + d.start[d.n]);
   const int nn = d.narrow_blocks ? d.nd.N : 1;
+  // (the same selection as dw_group_fn)
   if (d.tile_n == kDwTW) {
     if (nn <= 1) hipLaunchKernelGGL((dw_group_kernel<1, kDwTW>), grid, dim3(256), 0, st, d);
     else if (nn <= 4) hipLaunchKernelGGL((dw_group_kernel<4, kDwTW>), grid, dim3(256), 0, st, d);

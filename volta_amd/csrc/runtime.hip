@@ -127,7 +127,8 @@ struct Handle {
   bool dx_alone = false;       // small-batch backward: dX launches alone, dW products grouped
   bool dw_group = false;       // ... in one launch (off with VOLTA_NO_PAIR)
   bool ext_dw_group = false;   // codegen extras: phase 2's dW products in one launch likewise
-  int dw_group_tn = 32;        // columns of the group's small-K tiles (VOLTA_DW_GROUP_TN: 32 or 64)
+  int dw_group_tn = 0;         // columns of the group's small-K tiles: 0 picks per group; VOLTA_DW_GROUP_TN 32 or 64
+  int dw_tn_pick[2] = {0, 0};  // the width each group uses (main, extras), fixed at its first build
   size_t infer_ws_floats = 0;
   SegTable segs{};
   std::vector<LayerPlan> layers;
@@ -224,8 +225,20 @@ static HiddenFwdArgs hidden_fwd_args(const Handle* h, int i, int rows, bool trai
   return f;
 }
 
-// Enqueue one whole step on `st` (captured into the graph once).  With a
-// recorder attached, an event follows every kernel (profiling only).
+// Tile width of a dW group (VOLTA_DW_GROUP_TN, else picked once from the
+// group's tile counts and the device's residency) and its products' first
+// workgroups.  `which`: 0 the step's group, 1 the extras step's.
+static void set_group_width(Handle* h, DwGroup& d, int which) {
+  int& tn = h->dw_tn_pick[which];
+  if (!tn) tn = h->dw_group_tn ? h->dw_group_tn : dw_group_pick_tile_n(d, h->num_cus);
+  d.tile_n = tn;
+  d.start[0] = 0;
+  for (int i = 0; i < d.n; ++i) d.start[i + 1] = d.start[i] + dw_group_tiles(d.g[i], tn);
+}
+
+// Enqueue one whole step on `st` (captured into the graph once, with
+// VOLTA_GRAPH=1).  With a recorder attached, an event follows every kernel
+// (profiling only).
 static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
   const volta_mlp_spec& s = h->spec;
   const int n = h->n, B = h->B;
@@ -345,7 +358,6 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
   // whether it may leave the step's loss sum to that launch (no arrival
   // ticket and agent-scope fences in the output launch).
   DwGroup group;
-  group.tile_n = h->dw_group_tn;
   std::string group_label;
   double group_fl = 0.0, group_by = 0.0;
   bool group_ok = false, defer_loss = false;
@@ -358,7 +370,6 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
       } else {
         group.g[group.n] = o.args;
         group.g[group.n].k_per_split = o.plan.k_per_split;
-        group.start[group.n + 1] = group.start[group.n] + dw_group_tiles(o.args, h->dw_group_tn);
         ++group.n;
       }
       char lx[32];
@@ -367,6 +378,7 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
       group_fl += dw_cost(i).first;
       group_by += dw_cost(i).second;
     }
+    set_group_width(h, group, 0);
     defer_loss = h->dw_group && h->out_mode == OUT_NARROW && h->out_dx_merged && !h->fwd_head;
     if (defer_loss) {
       group.loss_partials = h->loss_partials;
@@ -636,7 +648,6 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
     };
     if (h->ext_dw_group) {
       DwGroup d;
-      d.tile_n = h->dw_group_tn;
       std::string lab;
       double fl = 0.0, by = 0.0;
       for (int i = n - 1; i >= 0; --i) {
@@ -647,7 +658,6 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
         } else {
           d.g[d.n] = o.args;
           d.g[d.n].k_per_split = o.plan.k_per_split;
-          d.start[d.n + 1] = d.start[d.n] + dw_group_tiles(o.args, h->dw_group_tn);
           ++d.n;
         }
         std::snprintf(lx, sizeof lx, h->ext_clip ? "dw%d+opt" : "dw%d+db+opt", i);
@@ -655,6 +665,7 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
         fl += dw_cost(i).first;
         by += dw_cost(i).second;
       }
+      set_group_width(h, d, 1);
       if (dw_group_supported(d)) {
         VOLTA_CHECK(dw_group_launch(d, st, rec, lab.c_str(), fl, by));
         return true;
@@ -891,6 +902,7 @@ static bool build(Handle* h) {
   h->ext_dw_group = h->extras() && all_small && n_small <= kMaxDwGroup && !(np && *np && *np != '0');
   const char* gtn = std::getenv("VOLTA_DW_GROUP_TN");
   if (gtn && *gtn) h->dw_group_tn = std::atoi(gtn) == 64 ? 64 : 32;
+  else h->dw_group_tn = 0;
   if (h->dx_alone || h->ext_dw_group)
     for (int i = 1; i < n; ++i) {
       LayerPlan& lp = h->layers[i];
