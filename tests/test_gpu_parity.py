@@ -156,6 +156,78 @@ def test_gemm_big_tile_integer_exact(layout, M, N, K):
     np.testing.assert_array_equal(got, (Am.astype(np.int64) @ Bm.astype(np.int64)).astype(np.float32))
 
 
+TILE_BIG128 = 6
+
+
+@pytest.mark.parametrize("layout", [0, 1, 2], ids=["NN", "NT", "TN"])
+@pytest.mark.parametrize("M,N,K", [(128, 128, 128), (384, 256, 256), (256, 640, 1024), (128, 256, 4096)])
+def test_gemm_big128_tile_integer_exact(layout, M, N, K):
+    """The 128x128 direct-to-LDS tile (C5's 4096 x 1024 products): exact on
+    integer operands for all three layouts, which pins its swizzled
+    K-contiguous LDS layout (16 chunks a row), the two-k-row MN layout, the
+    wave/lane -> block mapping and the XCD tile order."""
+    say(f"gemm big128 tile layout={layout} M={M} N={N} K={K}")
+    rng = np.random.default_rng(M * 5 + N * 7 + K * 3 + layout)
+    a_shape = (K, M) if layout == 2 else (M, K)
+    b_shape = (N, K) if layout == 1 else (K, N)
+    A = rng.integers(-4, 5, a_shape).astype(np.float32)
+    B = rng.integers(-4, 5, b_shape).astype(np.float32)
+    got = _gemm(layout, A, B, M, N, K, tile=TILE_BIG128)
+    Am = A.T if layout == 2 else A
+    Bm = B.T if layout == 1 else B
+    np.testing.assert_array_equal(got, (Am.astype(np.int64) @ Bm.astype(np.int64)).astype(np.float32))
+
+
+@pytest.mark.parametrize("layout", [0, 1, 2], ids=["NN", "NT", "TN"])
+@pytest.mark.parametrize("M,N,K", [(512, 512, 512), (256, 768, 1024)])
+def test_gemm_big128_tile_bit_identical_to_big_tile(layout, M, N, K):
+    """Random fp32 operands: the 128x128 tile adds every output's products in
+    the 256x256 tile's k order, so both give the same bits (and the 256x256
+    tile's float bound, test_gemm_big_tile_float_bound, carries over)."""
+    say(f"gemm big128 vs big layout={layout} M={M} N={N} K={K}")
+    rng = np.random.default_rng(31 + layout + M)
+    A = rng.standard_normal((K, M) if layout == 2 else (M, K)).astype(np.float32)
+    B = rng.standard_normal((N, K) if layout == 1 else (K, N)).astype(np.float32)
+    np.testing.assert_array_equal(_gemm(layout, A, B, M, N, K, tile=TILE_BIG128),
+                                  _gemm(layout, A, B, M, N, K, tile=TILE_BIG))
+
+
+@pytest.mark.parametrize("layout", [0, 1, 2], ids=["NN", "NT", "TN"])
+def test_gemm_big128_tile_unaligned_output(layout):
+    """An output 4 bytes past a 16-byte boundary: the same bits as into an
+    aligned output (the epilogue's per-element accesses)."""
+    M, N, K = 256, 384, 256
+    say(f"gemm big128 tile unaligned output layout={layout}")
+    rng = np.random.default_rng(29 + layout)
+    A = rng.standard_normal((K, M) if layout == 2 else (M, K)).astype(np.float32)
+    B = rng.standard_normal((N, K) if layout == 1 else (K, N)).astype(np.float32)
+    aligned = _gemm(layout, A, B, M, N, K, tile=TILE_BIG128)
+    lib = load_hip()
+    dA, dB = DeviceArray(A), DeviceArray(B)
+    dC = DeviceArray(np.zeros(M * N + 1, np.float32))
+    rc = lib.lib.volta_hip_gemm(layout, dA.ptr, dB.ptr, dC.ptr + 4, M, N, K, TILE_BIG128, 0)
+    assert rc == 0, lib.last_error()
+    got = dC.numpy()
+    for d in (dA, dB, dC):
+        d.free()
+    assert got[0] == 0.0
+    np.testing.assert_array_equal(got[1:].reshape(M, N), aligned)
+
+
+def test_gemm_big128_tile_rejects_inexact_shapes():
+    """Shapes the tile does not serve exactly are refused on the host (no
+    launch): M or N not a multiple of 128, K not a multiple of 128."""
+    lib = load_hip()
+    for (M, N, K) in [(192, 128, 128), (128, 200, 128), (128, 128, 192)]:
+        A = np.ones((M, K), np.float32)
+        B = np.ones((K, N), np.float32)
+        dA, dB = DeviceArray(A), DeviceArray(B)
+        dC = DeviceArray(np.zeros((M, N), np.float32))
+        assert lib.lib.volta_hip_gemm(0, dA.ptr, dB.ptr, dC.ptr, M, N, K, TILE_BIG128, 0) != 0
+        for d in (dA, dB, dC):
+            d.free()
+
+
 KGROUP_CASES = [  # (tile, groups, M, N, K): ragged K, M and N included
     (0, 2, 130, 70, 300), (0, 4, 96, 64, 1000), (0, 4, 64, 200, 202), (1, 2, 256, 384, 520), (1, 2, 200, 130, 64),
 ]

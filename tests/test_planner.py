@@ -12,7 +12,7 @@ from volta_amd import HIP_LIB, load_hip
 pytestmark = pytest.mark.skipif(not os.path.exists(HIP_LIB), reason="libvolta_hip.so not built")
 
 NN, NT, TN = 0, 1, 2
-TILE_64, TILE_128, TILE_SMALLM, TILE_DW_SMALLK, TILE_BIG = 0, 1, 3, 4, 5
+TILE_64, TILE_128, TILE_SMALLM, TILE_DW_SMALLK, TILE_BIG, TILE_BIG128 = 0, 1, 3, 4, 5, 6
 CUS = 256
 
 
@@ -41,12 +41,30 @@ def test_big_tile_for_full_grids_of_256_multiples():
     assert plan(NN, 4096, 4096, 4096, env={"VOLTA_BIG_TILE": "0"})[0] == TILE_128
 
 
+def test_big128_tile_for_full_grids_of_128_multiples():
+    """C5's 4096x1024 and 1024x4096 products (256 tiles of 128x128, 64 of
+    256x256): the 128x128 direct-to-LDS tile, one per CU, whole K; not for
+    a K that is below 1024 or no multiple of 128, a grid of fewer tiles
+    than CUs, or with VOLTA_BIG128=0."""
+    assert plan(NN, 4096, 1024, 4096) == (TILE_BIG128, 1, 4096, 1, 0)
+    assert plan(TN, 1024, 4096, 4096) == (TILE_BIG128, 1, 4096, 1, 0)
+    assert plan(TN, 4096, 1024, 4096)[:2] == (TILE_BIG128, 1)
+    assert plan(NT, 4096, 1024, 1024)[:2] == (TILE_BIG128, 1)
+    assert plan(NN, 4096, 1024, 4160)[0] == TILE_128  # K % 128 != 0
+    assert plan(NN, 4096, 1024, 512)[0] == TILE_128  # K < 1024
+    assert plan(NN, 2048, 1024, 4096)[0] != TILE_BIG128  # 128 tiles
+    assert plan(NN, 4096, 1024, 4096, vec=False)[0] != TILE_BIG128
+    assert plan(NN, 4096, 4096, 4096)[0] == TILE_BIG  # the 256x256 grid has a tile per CU
+
+
 def test_128_tiles_from_a_tile_per_cu():
-    """128x128 tiles where their grid has a tile per CU (M*N >= 4M outputs,
-    K > 256), split in two to two workgroups per CU: C5's 4096x1024
-    products.  Below that (C4 B=1024's 1024x1024 products) 64x64 tiles."""
-    assert plan(NN, 4096, 1024, 4096) == (TILE_128, 2, 2048, 1, 0)
-    assert plan(TN, 1024, 4096, 4096)[:2] == (TILE_128, 2)
+    """Without the direct-to-LDS tile (VOLTA_BIG128=0), 128x128 tiles where
+    their grid has a tile per CU (M*N >= 4M outputs, K > 256), split in two
+    to two workgroups per CU: C5's 4096x1024 products.  Below that (C4
+    B=1024's 1024x1024 products) 64x64 tiles."""
+    off = {"VOLTA_BIG128": "0"}
+    assert plan(NN, 4096, 1024, 4096, env=off) == (TILE_128, 2, 2048, 1, 0)
+    assert plan(TN, 1024, 4096, 4096, env=off)[:2] == (TILE_128, 2)
     assert plan(NN, 1024, 1024, 1024)[0] == TILE_64
     assert plan(NN, 4096, 1024, 256)[0] == TILE_64  # short K
     # the knob restores 128x128 tiles from 2^20 outputs: 64 tiles, split 8 ways

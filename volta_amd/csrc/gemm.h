@@ -79,9 +79,11 @@ struct GemmArgs {
 // (K = B <= 256), the optimizer applied on 16-byte rows.
 // TILE_BIG: 256x256 tiles, direct-to-LDS operand loads, one workgroup per
 // CU, for exact 256-multiples with at least one tile per CU (C5's 4096 x 4096
-// products).
+// products).  TILE_BIG128: the same pipeline on 128x128 tiles, for exact
+// 128-multiples whose 128x128 grid has a tile per CU and whose 256x256 grid
+// does not (C5's 4096 x 1024 and 1024 x 4096 products).
 enum GemmTile { TILE_64x64 = 0, TILE_128x128 = 1, TILE_64x64_K64 = 2, TILE_SMALLM = 3, TILE_DW_SMALLK = 4,
-                TILE_BIG = 5 };
+                TILE_BIG = 5, TILE_BIG128 = 6 };
 
 struct GemmPlan {
   int layout = GEMM_NN;
@@ -93,7 +95,7 @@ struct GemmPlan {
   int waves = 0;                 // TILE_SMALLM: waves per workgroup (4 or 8)
   int kgroups = 1;               // 64x64 / 128x128: K slices inside one workgroup (splits = 1)
   int tiles(int M, int N) const {
-    const int t = tile == TILE_BIG ? 256 : tile == TILE_128x128 ? 128 : tile == TILE_SMALLM ? 16
+    const int t = tile == TILE_BIG ? 256 : tile == TILE_128x128 || tile == TILE_BIG128 ? 128 : tile == TILE_SMALLM ? 16
                   : tile == TILE_DW_SMALLK ? 32 : 64;
     return ((M + t - 1) / t) * ((N + t - 1) / t);
   }

@@ -1169,6 +1169,182 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) g
   }
 }
 
+// ---------------------------------------------------------------------------
+// 128x128 direct-to-LDS tile (TILE_BIG128): the 256x256 tile's pipeline for
+// products whose 256x256 grid would leave CUs idle while their 128x128 grid
+// has a tile per CU (C5's 4096 x 1024 and 1024 x 4096 products: 256 tiles,
+// the whole K in each workgroup, no split and no reduce launch).  Eight
+// waves (two per SIMD) in a 2 x 4 grid, each a 64x32 sub-tile: two 32x32
+// blocks of v_mfma_f32_32x32x2f32.  BK = 64: a stage is 64 KB of operands
+// (the 256x256 tile's bytes and load instructions per stage) and 8192 MFMA
+// cycles per SIMD between two barriers.  Every sum runs in the 256x256
+// tile's k order (k-group g, lane half h, step s: k = 8g + 4h + s), the bias
+// column sums too, and the epilogue arithmetic is the same, so both tiles
+// give the same bits on the products they both serve.
+//
+// LDS layouts.  K-contiguous [128 rows][64 k] in 16-byte chunks: (row r,
+// k-quad q) at chunk 16r + (q ^ (r & 15)): a row spans the 64 banks once,
+// and the fragment reads of 16 consecutive rows at one k-quad hit all 16
+// four-bank groups; each load instruction fills 64 consecutive chunks (4
+// whole rows, 16 lanes per 256-byte row segment).  MN-contiguous
+// [64 k][128]: a load instruction fills two k rows; fragments are read one
+// float per MFMA step, 32 lanes on 32 consecutive floats.
+//
+// Exact tiles only (M, N multiples of 128, K of 128, 16-byte aligned rows
+// and bases): every load is in bounds without a guard; gemm_launch checks.
+// ---------------------------------------------------------------------------
+constexpr int kB2 = 128, kB2K = 64;
+constexpr int kB2TileFloats = kB2 * kB2K;  // one operand tile of one stage (32 KB)
+
+// Issue this wave's 4 of the 32 one-kilobyte load instructions of an operand
+// tile (rows row0.., k k0..k0+63) into `tile`.  Instruction j = wave + 8t:
+// K-contiguous, rows 4j..4j+3 (lane: row 4j + lane/16, k-quad
+// (lane & 15) ^ (row & 15)); MN-contiguous, k rows 2j and 2j + 1 (lane: k row
+// 2j + lane/32, columns 4(lane & 31)..+3).  32-bit element offsets
+// (big128_tile_fits bounds the operands).
+template <bool KC>
+__device__ __forceinline__ void b128_load(const float* __restrict__ p, int ld, int row0, int k0, float* tile,
+                                          int wave, int lane) {
+  uint32_t off, step;
+  if constexpr (KC) {
+    const int r = 4 * wave + (lane >> 4);  // rows 32t apart share the swizzle
+    const int q = (lane & 15) ^ (r & 15);
+    off = (uint32_t)(row0 + r) * (uint32_t)ld + (uint32_t)(k0 + 4 * q);
+    step = 32u * (uint32_t)ld;
+  } else {
+    off = (uint32_t)(k0 + 2 * wave + (lane >> 5)) * (uint32_t)ld + (uint32_t)(row0 + 4 * (lane & 31));
+    step = 16u * (uint32_t)ld;
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+    __builtin_amdgcn_global_load_lds((const void*)(p + off + t * step), (LdsVoidPtr)(tile + (wave + 8 * t) * 256), 16,
+                                     0, 0);
+}
+
+// The 4 operands (k = 8g + 4h + s, s = 0..3) of lane (row, h) for k-group g.
+template <bool KC>
+__device__ __forceinline__ floatx4 b128_frag(const float* tile, int row, int h, int g) {
+  if constexpr (KC) {
+    const int q = 2 * g + h;
+    return *reinterpret_cast<const floatx4*>(tile + 4 * (16 * row + (q ^ (row & 15))));
+  } else {
+    floatx4 f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) f[s] = tile[(8 * g + 4 * h + s) * kB2 + row];
+    return f;
+  }
+}
+
+template <bool A_KC, bool B_KC, int EPI>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) gemm_big128(GemmArgs args) {
+  __shared__ __attribute__((aligned(16))) float lds_a0[kB2TileFloats];
+  __shared__ __attribute__((aligned(16))) float lds_b0[kB2TileFloats];
+  __shared__ __attribute__((aligned(16))) float lds_a1[kB2TileFloats];
+  __shared__ __attribute__((aligned(16))) float lds_b1[kB2TileFloats];
+  constexpr int TM = 2, WM = 64, WN = 32;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 2, wn = wave & 3, h = lane >> 5, l32 = lane & 31;
+  const int M = args.M, N = args.N, K = args.K;
+  const int tiles_n = N / kB2;
+  const int bx = xcd_tile(blockIdx.x, M / kB2, tiles_n);
+  const int tm = bx / tiles_n, tn = bx % tiles_n;
+  const int m0 = tm * kB2, n0 = tn * kB2;
+
+  constexpr bool kColsum = EPI == EPI_DW_OPT && !B_KC;
+  const bool colsum = kColsum && args.colsum_b && tm == 0 && wm == 0;
+  float cs = 0.0f;
+
+  floatx16 acc[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
+
+  const int arow = wm * WM + l32, bcol = wn * WN + l32;
+  // One stage: the fragments of k-group g + 1 are read from LDS before the
+  // 8 MFMAs of group g are issued; the wave's priority is raised while it
+  // issues MFMAs.
+  auto compute = [&](const float* a_s, const float* b_s) {
+    floatx4 fa_n[TM], fb_n;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa_n[i] = b128_frag<A_KC>(a_s, arow + 32 * i, h, 0);
+    fb_n = b128_frag<B_KC>(b_s, bcol, h, 0);
+#pragma unroll
+    for (int g = 0; g < kB2K / 8; ++g) {
+      floatx4 fa[TM], fb;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[i] = fa_n[i];
+      fb = fb_n;
+      if (g + 1 < kB2K / 8) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) fa_n[i] = b128_frag<A_KC>(a_s, arow + 32 * i, h, g + 1);
+        fb_n = b128_frag<B_KC>(b_s, bcol, h, g + 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < TM; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[s], acc[i], 0, 0, 0);
+      __builtin_amdgcn_s_setprio(0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (kColsum && colsum) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) cs = cs + fb[s];
+      }
+    }
+  };
+
+  // Stage s reads buffer s & 1; the loads of stage s + 1 go to the other
+  // buffer, which every wave finished reading before the barrier of stage s.
+  // S is even (K a multiple of 128), so every pass of the loop runs both.
+  const int S = K / kB2K;
+  b128_load<A_KC>(args.A, args.lda, m0, 0, lds_a0, wave, lane);
+  b128_load<B_KC>(args.B, args.ldb, n0, 0, lds_b0, wave, lane);
+  for (int s = 0; s < S; s += 2) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    b128_load<A_KC>(args.A, args.lda, m0, (s + 1) * kB2K, lds_a1, wave, lane);
+    b128_load<B_KC>(args.B, args.ldb, n0, (s + 1) * kB2K, lds_b1, wave, lane);
+    __builtin_amdgcn_sched_barrier(0);  // the loads stay ahead of this stage's MFMAs
+    compute(lds_a0, lds_b0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (s + 2 < S) {
+      b128_load<A_KC>(args.A, args.lda, m0, (s + 2) * kB2K, lds_a0, wave, lane);
+      b128_load<B_KC>(args.B, args.ldb, n0, (s + 2) * kB2K, lds_b0, wave, lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    compute(lds_a1, lds_b1);
+  }
+
+  if (kColsum && colsum) cs = cs + __shfl_xor(cs, 32, kWave);
+  const EpiArgs& e = args.epi;
+  static_for_blocks<0, TM, 1>([&](auto I, auto) {
+    constexpr int i = decltype(I)::value;
+    block_epilogue<EPI>(e, acc[i], m0 + wm * WM + i * 32 + 4 * h, n0 + bcol, M, N);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+  if constexpr (kColsum) {
+    if (colsum && h == 0 && e.b) apply_bias_update(e, n0 + bcol, N, cs, adam_rcp_of(e));
+  }
+}
+
+// Whether the 128x128 direct-to-LDS tile serves a product: exact
+// 128-multiples, K a multiple of 128 and at least 1024 (a shorter K keeps
+// the 64x64 grid's several workgroups per CU), 16-byte aligned operand rows,
+// a 128x128 grid of at least one workgroup per CU whose 256x256 grid has
+// fewer.
+static bool big128_tile_fits(int layout, int M, int N, int K, bool vec, int num_cus) {
+  const char* bt = std::getenv("VOLTA_BIG128");
+  if (bt && *bt == '0') return false;
+  const size_t a_elems = (size_t)M * K, b_elems = (size_t)N * K;
+  return vec && layout >= GEMM_NN && layout <= GEMM_TN && M % kB2 == 0 && N % kB2 == 0 && K % (2 * kB2K) == 0 &&
+         K >= 1024 && (M / kB2) * (N / kB2) >= num_cus && (M / kBigBM) * (N / kBigBM) < num_cus &&
+         a_elems < ((size_t)1 << 31) && b_elems < ((size_t)1 << 31);
+}
+
 // Whether the large tile serves a product: exact 256-multiples, K of 32,
 // 16-byte aligned operand rows, a grid of at least one workgroup per CU.
 static bool big_tile_fits(int layout, int M, int N, int K, bool vec, int num_cus) {
@@ -2205,6 +2381,32 @@ static hipError_t launch_big_epi(const GemmArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <bool A_KC, bool B_KC, int EPI>
+static hipError_t launch_big128_epi(const GemmArgs& a, hipStream_t st) {
+  const dim3 grid((a.M / kB2) * (a.N / kB2));
+  hipLaunchKernelGGL((gemm_big128<A_KC, B_KC, EPI>), grid, dim3(512), 0, st, a);
+  return hipGetLastError();
+}
+
+static hipError_t launch_big128(const GemmArgs& a, int layout, hipStream_t st) {
+  const int k = a.epi.kind;
+  switch (layout) {
+    case GEMM_NN:
+      if (k == EPI_BIAS_ACT) return launch_big128_epi<true, false, EPI_BIAS_ACT>(a, st);
+      if (k == EPI_STORE) return launch_big128_epi<true, false, EPI_STORE>(a, st);
+      break;
+    case GEMM_NT:
+      if (k == EPI_DX_ACT) return launch_big128_epi<true, true, EPI_DX_ACT>(a, st);
+      if (k == EPI_STORE) return launch_big128_epi<true, true, EPI_STORE>(a, st);
+      break;
+    case GEMM_TN:
+      if (k == EPI_DW_OPT) return launch_big128_epi<false, false, EPI_DW_OPT>(a, st);
+      if (k == EPI_STORE) return launch_big128_epi<false, false, EPI_STORE>(a, st);
+      break;
+  }
+  return hipErrorInvalidValue;
+}
+
 static hipError_t launch_big(const GemmArgs& a, int layout, hipStream_t st) {
   const int k = a.epi.kind;
   switch (layout) {
@@ -2247,6 +2449,14 @@ hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& args_in, hipStream_t s
                       a.lda % 4 == 0 && a.ldb % 4 == 0 && ((uintptr_t)a.A & 15) == 0 && ((uintptr_t)a.B & 15) == 0;
     if (!fits) return hipErrorInvalidValue;
     if ((err = launch_big(a, p.layout, st)) != hipSuccess) return err;
+    return mark(rec, label, 2.0 * a.M * a.N * a.K, bytes);
+  }
+  if (p.tile == TILE_BIG128) {
+    const bool fits = p.splits == 1 && a.M % kB2 == 0 && a.N % kB2 == 0 && a.K % (2 * kB2K) == 0 &&
+                      a.lda % 4 == 0 && a.ldb % 4 == 0 && ((uintptr_t)a.A & 15) == 0 && ((uintptr_t)a.B & 15) == 0 &&
+                      (size_t)a.M * a.K < ((size_t)1 << 31) && (size_t)a.N * a.K < ((size_t)1 << 31);
+    if (!fits) return hipErrorInvalidValue;
+    if ((err = launch_big128(a, p.layout, st)) != hipSuccess) return err;
     return mark(rec, label, 2.0 * a.M * a.N * a.K, bytes);
   }
   if (p.tile == TILE_DW_SMALLK) {
@@ -2605,6 +2815,17 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus, bool 
   if (p.tile == TILE_64x64 && sb && std::atoi(sb) == 64) p.tile = TILE_64x64_K64;
   if (big_tile_fits(layout, M, N, K, vec, num_cus)) {
     p.tile = TILE_BIG;
+    p.splits = 1;
+    p.k_per_split = K;
+    return p;
+  }
+  // The 128x128 direct-to-LDS tile where the 256x256 grid would leave CUs
+  // idle but the 128x128 grid has a tile per CU: no split, no reduce launch
+  // (C5's 4096 x 1024 and 1024 x 4096 products, which the register-staged
+  // 128x128 tile ran split in two plus a reduce).  VOLTA_BIG128=0 turns it
+  // off.
+  if (big128_tile_fits(layout, M, N, K, vec, num_cus)) {
+    p.tile = TILE_BIG128;
     p.splits = 1;
     p.k_per_split = K;
     return p;

@@ -78,7 +78,7 @@ int32_t volta_hip_gemm(int32_t layout, const float* A, const float* B, float* Cm
   const int contig_b = layout == GEMM_NT ? K : N;
   const bool vec = contig_a % 4 == 0 && contig_b % 4 == 0;
   GemmPlan p = gemm_plan(layout, M, N, K, vec, cus);
-  if (force_tile > TILE_BIG) {
+  if (force_tile > TILE_BIG128) {
     set_last_error("volta_hip_gemm: unknown tile");
     return -1;
   }
@@ -92,7 +92,8 @@ int32_t volta_hip_gemm(int32_t layout, const float* A, const float* B, float* Cm
     const char* w = std::getenv("VOLTA_SMALLM_WAVES");
     p.waves = layout == GEMM_NT || (w && std::atoi(w) == 4) ? 4 : (w && std::atoi(w) == 16) ? 16 : 8;
   }
-  if (force_tile == TILE_SMALLM || force_tile == TILE_DW_SMALLK || force_tile == TILE_BIG) {  // whole K in each workgroup
+  if (force_tile == TILE_SMALLM || force_tile == TILE_DW_SMALLK || force_tile == TILE_BIG ||
+      force_tile == TILE_BIG128) {  // whole K in each workgroup
     p.splits = 1;
     p.k_per_split = K;
   }
