@@ -926,6 +926,85 @@ def test_graph_replay_bit_identical_to_direct_launches(name):
         np.testing.assert_array_equal(a, b)
 
 
+KHALF_BITS_CASES = {
+    # the hidden forward product over two halves of K (VOLTA_FWD_SPLIT=1):
+    # C2's fwd2 -> fwd3 and C1's fwd1 -> fwd2, whose halves are whole wave
+    # ranges of the one-launch product
+    "c2": (MlpSpec([512, 1024, 1024, 512, 256, 1], "relu", "adam"), 64, 1e-3),
+    "c1": (MlpSpec([256, 512, 512, 256, 1], "relu", "sgd"), 64, 0.01),
+}
+
+
+@pytest.mark.parametrize("name", sorted(KHALF_BITS_CASES))
+def test_forward_khalves_bit_identical(name):
+    """The forward product over two halves of K, its partial planes added by
+    the next forward launch as it forms its A operand (opt-in
+    VOLTA_FWD_SPLIT=1), gives the one-launch product's bits where each half
+    is a whole set of that product's wave ranges (the same summation tree):
+    losses, parameters, activations and deltas after 4 steps."""
+    spec, B, lr = KHALF_BITS_CASES[name]
+    say(f"forward K halves vs one launch {name}")
+    l1, p1, b1 = _run_with_env({"VOLTA_FWD_SPLIT": "0"}, spec, B, lr, 4)
+    l2, p2, b2 = _run_with_env({"VOLTA_FWD_SPLIT": "1"}, spec, B, lr, 4)
+    np.testing.assert_array_equal(l1, l2)
+    for a, b in zip(p1 + b1, p2 + b2):
+        np.testing.assert_array_equal(a, b)
+
+
+KHALF_CASES = {
+    # a pre-activation kept (SiLU), and a ragged batch and K (48 rows; K = 528
+    # in halves of 272 and 256, not whole wave ranges) with GELU
+    "c2_silu": (MlpSpec([512, 1024, 1024, 512, 256, 1], "silu", "sgd"), 64, 1e-3),
+    "ragged_gelu": (MlpSpec([96, 528, 512, 200, 3], "gelu", "sgd"), 48, 0.01),
+}
+
+
+@pytest.mark.parametrize("name", sorted(KHALF_CASES))
+def test_forward_khalves_against_oracle(name):
+    """The forward product over two halves of K (VOLTA_FWD_SPLIT=1) where
+    the bits need not match the one-launch form: losses and parameters after
+    5 SGD steps within rel 1e-4 / abs 1e-5 of the oracle, and the layer
+    outputs and pre-activations the next launch stores within the same
+    bound after one step."""
+    from volta_amd.abi import BUF_ACT, BUF_PRE
+
+    spec, B, lr = KHALF_CASES[name]
+    say(f"forward K halves {name}")
+    ws, bs, batches = config_inputs(spec, B, seed=13)
+    old = os.environ.get("VOLTA_FWD_SPLIT")
+    os.environ["VOLTA_FWD_SPLIT"] = "1"
+    try:
+        lh, wh, bh, st = run_steps(load_hip(), spec, B, ws, bs, batches, lr, 5)
+        t = Trainer(load_hip(), spec, B)
+        t.set_all_params(ws, bs)
+        t.step(*batches[0], lr)
+        acts = [t.debug_buffer(BUF_ACT, i) for i in range(1, len(spec.sizes) - 1)]
+        # pre-activations are kept only where the activation's derivative needs them
+        pres = [t.debug_buffer(BUF_PRE, i) for i in range(len(spec.sizes) - 2)]
+        assert t.status() == 0
+        t.close()
+    finally:
+        if old is None:
+            os.environ.pop("VOLTA_FWD_SPLIT", None)
+        else:
+            os.environ["VOLTA_FWD_SPLIT"] = old
+    lo, wo, bo, _ = run_steps(load_oracle(), spec, B, ws, bs, batches, lr, 5)
+    assert st == 0, f"status {st}"
+    ok, mx, _ = close_enough(lh, lo)
+    assert ok, f"{name}: losses differ, max abs {mx:.3e}"
+    assert_params_close(wh, bh, wo, bo, name)
+    to = Trainer(load_oracle(), spec, B)
+    to.set_all_params(ws, bs)
+    to.step(*batches[0], lr)
+    for i, a in enumerate(acts):
+        ok, mx, _ = close_enough(a, to.debug_buffer(BUF_ACT, i + 1))
+        assert ok, f"{name}: act{i + 1} max abs {mx:.3e}"
+    for i, p in enumerate(pres):
+        ok, mx, _ = close_enough(p, to.debug_buffer(BUF_PRE, i))
+        assert ok, f"{name}: pre{i} max abs {mx:.3e}"
+    to.close()
+
+
 WIDTH_CASES = {
     # K = 64, 64 and 256 (one and four 64-k slices); the extras step's group
     "c2": PAIR_CASES["c2"],

@@ -122,6 +122,21 @@ hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& a, hipStream_t st, Rec
 // n_counters), left zero.
 // The one-column output layer (loss head, dX_{n-1}) and the dX_{n-2}
 // product planned as `p` in one launch (gemm_smallm_tail; loss deferred).
+// A hidden forward product over two halves of its K (plan p: 16-wave small-M
+// tile, 16-byte rows), each half's raw partial tile into its plane of
+// `planes` (2*M*N floats, 16-byte aligned); k_half a multiple of 16 inside
+// (0, K).  The next forward product adds them as it loads its A operand:
+struct PlaneArgs {
+  const float* p1 = nullptr;    // the second plane (args.A is the first; row stride args.lda)
+  const float* bias = nullptr;  // the previous layer's bias
+  float* act_out = nullptr;     // the previous layer's output [M x lda]
+  float* pre_out = nullptr;     // the previous layer's pre-activation, or null
+  int act = 0;                  // the previous layer's activation (device code)
+};
+bool khalves_supported(const GemmPlan& p, const GemmArgs& a, int k_half);
+hipError_t launch_smallm_khalves(const GemmPlan& p, const GemmArgs& a, float* planes, int k_half, hipStream_t st);
+bool planes_supported(const GemmPlan& p, const GemmArgs& a, const PlaneArgs& pa);
+hipError_t launch_smallm_planes(const GemmPlan& p, const GemmArgs& a, const PlaneArgs& pa, hipStream_t st);
 bool tail_supported(const GemmPlan& p, const GemmArgs& a, const OutLayerArgs& o);
 hipError_t launch_smallm_tail(const GemmPlan& p, const GemmArgs& a, const OutLayerArgs& o, hipStream_t st);
 bool fwd_head_supported(const GemmPlan& p, const GemmArgs& a, const OutLayerArgs& o, int n_counters);

@@ -1413,12 +1413,20 @@ __device__ __forceinline__ void smallm_coords(int blk, int tiles_m, int tiles_n,
 // the A values it forms, its rows of delta_{n-2}, every element once: the
 // last chunk's after the tile's last barrier (from the operand registers
 // they replace), earlier chunks' as they are formed.
+//
+// AH == 3 (a forward product whose A operand is the previous layer's output,
+// left by that layer's launch as two partial planes over halves of its K):
+// A(m, k) = f((P0[m][k] + P1[m][k]) + b[k]) with args.A = P0, `pre` = P1
+// (both of row stride lda), `w` = b and `act` = f; with `dx_out` set the
+// tile also stores the A values (the previous layer's output) and, with
+// `pre_out` set, the pre-activations, every element once.
 struct SmallHead {
-  const float* pre = nullptr;  // pre-activation of layer n-2 [M x lda]
-  const float* w = nullptr;    // W_{n-1} [K x 1]
+  const float* pre = nullptr;  // pre-activation of layer n-2 [M x lda] (AH == 3: the second plane)
+  const float* w = nullptr;    // W_{n-1} [K x 1] (AH == 3: the previous layer's bias)
   const float* d = nullptr;    // the tile's 16 row deltas delta_{n-1} (LDS)
-  float* dx_out = nullptr;     // delta_{n-2} [M x lda], or null
-  int act = 0;                 // activation of layer n-2
+  float* dx_out = nullptr;     // delta_{n-2} [M x lda] (AH == 3: the previous layer's output), or null
+  float* pre_out = nullptr;    // AH == 3: the previous layer's pre-activation [M x lda], or null
+  int act = 0;                 // activation of layer n-2 (AH == 3: of the previous layer)
 };
 struct SmallNoop {
   __device__ void operator()() const {}
@@ -1433,8 +1441,10 @@ template <bool B_KC, bool VEC, int EPI, int NW, int AH = 0, class Pre = SmallNoo
 __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float* lds,
                                             const SmallHead& hd = SmallHead{}, Pre pre = Pre{}, Post post = Post{}) {
   static_assert(NW == 4 || NW == 8 || NW == 16, "wave trees for 4, 8 or 16 partial tiles");
-  static_assert(AH == 0 || (B_KC && VEC && EPI == EPI_DX_ACT && NW == 16),
+  static_assert(AH == 0 || AH == 3 || (B_KC && VEC && EPI == EPI_DX_ACT && NW == 16),
                 "head operand: NT dX product, 16-byte rows, 16 waves");
+  static_assert(AH != 3 || (!B_KC && VEC && EPI == EPI_BIAS_ACT && NW == 16),
+                "plane operand: NN forward product, 16-byte rows, 16 waves");
   // 16-wave workgroups (four waves per SIMD) hold a quarter chunk per wave
   constexpr int CH = NW == 16 ? kSmallChunk / 4 : kSmallChunk;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1453,8 +1463,10 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
   // (row 0 / column 0 stand in for rows and columns outside the matrix)
   const float* pa = args.A + (size_t)(row_ok ? m0 + r : 0) * lda;
   const float* pb = B_KC ? args.B + (size_t)(col_ok ? n0 + r : 0) * ldb : args.B + (col_ok ? n0 + r : 0);
-  const float* pp = AH == 2 ? hd.pre + (size_t)(row_ok ? m0 + r : 0) * lda : pa;
-  floatx4 fp[AH == 2 ? CH : 1], fw[AH > 0 ? CH : 1];  // head operand: pre-activation, W_{n-1}
+  const float* pp = AH >= 2 ? hd.pre + (size_t)(row_ok ? m0 + r : 0) * lda : pa;
+  // head operand: pre-activation (AH == 3: the second plane, then the
+  // pre-activation formed), W_{n-1} (AH == 3: the bias)
+  floatx4 fp[AH >= 2 ? CH : 1], fw[AH > 0 ? CH : 1];
 
   // A chunk's loads: per group unconditional within the lane (k clamped
   // into the wave's range), keeping the raw values; compute() replaces those
@@ -1470,7 +1482,7 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
       if (VEC) {  // K % 4 == 0 and every range bound is a multiple of 4
         const int kl = min(k, kend - 4);
         fa[g] = *reinterpret_cast<const floatx4*>(pa + kl);
-        if constexpr (AH == 2) fp[g] = *reinterpret_cast<const floatx4*>(pp + kl);
+        if constexpr (AH >= 2) fp[g] = *reinterpret_cast<const floatx4*>(pp + kl);
         if constexpr (AH > 0) fw[g] = *reinterpret_cast<const floatx4*>(hd.w + kl);
         if (B_KC) {
           fb[g] = *reinterpret_cast<const floatx4*>(pb + kl);
@@ -1517,7 +1529,15 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
       if (kc + 16 * g < kend) {  // wave-uniform
         const int k = kc + 16 * g + 4 * q;
         floatx4 xa;  // head operand: the lane's four A values of the group
-        if constexpr (AH > 0) {
+        if constexpr (AH == 3) {
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const float pv = (fa[g][s] + fp[g][s]) + fw[g][s];  // pre = act W + b (:716-724), two halves of K
+            fp[g][s] = pv;
+            xa[s] = act_forward(hd.act, pv);  // (:725-743)
+          }
+          fa[g] = xa;
+        } else if constexpr (AH > 0) {
 #pragma unroll
           for (int s = 0; s < 4; ++s) {
             const float av = fa[g][s];
@@ -1551,14 +1571,20 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
       for (int g = 0; g < CH; ++g) {
         const int k = kc + 16 * g + 4 * q;
         if (kc + 16 * g < kend && k < kend) *reinterpret_cast<floatx4*>(hd.dx_out + (size_t)(m0 + r) * lda + k) = fa[g];
+        if constexpr (AH == 3) {
+          if (hd.pre_out && kc + 16 * g < kend && k < kend)
+            *reinterpret_cast<floatx4*>(hd.pre_out + (size_t)(m0 + r) * lda + k) = fp[g];
+        }
       }
     }
   };
   int last_kc = -1;
   if constexpr (AH > 0) {
     if (kbeg < kend) load(fa, fb, kbeg);
-    pre();  // every wave, once
-    dr = hd.d[r];
+    if constexpr (AH != 3) {
+      pre();  // every wave, once
+      dr = hd.d[r];
+    }
     for (int kc = kbeg; kc < kend; kc += 16 * CH) {
       if (kc != kbeg) load(fa, fb, kc);
       compute(fa, fb, kc);
@@ -1614,6 +1640,50 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW
 gemm_smallm(GemmArgs args) {
   __shared__ float lds[SmallLds<NW>::kFloats];
   smallm_tile<B_KC, VEC, EPI, NW>(args, blockIdx.x, lds);
+}
+
+// A forward product over two halves of its K (a grid of at most half a
+// workgroup per CU: C2's fwd2, 128 tiles): workgroup (z, t) runs tile t over
+// half z of K on the 16-wave small-M tile and stores its raw partial tile to
+// plane z, planes + z*M*N (row stride N).  The next forward launch adds the
+// two planes, the bias and the activation as it loads its A operand
+// (gemm_smallm_planes).
+template <bool VEC>
+__global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4)))
+gemm_smallm_khalves(GemmArgs args, float* planes, int k_half) {
+  __shared__ float lds[SmallLds<16>::kFloats];
+  const int tiles = ((args.M + 15) / 16) * ((args.N + 15) / 16);
+  const int z = blockIdx.x >= tiles ? 1 : 0;
+  GemmArgs a = args;
+  a.A = args.A + (size_t)z * k_half;
+  a.B = args.B + (size_t)z * k_half * args.ldb;
+  a.K = z ? args.K - k_half : k_half;
+  a.epi.kind = EPI_STORE;
+  a.epi.ldc = args.N;
+  a.epi.out = planes + (size_t)z * args.M * args.N;
+  smallm_tile<false, VEC, EPI_STORE, 16>(a, blockIdx.x - z * tiles, lds);
+}
+
+// The forward product after gemm_smallm_khalves: A(m, k) = f((P0 + P1)[m][k]
+// + b[k]) formed as it is loaded (smallm_tile, AH == 3), then the product,
+// bias and activation of this layer as usual.  The first column tile of
+// every 16-row strip also stores the strip's A values (the previous layer's
+// output) and pre-activations, so later launches read them as if the
+// previous layer had run on its own.
+template <bool VEC>
+__global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4)))
+gemm_smallm_planes(GemmArgs args, PlaneArgs p) {
+  __shared__ float lds[SmallLds<16>::kFloats];
+  const int tiles_m = (args.M + 15) / 16, tiles_n = (args.N + 15) / 16;
+  int tm, tn;
+  smallm_coords<2>(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  SmallHead hd;
+  hd.pre = p.p1;
+  hd.w = p.bias;
+  hd.act = p.act;
+  hd.dx_out = tn == 0 ? p.act_out : nullptr;
+  hd.pre_out = tn == 0 ? p.pre_out : nullptr;
+  smallm_tile<false, VEC, EPI_BIAS_ACT, 16, 3>(args, blockIdx.x, lds, hd);
 }
 
 // The last hidden layer's forward product (small-M tile, bias + activation)
@@ -2371,6 +2441,33 @@ hipError_t launch_smallm_tail(const GemmPlan& p, const GemmArgs& args_in, const 
   const dim3 grid(((a.M + 15) / 16) * ((a.N + 15) / 16));
   if (o.dx_pre) hipLaunchKernelGGL(gemm_smallm_tail<true>, grid, dim3(1024), 0, st, a, o);
   else hipLaunchKernelGGL(gemm_smallm_tail<false>, grid, dim3(1024), 0, st, a, o);
+  return hipGetLastError();
+}
+
+bool khalves_supported(const GemmPlan& p, const GemmArgs& a, int k_half) {
+  return p.tile == TILE_SMALLM && p.layout == GEMM_NN && p.splits == 1 && p.vec && a.M > 0 && a.N > 0 &&
+         k_half > 0 && k_half < a.K && k_half % 16 == 0 && a.ldb % 4 == 0 && smallm_vec_ok(a, GEMM_NN);
+}
+
+hipError_t launch_smallm_khalves(const GemmPlan& p, const GemmArgs& args_in, float* planes, int k_half,
+                                 hipStream_t st) {
+  if (!khalves_supported(p, args_in, k_half) || !planes || ((uintptr_t)planes & 15u)) return hipErrorInvalidValue;
+  const dim3 grid(2 * ((args_in.M + 15) / 16) * ((args_in.N + 15) / 16));
+  hipLaunchKernelGGL(gemm_smallm_khalves<true>, grid, dim3(1024), 0, st, args_in, planes, k_half);
+  return hipGetLastError();
+}
+
+bool planes_supported(const GemmPlan& p, const GemmArgs& a, const PlaneArgs& pa) {
+  const auto al = [](const void* q) { return ((uintptr_t)q & 15u) == 0; };
+  return p.tile == TILE_SMALLM && p.layout == GEMM_NN && p.splits == 1 && p.vec && p.waves == 16 &&
+         a.epi.kind == EPI_BIAS_ACT && smallm_vec_ok(a, GEMM_NN) && pa.p1 && al(pa.p1) && pa.bias && al(pa.bias) &&
+         pa.act_out && al(pa.act_out) && (!pa.pre_out || al(pa.pre_out));
+}
+
+hipError_t launch_smallm_planes(const GemmPlan& p, const GemmArgs& a, const PlaneArgs& pa, hipStream_t st) {
+  if (!planes_supported(p, a, pa)) return hipErrorInvalidValue;
+  const dim3 grid(((a.M + 15) / 16) * ((a.N + 15) / 16));
+  hipLaunchKernelGGL(gemm_smallm_planes<true>, grid, dim3(1024), 0, st, a, pa);
   return hipGetLastError();
 }
 

@@ -11,7 +11,10 @@
 //
 // The step's launch order (a topological order of the step's dataflow):
 //   fwd_0 .. fwd_{n-2}          GEMM NN + bias + activation (in the split-K
-//                               reduction when K is split)
+//                               reduction when K is split); opt-in, a
+//                               small-batch product on few CUs over two halves
+//                               of K into two planes, which the next forward
+//                               launch adds with the bias and activation
 //   fwd_{n-1} + loss            narrow output kernel (L_n <= 16), GEMM with the
 //                               loss head in its epilogue (<= 64), or GEMM +
 //                               loss kernel: delta_{n-1}, loss, Adam t
@@ -117,6 +120,8 @@ struct Handle {
   bool fwd_head = false;      // ... and that launch folded into the last hidden forward launch (opt-in)
   bool tail_merge = false;    // ... or that launch and dX_{n-2} in one (gemm_smallm_tail; VOLTA_NO_TAIL=1: off)
   bool narrow_dw = false;     // dW of the output layer by narrow_dw_kernel
+  std::vector<int> fwd_khalf; // per layer: > 0 runs its forward over two halves of K (this one first),
+                              // its output formed by the next forward launch (0: one launch)
   bool keep_grads = false;    // also store dW/db in `grads` (VOLTA_KEEP_GRADS=1)
   DevScalars* scalars = nullptr;
   float2* bc_table = nullptr;  // own allocation (its length depends on beta1/beta2)
@@ -495,6 +500,31 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
     // algorithmic bytes: 4(B*r + r*c + B*c*(2 if hidden else 1)) (+ loss head)
     const double bytes = 4.0 * ((double)B * lp.r + (double)lp.r * lp.c + (double)B * lp.c * (last ? 1 : 2)) +
                          (last && h->out_mode == OUT_GEMM_LOSS ? 8.0 * B * Ln : 0.0);
+    if (!last && h->fwd_khalf[i]) {
+      // two halves of K into the workspace's planes (4(B*r + r*c + 2*B*c))
+      VOLTA_CHECK(launch_smallm_khalves(lp.fwd, a, h->gemm_ws, h->fwd_khalf[i], st));
+      std::snprintf(label, sizeof label, "fwd%d.khalves", i);
+      VOLTA_CHECK(mark(rec, label, 2.0 * a.M * a.N * a.K,
+                       4.0 * ((double)B * lp.r + (double)lp.r * lp.c + 2.0 * B * lp.c)));
+      continue;
+    }
+    if (!last && i > 0 && h->fwd_khalf[i - 1]) {
+      // layer i-1's planes + bias + activation as this product's A operand
+      // (+ 4(B*r + r + B*r [+ B*r pre]) beyond this layer's own bytes)
+      const LayerPlan& pl = h->layers[i - 1];
+      PlaneArgs pa;
+      pa.p1 = h->gemm_ws + (size_t)B * pl.c;
+      pa.bias = h->params + pl.b_off;
+      pa.act_out = h->act[i];
+      pa.pre_out = h->pre[i - 1];
+      pa.act = h->gemm_act();
+      a.A = h->gemm_ws;
+      VOLTA_CHECK(launch_smallm_planes(lp.fwd, a, pa, st));
+      std::snprintf(label, sizeof label, "fwd%d.sum+fwd%d", i - 1, i);
+      VOLTA_CHECK(mark(rec, label, 2.0 * a.M * a.N * a.K,
+                       bytes + 4.0 * ((double)B * lp.r * (pa.pre_out ? 3.0 : 2.0) + lp.r)));
+      continue;
+    }
     if (i == n - 2 && h->fwd_head) {
       const OutLayerArgs o = out_args();
       GemmArgs af = a;
@@ -907,6 +937,34 @@ static bool build(Handle* h) {
     for (int i = 1; i < n; ++i) {
       LayerPlan& lp = h->layers[i];
       if (lp.dx.tile == TILE_SMALLM) lp.dx.waves = gemm_smallm_waves(false, B, lp.r, h->num_cus);
+    }
+  // Opt-in (VOLTA_FWD_SPLIT=1): a hidden forward product on the 16-wave
+  // small-M tile whose grid has at most half a workgroup per CU and a K of
+  // at least 512, followed by another hidden forward product on the 16-wave
+  // small-M tile, runs its two halves of K as two workgroups each (twice the
+  // CUs, half the K each) into two partial planes of the workspace, and the
+  // next launch adds them, the bias and the activation as it loads its A
+  // operand and stores the layer's output (C2's fwd2 into fwd3, C1's fwd1
+  // into fwd2).  Where the halves are whole wave ranges of the one-launch
+  // product (K a power-of-two multiple of 512: C1, C2) the sums are the same
+  // tree, so the bits are too.  Slower: the halves save 1.6 us of C2's fwd2,
+  // and forming the A operand from the planes costs fwd3 2.1 us (C2 50.3 ->
+  // 51.2 us, C1 28.6 -> 30.1).  Not with the codegen extras (their row
+  // kernels run between the forward launches) or into the opt-in head
+  // launch.
+  h->fwd_khalf.assign(n, 0);
+  const char* fsp = std::getenv("VOLTA_FWD_SPLIT");
+  if (!h->extras() && fsp && *fsp && *fsp != '0')
+    for (int i = 0; i + 2 < n; ++i) {
+      if ((i > 0 && h->fwd_khalf[i - 1]) || (i + 1 == n - 2 && h->fwd_head)) continue;
+      const LayerPlan& pl = h->layers[i];
+      const LayerPlan& cl = h->layers[i + 1];
+      const int tiles = pl.fwd.tiles(B, pl.c);
+      if (pl.fwd.tile == TILE_SMALLM && pl.fwd.vec && pl.fwd.waves == 16 && pl.r >= 512 &&
+          2 * tiles <= h->num_cus && cl.fwd.tile == TILE_SMALLM && cl.fwd.vec && cl.fwd.waves == 16) {
+        h->fwd_khalf[i] = (pl.r / 2 + 15) / 16 * 16;
+        ws_floats = std::max(ws_floats, (size_t)2 * B * pl.c);
+      }
     }
   ws_floats = align_up(ws_floats, 64);
   h->ws_half = ws_floats;
