@@ -1005,6 +1005,43 @@ def test_forward_khalves_against_oracle(name):
     to.close()
 
 
+OUT_MFMA_CASES = {
+    # the narrow output layer of a large batch on MFMA with the loss summed
+    # by the dX_{n-1} launch: a ragged batch (1000 rows: a last strip of 8),
+    # MSE of width 3 and softmax-CE of 10 classes, and C4 B=1024's width-1 head
+    "mse3_b1000": (MlpSpec([64, 256, 128, 3], "tanh", "sgd"), 1000, 0.01),
+    "ce10_b1000": (MlpSpec([64, 256, 128, 10], "relu", "sgd", "ce"), 1000, 0.05),
+    "mse1_b1024": (MlpSpec([512, 1024, 1024, 512, 256, 1], "silu", "sgd"), 1024, 0.01),
+}
+
+
+@pytest.mark.parametrize("name", sorted(OUT_MFMA_CASES))
+@pytest.mark.parametrize("mfma", ["1", "0"])
+def test_large_batch_output_layer_against_oracle(name, mfma):
+    """The large-batch narrow output layer, on MFMA strips with its loss
+    summed by the next launch (the default) and as wave dot products with a
+    loss launch (VOLTA_OUT_MFMA=0): every loss and parameter after 5 SGD
+    steps within rel 1e-4 / abs 1e-5 of the oracle, and the step status
+    clean."""
+    spec, B, lr = OUT_MFMA_CASES[name]
+    say(f"large-batch output layer {name} mfma={mfma}")
+    ws, bs, batches = config_inputs(spec, B, seed=5)
+    old = os.environ.get("VOLTA_OUT_MFMA")
+    os.environ["VOLTA_OUT_MFMA"] = mfma
+    try:
+        lh, wh, bh, st = run_steps(load_hip(), spec, B, ws, bs, batches, lr, 5)
+    finally:
+        if old is None:
+            os.environ.pop("VOLTA_OUT_MFMA", None)
+        else:
+            os.environ["VOLTA_OUT_MFMA"] = old
+    lo, wo, bo, _ = run_steps(load_oracle(), spec, B, ws, bs, batches, lr, 5)
+    assert st == 0, f"status {st}"
+    ok, mx, _ = close_enough(lh, lo)
+    assert ok, f"{name}: losses differ, max abs {mx:.3e}\n hip={lh}\n ora={lo}"
+    assert_params_close(wh, bh, wo, bo, name)
+
+
 WIDTH_CASES = {
     # K = 64, 64 and 256 (one and four 64-k slices); the extras step's group
     "c2": PAIR_CASES["c2"],

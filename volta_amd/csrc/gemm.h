@@ -23,6 +23,7 @@ enum EpiKind {
   EPI_DX_ACT = 2,    // out = acc * f'(aux_pre, aux_act)
   EPI_DW_OPT = 3,    // acc is dW: optimizer update of W (and of b from the fused column sums)
   EPI_LOSS = 4,      // output layer + loss head: out = acc + bias, delta, loss
+  EPI_ROWS = 5,      // small-M tile only: acc + bias into the workgroup's LDS rows (the output head)
 };
 
 struct EpiArgs {
@@ -137,6 +138,16 @@ bool khalves_supported(const GemmPlan& p, const GemmArgs& a, int k_half);
 hipError_t launch_smallm_khalves(const GemmPlan& p, const GemmArgs& a, float* planes, int k_half, hipStream_t st);
 bool planes_supported(const GemmPlan& p, const GemmArgs& a, const PlaneArgs& pa);
 hipError_t launch_smallm_planes(const GemmPlan& p, const GemmArgs& a, const PlaneArgs& pa, hipStream_t st);
+// The narrow output layer of a large batch (L_n <= 16, more rows than the
+// one-launch output kernels take) on 16-wave small-M tiles, one per 16-row
+// strip: z = act_{n-1} W + b on MFMA, then the loss head per row
+// (head_row: z, delta_{n-1}, the row loss); each workgroup stores its rows'
+// loss sum in row order to o.partials[strip], block 0 advances the step
+// counter, and a later launch adds the partials (the outer-product dX_{n-1}
+// launch, LossDefer).  `a` carries A = act_{n-1}, B = W, M = B, N = L_n,
+// K = L_{n-1} and the bias (a.epi.bias).
+bool out_head_gemm_supported(const GemmArgs& a, const OutLayerArgs& o);
+hipError_t launch_smallm_out_head(const GemmArgs& a, const OutLayerArgs& o, hipStream_t st);
 bool tail_supported(const GemmPlan& p, const GemmArgs& a, const OutLayerArgs& o);
 hipError_t launch_smallm_tail(const GemmPlan& p, const GemmArgs& a, const OutLayerArgs& o, hipStream_t st);
 bool fwd_head_supported(const GemmPlan& p, const GemmArgs& a, const OutLayerArgs& o, int n_counters);

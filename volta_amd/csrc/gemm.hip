@@ -1427,6 +1427,7 @@ struct SmallHead {
   float* dx_out = nullptr;     // delta_{n-2} [M x lda] (AH == 3: the previous layer's output), or null
   float* pre_out = nullptr;    // AH == 3: the previous layer's pre-activation [M x lda], or null
   int act = 0;                 // activation of layer n-2 (AH == 3: of the previous layer)
+  float* zrows = nullptr;      // EPI_ROWS: the tile's 16 rows of acc + bias (LDS, row stride 17)
 };
 struct SmallNoop {
   __device__ void operator()() const {}
@@ -1511,7 +1512,7 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
   const bool eok = tid < 256 && em < M && en < N;
   const size_t eidx = eok ? (size_t)em * ep.ldc + en : 0;
   float e_y = 0.0f, e_p = 0.0f;
-  if constexpr (EPI == EPI_BIAS_ACT) e_y = ep.bias[eok ? en : 0];
+  if constexpr (EPI == EPI_BIAS_ACT || EPI == EPI_ROWS) e_y = ep.bias[eok ? en : 0];
   if constexpr (EPI == EPI_DX_ACT) {
     e_y = ep.aux_act[eidx];
     e_p = ep.aux_pre ? ep.aux_pre[eidx] : e_y;
@@ -1629,6 +1630,8 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
       ep.out[eidx] = act_forward(ep.act, v);  // (:725-743)
     } else if constexpr (EPI == EPI_DX_ACT) {
       ep.out[eidx] = sum * act_derivative(ep.act, e_p, e_y);  // (:893-929)
+    } else if constexpr (EPI == EPI_ROWS) {
+      hd.zrows[i * 17 + j] = sum + e_y;  // z = act_{n-1} W + b (:792-798)
     } else {
       apply_epilogue<EPI>(ep, m, n, sum);
     }
@@ -1640,6 +1643,54 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW
 gemm_smallm(GemmArgs args) {
   __shared__ float lds[SmallLds<NW>::kFloats];
   smallm_tile<B_KC, VEC, EPI, NW>(args, blockIdx.x, lds);
+}
+
+// The narrow output layer of a large batch on the small-M tile (one 16-row
+// strip per workgroup, the strip's z rows in LDS), then the loss head of
+// each row by one thread (head_row: the same per-row code as the
+// wave-dot-product output kernels), the strip's loss sum in row order into
+// partials[strip], and the step counter advanced by block 0.  The loss
+// itself is formed by a later launch of the step from the partials.
+template <bool VEC>
+__global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4)))
+gemm_smallm_out_head(GemmArgs args, OutLayerArgs p) {
+  __shared__ float lds[SmallLds<16>::kFloats];
+  __shared__ float zrows[16 * 17];
+  __shared__ float row_loss[16];
+  StepNext next{};
+  if (threadIdx.x == 0 && blockIdx.x == 0) next = step_prefetch(p.scalars, p.bc_table, p.bc_len);
+  const int tid = threadIdx.x, m0 = blockIdx.x * 16;  // tiles_n == 1: workgroup b owns strip b
+  // the row's targets or label, loaded before the product
+  const int rm = min(m0 + tid, p.B - 1);
+  float y[16];
+  int lab = 0;
+  if (tid < 16) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) y[j] = p.loss == VOLTA_LOSS_MSE ? p.y[(size_t)rm * p.N + min(j, p.N - 1)] : 0.0f;
+    if (p.loss != VOLTA_LOSS_MSE) lab = p.labels[rm];
+  }
+  SmallHead hd;
+  hd.zrows = zrows;
+  smallm_tile<false, VEC, EPI_ROWS, 16>(args, blockIdx.x, lds, hd);
+  __syncthreads();
+  if (tid < 16) {
+    float z[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) z[j] = zrows[tid * 17 + min(j, p.N - 1)];
+    row_loss[tid] = m0 + tid < p.B ? head_row<16>(p, z, y, lab, m0 + tid) : 0.0f;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    const int rows = min(16, p.B - m0);
+    float s = row_loss[0];
+    for (int r = 1; r < rows; ++r) s = s + row_loss[r];
+    p.partials[blockIdx.x] = s;
+    if (blockIdx.x == 0 && p.bc_table) {
+      p.scalars->t = next.t;
+      p.scalars->bc1 = next.bc.x;
+      p.scalars->bc2 = next.bc.y;
+    }
+  }
 }
 
 // A forward product over two halves of its K (a grid of at most half a
@@ -2441,6 +2492,20 @@ hipError_t launch_smallm_tail(const GemmPlan& p, const GemmArgs& args_in, const 
   const dim3 grid(((a.M + 15) / 16) * ((a.N + 15) / 16));
   if (o.dx_pre) hipLaunchKernelGGL(gemm_smallm_tail<true>, grid, dim3(1024), 0, st, a, o);
   else hipLaunchKernelGGL(gemm_smallm_tail<false>, grid, dim3(1024), 0, st, a, o);
+  return hipGetLastError();
+}
+
+bool out_head_gemm_supported(const GemmArgs& a, const OutLayerArgs& o) {
+  return o.N >= 1 && o.N <= 16 && o.B == a.M && o.N == a.N && o.K == a.K && a.M > 0 && o.partials && o.scalars &&
+         o.out && o.delta && a.epi.bias && (o.loss == VOLTA_LOSS_MSE ? o.y != nullptr : o.labels != nullptr) &&
+         a.ldb == o.N && a.lda == o.K;
+}
+
+hipError_t launch_smallm_out_head(const GemmArgs& a, const OutLayerArgs& o, hipStream_t st) {
+  if (!out_head_gemm_supported(a, o)) return hipErrorInvalidValue;
+  const dim3 grid((a.M + 15) / 16);
+  if (smallm_vec_ok(a, GEMM_NN)) hipLaunchKernelGGL(gemm_smallm_out_head<true>, grid, dim3(1024), 0, st, a, o);
+  else hipLaunchKernelGGL(gemm_smallm_out_head<false>, grid, dim3(1024), 0, st, a, o);
   return hipGetLastError();
 }
 

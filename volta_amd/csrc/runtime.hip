@@ -120,6 +120,7 @@ struct Handle {
   bool fwd_head = false;      // ... and that launch folded into the last hidden forward launch (opt-in)
   bool tail_merge = false;    // ... or that launch and dX_{n-2} in one (gemm_smallm_tail; VOLTA_NO_TAIL=1: off)
   bool narrow_dw = false;     // dW of the output layer by narrow_dw_kernel
+  bool out_mfma = false;      // large batch: the narrow output layer on small-M tiles, its loss summed by dX_{n-1}
   std::vector<int> fwd_khalf; // per layer: > 0 runs its forward over two halves of K (this one first),
                               // its output formed by the next forward launch (0: one launch)
   bool keep_grads = false;    // also store dW/db in `grads` (VOLTA_KEEP_GRADS=1)
@@ -447,6 +448,23 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
     const LayerPlan& lp = h->layers[i];
     const bool last = i == n - 1;
     if (last && head_done) continue;
+    if (last && h->out_mfma) {
+      GemmArgs a{};
+      base_args(a);
+      a.A = h->act[i];
+      a.lda = lp.r;
+      a.B = h->params + lp.w_off;
+      a.ldb = lp.c;
+      a.M = B;
+      a.N = lp.c;
+      a.K = lp.r;
+      a.epi.kind = EPI_ROWS;
+      a.epi.bias = h->params + lp.b_off;
+      VOLTA_CHECK(launch_smallm_out_head(a, out_args(), st));
+      std::snprintf(label, sizeof label, "fwd%d+loss", i);
+      VOLTA_CHECK(mark(rec, label, 2.0 * B * lp.r * lp.c, out_bytes()));
+      continue;
+    }
     if (last && h->out_mode == OUT_NARROW) {
       const OutLayerArgs o = out_args();
       const double fb = out_bytes();
@@ -713,8 +731,15 @@ static bool enqueue_step(Handle* h, hipStream_t st, Recorder* rec = nullptr) {
     const LayerPlan& lp = h->layers[i];
     std::snprintf(lx, sizeof lx, "dx%d", i);
     if (h->narrow_dx) {
+      LossDefer ld;
+      if (h->out_mfma) {  // the step's loss from the output launch's strip partials
+        ld.partials = h->loss_partials;
+        ld.blocks = (B + 15) / 16;
+        ld.denom = s.loss == VOLTA_LOSS_MSE ? (float)(B * Ln) : (float)B;
+        ld.scalars = h->scalars;
+      }
       VOLTA_CHECK(launch_outer_dx(h->delta[i], h->params + lp.w_off, B, lp.r, lp.c, s.activation, h->act[i],
-                                  h->pre[i - 1], h->delta[i - 1], st));
+                                  h->pre[i - 1], h->delta[i - 1], st, ld));
       VOLTA_CHECK(mark(rec, lx, dx_cost(i).first, dx_cost(i).second));
     } else if (!run_single(make_dx(i, ws0), lx, dx_cost(i))) {
       return false;
@@ -894,6 +919,16 @@ static bool build(Handle* h) {
   const char* nt = std::getenv("VOLTA_NO_TAIL");
   h->tail_merge = h->out_dx_merged && !h->fwd_head && Ln == 1 && n >= 3 && !(nt && *nt && *nt != '0');
   h->narrow_dw = Ln <= 16 && B <= kNarrowMaxB;
+  // A narrow output layer of more rows than the one-launch output kernels
+  // take (C5: 4096 rows of 10 classes) runs on MFMA, one 16-row strip per
+  // 16-wave small-M workgroup, with each row's loss head after the product;
+  // the strips' loss partials are added by the outer-product dX_{n-1}
+  // launch that follows (no loss launch of its own).  The wave dot
+  // products of out_layer_kernel plus the loss launch took 28.7 us at C5.
+  // VOLTA_OUT_MFMA=0 keeps them.
+  const char* om = std::getenv("VOLTA_OUT_MFMA");
+  h->out_mfma = h->out_mode == OUT_NARROW && !h->extras() && h->narrow_dx && !h->out_dx_merged &&
+                out_layer_blocks(B) > 1 && !(om && *om == '0');
   size_t ws_floats = 0;
   int max_tiles = 1;
   for (int i = 0; i < n; ++i) {

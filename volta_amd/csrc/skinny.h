@@ -64,8 +64,18 @@ hipError_t launch_out_layer(const OutLayerArgs& p, hipStream_t st);
 int out_layer_dx_blocks(int B);
 bool out_layer_dx_supported(int B, int K, int N);
 hipError_t launch_out_layer_dx(const OutLayerArgs& p, hipStream_t st);
+// The step's loss from the per-strip partials an earlier output launch
+// stored (launch_smallm_out_head), added by block (0, 0) of a later launch
+// in a fixed order (a tree over each 256 strips, the chunks in order); its
+// non-finite flag likewise.  partials == null: none.
+struct LossDefer {
+  const float* partials = nullptr;
+  int blocks = 0;
+  float denom = 1.0f;
+  DevScalars* scalars = nullptr;
+};
 hipError_t launch_outer_dx(const float* delta, const float* W, int B, int R, int K, int act, const float* aux_act,
-                           const float* aux_pre, float* out, hipStream_t st);
+                           const float* aux_pre, float* out, hipStream_t st, const LossDefer& ld = LossDefer{});
 hipError_t launch_narrow_dw(const NarrowDwArgs& p, hipStream_t st);
 
 }  // namespace volta

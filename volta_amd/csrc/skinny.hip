@@ -220,7 +220,8 @@ hipError_t launch_out_layer_dx(const OutLayerArgs& p, hipStream_t st) {
 template <int KMAX, int RB>
 __global__ void __launch_bounds__(256)
 outer_dx_kernel(const float* __restrict__ delta, const float* __restrict__ W, int B, int R, int K, int act,
-                const float* __restrict__ aux_act, const float* __restrict__ aux_pre, float* __restrict__ out) {
+                const float* __restrict__ aux_act, const float* __restrict__ aux_pre, float* __restrict__ out,
+                LossDefer ld) {
   static_assert(RB * KMAX <= 256, "one staged delta per thread");
   __shared__ float sd[RB * KMAX];
   const int t = threadIdx.x;
@@ -231,6 +232,10 @@ outer_dx_kernel(const float* __restrict__ delta, const float* __restrict__ W, in
 #pragma unroll
   for (int k = 0; k < KMAX; ++k) wv[k] = W[(size_t)jc * K + min(k, K - 1)];
   const float* pp = aux_pre ? aux_pre : aux_act;
+  // block (0, 0) also forms the step's loss (below): its first 256 partials
+  // are loaded now, so their latency runs under the block's products
+  const bool loss_block = ld.partials && blockIdx.x == 0 && blockIdx.y == 0;  // block-uniform
+  const float p0 = loss_block ? ld.partials[min(t, ld.blocks - 1)] : 0.0f;
   float y[RB], pr[RB];
 #pragma unroll
   for (int r = 0; r < RB; ++r) {
@@ -249,6 +254,28 @@ outer_dx_kernel(const float* __restrict__ delta, const float* __restrict__ W, in
       s = k < K ? u : s;
     }
     if (j < R && b0 + r < B) out[(size_t)(b0 + r) * R + j] = s * act_derivative(act, pr[r], y[r]);
+  }
+  if (loss_block) {
+    // the step's loss: the output launch's strip partials, 256 at a time
+    // (one per thread), each chunk added as a fixed tree (wave butterflies,
+    // then the four waves in order), the chunks in order
+    __shared__ float wsum[4];
+    float sum = 0.0f;
+    for (int c = 0; c < ld.blocks; c += 256) {
+      float v = c == 0 ? p0 : ld.partials[min(c + t, ld.blocks - 1)];
+      v = c + t < ld.blocks ? v : 0.0f;
+      v = wave_sum(v);
+      __syncthreads();
+      if ((t & 63) == 0) wsum[t >> 6] = v;
+      __syncthreads();
+      const float cs = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+      sum = c == 0 ? cs : sum + cs;
+    }
+    if (t == 0) {
+      const float loss = sum / ld.denom;
+      ld.scalars->loss = loss;
+      if (!(fabsf(loss) <= 3.402823466e38f)) atomicOr(&ld.scalars->flags, (uint32_t)VOLTA_STATUS_NONFINITE_LOSS);
+    }
   }
 }
 
@@ -288,24 +315,26 @@ hipError_t launch_out_layer(const OutLayerArgs& p, hipStream_t st) {
 
 template <int KMAX>
 static void launch_outer_k(bool big, dim3 blocks, hipStream_t st, const float* delta, const float* W, int B, int R,
-                           int K, int act, const float* aux_act, const float* aux_pre, float* out) {
+                           int K, int act, const float* aux_act, const float* aux_pre, float* out,
+                           const LossDefer& ld) {
   if (big)
     hipLaunchKernelGGL((outer_dx_kernel<KMAX, 16>), blocks, dim3(256), 0, st, delta, W, B, R, K, act, aux_act,
-                       aux_pre, out);
+                       aux_pre, out, ld);
   else
     hipLaunchKernelGGL((outer_dx_kernel<KMAX, 1>), blocks, dim3(256), 0, st, delta, W, B, R, K, act, aux_act,
-                       aux_pre, out);
+                       aux_pre, out, ld);
 }
 
 hipError_t launch_outer_dx(const float* delta, const float* W, int B, int R, int K, int act, const float* aux_act,
-                           const float* aux_pre, float* out, hipStream_t st) {
+                           const float* aux_pre, float* out, hipStream_t st, const LossDefer& ld) {
   if (K > 16 || K < 1) return hipErrorInvalidValue;
+  if (ld.partials && (ld.blocks < 1 || !ld.scalars)) return hipErrorInvalidValue;
   // 16 batch rows per block once the layer has a million outputs
   const bool big = (size_t)B * R >= ((size_t)1 << 20);
   const dim3 blocks((R + 255) / 256, (B + (big ? 16 : 1) - 1) / (big ? 16 : 1));
-  if (K <= 1) launch_outer_k<1>(big, blocks, st, delta, W, B, R, K, act, aux_act, aux_pre, out);
-  else if (K <= 4) launch_outer_k<4>(big, blocks, st, delta, W, B, R, K, act, aux_act, aux_pre, out);
-  else launch_outer_k<16>(big, blocks, st, delta, W, B, R, K, act, aux_act, aux_pre, out);
+  if (K <= 1) launch_outer_k<1>(big, blocks, st, delta, W, B, R, K, act, aux_act, aux_pre, out, ld);
+  else if (K <= 4) launch_outer_k<4>(big, blocks, st, delta, W, B, R, K, act, aux_act, aux_pre, out, ld);
+  else launch_outer_k<16>(big, blocks, st, delta, W, B, R, K, act, aux_act, aux_pre, out, ld);
   return hipGetLastError();
 }
 
