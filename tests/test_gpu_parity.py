@@ -214,6 +214,22 @@ def test_gemm_big128_tile_unaligned_output(layout):
     np.testing.assert_array_equal(got[1:].reshape(M, N), aligned)
 
 
+TILE_NARROW_TN = 7
+
+
+@pytest.mark.parametrize("M,N,K", [(1024, 10, 4096), (256, 1, 1024), (200, 3, 1000), (64, 16, 300), (130, 7, 257)])
+def test_gemm_narrow_tn_integer_exact(M, N, K):
+    """The narrow TN product with a long K (the output layer's dW at a large
+    batch: 64 rows per workgroup over K slices, then the reduce launch):
+    exact on integer operands, ragged M and K included."""
+    say(f"gemm narrow TN M={M} N={N} K={K}")
+    rng = np.random.default_rng(M + 7 * N + 11 * K)
+    A = rng.integers(-4, 5, (K, M)).astype(np.float32)
+    B = rng.integers(-4, 5, (K, N)).astype(np.float32)
+    got = _gemm(2, A, B, M, N, K, tile=TILE_NARROW_TN)
+    np.testing.assert_array_equal(got, (A.T.astype(np.int64) @ B.astype(np.int64)).astype(np.float32))
+
+
 def test_gemm_big128_tile_rejects_inexact_shapes():
     """Shapes the tile does not serve exactly are refused on the host (no
     launch): M or N not a multiple of 128, K not a multiple of 128."""

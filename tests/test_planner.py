@@ -12,7 +12,7 @@ from volta_amd import HIP_LIB, load_hip
 pytestmark = pytest.mark.skipif(not os.path.exists(HIP_LIB), reason="libvolta_hip.so not built")
 
 NN, NT, TN = 0, 1, 2
-TILE_64, TILE_128, TILE_SMALLM, TILE_DW_SMALLK, TILE_BIG, TILE_BIG128 = 0, 1, 3, 4, 5, 6
+TILE_64, TILE_128, TILE_SMALLM, TILE_DW_SMALLK, TILE_BIG, TILE_BIG128, TILE_NARROW_TN = 0, 1, 3, 4, 5, 6, 7
 CUS = 256
 
 
@@ -111,3 +111,16 @@ def test_planner_rejects_bad_arguments():
     assert lib.lib.volta_hip_gemm_plan(7, 64, 64, 64, 1, CUS, 1, out) == -1
     assert lib.lib.volta_hip_gemm_plan(NN, 0, 64, 64, 1, CUS, 1, out) == -1
     assert "volta_hip_gemm_plan" in lib.last_error()
+
+
+def test_narrow_tn_for_long_k():
+    """The output layer's dW at a large batch (N <= 16, K > 256): 64 rows of
+    the product per workgroup over K slices of at most 128, halved down to
+    32 until the grid has two workgroups per CU: C5's dW_3 (1024 x 10 x 4096)
+    in 32 slices of 128, C4 B=1024's dW_4 (256 x 1 x 1024) in 32 of 32; a
+    short K keeps the other tiles, and VOLTA_NARROW_TN=0 the 64x64 ones."""
+    assert plan(TN, 1024, 10, 4096) == (TILE_NARROW_TN, 32, 128, 1, 0)
+    assert plan(TN, 256, 1, 1024) == (TILE_NARROW_TN, 32, 32, 1, 0)
+    assert plan(TN, 64, 1, 256)[0] == TILE_64
+    assert plan(TN, 1024, 10, 4096, env={"VOLTA_NARROW_TN": "0"})[0] == TILE_64
+    assert plan(TN, 1024, 17, 4096)[0] != TILE_NARROW_TN

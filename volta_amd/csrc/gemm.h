@@ -82,9 +82,11 @@ struct GemmArgs {
 // CU, for exact 256-multiples with at least one tile per CU (C5's 4096 x 4096
 // products).  TILE_BIG128: the same pipeline on 128x128 tiles, for exact
 // 128-multiples whose 128x128 grid has a tile per CU and whose 256x256 grid
-// does not (C5's 4096 x 1024 and 1024 x 4096 products).
+// does not (C5's 4096 x 1024 and 1024 x 4096 products).  TILE_NARROW_TN: a
+// TN product of at most 16 columns with a long K (the output layer's dW at
+// a large batch), 64 rows per workgroup, K split, then the reduce launch.
 enum GemmTile { TILE_64x64 = 0, TILE_128x128 = 1, TILE_64x64_K64 = 2, TILE_SMALLM = 3, TILE_DW_SMALLK = 4,
-                TILE_BIG = 5, TILE_BIG128 = 6 };
+                TILE_BIG = 5, TILE_BIG128 = 6, TILE_NARROW_TN = 7 };
 
 struct GemmPlan {
   int layout = GEMM_NN;
@@ -106,6 +108,9 @@ struct GemmPlan {
 // Tile and split-K plan of one product.  `small_m`: the small-M tile may be
 // chosen (NN/NT products whose epilogue is per element: not the loss head).
 GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus, bool small_m = true);
+// TILE_NARROW_TN's K slice (a multiple of 4, at most 128) and split count
+// for an M x N x K product on num_cus CUs.
+void narrow_tn_split_plan(int M, int K, int num_cus, int* k_per_split, int* splits);
 
 // Waves per workgroup of a small-M product of M x N outputs: 4 when it runs
 // in a 256-thread paired launch, else by the grid's size (16, 8 or 4).

@@ -2157,6 +2157,92 @@ __global__ void __launch_bounds__(256) gemm_dw_smallk(GemmArgs args) {
   dw_smallk_tile<EPI>(args, blockIdx.x, lds, threadIdx.x);
 }
 
+// ---------------------------------------------------------------------------
+// Narrow TN product with a long reduction (TILE_NARROW_TN: the output
+// layer's dW at a large batch, N = L_n <= 16 columns, K = B rows of the
+// batch), where a 64x64 MFMA tile would be mostly padding on a grid of a few
+// dozen workgroups.  Workgroup (mb, z) owns rows m0..m0+63 of the product
+// (lane m of every wave) over K slice z: the slice's B rows (delta) are
+// staged in LDS, wave w adds the products of slice rows w, w + 4, w + 8, ...
+// in order (every A load of them issued first: one per row, 64 lanes on 256
+// consecutive bytes of act), and the four waves' sums are added
+// (w0 + w1) + (w2 + w3) into plane z of the split-K workspace; with a bias,
+// the slice's column sums of B (rows in order) go to the plane's row M.
+// splitk_reduce then adds the planes in order and runs the epilogue.
+constexpr int kNarrowTnK = 128;  // largest slice
+template <int NMAX>
+__global__ void __launch_bounds__(256) narrow_tn_split(GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) float sd[kNarrowTnK * NMAX];
+  __shared__ float red[3][64 * NMAX];
+  constexpr int PER = kNarrowTnK / 4;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int M = a.M, N = a.N;
+  const int m0 = blockIdx.x * 64, z = blockIdx.y;
+  const int k0 = z * a.k_per_split, nk = min(a.k_per_split, a.K - k0);
+  const int mc = min(m0 + lane, M - 1);
+  float av[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int kk = min(w + 4 * i, nk - 1);
+    av[i] = a.A[(size_t)(k0 + kk) * a.lda + mc];
+  }
+  for (int i = t; i < nk * NMAX; i += 256) {
+    const int kk = i / NMAX, n = i % NMAX;
+    sd[i] = a.B[(size_t)(k0 + kk) * a.ldb + min(n, N - 1)];
+  }
+  __syncthreads();
+  float acc[NMAX];
+#pragma unroll
+  for (int j = 0; j < NMAX; ++j) acc[j] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int kk = w + 4 * i;
+    if (kk < nk) {  // wave-uniform
+      // the row's B values: one broadcast read per four columns
+      float bv[NMAX];
+      if constexpr (NMAX % 4 == 0) {
+#pragma unroll
+        for (int q = 0; q < NMAX / 4; ++q) {
+          const floatx4 v = *reinterpret_cast<const floatx4*>(sd + kk * NMAX + 4 * q);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bv[4 * q + e] = v[e];
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < NMAX; ++j) bv[j] = sd[kk * NMAX + j];
+      }
+#pragma unroll
+      for (int j = 0; j < NMAX; ++j) acc[j] = acc[j] + av[i] * bv[j];
+    }
+  }
+  if (w > 0) {
+#pragma unroll
+    for (int j = 0; j < NMAX; ++j) red[w - 1][lane * NMAX + j] = acc[j];
+  }
+  __syncthreads();
+  float* plane = a.partial + (size_t)z * (M + 1) * N;
+  if (w == 0 && m0 + lane < M) {
+#pragma unroll
+    for (int j = 0; j < NMAX; ++j)
+      if (j < N)
+        plane[(size_t)(m0 + lane) * N + j] =
+            (acc[j] + red[0][lane * NMAX + j]) + (red[1][lane * NMAX + j] + red[2][lane * NMAX + j]);
+  }
+  if (a.colsum_b && blockIdx.x == 0 && w == 1 && lane < N) {
+    float cs = sd[lane];
+    for (int kk = 1; kk < nk; ++kk) cs = cs + sd[kk * NMAX + lane];
+    plane[(size_t)M * N + lane] = cs;
+  }
+}
+
+void narrow_tn_split_plan(int M, int K, int num_cus, int* k_per_split, int* splits) {
+  const int mb = (M + 63) / 64;
+  int kps = kNarrowTnK;
+  while (kps > 32 && (size_t)mb * ((K + kps - 1) / kps) < (size_t)2 * num_cus) kps /= 2;
+  *k_per_split = kps;
+  *splits = (K + kps - 1) / kps;
+}
+
 // Planes whose loads splitk_reduce issues together (more planes: a loop).
 constexpr int kReduceUnroll = 16;
 
@@ -2621,6 +2707,26 @@ hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& args_in, hipStream_t s
     if ((err = launch_big128(a, p.layout, st)) != hipSuccess) return err;
     return mark(rec, label, 2.0 * a.M * a.N * a.K, bytes);
   }
+  if (p.tile == TILE_NARROW_TN) {
+    // K slices of at most kNarrowTnK rows into the planes, then the reduce
+    const bool ok = p.layout == GEMM_TN && a.N >= 1 && a.N <= 16 && p.splits >= 2 && a.partial &&
+                    p.k_per_split >= 1 && p.k_per_split <= kNarrowTnK && p.k_per_split % 4 == 0 &&
+                    (size_t)(p.splits - 1) * p.k_per_split < (size_t)a.K &&
+                    (size_t)p.splits * p.k_per_split >= (size_t)a.K &&
+                    (a.epi.kind == EPI_DW_OPT || a.epi.kind == EPI_STORE);
+    if (!ok) return hipErrorInvalidValue;
+    const dim3 grid((a.M + 63) / 64, p.splits);
+    if (a.N <= 1) hipLaunchKernelGGL(narrow_tn_split<1>, grid, dim3(256), 0, st, a);
+    else if (a.N <= 4) hipLaunchKernelGGL(narrow_tn_split<4>, grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(narrow_tn_split<16>, grid, dim3(256), 0, st, a);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    if ((err = mark(rec, label, 2.0 * a.M * a.N * a.K, bytes)) != hipSuccess) return err;
+    err = a.epi.kind == EPI_DW_OPT ? launch_reduce<EPI_DW_OPT>(a, p.splits, st) : launch_reduce<EPI_STORE>(a, p.splits, st);
+    if (err != hipSuccess) return err;
+    const double t = (double)a.M * a.N;
+    return mark(rec, std::string(label) + ".splitk_reduce", (double)p.splits * t,
+                4.0 * ((double)p.splits * t + 2.0 * t));
+  }
   if (p.tile == TILE_DW_SMALLK) {
     if (p.splits != 1 || !dw_smallk_ok(a, p.layout)) return hipErrorInvalidValue;
     const dim3 grid(p.tiles(a.M, a.N));
@@ -3044,6 +3150,17 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus, bool 
     p.tile = TILE_DW_SMALLK;
     p.splits = 1;
     p.k_per_split = K;
+  }
+  // A narrow TN product (N <= 16) with a long K: 64 rows of the product per
+  // workgroup over K slices (TILE_NARROW_TN) and the reduce launch, instead
+  // of 64x64 MFMA tiles that are at least 3/4 padding (the output layer's
+  // dW of C4 B=1024 and C5).  VOLTA_NARROW_TN=0 keeps the 64x64 tiles.
+  const char* nt = std::getenv("VOLTA_NARROW_TN");
+  if (layout == GEMM_TN && N <= 16 && K > 256 && p.tile != TILE_DW_SMALLK && !(nt && *nt == '0')) {
+    p.tile = TILE_NARROW_TN;
+    p.kgroups = 1;
+    p.inkernel_reduce = false;
+    narrow_tn_split_plan(M, K, num_cus, &p.k_per_split, &p.splits);  // K > 256: at least 3 slices
   }
   // K groups (gemm_tile's KG): a split of up to 2 slices (4 on the 64x64
   // tile but for dW) runs inside one workgroup instead, the slices on groups

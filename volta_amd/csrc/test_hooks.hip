@@ -78,7 +78,7 @@ int32_t volta_hip_gemm(int32_t layout, const float* A, const float* B, float* Cm
   const int contig_b = layout == GEMM_NT ? K : N;
   const bool vec = contig_a % 4 == 0 && contig_b % 4 == 0;
   GemmPlan p = gemm_plan(layout, M, N, K, vec, cus);
-  if (force_tile > TILE_BIG128) {
+  if (force_tile > TILE_NARROW_TN) {
     set_last_error("volta_hip_gemm: unknown tile");
     return -1;
   }
@@ -97,6 +97,7 @@ int32_t volta_hip_gemm(int32_t layout, const float* A, const float* B, float* Cm
     p.splits = 1;
     p.k_per_split = K;
   }
+  if (force_tile == TILE_NARROW_TN) narrow_tn_split_plan(M, K, cus, &p.k_per_split, &p.splits);
   if (force_splits != 0) {
     const int g = force_splits > 0 ? force_splits : -force_splits;
     int kps = (K + g - 1) / g;
