@@ -134,6 +134,26 @@ def test_gemm_smallm_8_waves_integer_exact(layout, M, N, K, waves):
     np.testing.assert_array_equal(got, (A.astype(np.int64) @ Bm.astype(np.int64)).astype(np.float32))
 
 
+@pytest.mark.parametrize("M,N,K", [(64, 1024, 1024), (64, 512, 512), (48, 80, 1000), (33, 130, 260)])
+def test_gemm_smallm_nt_16_waves_integer_exact(M, N, K):
+    """The 16-wave small-M NT (dX) workgroup, as the small-batch step runs
+    its dX products: exact on integer operands, ragged shapes included."""
+    say(f"gemm small-M NT 16 waves M={M} N={N} K={K}")
+    rng = np.random.default_rng(M * 3 + N + K)
+    A = rng.integers(-4, 5, (M, K)).astype(np.float32)
+    B = rng.integers(-4, 5, (N, K)).astype(np.float32)
+    old = os.environ.get("VOLTA_SMALLM_WAVES")
+    os.environ["VOLTA_SMALLM_WAVES"] = "16"
+    try:
+        got = _gemm(1, A, B, M, N, K, tile=TILE_SMALLM)
+    finally:
+        if old is None:
+            os.environ.pop("VOLTA_SMALLM_WAVES", None)
+        else:
+            os.environ["VOLTA_SMALLM_WAVES"] = old
+    np.testing.assert_array_equal(got, (A.astype(np.int64) @ B.T.astype(np.int64)).astype(np.float32))
+
+
 TILE_BIG = 5
 
 

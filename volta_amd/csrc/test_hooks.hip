@@ -88,10 +88,12 @@ int32_t volta_hip_gemm(int32_t layout, const float* A, const float* B, float* Cm
     p.splits *= p.kgroups;
     p.kgroups = 1;
   }
+  const char* sw = std::getenv("VOLTA_SMALLM_WAVES");
   if (p.tile == TILE_SMALLM && p.waves == 0) {  // forced onto a shape planned otherwise
-    const char* w = std::getenv("VOLTA_SMALLM_WAVES");
-    p.waves = layout == GEMM_NT || (w && std::atoi(w) == 4) ? 4 : (w && std::atoi(w) == 16) ? 16 : 8;
+    p.waves = layout == GEMM_NT || (sw && std::atoi(sw) == 4) ? 4 : (sw && std::atoi(sw) == 16) ? 16 : 8;
   }
+  // a dX product as the small-batch step runs it (16 waves) on request
+  if (p.tile == TILE_SMALLM && layout == GEMM_NT && sw && std::atoi(sw) == 16) p.waves = 16;
   if (force_tile == TILE_SMALLM || force_tile == TILE_DW_SMALLK || force_tile == TILE_BIG ||
       force_tile == TILE_BIG128) {  // whole K in each workgroup
     p.splits = 1;
