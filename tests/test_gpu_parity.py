@@ -962,6 +962,30 @@ def test_graph_replay_bit_identical_to_direct_launches(name):
         np.testing.assert_array_equal(a, b)
 
 
+STAGE_CASES = {
+    # 16-wave small-M launches with their operands staged in LDS (the
+    # default) against the register path: C2 (every forward and dX launch
+    # at 16 waves), C1, and a ragged batch with a kept pre-activation
+    "c2": (MlpSpec([512, 1024, 1024, 512, 256, 1], "relu", "adam"), 64, 1e-3),
+    "c1": (MlpSpec([256, 512, 512, 256, 1], "relu", "sgd"), 64, 0.01),
+    "ragged_gelu": (MlpSpec([96, 528, 512, 200, 3], "gelu", "adam"), 48, 1e-3),
+}
+
+
+@pytest.mark.parametrize("name", sorted(STAGE_CASES))
+def test_staged_small_m_operands_bit_identical(name):
+    """The small-M tile with its operands staged in LDS by direct-to-LDS
+    loads gives the register path's bits (VOLTA_SMALLM_STAGE=0): losses,
+    parameters, activations and deltas after 4 steps."""
+    spec, B, lr = STAGE_CASES[name]
+    say(f"staged small-M operands vs registers {name}")
+    l1, p1, b1 = _run_with_env({"VOLTA_SMALLM_STAGE": "0"}, spec, B, lr, 4)
+    l2, p2, b2 = _run_with_env({"VOLTA_SMALLM_STAGE": "1"}, spec, B, lr, 4)
+    np.testing.assert_array_equal(l1, l2)
+    for a, b in zip(p1 + b1, p2 + b2):
+        np.testing.assert_array_equal(a, b)
+
+
 KHALF_BITS_CASES = {
     # the hidden forward product over two halves of K (VOLTA_FWD_SPLIT=1):
     # C2's fwd2 -> fwd3 and C1's fwd1 -> fwd2, whose halves are whole wave

@@ -97,6 +97,7 @@ struct GemmPlan {
   bool inkernel_reduce = false;  // split-K reduced by the last slice (else a second kernel)
   int waves = 0;                 // TILE_SMALLM: waves per workgroup (4 or 8)
   int kgroups = 1;               // 64x64 / 128x128: K slices inside one workgroup (splits = 1)
+  bool stage = true;             // TILE_SMALLM at 16 waves: operands staged in LDS (VOLTA_SMALLM_STAGE=0: off)
   int tiles(int M, int N) const {
     const int t = tile == TILE_BIG ? 256 : tile == TILE_128x128 || tile == TILE_BIG128 ? 128 : tile == TILE_SMALLM ? 16
                   : tile == TILE_DW_SMALLK ? 32 : 64;

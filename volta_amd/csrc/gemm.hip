@@ -1380,6 +1380,7 @@ static bool big_tile_fits(int layout, int M, int N, int K, bool vec, int num_cus
 // order, with shorter rounding chains than one running sum.
 // ---------------------------------------------------------------------------
 constexpr int kSmallChunk = 16;    // 16-k groups per register chunk (256 k)
+constexpr int kSmallStage = 16 * 64;  // floats of one staged operand strip (16 rows x 64 k)
 constexpr int kSmallRedStride = 80;  // LDS floats per (wave, register) row of partials
 template <int NW>
 struct SmallLds {
@@ -1438,9 +1439,25 @@ struct SmallNoop {
 // after its first chunk's loads are issued and before any product term (the
 // row deltas hd.d are read after it), and `post` once, after the tile's last
 // barrier.
-template <bool B_KC, bool VEC, int EPI, int NW, int AH = 0, class Pre = SmallNoop, class Post = SmallNoop>
+//
+// STG = SW > 0 (16 waves, 16-byte rows, AH == 0): the A strip of each
+// wave's chunk, SW k wide (and the B strip of an NT product), goes to a
+// wave-private LDS area `stg` (kSmallStage floats per operand and wave) by
+// direct-to-LDS loads whose lanes cover 256/SW rows x 4*SW contiguous bytes
+// per instruction, and the MFMA fragments are read from there (16-byte
+// chunk (r, c) of a strip at r*SW/4 + (c ^ (r % (SW/4))): conflict-free
+// reads of 8 rows at one k-quad).  A load instruction of the register path
+// covers 16 rows x 64 bytes, which the memory pipeline serves measurably
+// slower.  SW = 32 only for a wave range of at most 32 k (one chunk, two
+// groups).  Same operands, same order: bit-identical to the register path.
+template <bool B_KC, bool VEC, int EPI, int NW, int AH = 0, class Pre = SmallNoop, class Post = SmallNoop,
+          int SW = 0>
 __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float* lds,
-                                            const SmallHead& hd = SmallHead{}, Pre pre = Pre{}, Post post = Post{}) {
+                                            const SmallHead& hd = SmallHead{}, Pre pre = Pre{}, Post post = Post{},
+                                            float* stg = nullptr) {
+  constexpr bool STG = SW > 0;
+  static_assert(SW == 0 || SW == 32 || SW == 64, "staged strips 32 or 64 k wide");
+  static_assert(!STG || (VEC && NW == 16 && AH == 0), "staged operands: 16 waves, 16-byte rows, no head operand");
   static_assert(NW == 4 || NW == 8 || NW == 16, "wave trees for 4, 8 or 16 partial tiles");
   static_assert(AH == 0 || AH == 3 || (B_KC && VEC && EPI == EPI_DX_ACT && NW == 16),
                 "head operand: NT dX product, 16-byte rows, 16 waves");
@@ -1592,6 +1609,55 @@ __device__ __forceinline__ void smallm_tile(const GemmArgs& args, int blk, float
       if (kc + 16 * CH < kend) store_a(kc);
       else last_kc = kc;
     }
+  } else if constexpr (STG) {
+    // this wave's strips: 16 rows x SW k each (SW / 16 groups of 16 k; with
+    // SW = 32 the wave's range is one chunk of at most 32 k, so compute()
+    // stops after group 1)
+    static_assert(CH == 4, "a chunk is 64 k");
+    constexpr int LPR = SW / 4;    // lanes (16-byte chunks) per strip row
+    constexpr int RPI = 64 / LPR;  // strip rows per load instruction
+    float* sa = stg + wave * kSmallStage;
+    float* sb = stg + (NW + wave) * kSmallStage;
+    const float* ra = args.A;
+    const float* rb = args.B;
+    for (int kc = kbeg; kc < kend; kc += 16 * CH) {
+      // instruction i fills rows RPI*i..RPI*i+RPI-1: lane l takes row
+      // RPI*i + l/LPR and the k-quad whose swizzled slot is l % LPR; k
+      // clamped into the wave's range, rows outside the matrix read row 0
+      // (both masked at the MFMAs)
+#pragma unroll
+      for (int i = 0; i < 16 / RPI; ++i) {
+        const int rr = RPI * i + lane / LPR;
+        const int c = (lane % LPR) ^ (rr % LPR);
+        const int kl = min(kc + 4 * c, kend - 4);
+        const int ar = m0 + rr < M ? m0 + rr : 0;
+        __builtin_amdgcn_global_load_lds((const void*)(ra + (size_t)ar * lda + kl), (LdsVoidPtr)(sa + 256 * i), 16,
+                                         0, 0);
+        if constexpr (B_KC) {
+          const int br = n0 + rr < N ? n0 + rr : 0;
+          __builtin_amdgcn_global_load_lds((const void*)(rb + (size_t)br * ldb + kl), (LdsVoidPtr)(sb + 256 * i),
+                                           16, 0, 0);
+        }
+      }
+      if constexpr (!B_KC) {  // NN: the B operand's columns straight into registers
+#pragma unroll
+        for (int g = 0; g < CH; ++g) {
+          if (kc + 16 * g >= kend) break;
+          const int kl = min(kc + 16 * g + 4 * q, kend - 4);
+#pragma unroll
+          for (int s2 = 0; s2 < 4; ++s2) fb[g][s2] = pb[(size_t)(kl + s2) * ldb];
+        }
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int g = 0; g < SW / 16; ++g) {
+        if (kc + 16 * g >= kend) break;
+        const int slot = 4 * (r * LPR + ((4 * g + q) ^ (r % LPR)));
+        fa[g] = *reinterpret_cast<const floatx4*>(sa + slot);
+        if constexpr (B_KC) fb[g] = *reinterpret_cast<const floatx4*>(sb + slot);
+      }
+      compute(fa, fb, kc);
+    }
   } else {
     for (int kc = kbeg; kc < kend; kc += 16 * CH) {
       load(fa, fb, kc);
@@ -1643,6 +1709,26 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW
 gemm_smallm(GemmArgs args) {
   __shared__ float lds[SmallLds<NW>::kFloats];
   smallm_tile<B_KC, VEC, EPI, NW>(args, blockIdx.x, lds);
+}
+
+// 16 waves with staged operands (smallm_tile's STG), strips SW k wide:
+// 64 KB of LDS per operand staged (A; B too for the NT product).
+template <bool B_KC, int EPI, int SW>
+__global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4)))
+gemm_smallm_stg(GemmArgs args) {
+  __shared__ float lds[SmallLds<16>::kFloats];
+  __shared__ __attribute__((aligned(16))) float stg[(B_KC ? 32 : 16) * kSmallStage];
+  smallm_tile<B_KC, true, EPI, 16, 0, SmallNoop, SmallNoop, SW>(args, blockIdx.x, lds, SmallHead{}, SmallNoop{},
+                                                               SmallNoop{}, stg);
+}
+
+// Staged strip width of a 16-wave small-M launch: 64 k for wave ranges of
+// 48 k or more, 32 k for 32-k ranges, none (registers) for 16-k ranges, whose
+// register loads already cover a whole range per instruction.  (smallm_tile's
+// wave range: K / 16 rounded up to whole 16-k groups.)
+static int smallm_stage_width(int K) {
+  const int kq = (K + 255) / 256 * 16;
+  return kq >= 48 ? 64 : kq == 32 ? 32 : 0;
 }
 
 // The narrow output layer of a large batch on the small-M tile (one 16-row
@@ -2488,10 +2574,13 @@ static int smallm_waves(bool b_kc, int blocks, int num_cus) {
 }
 
 template <bool B_KC, int EPI>
-static hipError_t launch_smallm_epi(const GemmArgs& a, bool vec, int waves, hipStream_t st) {
+static hipError_t launch_smallm_epi(const GemmArgs& a, bool vec, int waves, bool stage, hipStream_t st) {
   const int blocks = ((a.M + 15) / 16) * ((a.N + 15) / 16);
   if (waves == 16) {
-    if (vec) hipLaunchKernelGGL((gemm_smallm<B_KC, true, EPI, 16>), dim3(blocks), dim3(1024), 0, st, a);
+    const int sw = vec && stage ? smallm_stage_width(a.K) : 0;
+    if (sw == 64) hipLaunchKernelGGL((gemm_smallm_stg<B_KC, EPI, 64>), dim3(blocks), dim3(1024), 0, st, a);
+    else if (sw == 32) hipLaunchKernelGGL((gemm_smallm_stg<B_KC, EPI, 32>), dim3(blocks), dim3(1024), 0, st, a);
+    else if (vec) hipLaunchKernelGGL((gemm_smallm<B_KC, true, EPI, 16>), dim3(blocks), dim3(1024), 0, st, a);
     else hipLaunchKernelGGL((gemm_smallm<B_KC, false, EPI, 16>), dim3(blocks), dim3(1024), 0, st, a);
   } else if (waves == 8) {
     if (vec) hipLaunchKernelGGL((gemm_smallm<B_KC, true, EPI, 8>), dim3(blocks), dim3(512), 0, st, a);
@@ -2521,17 +2610,17 @@ static bool dw_smallk_ok(const GemmArgs& a, int layout) {
   return (size_t)a.M * e.ldc < ((size_t)1 << 30);
 }
 
-static hipError_t launch_smallm(const GemmArgs& a, int layout, bool vec, int waves, hipStream_t st) {
+static hipError_t launch_smallm(const GemmArgs& a, int layout, bool vec, int waves, bool stage, hipStream_t st) {
   if (vec && !smallm_vec_ok(a, layout)) return hipErrorInvalidValue;
   if (waves != 4 && waves != 8 && waves != 16) return hipErrorInvalidValue;
   if (layout == GEMM_NT && waves == 16 && !vec) return hipErrorInvalidValue;
   const int k = a.epi.kind;
   if (layout == GEMM_NN) {
-    if (k == EPI_BIAS_ACT) return launch_smallm_epi<false, EPI_BIAS_ACT>(a, vec, waves, st);
-    if (k == EPI_STORE) return launch_smallm_epi<false, EPI_STORE>(a, vec, waves, st);
+    if (k == EPI_BIAS_ACT) return launch_smallm_epi<false, EPI_BIAS_ACT>(a, vec, waves, stage, st);
+    if (k == EPI_STORE) return launch_smallm_epi<false, EPI_STORE>(a, vec, waves, stage, st);
   } else if (layout == GEMM_NT) {
-    if (k == EPI_DX_ACT) return launch_smallm_epi<true, EPI_DX_ACT>(a, vec, waves, st);
-    if (k == EPI_STORE) return launch_smallm_epi<true, EPI_STORE>(a, vec, waves, st);
+    if (k == EPI_DX_ACT) return launch_smallm_epi<true, EPI_DX_ACT>(a, vec, waves, stage, st);
+    if (k == EPI_STORE) return launch_smallm_epi<true, EPI_STORE>(a, vec, waves, stage, st);
   }
   return hipErrorInvalidValue;
 }
@@ -2688,7 +2777,7 @@ hipError_t gemm_launch(const GemmPlan& p, const GemmArgs& args_in, hipStream_t s
   hipError_t err;
   if (p.tile == TILE_SMALLM) {
     if (p.splits != 1) return hipErrorInvalidValue;
-    if ((err = launch_smallm(a, p.layout, p.vec, p.waves, st)) != hipSuccess) return err;
+    if ((err = launch_smallm(a, p.layout, p.vec, p.waves, p.stage, st)) != hipSuccess) return err;
     return mark(rec, label, 2.0 * a.M * a.N * a.K, bytes);
   }
   if (p.tile == TILE_BIG) {
@@ -3069,6 +3158,10 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus, bool 
   GemmPlan p;
   p.layout = layout;
   p.vec = vec;
+  // 16-wave small-M launches stage their operands in LDS (smallm_tile's
+  // STG); VOLTA_SMALLM_STAGE=0 loads them straight into registers
+  const char* sg = std::getenv("VOLTA_SMALLM_STAGE");
+  p.stage = !(sg && *sg == '0');
   // 128x128 tiles only where there is enough K to amortise them (a short K,
   // dW at small batch, is epilogue bound and wants the 4x larger grid) and
   // where their grid has a tile per CU (M*N >= 256 * 128^2 = 4M outputs):
