@@ -2256,6 +2256,51 @@ __global__ void __launch_bounds__(256) gemm_dw_smallk(GemmArgs args) {
 // the slice's column sums of B (rows in order) go to the plane's row M.
 // splitk_reduce then adds the planes in order and runs the epilogue.
 constexpr int kNarrowTnK = 128;  // largest slice
+
+// sd[kk*NMAX + n] = B[(k0 + kk)*ldb + min(n, N-1)] for the slice's nk rows,
+// by the workgroup's 256 threads: load() issues every load, store() writes
+// them to LDS (split so that other loads can be issued in between; a loop
+// with a run-time trip count would wait for each load in turn).
+template <int NMAX>
+struct SliceStage {
+  static constexpr int IT = (kNarrowTnK * NMAX + 255) / 256;
+  float v[IT];
+  __device__ __forceinline__ void load(const float* B, int ldb, int k0, int nk, int N, int t) {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int i = min(t + 256 * it, nk * NMAX - 1);
+      const int kk = i / NMAX, n = i % NMAX;
+      v[it] = B[(size_t)(k0 + kk) * ldb + min(n, N - 1)];
+    }
+  }
+  __device__ __forceinline__ void store(float* sd, int nk, int t) const {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int i = t + 256 * it;
+      if (i < nk * NMAX) sd[i] = v[it];
+    }
+  }
+};
+
+// Column n of the staged slice summed in row order, sd[n] + sd[NMAX + n] +
+// ... (rows < nk), its LDS reads issued eight at a time.
+template <int NMAX>
+__device__ __forceinline__ float slice_colsum(const float* sd, int nk, int n) {
+  float cs = sd[n];
+#pragma unroll
+  for (int k1 = 1; k1 < kNarrowTnK; k1 += 8) {
+    float col[8];
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) col[kk] = sd[min(k1 + kk, kNarrowTnK - 1) * NMAX + n];
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const float u = cs + col[kk];
+      cs = k1 + kk < nk ? u : cs;
+    }
+  }
+  return cs;
+}
+
 template <int NMAX>
 __global__ void __launch_bounds__(256) narrow_tn_split(GemmArgs a) {
   __shared__ __attribute__((aligned(16))) float sd[kNarrowTnK * NMAX];
@@ -2266,16 +2311,17 @@ __global__ void __launch_bounds__(256) narrow_tn_split(GemmArgs a) {
   const int m0 = blockIdx.x * 64, z = blockIdx.y;
   const int k0 = z * a.k_per_split, nk = min(a.k_per_split, a.K - k0);
   const int mc = min(m0 + lane, M - 1);
+  // the slice's B rows first, then every A load: the products of row i
+  // wait only for the loads up to row i's
+  SliceStage<NMAX> stage;
+  stage.load(a.B, a.ldb, k0, nk, N, t);
   float av[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int kk = min(w + 4 * i, nk - 1);
     av[i] = a.A[(size_t)(k0 + kk) * a.lda + mc];
   }
-  for (int i = t; i < nk * NMAX; i += 256) {
-    const int kk = i / NMAX, n = i % NMAX;
-    sd[i] = a.B[(size_t)(k0 + kk) * a.ldb + min(n, N - 1)];
-  }
+  stage.store(sd, nk, t);
   __syncthreads();
   float acc[NMAX];
 #pragma unroll
@@ -2315,9 +2361,7 @@ __global__ void __launch_bounds__(256) narrow_tn_split(GemmArgs a) {
             (acc[j] + red[0][lane * NMAX + j]) + (red[1][lane * NMAX + j] + red[2][lane * NMAX + j]);
   }
   if (a.colsum_b && blockIdx.x == 0 && w == 1 && lane < N) {
-    float cs = sd[lane];
-    for (int kk = 1; kk < nk; ++kk) cs = cs + sd[kk * NMAX + lane];
-    plane[(size_t)M * N + lane] = cs;
+    plane[(size_t)M * N + lane] = slice_colsum<NMAX>(sd, nk, lane);
   }
 }
 

@@ -237,11 +237,19 @@ outer_dx_kernel(const float* __restrict__ delta, const float* __restrict__ W, in
   const bool loss_block = ld.partials && blockIdx.x == 0 && blockIdx.y == 0;  // block-uniform
   const float p0 = loss_block ? ld.partials[min(t, ld.blocks - 1)] : 0.0f;
   float y[RB], pr[RB];
+  if (aux_pre) {  // uniform: f' from the kept pre-activation
 #pragma unroll
-  for (int r = 0; r < RB; ++r) {
-    const size_t o = (size_t)min(b0 + r, B - 1) * R + jc;
-    y[r] = aux_act[o];
-    pr[r] = pp[o];
+    for (int r = 0; r < RB; ++r) {
+      const size_t o = (size_t)min(b0 + r, B - 1) * R + jc;
+      y[r] = aux_act[o];
+      pr[r] = pp[o];
+    }
+  } else {  // f' from the output: one load per element
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      y[r] = aux_act[(size_t)min(b0 + r, B - 1) * R + jc];
+      pr[r] = y[r];
+    }
   }
   if (t < RB * KMAX) sd[t] = dv;
   __syncthreads();
