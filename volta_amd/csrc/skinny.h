@@ -74,6 +74,32 @@ struct LossDefer {
   float denom = 1.0f;
   DevScalars* scalars = nullptr;
 };
+
+// The step's loss from the output launch's strip partials, by a 256-thread
+// block: 256 partials at a time (one per thread; `p0`, the first chunk's,
+// loaded by the caller before its own work), each chunk added as a fixed
+// tree (wave butterflies, then the four waves in order), the chunks in
+// order; thread 0 stores loss = sum / denom and flags a non-finite one.
+// Every thread of the block calls it (it synchronizes the block).
+__device__ __forceinline__ void deferred_loss_tree(const LossDefer& ld, float p0, int t) {
+  __shared__ float wsum[4];
+  float sum = 0.0f;
+  for (int c = 0; c < ld.blocks; c += 256) {
+    float v = c == 0 ? p0 : ld.partials[min(c + t, ld.blocks - 1)];
+    v = c + t < ld.blocks ? v : 0.0f;
+    v = wave_sum(v);
+    __syncthreads();
+    if ((t & 63) == 0) wsum[t >> 6] = v;
+    __syncthreads();
+    const float cs = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+    sum = c == 0 ? cs : sum + cs;
+  }
+  if (t == 0) {
+    const float loss = sum / ld.denom;
+    ld.scalars->loss = loss;
+    if (!(fabsf(loss) <= 3.402823466e38f)) atomicOr(&ld.scalars->flags, (uint32_t)VOLTA_STATUS_NONFINITE_LOSS);
+  }
+}
 hipError_t launch_outer_dx(const float* delta, const float* W, int B, int R, int K, int act, const float* aux_act,
                            const float* aux_pre, float* out, hipStream_t st, const LossDefer& ld = LossDefer{});
 hipError_t launch_narrow_dw(const NarrowDwArgs& p, hipStream_t st);

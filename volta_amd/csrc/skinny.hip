@@ -263,28 +263,7 @@ outer_dx_kernel(const float* __restrict__ delta, const float* __restrict__ W, in
     }
     if (j < R && b0 + r < B) out[(size_t)(b0 + r) * R + j] = s * act_derivative(act, pr[r], y[r]);
   }
-  if (loss_block) {
-    // the step's loss: the output launch's strip partials, 256 at a time
-    // (one per thread), each chunk added as a fixed tree (wave butterflies,
-    // then the four waves in order), the chunks in order
-    __shared__ float wsum[4];
-    float sum = 0.0f;
-    for (int c = 0; c < ld.blocks; c += 256) {
-      float v = c == 0 ? p0 : ld.partials[min(c + t, ld.blocks - 1)];
-      v = c + t < ld.blocks ? v : 0.0f;
-      v = wave_sum(v);
-      __syncthreads();
-      if ((t & 63) == 0) wsum[t >> 6] = v;
-      __syncthreads();
-      const float cs = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
-      sum = c == 0 ? cs : sum + cs;
-    }
-    if (t == 0) {
-      const float loss = sum / ld.denom;
-      ld.scalars->loss = loss;
-      if (!(fabsf(loss) <= 3.402823466e38f)) atomicOr(&ld.scalars->flags, (uint32_t)VOLTA_STATUS_NONFINITE_LOSS);
-    }
-  }
+  if (loss_block) deferred_loss_tree(ld, p0, t);  // the step's loss
 }
 
 // Stand-alone launch: 64 rows of W per block.
