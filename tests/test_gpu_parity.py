@@ -111,12 +111,16 @@ def test_gemm_integer_exact(layout, M, N, K, tile):
 
 
 @pytest.mark.parametrize("layout", [0], ids=["NN"])
-@pytest.mark.parametrize("M,N,K", [(64, 512, 256), (33, 130, 257), (7, 5, 3), (64, 64, 1024)])
+@pytest.mark.parametrize("M,N,K", [(64, 512, 256), (33, 130, 257), (7, 5, 3), (64, 64, 1024), (48, 200, 512),
+                                   (33, 100, 260), (40, 96, 700)])
 @pytest.mark.parametrize("waves", [8, 16])
 def test_gemm_smallm_8_waves_integer_exact(layout, M, N, K, waves):
     """The 8- and 16-wave small-M workgroups (eighths / sixteenths of K, trees
     of four-tile sums; the forward products' defaults) are exact on integer
-    operands, ragged shapes included."""
+    operands, ragged shapes included.  At 16 waves the A operand goes
+    through LDS strips 64 k wide (K = 1024; K = 700, its last wave range
+    clamped) or 32 k wide (K = 512; K = 260, clamped), K = 256 and 257 on
+    the register path."""
     say(f"gemm small-M {waves} waves layout={layout} M={M} N={N} K={K}")
     rng = np.random.default_rng(M * 5 + N * 3 + K)
     A = rng.integers(-4, 5, (M, K)).astype(np.float32)
