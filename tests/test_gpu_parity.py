@@ -158,6 +158,34 @@ def test_gemm_smallm_nt_16_waves_integer_exact(M, N, K):
     np.testing.assert_array_equal(got, (A.astype(np.int64) @ B.T.astype(np.int64)).astype(np.float32))
 
 
+STAGED_SWEEP = [(m, n, k) for m, n in ((64, 96), (33, 40), (16, 16)) for k in (252, 256, 260, 508, 516, 764, 772, 1020, 1028)]
+
+
+@pytest.mark.parametrize("layout", [0, 1], ids=["NN", "NT"])
+@pytest.mark.parametrize("M,N,K", STAGED_SWEEP)
+def test_gemm_smallm_16_waves_strip_widths_integer_exact(layout, M, N, K):
+    """The 16-wave small-M tile around the staged strip widths' boundaries:
+    wave ranges of 16 k (registers; K <= 256), 32 k (32-k strips; K <= 512),
+    48 k and 64 k (64-k strips, the last wave's range clamped inside its
+    strip), with full, ragged and single-tile M and N: exact on integer
+    operands."""
+    say(f"gemm small-M 16 waves strips layout={layout} M={M} N={N} K={K}")
+    rng = np.random.default_rng(M * 13 + N * 7 + K * 3 + layout)
+    A = rng.integers(-4, 5, (M, K)).astype(np.float32)
+    B = rng.integers(-4, 5, (N, K) if layout == 1 else (K, N)).astype(np.float32)
+    old = os.environ.get("VOLTA_SMALLM_WAVES")
+    os.environ["VOLTA_SMALLM_WAVES"] = "16"
+    try:
+        got = _gemm(layout, A, B, M, N, K, tile=TILE_SMALLM)
+    finally:
+        if old is None:
+            os.environ.pop("VOLTA_SMALLM_WAVES", None)
+        else:
+            os.environ["VOLTA_SMALLM_WAVES"] = old
+    Bm = B.T if layout == 1 else B
+    np.testing.assert_array_equal(got, (A.astype(np.int64) @ Bm.astype(np.int64)).astype(np.float32))
+
+
 TILE_BIG = 5
 
 
