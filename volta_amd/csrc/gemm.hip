@@ -3237,11 +3237,17 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus, bool 
   }
   const int tiles = p.tiles(M, N);
   const int bk = p.tile == TILE_64x64_K64 ? 64 : 32;
-  // Smallest K slice: 64 for the forward products (their reduction is the
-  // bias/activation epilogue, read back by one latency-bound launch), 128
-  // for dX/dW, whose launches are paired and already hold enough workgroups.
+  // Smallest K slice (VOLTA_SPLITK_MIN_K): 128, and 64 for a forward product
+  // with few enough rows for the small-M tile below (a plan that splits K is
+  // what sends it there, K >= 128; the loss-head GEMM of those batches too).  64 for every forward product split C4
+  // B=1024's fwd3 (1024 x 256, K = 512, 64 tiles) four ways instead of two:
+  // 0.2398 -> 0.2382 ms/step with 128 (two alternating rounds), the reduce
+  // reading half the planes.
+  const char* sm = std::getenv("VOLTA_SMALLM_MAX_M");
+  const int small_max = sm && *sm ? std::atoi(sm) : 256;
   const char* mk = std::getenv("VOLTA_SPLITK_MIN_K");
-  const int min_k = mk && *mk ? std::max(32, std::atoi(mk)) : (layout == GEMM_NN ? 64 : 128);
+  const int min_k =
+      mk && *mk ? std::max(32, std::atoi(mk)) : (layout == GEMM_NN && M <= small_max ? 64 : 128);
   const char* ik = std::getenv("VOLTA_SPLITK_INKERNEL");
   p.inkernel_reduce = ik && *ik && *ik != '0';
   const char* sw = std::getenv("VOLTA_SPLITK_WGS_PER_CU");
@@ -3262,8 +3268,6 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus, bool 
   // VOLTA_SMALLM_MAX_M changes the limit, 0 turns the tile off).  Measured
   // with the small-K dW tile below: C4 B=256 0.1624 -> 0.1415 ms/step; at
   // B=1024 both tiles are slower than the 64x64 family (0.45 vs 0.30 ms).
-  const char* sm = std::getenv("VOLTA_SMALLM_MAX_M");
-  const int small_max = sm && *sm ? std::atoi(sm) : 256;
   // ... except a dX product (NT) with a long reduction: there the 16x16
   // tiles' operand re-reads from L2 cost more than the split's reduce launch
   // (C3's dX_1, 64 x 2048 x 2048: 18.4 us on the small-M tile against
