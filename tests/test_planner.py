@@ -124,3 +124,14 @@ def test_narrow_tn_for_long_k():
     assert plan(TN, 64, 1, 256)[0] == TILE_64
     assert plan(TN, 1024, 10, 4096, env={"VOLTA_NARROW_TN": "0"})[0] == TILE_64
     assert plan(TN, 1024, 17, 4096)[0] != TILE_NARROW_TN
+
+
+def test_split_k_smallest_slice():
+    """K slices of at least 128 k, except for forward products of at most 256
+    rows (64: a split plan is what sends them to the small-M tile): C4
+    B=1024's fwd3 (1024 x 256, K = 512) splits in four, not eight;
+    VOLTA_SPLITK_MIN_K=64 restores eight; a 19-row forward product with
+    K = 130 still takes the small-M tile."""
+    assert plan(NN, 1024, 256, 512)[:3] == (TILE_64, 4, 128)
+    assert plan(NN, 1024, 256, 512, env={"VOLTA_SPLITK_MIN_K": "64"})[:3] == (TILE_64, 8, 64)
+    assert plan(NN, 19, 66, 130)[0] == TILE_SMALLM

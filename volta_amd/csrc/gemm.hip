@@ -3239,10 +3239,10 @@ GemmPlan gemm_plan(int layout, int M, int N, int K, bool vec, int num_cus, bool 
   const int bk = p.tile == TILE_64x64_K64 ? 64 : 32;
   // Smallest K slice (VOLTA_SPLITK_MIN_K): 128, and 64 for a forward product
   // with few enough rows for the small-M tile below (a plan that splits K is
-  // what sends it there, K >= 128; the loss-head GEMM of those batches too).  64 for every forward product split C4
-  // B=1024's fwd3 (1024 x 256, K = 512, 64 tiles) four ways instead of two:
-  // 0.2398 -> 0.2382 ms/step with 128 (two alternating rounds), the reduce
-  // reading half the planes.
+  // what sends it there, K >= 128; the loss-head GEMM of those batches too).
+  // 64 for every forward product split C4 B=1024's fwd3 (1024 x 256, K =
+  // 512, 64 tiles) eight ways instead of four: 0.2398 -> 0.2380 ms/step with
+  // 128, the reduce reading half the planes.
   const char* sm = std::getenv("VOLTA_SMALLM_MAX_M");
   const int small_max = sm && *sm ? std::atoi(sm) : 256;
   const char* mk = std::getenv("VOLTA_SPLITK_MIN_K");
